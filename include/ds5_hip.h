@@ -1,0 +1,290 @@
+/*
+ * ds5_hip.h -- C ABI of the MI355X (gfx950) backend for DS5's attention path.
+ *
+ * libds5hip.so is a third kernel backend beside DS5's `cpu` and `metal`
+ * providers. The Zig host binds it with @cImport (the binding is shown in
+ * INTEGRATION.md); every entry point takes plain pointers, sizes and the
+ * structs below, never a torch type.
+ *
+ * Two groups of entry points:
+ *   1. the device context, one per engine, replacing the frozen GPU API
+ *      contracts.assertGpuApi (src/shared/contracts.zig:374-384) that
+ *      src/kernels/cpu/ctx.zig and src/metal/metal.zig implement;
+ *   2. the kernel-provider ops of the attention path, replacing
+ *      rmsNorm / rope / kvAppend / gqaAttention of contracts.assertKernelApi
+ *      (src/shared/contracts.zig:358-367), plus fused and paged extensions
+ *      that the engine may pick up with @hasDecl.
+ *
+ * Status codes are contracts.KernelError (src/shared/contracts.zig:201-206):
+ * every precondition the reference checks is checked here before any launch.
+ * All ops enqueue on the context's single HIP stream and return without
+ * waiting; ds5_hip_download and ds5_hip_submit synchronise.
+ */
+#ifndef DS5_HIP_H
+#define DS5_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: contracts.zig:201-206 KernelError ------------------- */
+#define DS5_OK 0
+#define DS5_SHAPE_MISMATCH 1    /* KernelError.ShapeMismatch */
+#define DS5_UNSUPPORTED_DTYPE 2 /* KernelError.UnsupportedDtype */
+#define DS5_DEVICE_FAILURE 3    /* KernelError.DeviceFailure: any HIP error */
+#define DS5_OUT_OF_MEMORY 4     /* KernelError.OutOfMemory */
+
+/* ---- dtypes: contracts.zig:22-24 (GGML type ids) ------------------------ */
+#define DS5_DTYPE_F32 0u
+#define DS5_DTYPE_F16 1u
+
+/* contracts.zig:210-214 `Buf = extern struct { handle, offset, len }`, 24 B.
+ * handle = base of a device allocation owned by the context; offset and len
+ * are bytes and every op honours them (ctx.zig:70-108 semantics). */
+typedef struct ds5_buf {
+    void* handle;
+    uint64_t offset;
+    uint64_t len;
+} ds5_buf;
+
+typedef struct ds5_hip_ctx ds5_hip_ctx;
+
+/* ========================================================================
+ * 1. Device context (contracts.zig:374-384 assertGpuApi)
+ * ======================================================================== */
+
+/* Ctx.init (metal.zig:131, ctx.zig:20): picks device `device_index`
+ * (0 for the first visible GPU) and creates the context's stream and
+ * timing events. */
+int ds5_hip_init(int device_index, ds5_hip_ctx** out);
+
+/* Ctx.deinit (ctx.zig:26-30): waits for the stream, frees every buffer the
+ * context created, destroys the stream. */
+void ds5_hip_deinit(ds5_hip_ctx* ctx);
+
+/* Ctx.createBuffer (ctx.zig:32-38, metal.zig:239-250): zero-filled device
+ * allocation of len bytes, owned by the context. */
+int ds5_hip_create_buffer(ds5_hip_ctx* ctx, uint64_t len, ds5_buf* out);
+
+/* Ctx.bufferFromBytes (metal.zig:280-306): HIP has no zero-copy wrap of
+ * pageable host memory into device storage, so this allocates a context-owned
+ * device buffer and copies the bytes; the caller keeps ownership of `bytes`. */
+int ds5_hip_buffer_from_bytes(ds5_hip_ctx* ctx, const void* bytes, uint64_t len, ds5_buf* out);
+
+/* Ctx.upload / Ctx.download (ctx.zig:47-55, metal.zig:309-336): byte copies
+ * at `offset` within the view. Both return after the copy is complete;
+ * download first drains everything already enqueued (the Metal glue's
+ * auto-flush, metal.zig:326-329). */
+int ds5_hip_upload(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t offset, const void* bytes, uint64_t len);
+int ds5_hip_download(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t offset, void* out, uint64_t len);
+
+/* Ctx.begin / Ctx.submit / Ctx.gpuElapsedNs (metal.zig:360-393): begin records
+ * a start event on the stream; submit records an end event and blocks until
+ * the stream is idle; gpu_elapsed_ns is the device time between the last
+ * begin/submit pair (0 if no batch completed). */
+void ds5_hip_begin(ds5_hip_ctx* ctx);
+int ds5_hip_submit(ds5_hip_ctx* ctx);
+uint64_t ds5_hip_gpu_elapsed_ns(ds5_hip_ctx* ctx);
+
+/* Text of the most recent failure on this context (empty if none). */
+const char* ds5_hip_last_error(ds5_hip_ctx* ctx);
+
+/* The context's HIP stream (a hipStream_t), for hosts that interleave their
+ * own device work with these ops. */
+void* ds5_hip_stream(ds5_hip_ctx* ctx);
+
+/* Per-kernel device timing (no reference counterpart; the reference times
+ * whole command buffers, metal.zig:369-389). When enabled, every kernel
+ * launch of this context is bracketed by events on its stream; submit and
+ * ds5_hip_kernel_time resolve them. Enabling (or disabling) clears the
+ * totals. kernel_time reports the launches and summed device nanoseconds of
+ * the kernel named `kernel` (e.g. "decode_splitk_kernel"). */
+int ds5_hip_set_kernel_timing(ds5_hip_ctx* ctx, int enable);
+int ds5_hip_kernel_time(ds5_hip_ctx* ctx, const char* kernel, uint64_t* launches, double* total_ns);
+
+/* Stream capture into a replayable HIP graph (no reference counterpart; the
+ * Metal glue batches a layer's dispatches into one command buffer,
+ * kernels/gpu/kernels.zig:112-119). Ops called between capture_begin and
+ * capture_end are recorded, not run; capture_end returns an executable graph
+ * (a hipGraphExec_t) that graph_launch replays on the context stream with the
+ * argument values of the capture. Ops that would allocate (a first split-K
+ * decode at a new size grows the workspace) must run once before capture. */
+int ds5_hip_capture_begin(ds5_hip_ctx* ctx);
+int ds5_hip_capture_end(ds5_hip_ctx* ctx, void** graph_exec);
+int ds5_hip_graph_launch(ds5_hip_ctx* ctx, void* graph_exec);
+void ds5_hip_graph_destroy(void* graph_exec);
+
+/* ========================================================================
+ * 2. Kernel-provider ops (contracts.zig:358-367 assertKernelApi)
+ * ======================================================================== */
+
+/* contracts.zig:218-225 RmsNormArgs. y = x * (1/sqrt(mean(x^2) + eps)) * w
+ * rowwise; `out` may alias `x`. Replaces kernels_a.zig:68-91 rmsNorm and the
+ * Metal rmsnorm_f32 dispatch (kernels/gpu/kernels.zig:146-157). */
+typedef struct ds5_rms_norm_args {
+    ds5_buf x;      /* f32 [n_rows, dim] */
+    ds5_buf weight; /* f32 [dim] */
+    ds5_buf out;    /* f32 [n_rows, dim] */
+    uint32_t n_rows;
+    uint32_t dim;
+    float eps;
+} ds5_rms_norm_args;
+int ds5_hip_rms_norm(ds5_hip_ctx* ctx, const ds5_rms_norm_args* args);
+
+/* contracts.zig:230-238 RopeArgs. In-place NeoX rotation, element i pairs
+ * with i + head_dim/2, angle = pos * freq_scale * theta^(-2i/head_dim).
+ * Replaces kernels_a.zig:97-130 rope (Metal: kernels/gpu/kernels.zig:163-180).
+ * head_dim must be even and at most 512. */
+typedef struct ds5_rope_args {
+    ds5_buf x;         /* f32 [n_tokens, n_heads, head_dim], rotated in place */
+    ds5_buf positions; /* i32 [n_tokens] absolute positions */
+    uint32_t n_tokens;
+    uint32_t n_heads;
+    uint32_t head_dim;
+    float theta;
+    float freq_scale; /* 1.0 in the reference engine */
+} ds5_rope_args;
+int ds5_hip_rope(ds5_hip_ctx* ctx, const ds5_rope_args* args);
+
+/* contracts.zig:256-267 KvAppendArgs. Scatter [n_tokens, n_kv_heads,
+ * head_dim] f32 into the frozen cache layout [n_kv_heads, max_ctx, head_dim]
+ * at positions pos..pos+n_tokens-1; an f16 cache stores the IEEE
+ * round-to-nearest-even cast. Replaces kernels_a.zig:169-217 kvAppend
+ * (Metal: kernels/gpu/kernels.zig:210-235). */
+typedef struct ds5_kv_append_args {
+    ds5_buf k_new;   /* f32 [n_tokens, n_kv_heads, head_dim] */
+    ds5_buf v_new;   /* f32 [n_tokens, n_kv_heads, head_dim] */
+    ds5_buf k_cache; /* kv_dtype [n_kv_heads, max_ctx, head_dim] */
+    ds5_buf v_cache; /* kv_dtype [n_kv_heads, max_ctx, head_dim] */
+    uint32_t kv_dtype;
+    uint32_t pos;
+    uint32_t n_tokens;
+    uint32_t n_kv_heads;
+    uint32_t head_dim;
+    uint32_t max_ctx;
+} ds5_kv_append_args;
+int ds5_hip_kv_append(ds5_hip_ctx* ctx, const ds5_kv_append_args* args);
+
+/* contracts.zig:272-286 AttnArgs. Causal GQA attention: query token t sits at
+ * pos + t and attends cache positions 0..pos+t; q head h reads kv head
+ * h / (n_q_heads / n_kv_heads); softmax in f32. max_ctx is the cache STRIDE,
+ * not the valid length. Replaces kernels_b.zig:29-133 gqaAttention (Metal:
+ * kernels/gpu/kernels.zig:254-286). n_tokens == 1 runs the split-K
+ * flash-decoding kernels, n_tokens > 1 the causal MFMA prefill kernel
+ * (f16 cache, head_dim 64 or 128); other shapes and f32 caches run a generic
+ * streaming kernel. All paths are device code. */
+typedef struct ds5_attn_args {
+    ds5_buf q;       /* f32 [n_tokens, n_q_heads, head_dim], post-norm post-rope */
+    ds5_buf k_cache; /* kv_dtype [n_kv_heads, max_ctx, head_dim] */
+    ds5_buf v_cache; /* kv_dtype [n_kv_heads, max_ctx, head_dim] */
+    uint32_t kv_dtype;
+    ds5_buf out;     /* f32 [n_tokens, n_q_heads * head_dim] */
+    uint32_t pos;
+    uint32_t n_tokens;
+    uint32_t n_q_heads;
+    uint32_t n_kv_heads;
+    uint32_t head_dim;
+    uint32_t max_ctx;
+    float scale; /* 1/sqrt(head_dim) in the engine (forward.zig:308) */
+} ds5_attn_args;
+int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* args);
+
+/* ========================================================================
+ * 3. Fused extensions (optional decls; the engine uses them via @hasDecl)
+ * ======================================================================== */
+
+/* One layer's attention block in the engine's op order
+ * (src/engine/forward.zig:345-412): per-head RMSNorm of q and k with
+ * q_norm / k_norm, NeoX rope of q and k, append of k and v into the cache,
+ * then causal GQA attention -- with the same cache rows and attention output
+ * as the six separate ops. q and k are scratch: their contents after the call
+ * are unspecified (the fused kernels leave them as they were; other shapes run
+ * the separate ops in place). Decode (n_tokens == 1, f16 cache, head_dim
+ * 64/128) is ONE kernel launch plus, for long contexts, a split-K merge
+ * launch; prefill is a k/v append launch plus one attention launch that
+ * normalises and rotates q itself. The engine's per-op trace points
+ * (forward.zig:361-380) are not produced on this path. */
+typedef struct ds5_attention_step_args {
+    ds5_buf q;         /* f32 [n_tokens, n_q_heads, head_dim] q projection (in/out) */
+    ds5_buf k;         /* f32 [n_tokens, n_kv_heads, head_dim] k projection (in/out) */
+    ds5_buf v;         /* f32 [n_tokens, n_kv_heads, head_dim] v projection */
+    ds5_buf q_norm;    /* f32 [head_dim] */
+    ds5_buf k_norm;    /* f32 [head_dim] */
+    ds5_buf positions; /* i32 [n_tokens]; the engine passes pos..pos+n_tokens-1 */
+    ds5_buf k_cache;   /* kv_dtype [n_kv_heads, max_ctx, head_dim] */
+    ds5_buf v_cache;
+    ds5_buf out;       /* f32 [n_tokens, n_q_heads * head_dim] */
+    uint32_t kv_dtype;
+    uint32_t pos;
+    uint32_t n_tokens;
+    uint32_t n_q_heads;
+    uint32_t n_kv_heads;
+    uint32_t head_dim;
+    uint32_t max_ctx;
+    float eps;
+    float theta;
+    float freq_scale;
+    float scale;
+} ds5_attention_step_args;
+int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* args);
+
+/* ========================================================================
+ * 4. Paged KV decode (no reference counterpart: the reference has no paged
+ *    cache; its spec names a "KV page table", docs/specs/DS5_Project_Spec_v0.3.md:65)
+ * ======================================================================== */
+
+/* Pool layout: the frozen cache layout with the pool as the position axis,
+ * f16 [n_kv_heads, n_pages * page_size, head_dim]; a page is page_size
+ * consecutive slots. Sequence b's position p lives in slot
+ *     page_table[b * max_pages + p / page_size] * page_size + p % page_size.
+ * One decode token per sequence: its q/k/v are normalised and rotated at
+ * position seq_lens[b] - 1, k/v are appended into that slot, and the token
+ * attends positions 0..seq_lens[b]-1. max_seq_len is a host-side upper bound
+ * of seq_lens (it sizes the launch); sequences longer than it are rejected by
+ * the kernel through the status buffer. */
+typedef struct ds5_paged_decode_args {
+    ds5_buf q;          /* f32 [n_seqs, n_q_heads, head_dim] (in/out: normalised + rotated) */
+    ds5_buf k;          /* f32 [n_seqs, n_kv_heads, head_dim] (in/out) */
+    ds5_buf v;          /* f32 [n_seqs, n_kv_heads, head_dim] */
+    ds5_buf q_norm;     /* f32 [head_dim] */
+    ds5_buf k_norm;     /* f32 [head_dim] */
+    ds5_buf k_pool;     /* f16 [n_kv_heads, n_pages * page_size, head_dim] */
+    ds5_buf v_pool;
+    ds5_buf page_table; /* i32 [n_seqs, max_pages] */
+    ds5_buf seq_lens;   /* i32 [n_seqs], each >= 1, includes the appended token */
+    ds5_buf out;        /* f32 [n_seqs, n_q_heads * head_dim] */
+    uint32_t n_seqs;
+    uint32_t n_q_heads;
+    uint32_t n_kv_heads;
+    uint32_t head_dim;
+    uint32_t page_size;
+    uint32_t n_pages;
+    uint32_t max_pages;
+    uint32_t max_seq_len;
+    float eps;
+    float theta;
+    float freq_scale;
+    float scale;
+} ds5_paged_decode_args;
+int ds5_hip_paged_decode(ds5_hip_ctx* ctx, const ds5_paged_decode_args* args);
+
+/* ========================================================================
+ * 5. Bench/test utility (no reference counterpart)
+ * ======================================================================== */
+
+/* inv_freq[i] = theta^(-(2i)/head_dim), i < head_dim/2, exactly as the rope
+ * kernels use it (std.math.pow(f32) evaluation order, kernels_a.zig:119-120).
+ * Host-only; lets tests pin the table against the CPU reference. */
+int ds5_hip_rope_table(float theta, uint32_t head_dim, float* out);
+
+/* Fill `n` f16 values at buf with N(0,1) draws from a counter-based generator
+ * (seed, element index) on the device. Lets benchmarks build multi-GB caches
+ * without host generation; results are deterministic for a given seed. */
+int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DS5_HIP_H */

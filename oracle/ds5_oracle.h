@@ -1,0 +1,120 @@
+/*
+ * ds5_oracle.h -- CPU restatement of DS5's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP backend:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * it. Nothing in the qw3_amd product links or calls it.
+ *
+ * Each function restates one function of the reference's CPU backend, in the
+ * same loop order and with the same f32 operation order (compiled with
+ * -ffp-contract=off, so a*b+c is never fused, like Zig's strict float mode):
+ *
+ *   ds5o_rms_norm       src/kernels/cpu/kernels_a.zig:68-91
+ *   ds5o_rope           src/kernels/cpu/kernels_a.zig:97-130
+ *   ds5o_kv_append      src/kernels/cpu/kernels_a.zig:169-217
+ *   ds5o_gqa_attention  src/kernels/cpu/kernels_b.zig:29-133
+ *
+ * Argument structs mirror src/shared/contracts.zig:210-286 (Buf and the
+ * RmsNorm/Rope/KvAppend/Attn args); buffer views honour offset and len as
+ * src/kernels/cpu/ctx.zig:70-108 does, and the same ShapeMismatch /
+ * UnsupportedDtype checks run before any arithmetic.
+ *
+ * The paged-KV functions have no reference code (the reference has no paged
+ * cache); they are defined by reduction to the contiguous functions above.
+ */
+#ifndef DS5_ORACLE_H
+#define DS5_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* contracts.zig:201-206 KernelError, as status codes. */
+enum {
+    DS5O_OK = 0,
+    DS5O_SHAPE_MISMATCH = 1,
+    DS5O_UNSUPPORTED_DTYPE = 2,
+    DS5O_DEVICE_FAILURE = 3,
+    DS5O_OUT_OF_MEMORY = 4,
+};
+
+/* contracts.zig:22-24 Dtype ids (GGML type ids). */
+enum { DS5O_F32 = 0, DS5O_F16 = 1 };
+
+/* contracts.zig:210-214 Buf: handle is a host pointer for this oracle. */
+typedef struct ds5o_buf {
+    void* handle;
+    uint64_t offset;
+    uint64_t len;
+} ds5o_buf;
+
+typedef struct ds5o_rms_norm_args { /* contracts.zig:218-225 */
+    ds5o_buf x, weight, out;
+    uint32_t n_rows, dim;
+    float eps;
+} ds5o_rms_norm_args;
+
+typedef struct ds5o_rope_args { /* contracts.zig:230-238 */
+    ds5o_buf x, positions;
+    uint32_t n_tokens, n_heads, head_dim;
+    float theta, freq_scale;
+} ds5o_rope_args;
+
+typedef struct ds5o_kv_append_args { /* contracts.zig:256-267 */
+    ds5o_buf k_new, v_new, k_cache, v_cache;
+    uint32_t kv_dtype, pos, n_tokens, n_kv_heads, head_dim, max_ctx;
+} ds5o_kv_append_args;
+
+typedef struct ds5o_attn_args { /* contracts.zig:272-286 */
+    ds5o_buf q, k_cache, v_cache;
+    uint32_t kv_dtype;
+    ds5o_buf out;
+    uint32_t pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
+    float scale;
+} ds5o_attn_args;
+
+int ds5o_rms_norm(const ds5o_rms_norm_args* a);
+int ds5o_rope(const ds5o_rope_args* a);
+int ds5o_kv_append(const ds5o_kv_append_args* a);
+int ds5o_gqa_attention(const ds5o_attn_args* a);
+
+/* std.math.pow(f32, x, y) as Zig's standard library computes it (see the
+ * definition for the algorithm); exported so tests can pin it. */
+float ds5o_zig_powf(float x, float y);
+
+/* f32 -> f16 bits, IEEE-754 round-to-nearest-even (Zig's @floatCast), and the
+ * exact widening f16 -> f32. */
+uint16_t ds5o_f32_to_f16(float x);
+float ds5o_f16_to_f32(uint16_t h);
+void ds5o_f32_to_f16_array(const float* x, uint16_t* out, uint64_t n);
+void ds5o_f16_to_f32_array(const uint16_t* h, float* out, uint64_t n);
+
+/* Paged KV (no reference counterpart). Pool layout is the frozen cache layout
+ * [n_kv_heads, n_pages * page_size, head_dim] with slots grouped into pages of
+ * page_size consecutive slots. Sequence position p lives in slot
+ *     page_table[p / page_size] * page_size + p % page_size.             */
+int64_t ds5o_paged_slot(const int32_t* page_table, uint32_t n_table, uint32_t page_size, uint32_t p);
+
+/* Copy positions 0..len-1 of one sequence from a paged f16 pool into a
+ * contiguous f16 cache [n_kv_heads, len, head_dim]. Returns a status code. */
+int ds5o_paged_gather_f16(const uint16_t* pool, uint64_t pool_slots, const int32_t* page_table,
+                          uint32_t n_table, uint32_t page_size, uint32_t len, uint32_t n_kv_heads,
+                          uint32_t head_dim, uint16_t* out);
+
+/* Post-norm, post-rope f32 per-head pipeline of one engine step on the
+ * contiguous cache, in the engine's op order (src/engine/forward.zig:345-412):
+ * q_norm, k_norm, rope q, rope k, kvAppend, gqaAttention. q, k, v are
+ * modified in place like the engine's scratch buffers. */
+typedef struct ds5o_step_args {
+    ds5o_buf q, k, v, q_norm_w, k_norm_w, positions, k_cache, v_cache, out;
+    uint32_t kv_dtype, pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
+    float eps, theta, freq_scale, scale;
+} ds5o_step_args;
+int ds5o_attention_step(const ds5o_step_args* a);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,211 @@
+// ds5_common.hpp -- shared types and helpers of the gfx950 attention backend.
+//
+// Host side: the context object behind ds5_hip_ctx, error helpers, and the
+// launch functions each kernel file exports to the C-ABI op layer.
+// Device side: vector types, MFMA wrappers, wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ds5_hip.h"
+
+// ---------------------------------------------------------------------------
+// Vector types (clang ext_vector_type: what the MFMA builtins take)
+// ---------------------------------------------------------------------------
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Rope inverse-frequency table: inv[i] = theta^(-(2i)/head_dim) evaluated the
+// way the reference's std.math.pow(f32) evaluates it (see ds5_rope_table in
+// ds5_ops.hip). Passed by value as a kernel argument; head_dim <= 512.
+// ---------------------------------------------------------------------------
+constexpr int DS5_MAX_ROPE_HALF = 256;
+struct RopeTable {
+    float inv[DS5_MAX_ROPE_HALF];
+};
+
+// ---------------------------------------------------------------------------
+// Context (the object behind the opaque ds5_hip_ctx handle)
+// ---------------------------------------------------------------------------
+struct ds5_hip_ctx {
+    int device = 0;
+    int cu_count = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_begin = nullptr;
+    hipEvent_t ev_end = nullptr;
+    bool batch_open = false;
+    uint64_t elapsed_ns = 0;
+    std::vector<void*> owned;  // device allocations freed at deinit
+    std::string last_error;
+    // Split-K partial results: grown on demand, owned by the context.
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    // Decode tuning: positions per split-K workgroup (0 = heuristic).
+    uint32_t decode_chunk = 0;
+    // Optional per-kernel timing: events recorded around every launch on the
+    // context stream, resolved at submit / query time.
+    bool kernel_timing = false;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
+    struct Pending {
+        const char* name;
+        hipEvent_t start, end;
+    };
+    std::vector<Pending> pending;
+    std::map<std::string, std::pair<double, uint64_t>> kernel_ns;  // name -> (total ns, launches)
+};
+
+// Brackets one kernel launch with timing events when timing is enabled.
+int ds5_timer_start(ds5_hip_ctx* ctx, hipEvent_t* ev);
+void ds5_timer_stop(ds5_hip_ctx* ctx, const char* name, hipEvent_t start);
+int ds5_timers_resolve(ds5_hip_ctx* ctx);
+
+int ds5_fail(ds5_hip_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+int ds5_hip_status(ds5_hip_ctx* ctx, hipError_t err, const char* what);
+int ds5_after_launch(ds5_hip_ctx* ctx, const char* what);
+int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out);
+void ds5_rope_table(float theta, uint32_t head_dim, RopeTable* t);
+
+#define DS5_TIMED_LAUNCH(ctx, name, ...)        \
+    do {                                        \
+        hipEvent_t ds5_t0_ = nullptr;           \
+        ds5_timer_start((ctx), &ds5_t0_);       \
+        hipLaunchKernelGGL(__VA_ARGS__);        \
+        ds5_timer_stop((ctx), (name), ds5_t0_); \
+    } while (0)
+
+static inline void* ds5_ptr(ds5_buf b) { return (char*)b.handle + b.offset; }
+
+// ---------------------------------------------------------------------------
+// Launchers exported by the kernel files (preconditions already checked)
+// ---------------------------------------------------------------------------
+struct RmsNormLaunch {
+    const float* x;
+    const float* w;
+    float* out;
+    uint32_t n_rows, dim;
+    float eps;
+};
+int launch_rms_norm(ds5_hip_ctx* ctx, const RmsNormLaunch& a);
+
+struct RopeLaunch {
+    float* x;
+    const int32_t* positions;
+    uint32_t n_tokens, n_heads, head_dim;
+    float freq_scale;
+    const RopeTable* table;
+};
+int launch_rope(ds5_hip_ctx* ctx, const RopeLaunch& a);
+
+struct KvAppendLaunch {
+    const float* k_new;
+    const float* v_new;
+    void* k_cache;
+    void* v_cache;
+    uint32_t kv_dtype, pos, n_tokens, n_kv_heads, head_dim, max_ctx;
+};
+int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a);
+
+// Norm + rope of k, append of k and v, for n_tokens rows (prefill pre-pass
+// of the fused step). Leaves q untouched.
+struct KvPrepLaunch {
+    const float* k;
+    const float* v;
+    const float* k_norm;
+    const int32_t* positions;
+    f16* k_cache;
+    f16* v_cache;
+    uint32_t pos, n_tokens, n_kv_heads, head_dim, max_ctx;
+    float eps, freq_scale;
+    const RopeTable* table;
+};
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a);
+
+// Generic causal GQA attention (any head_dim <= 512, f32 or f16 cache).
+struct GenericAttnLaunch {
+    const float* q;
+    const void* k_cache;
+    const void* v_cache;
+    float* out;
+    uint32_t kv_dtype, pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
+    float scale;
+};
+int launch_generic_attention(ds5_hip_ctx* ctx, const GenericAttnLaunch& a);
+
+// Split-K MFMA decode (one query token per sequence), f16 cache, head_dim 64
+// or 128. Covers the contiguous and paged caches, with or without the fused
+// norm/rope/append prologue.
+struct DecodeLaunch {
+    // query / new token (fused: raw projections; unfused: q post-rope only)
+    const float* q;          // [n_seqs, n_q_heads, head_dim]
+    const float* k_new;      // fused only: [n_seqs, n_kv_heads, head_dim]
+    const float* v_new;      // fused only
+    const float* q_norm;     // fused only: [head_dim]
+    const float* k_norm;     // fused only
+    const int32_t* positions;  // fused contiguous: rope position of the token
+    // cache (contiguous when page_table == nullptr)
+    f16* k_cache;
+    f16* v_cache;
+    uint64_t cache_stride;   // positions per kv head: max_ctx or pool slots
+    const int32_t* page_table;  // [n_seqs, max_pages] or nullptr
+    const int32_t* seq_lens;    // [n_seqs] (paged) or nullptr
+    uint32_t page_size, max_pages;
+    uint32_t ctx_len;        // contiguous: attended positions (pos + 1)
+    uint32_t max_len;        // upper bound of attended positions (sizes the grid)
+    int32_t* status;         // paged: device flag set when a sequence is out of range
+    float* out;              // [n_seqs, n_q_heads * head_dim]
+    uint32_t n_seqs, n_q_heads, n_kv_heads, head_dim;
+    float scale, eps, freq_scale;
+    bool fused;
+    const RopeTable* table;
+};
+int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a);
+
+// Causal flash-attention prefill on f16 MFMA (head_dim 128 or 64).
+struct PrefillLaunch {
+    const float* q;          // [n_tokens, n_q_heads, head_dim]
+    const float* q_norm;     // non-null: q is raw and is normalised + rotated in-kernel
+    const int32_t* positions;
+    const f16* k_cache;
+    const f16* v_cache;
+    float* out;
+    uint32_t pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
+    float scale, eps, freq_scale;
+    const RopeTable* table;
+};
+int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a);
+
+int launch_fill_normal_f16(ds5_hip_ctx* ctx, f16* out, uint64_t n, uint64_t seed);
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+#if defined(__HIP_DEVICE_COMPILE__)
+#define DS5_DEVICE_INLINE __device__ __forceinline__
+#else
+#define DS5_DEVICE_INLINE __device__ inline
+#endif
+
+DS5_DEVICE_INLINE f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+DS5_DEVICE_INLINE f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Lane exchange within the 64-wide wavefront (ds_bpermute based).
+DS5_DEVICE_INLINE float lane_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+DS5_DEVICE_INLINE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -1,0 +1,398 @@
+// ds5_ops.hip -- the kernel-provider entry points of the C ABI.
+//
+// Each entry point checks the reference's preconditions, in the reference's
+// order, before anything is enqueued (the GPU kernels have no error channel,
+// as PORTING-kernels-a.md / -b.md require of the Metal glue), then dispatches:
+//   rmsNorm       kernels_a.zig:68-91   -> rms_norm_kernel
+//   rope          kernels_a.zig:97-130  -> rope_kernel
+//   kvAppend      kernels_a.zig:169-217 -> kv_append_kernel
+//   gqaAttention  kernels_b.zig:29-133  -> decode_splitk_kernel (+ merge),
+//                                          prefill_kernel, or the generic kernel
+#include <math.h>
+
+#include "ds5_common.hpp"
+
+// ---------------------------------------------------------------------------
+// Rope inverse frequencies, evaluated as the reference evaluates
+// std.math.pow(f32, theta, -(2i/head_dim)) in kernels_a.zig:119-120: the Zig
+// standard library splits |y| into integer and fraction parts, takes
+// exp(frac * log x) (fractions above one half are shifted down by one into the
+// integer part), multiplies in x^int by repeated squaring of frexp(x), and for
+// a negative exponent takes the reciprocal before the final ldexp. The host C
+// library supplies expf/logf. Built once per (theta, head_dim) on the host and
+// passed to the kernels by value.
+// ---------------------------------------------------------------------------
+static float pow_f32_like_reference(float x, float y) {
+    if (y == 0.0f || x == 1.0f) return 1.0f;
+    if (isnan(x) || isnan(y)) return NAN;
+    if (y == 1.0f) return x;
+    if (!(x > 0.0f) || isinf(x) || isinf(y)) return powf(x, y);
+    if (y == 0.5f) return sqrtf(x);
+    if (y == -0.5f) return 1.0f / sqrtf(x);
+    float int_part;
+    float frac = modff(fabsf(y), &int_part);
+    if (int_part >= 2147483648.0f) return powf(x, y);
+    float mant_acc = 1.0f;
+    int exp_acc = 0;
+    if (frac != 0.0f) {
+        if (frac > 0.5f) {
+            frac -= 1.0f;
+            int_part += 1.0f;
+        }
+        mant_acc = expf(frac * logf(x));
+    }
+    int xe;
+    float xm = frexpf(x, &xe);
+    for (int32_t n = (int32_t)int_part; n != 0; n >>= 1) {
+        if (xe < -512 || xe > 512) {
+            exp_acc += xe;
+            break;
+        }
+        if (n & 1) {
+            mant_acc *= xm;
+            exp_acc += xe;
+        }
+        xm *= xm;
+        xe <<= 1;
+        if (xm < 0.5f) {
+            xe -= 1;
+            xm += xm;
+        }
+    }
+    if (y < 0.0f) {
+        mant_acc = 1.0f / mant_acc;
+        exp_acc = -exp_acc;
+    }
+    return scalbnf(mant_acc, exp_acc);
+}
+
+void ds5_rope_table(float theta, uint32_t head_dim, RopeTable* t) {
+    const uint32_t half = head_dim / 2;
+    for (uint32_t i = 0; i < DS5_MAX_ROPE_HALF; i++) {
+        if (i < half) {
+            const float expnt = (float)(2 * i) / (float)head_dim;
+            t->inv[i] = pow_f32_like_reference(theta, -expnt);
+        } else {
+            t->inv[i] = 0.0f;
+        }
+    }
+}
+
+namespace {
+
+bool covers(ds5_buf b, uint64_t bytes) { return b.len >= bytes && (bytes == 0 || b.handle != nullptr); }
+
+bool aligned16(ds5_buf b) { return ((uintptr_t)ds5_ptr(b) & 15u) == 0; }
+
+uint64_t cache_elem_bytes(uint32_t kv_dtype) {
+    return kv_dtype == DS5_DTYPE_F32 ? 4 : kv_dtype == DS5_DTYPE_F16 ? 2 : 0;
+}
+
+struct TableCache {
+    float theta = NAN;
+    uint32_t head_dim = 0;
+    RopeTable table;
+};
+
+const RopeTable* rope_table_for(float theta, uint32_t head_dim) {
+    static thread_local TableCache cache;
+    if (!(cache.theta == theta) || cache.head_dim != head_dim) {
+        ds5_rope_table(theta, head_dim, &cache.table);
+        cache.theta = theta;
+        cache.head_dim = head_dim;
+    }
+    return &cache.table;
+}
+
+// Runs after the preconditions, so shape errors are reported even without a
+// device context (a null context then fails with DeviceFailure).
+int set_device(ds5_hip_ctx* ctx) {
+    if (!ctx) return DS5_DEVICE_FAILURE;
+    return ds5_hip_status(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+}
+
+}  // namespace
+
+extern "C" {
+
+int ds5_hip_rms_norm(ds5_hip_ctx* ctx, const ds5_rms_norm_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t n_rows = a->n_rows, dim = a->dim;
+    if (dim == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rms_norm: dim == 0");
+    if (!covers(a->x, n_rows * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rms_norm: x too small");
+    if (!covers(a->out, n_rows * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rms_norm: out too small");
+    if (!covers(a->weight, dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rms_norm: weight too small");
+    if (int rc = set_device(ctx)) return rc;
+    RmsNormLaunch l{(const float*)ds5_ptr(a->x), (const float*)ds5_ptr(a->weight), (float*)ds5_ptr(a->out),
+                    a->n_rows, a->dim, a->eps};
+    return launch_rms_norm(ctx, l);
+}
+
+int ds5_hip_rope(ds5_hip_ctx* ctx, const ds5_rope_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t T = a->n_tokens, H = a->n_heads, hd = a->head_dim;
+    if (hd == 0 || hd % 2 != 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rope: head_dim must be even and > 0");
+    if (!covers(a->x, T * H * hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rope: x too small");
+    if (!covers(a->positions, T * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rope: positions too small");
+    if (hd > 2 * DS5_MAX_ROPE_HALF) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "rope: head_dim > 512");
+    if (int rc = set_device(ctx)) return rc;
+    RopeLaunch l{(float*)ds5_ptr(a->x), (const int32_t*)ds5_ptr(a->positions), a->n_tokens, a->n_heads,
+                 a->head_dim, a->freq_scale, rope_table_for(a->theta, a->head_dim)};
+    return launch_rope(ctx, l);
+}
+
+int ds5_hip_kv_append(ds5_hip_ctx* ctx, const ds5_kv_append_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t T = a->n_tokens, H = a->n_kv_heads, hd = a->head_dim, cap = a->max_ctx;
+    if (hd == 0 || H == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "kv_append: head_dim/n_kv_heads == 0");
+    if ((uint64_t)a->pos + T > cap) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "kv_append: pos + n_tokens > max_ctx");
+    const uint64_t new_bytes = T * H * hd * 4;
+    if (!covers(a->k_new, new_bytes) || !covers(a->v_new, new_bytes))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "kv_append: k_new/v_new too small");
+    const uint64_t eb = cache_elem_bytes(a->kv_dtype);
+    if (!eb) return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "kv_append: kv_dtype %u", a->kv_dtype);
+    if (!covers(a->k_cache, H * cap * hd * eb) || !covers(a->v_cache, H * cap * hd * eb))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "kv_append: cache too small");
+    if (int rc = set_device(ctx)) return rc;
+    KvAppendLaunch l{(const float*)ds5_ptr(a->k_new), (const float*)ds5_ptr(a->v_new), ds5_ptr(a->k_cache),
+                     ds5_ptr(a->v_cache), a->kv_dtype, a->pos, a->n_tokens, a->n_kv_heads, a->head_dim,
+                     a->max_ctx};
+    return launch_kv_append(ctx, l);
+}
+
+static int check_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
+    const uint64_t hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
+    const uint64_t T = a->n_tokens, pos = a->pos, cap = a->max_ctx;
+    if (hq == 0 || hkv == 0 || hd == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: zero heads or head_dim");
+    if (hq % hkv != 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: n_q_heads %% n_kv_heads != 0");
+    if (pos + T > cap) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: pos + n_tokens > max_ctx");
+    const uint64_t q_bytes = T * hq * hd * 4;
+    if (!covers(a->q, q_bytes) || !covers(a->out, q_bytes))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: q/out too small");
+    const uint64_t eb = cache_elem_bytes(a->kv_dtype);
+    if (!eb) return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "attention: kv_dtype %u", a->kv_dtype);
+    if (!covers(a->k_cache, hkv * cap * hd * eb) || !covers(a->v_cache, hkv * cap * hd * eb))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: cache too small");
+    if (hd > 512) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention: head_dim > 512");
+    return DS5_OK;
+}
+
+// MFMA kernels: f16 cache, head_dim 64 or 128, 16-byte aligned views.
+static bool mfma_shape(uint32_t kv_dtype, uint32_t head_dim, std::initializer_list<ds5_buf> bufs) {
+    if (kv_dtype != DS5_DTYPE_F16 || (head_dim != 64 && head_dim != 128)) return false;
+    for (const ds5_buf& b : bufs)
+        if (!aligned16(b)) return false;
+    return true;
+}
+
+int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (int rc = check_attention(ctx, a)) return rc;
+    if (a->n_tokens == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    if (mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k_cache, a->v_cache, a->out})) {
+        if (a->n_tokens == 1) {
+            DecodeLaunch l{};
+            l.q = (const float*)ds5_ptr(a->q);
+            l.k_cache = (f16*)ds5_ptr(a->k_cache);
+            l.v_cache = (f16*)ds5_ptr(a->v_cache);
+            l.cache_stride = a->max_ctx;
+            l.ctx_len = a->pos + 1;
+            l.max_len = a->pos + 1;
+            l.out = (float*)ds5_ptr(a->out);
+            l.n_seqs = 1;
+            l.n_q_heads = a->n_q_heads;
+            l.n_kv_heads = a->n_kv_heads;
+            l.head_dim = a->head_dim;
+            l.scale = a->scale;
+            return launch_decode(ctx, l);
+        }
+        PrefillLaunch l{};
+        l.q = (const float*)ds5_ptr(a->q);
+        l.k_cache = (const f16*)ds5_ptr(a->k_cache);
+        l.v_cache = (const f16*)ds5_ptr(a->v_cache);
+        l.out = (float*)ds5_ptr(a->out);
+        l.pos = a->pos;
+        l.n_tokens = a->n_tokens;
+        l.n_q_heads = a->n_q_heads;
+        l.n_kv_heads = a->n_kv_heads;
+        l.head_dim = a->head_dim;
+        l.max_ctx = a->max_ctx;
+        l.scale = a->scale;
+        return launch_prefill(ctx, l);
+    }
+    GenericAttnLaunch g{(const float*)ds5_ptr(a->q), ds5_ptr(a->k_cache), ds5_ptr(a->v_cache), (float*)ds5_ptr(a->out),
+                        a->kv_dtype, a->pos, a->n_tokens, a->n_q_heads, a->n_kv_heads, a->head_dim, a->max_ctx,
+                        a->scale};
+    return launch_generic_attention(ctx, g);
+}
+
+int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t T = a->n_tokens, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
+    // rmsNorm(q), rmsNorm(k), rope(q), rope(k), kvAppend, gqaAttention checks, in that order.
+    if (hd == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: head_dim == 0");
+    if (!covers(a->q, T * hq * hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: q too small");
+    if (!covers(a->q_norm, hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: q_norm too small");
+    if (!covers(a->k, T * hkv * hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: k too small");
+    if (!covers(a->k_norm, hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: k_norm too small");
+    if (hd % 2 != 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: head_dim must be even");
+    if (!covers(a->positions, T * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: positions too small");
+    if (hkv == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: n_kv_heads == 0");
+    if ((uint64_t)a->pos + T > a->max_ctx) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: pos + n_tokens > max_ctx");
+    if (!covers(a->v, T * hkv * hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: v too small");
+    const ds5_attn_args at{a->q, a->k_cache, a->v_cache, a->kv_dtype, a->out, a->pos, a->n_tokens,
+                           a->n_q_heads, a->n_kv_heads, a->head_dim, a->max_ctx, a->scale};
+    if (int rc = check_attention(ctx, &at)) return rc;
+    if (T == 0) return DS5_OK;
+    if (hd > 2 * DS5_MAX_ROPE_HALF) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: head_dim > 512");
+    if (int rc = set_device(ctx)) return rc;
+    const RopeTable* table = rope_table_for(a->theta, a->head_dim);
+
+    if (mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k, a->v, a->k_cache, a->v_cache, a->out})) {
+        if (T == 1) {
+            DecodeLaunch l{};
+            l.q = (const float*)ds5_ptr(a->q);
+            l.k_new = (const float*)ds5_ptr(a->k);
+            l.v_new = (const float*)ds5_ptr(a->v);
+            l.q_norm = (const float*)ds5_ptr(a->q_norm);
+            l.k_norm = (const float*)ds5_ptr(a->k_norm);
+            l.positions = (const int32_t*)ds5_ptr(a->positions);
+            l.k_cache = (f16*)ds5_ptr(a->k_cache);
+            l.v_cache = (f16*)ds5_ptr(a->v_cache);
+            l.cache_stride = a->max_ctx;
+            l.ctx_len = a->pos + 1;
+            l.max_len = a->pos + 1;
+            l.out = (float*)ds5_ptr(a->out);
+            l.n_seqs = 1;
+            l.n_q_heads = a->n_q_heads;
+            l.n_kv_heads = a->n_kv_heads;
+            l.head_dim = a->head_dim;
+            l.scale = a->scale;
+            l.eps = a->eps;
+            l.freq_scale = a->freq_scale;
+            l.fused = true;
+            l.table = table;
+            return launch_decode(ctx, l);
+        }
+        KvPrepLaunch kp{};
+        kp.k = (const float*)ds5_ptr(a->k);
+        kp.v = (const float*)ds5_ptr(a->v);
+        kp.k_norm = (const float*)ds5_ptr(a->k_norm);
+        kp.positions = (const int32_t*)ds5_ptr(a->positions);
+        kp.k_cache = (f16*)ds5_ptr(a->k_cache);
+        kp.v_cache = (f16*)ds5_ptr(a->v_cache);
+        kp.pos = a->pos;
+        kp.n_tokens = a->n_tokens;
+        kp.n_kv_heads = a->n_kv_heads;
+        kp.head_dim = a->head_dim;
+        kp.max_ctx = a->max_ctx;
+        kp.eps = a->eps;
+        kp.freq_scale = a->freq_scale;
+        kp.table = table;
+        if (int rc = launch_kv_prep(ctx, kp)) return rc;
+        PrefillLaunch l{};
+        l.q = (const float*)ds5_ptr(a->q);
+        l.q_norm = (const float*)ds5_ptr(a->q_norm);
+        l.positions = (const int32_t*)ds5_ptr(a->positions);
+        l.k_cache = (const f16*)ds5_ptr(a->k_cache);
+        l.v_cache = (const f16*)ds5_ptr(a->v_cache);
+        l.out = (float*)ds5_ptr(a->out);
+        l.pos = a->pos;
+        l.n_tokens = a->n_tokens;
+        l.n_q_heads = a->n_q_heads;
+        l.n_kv_heads = a->n_kv_heads;
+        l.head_dim = a->head_dim;
+        l.max_ctx = a->max_ctx;
+        l.scale = a->scale;
+        l.eps = a->eps;
+        l.freq_scale = a->freq_scale;
+        l.table = table;
+        return launch_prefill(ctx, l);
+    }
+
+    // Other shapes: the six separate device ops, in place on q and k.
+    float* q = (float*)ds5_ptr(a->q);
+    float* k = (float*)ds5_ptr(a->k);
+    int rc = launch_rms_norm(ctx, RmsNormLaunch{q, (const float*)ds5_ptr(a->q_norm), q, (uint32_t)(T * hq),
+                                                a->head_dim, a->eps});
+    if (!rc) rc = launch_rms_norm(ctx, RmsNormLaunch{k, (const float*)ds5_ptr(a->k_norm), k, (uint32_t)(T * hkv),
+                                                     a->head_dim, a->eps});
+    const int32_t* positions = (const int32_t*)ds5_ptr(a->positions);
+    if (!rc) rc = launch_rope(ctx, RopeLaunch{q, positions, a->n_tokens, a->n_q_heads, a->head_dim, a->freq_scale, table});
+    if (!rc) rc = launch_rope(ctx, RopeLaunch{k, positions, a->n_tokens, a->n_kv_heads, a->head_dim, a->freq_scale, table});
+    if (!rc) rc = launch_kv_append(ctx, KvAppendLaunch{k, (const float*)ds5_ptr(a->v), ds5_ptr(a->k_cache),
+                                                       ds5_ptr(a->v_cache), a->kv_dtype, a->pos, a->n_tokens,
+                                                       a->n_kv_heads, a->head_dim, a->max_ctx});
+    if (!rc) rc = ds5_hip_gqa_attention(ctx, &at);
+    return rc;
+}
+
+int ds5_hip_paged_decode(ds5_hip_ctx* ctx, const ds5_paged_decode_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t B = a->n_seqs, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
+    if (hq == 0 || hkv == 0 || hd == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: zero heads or head_dim");
+    if (hq % hkv != 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: n_q_heads %% n_kv_heads != 0");
+    if (hd != 64 && hd != 128) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: head_dim must be 64 or 128");
+    if (a->page_size == 0 || a->n_pages == 0 || a->max_pages == 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: empty page geometry");
+    if ((uint64_t)a->max_seq_len > (uint64_t)a->max_pages * a->page_size)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: max_seq_len exceeds max_pages * page_size");
+    const uint64_t slots = (uint64_t)a->n_pages * a->page_size;
+    if (!covers(a->q, B * hq * hd * 4) || !covers(a->out, B * hq * hd * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: q/out too small");
+    if (!covers(a->k, B * hkv * hd * 4) || !covers(a->v, B * hkv * hd * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: k/v too small");
+    if (!covers(a->q_norm, hd * 4) || !covers(a->k_norm, hd * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: norm weights too small");
+    if (!covers(a->k_pool, hkv * slots * hd * 2) || !covers(a->v_pool, hkv * slots * hd * 2))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: pool too small");
+    if (!covers(a->page_table, B * a->max_pages * 4) || !covers(a->seq_lens, B * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: page_table/seq_lens too small");
+    for (const ds5_buf& b : {a->q, a->k, a->v, a->k_pool, a->v_pool, a->out})
+        if (!aligned16(b)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: views must be 16-byte aligned");
+    if (B == 0 || a->max_seq_len == 0) return DS5_OK;
+    if (hd > 2 * DS5_MAX_ROPE_HALF) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: head_dim > 512");
+    if (int rc = set_device(ctx)) return rc;
+    DecodeLaunch l{};
+    l.q = (const float*)ds5_ptr(a->q);
+    l.k_new = (const float*)ds5_ptr(a->k);
+    l.v_new = (const float*)ds5_ptr(a->v);
+    l.q_norm = (const float*)ds5_ptr(a->q_norm);
+    l.k_norm = (const float*)ds5_ptr(a->k_norm);
+    l.k_cache = (f16*)ds5_ptr(a->k_pool);
+    l.v_cache = (f16*)ds5_ptr(a->v_pool);
+    l.cache_stride = slots;
+    l.page_table = (const int32_t*)ds5_ptr(a->page_table);
+    l.seq_lens = (const int32_t*)ds5_ptr(a->seq_lens);
+    l.page_size = a->page_size;
+    l.max_pages = a->max_pages;
+    l.max_len = a->max_seq_len;
+    l.out = (float*)ds5_ptr(a->out);
+    l.n_seqs = a->n_seqs;
+    l.n_q_heads = a->n_q_heads;
+    l.n_kv_heads = a->n_kv_heads;
+    l.head_dim = a->head_dim;
+    l.scale = a->scale;
+    l.eps = a->eps;
+    l.freq_scale = a->freq_scale;
+    l.fused = true;
+    l.table = rope_table_for(a->theta, a->head_dim);
+    return launch_decode(ctx, l);
+}
+
+int ds5_hip_rope_table(float theta, uint32_t head_dim, float* out) {
+    if (!out || head_dim == 0 || head_dim % 2 != 0 || head_dim > 2 * DS5_MAX_ROPE_HALF) return DS5_SHAPE_MISMATCH;
+    RopeTable t;
+    ds5_rope_table(theta, head_dim, &t);
+    for (uint32_t i = 0; i < head_dim / 2; i++) out[i] = t.inv[i];
+    return DS5_OK;
+}
+
+int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t seed) {
+    if (!covers(buf, n * 2)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "fill_normal_f16: buffer too small");
+    if (int rc = set_device(ctx)) return rc;
+    return launch_fill_normal_f16(ctx, (f16*)ds5_ptr(buf), n, seed);
+}
+
+}  // extern "C"

@@ -1,0 +1,204 @@
+// k_norm_rope.hip -- rmsNorm, rope and kvAppend on gfx950, plus the prefill
+// k/v pre-pass (norm + rope of k, append of k and v) of the fused step.
+//
+// Arithmetic follows the reference CPU path operation for operation so that
+// results are bit-exact where the operations are IEEE-exact:
+//   rmsNorm  kernels_a.zig:84-89: sumsq is a serial f32 sum in element order,
+//            inv = 1/sqrt(sumsq/dim + eps) (correctly rounded div and sqrt),
+//            o = (v*inv)*w -- one thread owns a row for the sum.
+//   rope     kernels_a.zig:117-126: angle = (pos*freq_scale)*inv_freq[i] with
+//            the host-built inv_freq table (std.math.pow(f32) evaluation);
+//            x0' = x0*c - x1*s, x1' = x0*s + x1*c, never fused into fma.
+//   kvAppend kernels_a.zig:196-211: dst = (h*max_ctx + pos + t)*head_dim, f16
+//            by round-to-nearest-even conversion.
+// cosf/sinf are the device library's full-range versions; they may differ
+// from the host C library by an ulp.
+#pragma clang fp contract(off)
+
+#include "ds5_common.hpp"
+
+namespace {
+
+constexpr int kRowsPerBlock = 64;  // one wavefront, one row per lane
+constexpr int kColTile = 64;
+
+// Serial sum of squares of 64 rows, one row per lane, in element order.
+// The tile is staged transposed through LDS so global reads stay coalesced.
+__device__ void rows_sumsq(const float* __restrict__ x, uint32_t row0, uint32_t n_rows, uint32_t dim,
+                           float (*tile)[kColTile + 1], float* sumsq_out) {
+    const int lane = threadIdx.x;
+    float sumsq = 0.0f;
+    for (uint32_t c0 = 0; c0 < dim; c0 += kColTile) {
+        const uint32_t ncol = min((uint32_t)kColTile, dim - c0);
+        for (int r = 0; r < kRowsPerBlock; r++) {
+            const uint32_t row = row0 + r;
+            float v = 0.0f;
+            if (row < n_rows && (uint32_t)lane < ncol) v = x[(uint64_t)row * dim + c0 + lane];
+            tile[r][lane] = v;
+        }
+        __syncthreads();
+        for (uint32_t j = 0; j < ncol; j++) {
+            const float v = tile[lane][j];
+            sumsq += v * v;
+        }
+        __syncthreads();
+    }
+    *sumsq_out = sumsq;
+}
+
+__global__ __launch_bounds__(kRowsPerBlock) void rms_norm_kernel(const float* x, const float* __restrict__ w,
+                                                                 float* out, uint32_t n_rows, uint32_t dim,
+                                                                 float eps) {
+    __shared__ float tile[kRowsPerBlock][kColTile + 1];
+    __shared__ float s_inv[kRowsPerBlock];
+    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
+    const int lane = threadIdx.x;
+    float sumsq;
+    rows_sumsq(x, row0, n_rows, dim, tile, &sumsq);
+    s_inv[lane] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)dim) + eps));
+    __syncthreads();
+    // out may alias x: every element is read before the same thread writes it.
+    for (int r = 0; r < kRowsPerBlock; r++) {
+        const uint32_t row = row0 + r;
+        if (row >= n_rows) break;
+        const float inv = s_inv[r];
+        for (uint32_t c = lane; c < dim; c += kRowsPerBlock) {
+            const uint64_t idx = (uint64_t)row * dim + c;
+            out[idx] = x[idx] * inv * w[c];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(float* x, const int32_t* __restrict__ positions,
+                                                   uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim,
+                                                   float freq_scale, RopeTable table) {
+    const uint32_t half = head_dim / 2;
+    const uint64_t total = (uint64_t)n_tokens * n_heads * half;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t i = idx % half;
+        const uint64_t th = idx / half;  // t * n_heads + h
+        const uint32_t t = th / n_heads;
+        const float pos = (float)positions[t];
+        const float angle = pos * freq_scale * table.inv[i];
+        const float c = cosf(angle);
+        const float s = sinf(angle);
+        float* head = x + th * head_dim;
+        const float x0 = head[i];
+        const float x1 = head[i + half];
+        head[i] = x0 * c - x1 * s;
+        head[i + half] = x0 * s + x1 * c;
+    }
+}
+
+template <typename T>
+__device__ inline T to_cache(float v);
+template <>
+__device__ inline float to_cache<float>(float v) {
+    return v;
+}
+template <>
+__device__ inline f16 to_cache<f16>(float v) {
+    return (f16)v;  // v_cvt_f16_f32: round to nearest even
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict__ k_new,
+                                                        const float* __restrict__ v_new, T* k_cache, T* v_cache,
+                                                        uint32_t pos, uint32_t n_tokens, uint32_t n_kv_heads,
+                                                        uint32_t head_dim, uint32_t max_ctx) {
+    const uint64_t total = (uint64_t)n_tokens * n_kv_heads * head_dim;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t d = idx % head_dim;
+        const uint64_t th = idx / head_dim;
+        const uint32_t h = th % n_kv_heads;
+        const uint32_t t = th / n_kv_heads;
+        const uint64_t dst = ((uint64_t)h * max_ctx + pos + t) * head_dim + d;
+        k_cache[dst] = to_cache<T>(k_new[idx]);
+        v_cache[dst] = to_cache<T>(v_new[idx]);
+    }
+}
+
+// Prefill pre-pass of the fused step: 64 k rows (row = t*n_kv_heads + h) per
+// block: serial-order norm, rope at positions[t], f16 append; v rows are
+// converted and appended. k and v inputs are not modified.
+__global__ __launch_bounds__(kRowsPerBlock) void kv_prep_kernel(KvPrepLaunch a, RopeTable table) {
+    __shared__ float tile[kRowsPerBlock][kColTile + 1];
+    __shared__ float s_inv[kRowsPerBlock];
+    const uint32_t n_rows = a.n_tokens * a.n_kv_heads;
+    const uint32_t dim = a.head_dim, half = dim / 2;
+    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
+    const int lane = threadIdx.x;
+    float sumsq;
+    rows_sumsq(a.k, row0, n_rows, dim, tile, &sumsq);
+    s_inv[lane] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)dim) + a.eps));
+    __syncthreads();
+    for (int r = 0; r < kRowsPerBlock; r++) {
+        const uint32_t row = row0 + r;
+        if (row >= n_rows) break;
+        const uint32_t t = row / a.n_kv_heads, h = row % a.n_kv_heads;
+        const float inv = s_inv[r];
+        const float pos = (float)a.positions[t];
+        const float* src = a.k + (uint64_t)row * dim;
+        const uint64_t dst = ((uint64_t)h * a.max_ctx + a.pos + t) * dim;
+        for (uint32_t i = lane; i < half; i += kRowsPerBlock) {
+            const float x0 = src[i] * inv * a.k_norm[i];
+            const float x1 = src[i + half] * inv * a.k_norm[i + half];
+            const float angle = pos * a.freq_scale * table.inv[i];
+            const float c = cosf(angle);
+            const float s = sinf(angle);
+            a.k_cache[dst + i] = (f16)(x0 * c - x1 * s);
+            a.k_cache[dst + i + half] = (f16)(x0 * s + x1 * c);
+        }
+        const float* vsrc = a.v + (uint64_t)row * dim;
+        for (uint32_t c = lane; c < dim; c += kRowsPerBlock) a.v_cache[dst + c] = (f16)vsrc[c];
+    }
+}
+
+inline uint32_t grid_for(uint64_t total, uint32_t block) {
+    const uint64_t g = (total + block - 1) / block;
+    return (uint32_t)(g > 65535u * 16u ? 65535u * 16u : (g ? g : 1));
+}
+
+}  // namespace
+
+int launch_rms_norm(ds5_hip_ctx* ctx, const RmsNormLaunch& a) {
+    if (a.n_rows == 0) return DS5_OK;
+    const uint32_t blocks = (a.n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    DS5_TIMED_LAUNCH(ctx, "rms_norm_kernel", rms_norm_kernel, dim3(blocks), dim3(kRowsPerBlock), 0, ctx->stream, a.x, a.w, a.out,
+                       a.n_rows, a.dim, a.eps);
+    return ds5_after_launch(ctx, "rms_norm_kernel");
+}
+
+int launch_rope(ds5_hip_ctx* ctx, const RopeLaunch& a) {
+    const uint64_t total = (uint64_t)a.n_tokens * a.n_heads * (a.head_dim / 2);
+    if (total == 0) return DS5_OK;
+    DS5_TIMED_LAUNCH(ctx, "rope_kernel", rope_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, a.x, a.positions,
+                       a.n_tokens, a.n_heads, a.head_dim, a.freq_scale, *a.table);
+    return ds5_after_launch(ctx, "rope_kernel");
+}
+
+int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a) {
+    const uint64_t total = (uint64_t)a.n_tokens * a.n_kv_heads * a.head_dim;
+    if (total == 0) return DS5_OK;
+    const dim3 grid(grid_for(total, 256));
+    if (a.kv_dtype == DS5_DTYPE_F16) {
+        DS5_TIMED_LAUNCH(ctx, "kv_append_kernel", kv_append_kernel<f16>, grid, dim3(256), 0, ctx->stream, a.k_new, a.v_new,
+                           (f16*)a.k_cache, (f16*)a.v_cache, a.pos, a.n_tokens, a.n_kv_heads, a.head_dim,
+                           a.max_ctx);
+    } else {
+        DS5_TIMED_LAUNCH(ctx, "kv_append_kernel", kv_append_kernel<float>, grid, dim3(256), 0, ctx->stream, a.k_new, a.v_new,
+                           (float*)a.k_cache, (float*)a.v_cache, a.pos, a.n_tokens, a.n_kv_heads, a.head_dim,
+                           a.max_ctx);
+    }
+    return ds5_after_launch(ctx, "kv_append_kernel");
+}
+
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a) {
+    const uint32_t n_rows = a.n_tokens * a.n_kv_heads;
+    if (n_rows == 0) return DS5_OK;
+    const uint32_t blocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    DS5_TIMED_LAUNCH(ctx, "kv_prep_kernel", kv_prep_kernel, dim3(blocks), dim3(kRowsPerBlock), 0, ctx->stream, a, *a.table);
+    return ds5_after_launch(ctx, "kv_prep_kernel");
+}

@@ -1,0 +1,42 @@
+// k_util.hip -- device-side synthetic data for benchmarks: N(0,1) f16 values
+// from a counter-based generator, so multi-GB KV caches need no host
+// generation or PCIe transfer. Value i depends only on (seed, i):
+//   u64 z = splitmix64(seed * 0x9E3779B97F4A7C15 + (i >> 1));
+//   u1, u2 = the high and low 32-bit halves mapped into (0, 1];
+//   r = sqrt(-2 ln u1); even i -> r cos(2 pi u2), odd i -> r sin(2 pi u2).
+#include "ds5_common.hpp"
+
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_normal_f16_kernel(f16* out, uint64_t n, uint64_t seed) {
+    const uint64_t key = seed * 0x9E3779B97F4A7C15ull;
+    for (uint64_t pair = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * pair < n;
+         pair += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t z = splitmix64(key + pair);
+        const float u1 = ((float)(uint32_t)(z >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+        const float u2 = (float)(uint32_t)(z & 0xFFFFFFu) * (1.0f / 16777216.0f);     // [0, 1)
+        const float r = sqrtf(-2.0f * logf(u1));
+        const float th = 6.283185307179586f * u2;
+        const uint64_t i = 2 * pair;
+        out[i] = (f16)(r * cosf(th));
+        if (i + 1 < n) out[i + 1] = (f16)(r * sinf(th));
+    }
+}
+
+}  // namespace
+
+int launch_fill_normal_f16(ds5_hip_ctx* ctx, f16* out, uint64_t n, uint64_t seed) {
+    if (n == 0) return DS5_OK;
+    const uint64_t pairs = (n + 1) / 2;
+    uint64_t blocks = (pairs + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    DS5_TIMED_LAUNCH(ctx, "fill_normal_f16_kernel", fill_normal_f16_kernel, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, out, n, seed);
+    return ds5_after_launch(ctx, "fill_normal_f16_kernel");
+}

@@ -1,0 +1,323 @@
+"""Host-side mirror of DS5's kernel-provider interface over libds5hip.so.
+
+The reference engine (src/engine/forward.zig:154) is generic over a device
+context `Ctx` (contracts.assertGpuApi, src/shared/contracts.zig:374-384) and a
+kernel namespace `K` (contracts.assertKernelApi, :358-367). This module gives
+both the same names, argument meaning and error behaviour, bound to the gfx950
+backend through its C ABI (include/ds5_hip.h):
+
+    ctx = Ctx.init()                         # Ctx.init(allocator)
+    buf = ctx.createBuffer(n)                # zero-filled device buffer
+    ctx.upload(buf, 0, host_bytes); ctx.download(buf, 0, out)
+    rmsNorm(ctx, RmsNormArgs(...)); rope(ctx, RopeArgs(...))
+    kvAppend(ctx, KvAppendArgs(...)); gqaAttention(ctx, AttnArgs(...))
+    ctx.begin(); ...; ctx.submit(); ctx.gpuElapsedNs()
+
+Failures raise the KernelError subclasses named after the reference's error
+set (src/shared/contracts.zig:201-206). There is no CPU fallback: when the
+shared library is missing, importing this module fails.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libds5hip.so")
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+
+
+# ---------------------------------------------------------------------------
+# KernelError (contracts.zig:201-206)
+# ---------------------------------------------------------------------------
+class KernelError(Exception):
+    code = 0
+
+
+class ShapeMismatch(KernelError):
+    code = 1
+
+
+class UnsupportedDtype(KernelError):
+    code = 2
+
+
+class DeviceFailure(KernelError):
+    code = 3
+
+
+class OutOfMemory(KernelError):
+    code = 4
+
+
+_ERRORS = {c.code: c for c in (ShapeMismatch, UnsupportedDtype, DeviceFailure, OutOfMemory)}
+
+
+# ---------------------------------------------------------------------------
+# ABI structs (include/ds5_hip.h)
+# ---------------------------------------------------------------------------
+class Buf(C.Structure):
+    """contracts.zig:210-214 Buf: device base pointer + byte offset + byte length."""
+    _fields_ = [("handle", C.c_void_p), ("offset", C.c_uint64), ("len", C.c_uint64)]
+
+    def view(self, offset: int, length: int) -> "Buf":
+        """Sub-view [offset, offset+length) of this view (bytes)."""
+        return Buf(self.handle, self.offset + offset, length)
+
+
+class RmsNormArgs(C.Structure):
+    _fields_ = [("x", Buf), ("weight", Buf), ("out", Buf), ("n_rows", C.c_uint32), ("dim", C.c_uint32),
+                ("eps", C.c_float)]
+
+
+class RopeArgs(C.Structure):
+    _fields_ = [("x", Buf), ("positions", Buf), ("n_tokens", C.c_uint32), ("n_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("theta", C.c_float), ("freq_scale", C.c_float)]
+
+    def __init__(self, *args, **kw):
+        kw.setdefault("freq_scale", 1.0)  # contracts.zig:237 default
+        super().__init__(*args, **kw)
+
+
+class KvAppendArgs(C.Structure):
+    _fields_ = [("k_new", Buf), ("v_new", Buf), ("k_cache", Buf), ("v_cache", Buf), ("kv_dtype", C.c_uint32),
+                ("pos", C.c_uint32), ("n_tokens", C.c_uint32), ("n_kv_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("max_ctx", C.c_uint32)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [("q", Buf), ("k_cache", Buf), ("v_cache", Buf), ("kv_dtype", C.c_uint32), ("out", Buf),
+                ("pos", C.c_uint32), ("n_tokens", C.c_uint32), ("n_q_heads", C.c_uint32),
+                ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("max_ctx", C.c_uint32),
+                ("scale", C.c_float)]
+
+
+class AttentionStepArgs(C.Structure):
+    _fields_ = [(n, Buf) for n in ("q", "k", "v", "q_norm", "k_norm", "positions", "k_cache", "v_cache", "out")] + \
+               [(n, C.c_uint32) for n in ("kv_dtype", "pos", "n_tokens", "n_q_heads", "n_kv_heads", "head_dim",
+                                          "max_ctx")] + \
+               [(n, C.c_float) for n in ("eps", "theta", "freq_scale", "scale")]
+
+
+class PagedDecodeArgs(C.Structure):
+    _fields_ = [(n, Buf) for n in ("q", "k", "v", "q_norm", "k_norm", "k_pool", "v_pool", "page_table",
+                                   "seq_lens", "out")] + \
+               [(n, C.c_uint32) for n in ("n_seqs", "n_q_heads", "n_kv_heads", "head_dim", "page_size", "n_pages",
+                                          "max_pages", "max_seq_len")] + \
+               [(n, C.c_float) for n in ("eps", "theta", "freq_scale", "scale")]
+
+
+# Every symbol include/ds5_hip.h declares, with its ctypes signature.
+_P = C.c_void_p
+SIGNATURES = {
+    "ds5_hip_init": ([C.c_int, C.POINTER(C.c_void_p)], C.c_int),
+    "ds5_hip_deinit": ([_P], None),
+    "ds5_hip_create_buffer": ([_P, C.c_uint64, C.POINTER(Buf)], C.c_int),
+    "ds5_hip_buffer_from_bytes": ([_P, C.c_void_p, C.c_uint64, C.POINTER(Buf)], C.c_int),
+    "ds5_hip_upload": ([_P, Buf, C.c_uint64, C.c_void_p, C.c_uint64], C.c_int),
+    "ds5_hip_download": ([_P, Buf, C.c_uint64, C.c_void_p, C.c_uint64], C.c_int),
+    "ds5_hip_begin": ([_P], None),
+    "ds5_hip_submit": ([_P], C.c_int),
+    "ds5_hip_gpu_elapsed_ns": ([_P], C.c_uint64),
+    "ds5_hip_last_error": ([_P], C.c_char_p),
+    "ds5_hip_stream": ([_P], C.c_void_p),
+    "ds5_hip_capture_begin": ([_P], C.c_int),
+    "ds5_hip_capture_end": ([_P, C.POINTER(C.c_void_p)], C.c_int),
+    "ds5_hip_graph_launch": ([_P, C.c_void_p], C.c_int),
+    "ds5_hip_graph_destroy": ([C.c_void_p], None),
+    "ds5_hip_set_kernel_timing": ([_P, C.c_int], C.c_int),
+    "ds5_hip_kernel_time": ([_P, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double)], C.c_int),
+    "ds5_hip_rms_norm": ([_P, C.POINTER(RmsNormArgs)], C.c_int),
+    "ds5_hip_rope": ([_P, C.POINTER(RopeArgs)], C.c_int),
+    "ds5_hip_kv_append": ([_P, C.POINTER(KvAppendArgs)], C.c_int),
+    "ds5_hip_gqa_attention": ([_P, C.POINTER(AttnArgs)], C.c_int),
+    "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
+    "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
+    "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
+    "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
+}
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built: run `python -m qw3_amd.build` "
+                          "(the HIP backend has no CPU fallback)")
+    lib = C.CDLL(path)
+    for name, (argtypes, restype) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.argtypes = argtypes
+        f.restype = restype
+    return lib
+
+
+LIB = load_library()
+
+
+def _as_array(x) -> np.ndarray:
+    """A C-contiguous numpy view of a host buffer (ndarray, bytes, bytearray, memoryview)."""
+    if isinstance(x, np.ndarray):
+        if not x.flags["C_CONTIGUOUS"]:
+            raise ValueError("host buffer must be C-contiguous")
+        return x
+    return np.frombuffer(x, dtype=np.uint8)
+
+
+def _nbytes(x) -> int:
+    return _as_array(x).nbytes
+
+
+def _ptr(x):
+    return _as_array(x).ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# Ctx (contracts.assertGpuApi)
+# ---------------------------------------------------------------------------
+class Ctx:
+    def __init__(self, handle: C.c_void_p):
+        self._h = handle
+
+    @classmethod
+    def init(cls, device_index: int = 0) -> "Ctx":
+        h = C.c_void_p()
+        rc = LIB.ds5_hip_init(device_index, C.byref(h))
+        if rc:
+            raise _ERRORS.get(rc, KernelError)(f"ds5_hip_init failed ({rc})")
+        return cls(h)
+
+    def deinit(self) -> None:
+        if self._h:
+            LIB.ds5_hip_deinit(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.deinit()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def check(self, rc: int) -> None:
+        if rc:
+            raise _ERRORS.get(rc, KernelError)(LIB.ds5_hip_last_error(self._h).decode())
+
+    def createBuffer(self, length: int) -> Buf:
+        b = Buf()
+        self.check(LIB.ds5_hip_create_buffer(self._h, length, C.byref(b)))
+        return b
+
+    def bufferFromBytes(self, data) -> Buf:
+        b = Buf()
+        data = np.ascontiguousarray(data) if isinstance(data, np.ndarray) else data
+        self.check(LIB.ds5_hip_buffer_from_bytes(self._h, _ptr(data), _nbytes(data), C.byref(b)))
+        return b
+
+    def upload(self, buf: Buf, offset: int, data) -> None:
+        data = np.ascontiguousarray(data) if isinstance(data, np.ndarray) else data
+        self.check(LIB.ds5_hip_upload(self._h, buf, offset, _ptr(data), _nbytes(data)))
+
+    def download(self, buf: Buf, offset: int, out) -> None:
+        self.check(LIB.ds5_hip_download(self._h, buf, offset, _ptr(out), _nbytes(out)))
+
+    def begin(self) -> None:
+        LIB.ds5_hip_begin(self._h)
+
+    def submit(self) -> None:
+        self.check(LIB.ds5_hip_submit(self._h))
+
+    def gpuElapsedNs(self) -> int:
+        return LIB.ds5_hip_gpu_elapsed_ns(self._h)
+
+    # numpy conveniences (tests, bench)
+    def from_numpy(self, a: np.ndarray) -> Buf:
+        return self.bufferFromBytes(np.ascontiguousarray(a))
+
+    def to_numpy(self, buf: Buf, dtype, shape=None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = (buf.len - offset) // dtype.itemsize if shape is None else int(np.prod(shape))
+        out = np.empty(n, dtype)
+        self.download(buf, offset, out)
+        return out if shape is None else out.reshape(shape)
+
+    def capture(self, fn) -> "Graph":
+        """Records the device work `fn()` enqueues into a replayable graph."""
+        self.check(LIB.ds5_hip_capture_begin(self._h))
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = LIB.ds5_hip_capture_end(self._h, C.byref(g))
+        self.check(rc)
+        return Graph(self, g)
+
+    def set_kernel_timing(self, enable: bool) -> None:
+        self.check(LIB.ds5_hip_set_kernel_timing(self._h, int(enable)))
+
+    def kernel_time(self, kernel: str) -> tuple[int, float]:
+        """(launches, total device ns) of `kernel` since timing was enabled."""
+        n, t = C.c_uint64(), C.c_double()
+        self.check(LIB.ds5_hip_kernel_time(self._h, kernel.encode(), C.byref(n), C.byref(t)))
+        return n.value, t.value
+
+    def fill_normal_f16(self, buf: Buf, n: int, seed: int) -> None:
+        self.check(LIB.ds5_hip_fill_normal_f16(self._h, buf, n, seed))
+
+
+class Graph:
+    """An executable HIP graph captured on a context's stream."""
+
+    def __init__(self, ctx: Ctx, handle: C.c_void_p):
+        self.ctx, self._g = ctx, handle
+
+    def launch(self) -> None:
+        self.ctx.check(LIB.ds5_hip_graph_launch(self.ctx.handle, self._g))
+
+    def destroy(self) -> None:
+        if self._g:
+            LIB.ds5_hip_graph_destroy(self._g)
+            self._g = None
+
+
+# ---------------------------------------------------------------------------
+# Kernel provider (contracts.assertKernelApi: the attention-path ops)
+# ---------------------------------------------------------------------------
+def rmsNorm(ctx: Ctx, args: RmsNormArgs) -> None:
+    ctx.check(LIB.ds5_hip_rms_norm(ctx.handle, C.byref(args)))
+
+
+def rope(ctx: Ctx, args: RopeArgs) -> None:
+    ctx.check(LIB.ds5_hip_rope(ctx.handle, C.byref(args)))
+
+
+def kvAppend(ctx: Ctx, args: KvAppendArgs) -> None:
+    ctx.check(LIB.ds5_hip_kv_append(ctx.handle, C.byref(args)))
+
+
+def gqaAttention(ctx: Ctx, args: AttnArgs) -> None:
+    ctx.check(LIB.ds5_hip_gqa_attention(ctx.handle, C.byref(args)))
+
+
+def attentionStep(ctx: Ctx, args: AttentionStepArgs) -> None:
+    """Fused q/k norm + rope + kvAppend + gqaAttention (one engine layer's attention block)."""
+    ctx.check(LIB.ds5_hip_attention_step(ctx.handle, C.byref(args)))
+
+
+def rope_table(theta: float, head_dim: int) -> np.ndarray:
+    """The inv_freq table the rope kernels use (host computation, no device)."""
+    out = np.zeros(head_dim // 2, np.float32)
+    rc = LIB.ds5_hip_rope_table(theta, head_dim, out.ctypes.data)
+    if rc:
+        raise _ERRORS.get(rc, KernelError)("ds5_hip_rope_table")
+    return out
+
+
+def pagedDecode(ctx: Ctx, args: PagedDecodeArgs) -> None:
+    """Batched decode over a paged f16 pool (one new token per sequence)."""
+    ctx.check(LIB.ds5_hip_paged_decode(ctx.handle, C.byref(args)))

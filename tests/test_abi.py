@@ -1,0 +1,167 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol the header
+declares, its structs match the C compiler's layout, and every precondition
+the reference checks is rejected with the reference's error before any device
+work (a null context stands in for the device; valid shapes then report
+DeviceFailure instead of launching)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ds5_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|void|uint64_t|const char\*|void\*)\s+\**(ds5_hip_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol(hip):
+    names = header_functions()
+    assert len(names) >= 18
+    nm = subprocess.run(["nm", "-D", "--defined-only", hip.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r" T (ds5_hip_\w+)", nm.stdout))
+    assert set(names) <= exported, set(names) - exported
+    assert set(names) == set(hip.SIGNATURES), set(names) ^ set(hip.SIGNATURES)
+    for n in names:
+        assert getattr(hip.LIB, n) is not None
+
+
+STRUCTS = {
+    "ds5_buf": "Buf", "ds5_rms_norm_args": "RmsNormArgs", "ds5_rope_args": "RopeArgs",
+    "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
+    "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
+}
+
+
+def test_struct_layouts_match_c(hip, tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
+    for cname, pyname in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in getattr(hip, pyname)._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = dict(l.rsplit(" ", 1) for l in out if l)
+    for cname, pyname in STRUCTS.items():
+        py = getattr(hip, pyname)
+        assert int(got[f"{cname} size"]) == C.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert int(got[f"{cname}.{fname}"]) == getattr(py, fname).offset, (cname, fname)
+    assert C.sizeof(hip.Buf) == 24  # contracts.zig:210-214 extern struct
+
+
+# ---------------------------------------------------------------------------
+# Preconditions (no device): null ctx, fake device pointers never dereferenced
+# ---------------------------------------------------------------------------
+FAKE = 1 << 20  # a non-null handle; nothing is dereferenced before the checks pass
+
+
+def B(nbytes):
+    import qw3_amd.hip as H
+    return H.Buf(FAKE, 0, nbytes)
+
+
+def rc_of(hip, fn, args):
+    return getattr(hip.LIB, fn)(None, C.byref(args))
+
+
+def test_rms_norm_preconditions(hip):
+    ok = hip.RmsNormArgs(B(64), B(16), B(64), 4, 4, 1e-6)
+    assert rc_of(hip, "ds5_hip_rms_norm", ok) == 3  # valid: only the missing device fails
+    for bad in (hip.RmsNormArgs(B(64), B(16), B(64), 4, 0, 1e-6), hip.RmsNormArgs(B(60), B(16), B(64), 4, 4, 1e-6),
+                hip.RmsNormArgs(B(64), B(16), B(60), 4, 4, 1e-6), hip.RmsNormArgs(B(64), B(12), B(64), 4, 4, 1e-6)):
+        assert rc_of(hip, "ds5_hip_rms_norm", bad) == 1
+
+
+def test_rope_preconditions(hip):
+    assert rc_of(hip, "ds5_hip_rope", hip.RopeArgs(B(2 * 3 * 8 * 4), B(8), 2, 3, 8, 1e6)) == 3
+    for bad in (hip.RopeArgs(B(2 * 3 * 7 * 4), B(8), 2, 3, 7, 1e6), hip.RopeArgs(B(100), B(8), 2, 3, 0, 1e6),
+                hip.RopeArgs(B(2 * 3 * 8 * 4 - 1), B(8), 2, 3, 8, 1e6), hip.RopeArgs(B(2 * 3 * 8 * 4), B(4), 2, 3, 8, 1e6),
+                hip.RopeArgs(B(1 << 20), B(8), 1, 1, 1024, 1e6)):
+        assert rc_of(hip, "ds5_hip_rope", bad) == 1
+
+
+def test_kv_append_preconditions(hip):
+    def args(kv_dtype=1, pos=3, T=2, H=2, hd=4, cap=8, new=None, cache=None):
+        eb = 2 if kv_dtype == 1 else 4
+        new = T * H * hd * 4 if new is None else new
+        cache = H * cap * hd * eb if cache is None else cache
+        return hip.KvAppendArgs(B(new), B(new), B(cache), B(cache), kv_dtype, pos, T, H, hd, cap)
+    assert rc_of(hip, "ds5_hip_kv_append", args()) == 3
+    assert rc_of(hip, "ds5_hip_kv_append", args(kv_dtype=0)) == 3
+    assert rc_of(hip, "ds5_hip_kv_append", args(pos=7)) == 1           # kernels_a.zig:176 overflow
+    assert rc_of(hip, "ds5_hip_kv_append", args(hd=0)) == 1
+    assert rc_of(hip, "ds5_hip_kv_append", args(H=0)) == 1
+    assert rc_of(hip, "ds5_hip_kv_append", args(new=10)) == 1
+    assert rc_of(hip, "ds5_hip_kv_append", args(cache=10)) == 1
+    assert rc_of(hip, "ds5_hip_kv_append", args(kv_dtype=8, cache=1 << 20)) == 2  # q8_0 cache
+
+
+def test_attention_preconditions(hip):
+    def args(kv_dtype=1, pos=0, T=1, hq=2, hkv=2, hd=4, cap=8, q=None, cache=None):
+        eb = 2 if kv_dtype == 1 else 4
+        q = T * hq * hd * 4 if q is None else q
+        cache = hkv * cap * hd * eb if cache is None else cache
+        return hip.AttnArgs(B(q), B(cache), B(cache), kv_dtype, B(q), pos, T, hq, hkv, hd, cap, 0.5)
+    assert rc_of(hip, "ds5_hip_gqa_attention", args()) == 3
+    # kernels_b.zig:456-492 rejections
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(pos=8)) == 1
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(hq=3, hkv=2)) == 1
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(cap=64, cache=2 * 8 * 4 * 2)) == 1
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(hq=0)) == 1
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(q=8)) == 1
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(kv_dtype=30, cache=1 << 20)) == 2  # bf16 cache
+    assert rc_of(hip, "ds5_hip_gqa_attention", args(T=0)) == 0                        # nothing to do
+
+
+def test_step_and_paged_preconditions(hip):
+    T, hq, hkv, hd, cap = 1, 8, 2, 64, 16
+    f = lambda n: B(n * 4)
+    ok = hip.AttentionStepArgs(f(T * hq * hd), f(T * hkv * hd), f(T * hkv * hd), f(hd), f(hd), f(T),
+                               B(hkv * cap * hd * 2), B(hkv * cap * hd * 2), f(T * hq * hd),
+                               1, 15, T, hq, hkv, hd, cap, 1e-6, 1e6, 1.0, 0.125)
+    assert rc_of(hip, "ds5_hip_attention_step", ok) == 3
+    bad = hip.AttentionStepArgs.from_buffer_copy(ok)
+    bad.pos = 16
+    assert rc_of(hip, "ds5_hip_attention_step", bad) == 1
+    bad = hip.AttentionStepArgs.from_buffer_copy(ok)
+    bad.k_norm = f(hd - 1)
+    assert rc_of(hip, "ds5_hip_attention_step", bad) == 1
+    n_pages, ps, mp, B_ = 10, 16, 4, 3
+    pg = hip.PagedDecodeArgs(f(B_ * hq * hd), f(B_ * hkv * hd), f(B_ * hkv * hd), f(hd), f(hd),
+                             B(hkv * n_pages * ps * hd * 2), B(hkv * n_pages * ps * hd * 2), f(B_ * mp), f(B_),
+                             f(B_ * hq * hd), B_, hq, hkv, hd, ps, n_pages, mp, 64, 1e-6, 1e6, 1.0, 0.125)
+    assert rc_of(hip, "ds5_hip_paged_decode", pg) == 3
+    bad = hip.PagedDecodeArgs.from_buffer_copy(pg)
+    bad.max_seq_len = 65
+    assert rc_of(hip, "ds5_hip_paged_decode", bad) == 1
+    bad = hip.PagedDecodeArgs.from_buffer_copy(pg)
+    bad.head_dim = 96
+    assert rc_of(hip, "ds5_hip_paged_decode", bad) == 1
+
+
+def test_rope_table_is_the_oracle_pow(hip, oracle):
+    # The kernels' inv_freq table equals the oracle's std.math.pow(f32) restatement bit for bit.
+    for theta in (1e6, 5e6, 1e4, 100.0):
+        for hd in (4, 64, 128, 256):
+            t = hip.rope_table(theta, hd)
+            o = np.array([oracle.zig_powf(theta, -np.float32(2 * i) / np.float32(hd)) for i in range(hd // 2)],
+                         np.float32)
+            assert np.array_equal(t.view(np.uint32), o.view(np.uint32)), (theta, hd)
+    with pytest.raises(hip.ShapeMismatch):
+        hip.rope_table(1e6, 7)
+
+
+def test_library_missing_fails_loudly(hip, tmp_path):
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        hip.load_library(str(tmp_path / "nope.so"))

@@ -1,0 +1,403 @@
+"""Parity of the gfx950 backend with the CPU oracle, through the C ABI.
+
+Gates (BASELINE): KV slot/page indexing bit-exact; cached K/V within 1 f16 ulp;
+attention output max-abs <= 2e-3 and cosine >= 0.99999. Inputs are the same
+seeded host arrays for both sides. The reference's fixture tolerances apply to
+the vendored fixtures.
+"""
+import numpy as np
+import pytest
+
+from conftest import FIXTURES, cosine, f16_ulp_diff
+from qw3_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 2e-3     # attention output, max-abs
+OUT_COS = 0.99999   # attention output, cosine
+
+
+def check_out(got, want, atol=OUT_ATOL, cos=OUT_COS):
+    got = np.asarray(got, np.float32).ravel()
+    want = np.asarray(want, np.float32).ravel()
+    assert np.all(np.isfinite(got))
+    err = float(np.max(np.abs(got - want)))
+    c = cosine(got, want)
+    print(f"  max_abs={err:.3e} cosine={c:.9f}", flush=True)
+    assert err <= atol and c >= cos, (err, c)
+
+
+def dev(ctx, a):
+    return ctx.from_numpy(np.ascontiguousarray(a))
+
+
+def host(ctx, buf, like):
+    return ctx.to_numpy(buf, like.dtype, like.shape)
+
+
+# ---------------------------------------------------------------------------
+# single ops vs the reference fixtures and the oracle
+# ---------------------------------------------------------------------------
+
+def _cases(O, op):
+    return [c for c in O.load_manifest(FIXTURES)["cases"] if c["op"] == op]
+
+
+def _t(O, c, name):
+    return O.load_ds5t(f"{FIXTURES}/{c['tensors'][name]}").data
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_rmsnorm_fixtures_bit_exact(ctx, hip, oracle, i):
+    c = _cases(oracle, "rmsnorm")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w, want = (_t(oracle, c, n) for n in ("input", "weight", "output"))
+    xb = dev(ctx, x)
+    hip.rmsNorm(ctx, hip.RmsNormArgs(xb, dev(ctx, w), xb, p["n_rows"], p["dim"], p["eps"]))  # out aliases x
+    got = host(ctx, xb, x)
+    assert oracle.compare(want, got, tol["atol"], tol["rtol"]).passed
+    assert np.array_equal(got, oracle.rms_norm(x, w, p["eps"], p["n_rows"], p["dim"]))
+
+
+@pytest.mark.parametrize("i", range(3))
+def test_rope_fixtures(ctx, hip, oracle, i):
+    c = _cases(oracle, "rope")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, pos, want = (_t(oracle, c, n) for n in ("input", "positions", "output"))
+    xb = dev(ctx, x)
+    hip.rope(ctx, hip.RopeArgs(xb, dev(ctx, pos), p["n_tokens"], p["n_heads"], p["head_dim"], p["theta"],
+                               p["freq_scale"]))
+    got = host(ctx, xb, x)
+    assert oracle.compare(want, got, tol["atol"], tol["rtol"]).passed
+    ref = oracle.rope(x, pos, p["theta"], p["freq_scale"])
+    assert np.max(np.abs(got - ref)) <= 4 * np.finfo(np.float32).eps * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("i", range(6))
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_attention_fixtures(ctx, hip, oracle, i, kv_dtype):
+    """f32 caches: the reference fixture tolerance. f16 caches (MFMA decode and
+    prefill at head_dim 64): against the oracle's f16 branch."""
+    c = _cases(oracle, "attention")[i]
+    p, tol = c["params"], c["tolerance"]
+    q, kc, vc, want = (_t(oracle, c, n) for n in ("q", "k_cache", "v_cache", "output"))
+    if kv_dtype == 1:
+        kc, vc = oracle.f32_to_f16_bits(kc), oracle.f32_to_f16_bits(vc)
+        want = oracle.gqa_attention(q, kc, vc, 1, p["pos"], p["n_tokens"], p["n_q_heads"], p["n_kv_heads"],
+                                    p["head_dim"], p["max_ctx"], p["scale"])
+    out = ctx.createBuffer(want.nbytes)
+    hip.gqaAttention(ctx, hip.AttnArgs(dev(ctx, q), dev(ctx, kc), dev(ctx, vc), kv_dtype, out, p["pos"],
+                                       p["n_tokens"], p["n_q_heads"], p["n_kv_heads"], p["head_dim"], p["max_ctx"],
+                                       p["scale"]))
+    got = ctx.to_numpy(out, np.float32)
+    if kv_dtype == 0:
+        r = oracle.compare(want, got, tol["atol"], tol["rtol"])
+        assert r.passed, r
+    else:
+        check_out(got, want, atol=1e-4)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_kv_append_sentinel_bit_exact(ctx, hip, oracle, kv_dtype):
+    hkv, hd, cap, pos, T = 4, 128, 40, 13, 5
+    g = np.random.default_rng(11)
+    kn = g.standard_normal((T, hkv, hd)).astype(np.float32)
+    vn = g.standard_normal((T, hkv, hd)).astype(np.float32) * 300  # exercise f16 rounding far from 1
+    kn[0, 0, :8] = [65504.0, 65520.0, 6.0e-8, -3.0e-8, 1e-6, -0.0, 1.0009765625, 70000.0]
+    if kv_dtype == 0:
+        kc = g.standard_normal((hkv, cap, hd)).astype(np.float32)
+        vc = g.standard_normal((hkv, cap, hd)).astype(np.float32)
+    else:
+        kc = g.integers(0, 0x7C00, size=(hkv, cap, hd), dtype=np.uint64).astype(np.uint16)
+        vc = g.integers(0, 0x7C00, size=(hkv, cap, hd), dtype=np.uint64).astype(np.uint16)
+    kb, vb = dev(ctx, kc), dev(ctx, vc)
+    hip.kvAppend(ctx, hip.KvAppendArgs(dev(ctx, kn), dev(ctx, vn), kb, vb, kv_dtype, pos, T, hkv, hd, cap))
+    ko, vo = kc.copy(), vc.copy()
+    oracle.kv_append(kn, vn, ko, vo, kv_dtype, pos, T, hkv, hd, cap)
+    assert np.array_equal(host(ctx, kb, kc), ko)
+    assert np.array_equal(host(ctx, vb, vc), vo)
+
+
+def test_shape_errors_with_device(ctx, hip):
+    b = ctx.createBuffer(256)
+    with pytest.raises(hip.ShapeMismatch):  # kernels_b.zig:456-492
+        hip.gqaAttention(ctx, hip.AttnArgs(b, b, b, 0, b, 8, 1, 2, 2, 4, 8, 0.5))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.gqaAttention(ctx, hip.AttnArgs(b, b, b, 0, b, 0, 1, 3, 2, 4, 8, 0.5))
+    with pytest.raises(hip.UnsupportedDtype):
+        hip.kvAppend(ctx, hip.KvAppendArgs(b, b, b, b, 8, 0, 1, 1, 4, 2))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.kvAppend(ctx, hip.KvAppendArgs(b, b, b, b, 0, 7, 2, 1, 4, 8))
+
+
+# ---------------------------------------------------------------------------
+# hand cases (kernels_b.zig:228-454) on both cache dtypes
+# ---------------------------------------------------------------------------
+
+def _f16_nan_cache(shape):
+    return np.full(shape, 0x7E00, np.uint16)
+
+
+@pytest.mark.parametrize("hd,kv_dtype", [(4, 0), (64, 1), (128, 1)])
+def test_pos0_returns_v0_nan_tail(ctx, hip, oracle, hd, kv_dtype):
+    hq, hkv, cap = 8, 2, 3
+    g = np.random.default_rng(1)
+    q = g.standard_normal(hq * hd).astype(np.float32)
+    kf = np.full((hkv, cap, hd), np.nan, np.float32)
+    vf = np.full((hkv, cap, hd), np.nan, np.float32)
+    kf[:, 0] = g.standard_normal((hkv, hd))
+    for kh in range(hkv):
+        vf[kh, 0] = kh * 8 + np.arange(hd) / 8
+    k, v = (kf, vf) if kv_dtype == 0 else (oracle.f32_to_f16_bits(kf), oracle.f32_to_f16_bits(vf))
+    out = ctx.createBuffer(hq * hd * 4)
+    hip.gqaAttention(ctx, hip.AttnArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), kv_dtype, out, 0, 1, hq, hkv, hd,
+                                       cap, 0.5))
+    got = ctx.to_numpy(out, np.float32).reshape(hq, hd)
+    for h in range(hq):
+        np.testing.assert_allclose(got[h], (h // 4) * 8 + np.arange(hd) / 8, atol=1e-6)
+
+
+@pytest.mark.parametrize("hd,kv_dtype,T", [(8, 0, 2), (64, 1, 1), (128, 1, 1), (128, 1, 3), (64, 1, 40)])
+def test_ragged_pos_packed_equivalence(ctx, hip, oracle, hd, kv_dtype, T):
+    hq, hkv, pos = 8, 2, 37
+    valid, big = pos + T, pos + T + 29
+    g = np.random.default_rng(42)
+    q = g.standard_normal((T, hq, hd)).astype(np.float32)
+    kp = g.standard_normal((hkv, valid, hd)).astype(np.float32)
+    vp = g.standard_normal((hkv, valid, hd)).astype(np.float32)
+    if kv_dtype == 1:
+        kp, vp = oracle.f32_to_f16_bits(kp), oracle.f32_to_f16_bits(vp)
+        kb, vb = _f16_nan_cache((hkv, big, hd)), _f16_nan_cache((hkv, big, hd))
+    else:
+        kb, vb = np.full((hkv, big, hd), np.nan, np.float32), np.full((hkv, big, hd), np.nan, np.float32)
+    kb[:, :valid], vb[:, :valid] = kp, vp
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+
+    def run(k, v, cap):
+        out = ctx.createBuffer(T * hq * hd * 4)
+        hip.gqaAttention(ctx, hip.AttnArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), kv_dtype, out, pos, T, hq, hkv, hd,
+                                           cap, scale))
+        return ctx.to_numpy(out, np.float32)
+
+    a, b = run(kp, vp, valid), run(kb, vb, big)
+    assert np.array_equal(a, b)  # stride by max_ctx, never read past pos + t
+    check_out(b, oracle.gqa_attention(q, kp, vp, kv_dtype, pos, T, hq, hkv, hd, valid, scale))
+    if T > 1:  # perturb the last position: only the last query token changes
+        kb2, vb2 = kb.copy(), vb.copy()
+        if kv_dtype == 1:
+            kb2[:, valid - 1] ^= 0x0400
+            vb2[:, valid - 1] ^= 0x0400
+        else:
+            kb2[:, valid - 1] += 1.5
+            vb2[:, valid - 1] -= 2.0
+        c = run(kb2, vb2, big)
+        row = (T - 1) * hq * hd
+        assert np.array_equal(b[:row], c[:row]) and not np.array_equal(b[row:], c[row:])
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_softmax_stability(ctx, hip, oracle, kv_dtype):
+    # scores +-200 (kernels_b.zig:424-454), widened to head_dim 64 for the MFMA path
+    hd = 2 if kv_dtype == 0 else 64
+    q = np.zeros(hd, np.float32)
+    q[0] = 100
+    k = np.zeros((1, 2, hd), np.float32)
+    k[0, 0, 0], k[0, 1, 0] = -2, 2
+    v = np.zeros((1, 2, hd), np.float32)
+    v[0, 0, :2], v[0, 1, :2] = (7, -7), (3.5, -3.5)
+    if kv_dtype == 1:
+        k, v = oracle.f32_to_f16_bits(k), oracle.f32_to_f16_bits(v)
+    out = ctx.createBuffer(hd * 4)
+    hip.gqaAttention(ctx, hip.AttnArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), kv_dtype, out, 1, 1, 1, 1, hd, 2, 1.0))
+    got = ctx.to_numpy(out, np.float32)
+    np.testing.assert_allclose(got[:2], [3.5, -3.5], atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# decode: split-K kernel over many lengths and group sizes (separate-op path)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 127, 128, 129, 500, 1000, 4097])
+@pytest.mark.parametrize("hq,hkv,hd", [(32, 4, 128), (64, 4, 128), (8, 8, 64), (64, 2, 128), (12, 4, 64)])
+def test_decode_lengths_and_groups(ctx, hip, oracle, L, hq, hkv, hd):
+    g = np.random.default_rng(L * 7 + hq)
+    cap = L + 5
+    q = g.standard_normal((1, hq, hd)).astype(np.float32)
+    k = oracle.f32_to_f16_bits(g.standard_normal((hkv, cap, hd)).astype(np.float32))
+    v = oracle.f32_to_f16_bits(g.standard_normal((hkv, cap, hd)).astype(np.float32))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    out = ctx.createBuffer(hq * hd * 4)
+    hip.gqaAttention(ctx, hip.AttnArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), 1, out, L - 1, 1, hq, hkv, hd, cap,
+                                       scale))
+    check_out(ctx.to_numpy(out, np.float32), oracle.gqa_attention(q, k, v, 1, L - 1, 1, hq, hkv, hd, cap, scale))
+
+
+# ---------------------------------------------------------------------------
+# the fused step at the BASELINE configs
+# ---------------------------------------------------------------------------
+
+def _run_step(ctx, hip, q, k, v, qn, kn, positions, kc, vc, pos, s, fused):
+    """Runs one engine step on the GPU; returns (out, k_cache, v_cache)."""
+    T, hq, hd = q.shape
+    hkv, cap = kc.shape[0], kc.shape[1]
+    qb, kb, vb = dev(ctx, q), dev(ctx, k), dev(ctx, v)
+    qnb, knb, pb = dev(ctx, qn), dev(ctx, kn), dev(ctx, positions)
+    kcb, vcb = dev(ctx, kc), dev(ctx, vc)
+    out = ctx.createBuffer(T * hq * hd * 4)
+    if fused:
+        hip.attentionStep(ctx, hip.AttentionStepArgs(qb, kb, vb, qnb, knb, pb, kcb, vcb, out, 1, pos, T, hq, hkv, hd,
+                                                     cap, s.eps, s.theta, 1.0, s.scale))
+    else:  # forward.zig:345-412, op by op
+        hip.rmsNorm(ctx, hip.RmsNormArgs(qb, qnb, qb, T * hq, hd, s.eps))
+        hip.rmsNorm(ctx, hip.RmsNormArgs(kb, knb, kb, T * hkv, hd, s.eps))
+        hip.rope(ctx, hip.RopeArgs(qb, pb, T, hq, hd, s.theta))
+        hip.rope(ctx, hip.RopeArgs(kb, pb, T, hkv, hd, s.theta))
+        hip.kvAppend(ctx, hip.KvAppendArgs(kb, vb, kcb, vcb, 1, pos, T, hkv, hd, cap))
+        hip.gqaAttention(ctx, hip.AttnArgs(qb, kcb, vcb, 1, out, pos, T, hq, hkv, hd, cap, s.scale))
+    return ctx.to_numpy(out, np.float32), host(ctx, kcb, kc), host(ctx, vcb, vc)
+
+
+def _oracle_step(oracle, q, k, v, qn, kn, positions, kc, vc, pos, s):
+    T, hq, hd = q.shape
+    hkv, cap = kc.shape[0], kc.shape[1]
+    kc, vc = kc.copy(), vc.copy()
+    out, _, _ = oracle.attention_step(q, k, v, qn, kn, positions, kc, vc, kv_dtype=1, pos=pos, n_tokens=T,
+                                      n_q_heads=hq, n_kv_heads=hkv, head_dim=hd, max_ctx=cap, eps=s.eps,
+                                      theta=s.theta, scale=s.scale)
+    return out, kc, vc
+
+
+def check_cache(got_k, got_v, want_k, want_v, kc0, vc0, pos, T):
+    # rows outside pos..pos+T-1 untouched (bit-exact), appended rows within 1 f16 ulp
+    for got, want, old in ((got_k, want_k, kc0), (got_v, want_v, vc0)):
+        assert np.array_equal(got[:, :pos], old[:, :pos])
+        assert np.array_equal(got[:, pos + T:], old[:, pos + T:])
+        ulp = f16_ulp_diff(got[:, pos:pos + T], want[:, pos:pos + T])
+        print(f"  cache rows: max ulp {ulp.max()} ({int((ulp > 0).sum())} of {ulp.size} differ)", flush=True)
+        assert ulp.max() <= 1
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("config,layer", [(0, 0), (1, 0), (1, 47), (3, 0)])
+def test_decode_step_configs(ctx, hip, oracle, config, layer, fused):
+    cfg = synth.CONFIGS[config]
+    s, cap, pos = cfg["shape"], cfg["cap"], cfg["pos"]
+    q, k, v, qn, kn = synth.step_inputs(config, layer, 1, s)
+    kc, vc = synth.cache_f16(config, layer, s, cap, pos)
+    positions = np.array([pos], np.int32)
+    out, gk, gv = _run_step(ctx, hip, q, k, v, qn, kn, positions, kc, vc, pos, s, fused)
+    wout, wk, wv = _oracle_step(oracle, q, k, v, qn, kn, positions, kc, vc, pos, s)
+    check_cache(gk, gv, wk, wv, kc, vc, pos, 1)
+    check_out(out, wout)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("T,pos,hd", [(300, 0, 128), (130, 100, 128), (77, 5, 64), (2, 0, 128)])
+def test_prefill_step(ctx, hip, oracle, T, pos, hd, fused):
+    s = synth.Shape(head_dim=hd)
+    cap = pos + T + 7
+    q, k, v, qn, kn = synth.step_inputs(2, T, T, s, f16_exact=True)
+    kc, vc = synth.cache_f16(2, T, s, cap, pos)
+    positions = np.arange(pos, pos + T, dtype=np.int32)
+    out, gk, gv = _run_step(ctx, hip, q, k, v, qn, kn, positions, kc, vc, pos, s, fused)
+    wout, wk, wv = _oracle_step(oracle, q, k, v, qn, kn, positions, kc, vc, pos, s)
+    check_cache(gk, gv, wk, wv, kc, vc, pos, T)
+    check_out(out, wout)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_prefill_config2_full(ctx, hip, oracle, fused):
+    """C2 at full size: every cache row checked; attention checked on two q heads
+    of different kv groups against the oracle (the oracle per head is ~1 s)."""
+    cfg = synth.CONFIGS[2]
+    s, T = cfg["shape"], cfg["tokens"]
+    q, k, v, qn, kn = synth.step_inputs(2, 0, T, s, f16_exact=True)
+    kc, vc = synth.cache_f16(2, 0, s, T, 0)
+    positions = np.arange(T, dtype=np.int32)
+    out, gk, gv = _run_step(ctx, hip, q, k, v, qn, kn, positions, kc, vc, 0, s, fused)
+    # oracle cache: k norm + rope + append (cheap), then per-head attention
+    k_rot = oracle.rope(oracle.rms_norm(k, kn, s.eps), positions, s.theta)
+    wk, wv = kc.copy(), vc.copy()
+    oracle.kv_append(k_rot, v, wk, wv, 1, 0, T, s.n_kv_heads, s.head_dim, T)
+    check_cache(gk, gv, wk, wv, kc, vc, 0, T)
+    q_rot = oracle.rope(oracle.rms_norm(q, qn, s.eps), positions, s.theta)
+    out = out.reshape(T, s.n_q_heads, s.head_dim)
+    for h in (3, 29):
+        kh = h // (s.n_q_heads // s.n_kv_heads)
+        want = oracle.gqa_attention(np.ascontiguousarray(q_rot[:, h:h + 1]), np.ascontiguousarray(wk[kh:kh + 1]),
+                                    np.ascontiguousarray(wv[kh:kh + 1]), 1, 0, T, 1, 1, s.head_dim, T, s.scale)
+        check_out(out[:, h], want)
+
+
+# ---------------------------------------------------------------------------
+# paged decode (C4 layout)
+# ---------------------------------------------------------------------------
+
+def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None):
+    s = synth.Shape()
+    lay = synth.paged_layout(n_seqs, lo, hi, 16, seed=seed)
+    hq, hkv, hd = s.n_q_heads, s.n_kv_heads, s.head_dim
+    slots = lay.n_pages * 16
+    g = np.random.default_rng(seed)
+    kpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
+    vpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
+    q, k, v, qn, kn = synth.step_inputs(4, seed, n_seqs, s)
+    kpb, vpb = dev(ctx, kpool), dev(ctx, vpool)
+    out = ctx.createBuffer(n_seqs * hq * hd * 4)
+    max_len = int(lay.seq_lens.max())
+    hip.pagedDecode(ctx, hip.PagedDecodeArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), dev(ctx, qn), dev(ctx, kn), kpb,
+                                             vpb, dev(ctx, lay.page_table), dev(ctx, lay.seq_lens), out, n_seqs, hq,
+                                             hkv, hd, 16, lay.n_pages, lay.max_pages, max_len, s.eps, s.theta, 1.0,
+                                             s.scale))
+    got = ctx.to_numpy(out, np.float32).reshape(n_seqs, hq * hd)
+    gk, gv = host(ctx, kpb, kpool), host(ctx, vpb, vpool)
+    new_slots = [lay.slot(b, int(lay.seq_lens[b]) - 1) for b in range(n_seqs)]
+    mask = np.ones(slots, bool)
+    mask[new_slots] = False
+    assert np.array_equal(gk[:, mask], kpool[:, mask]) and np.array_equal(gv[:, mask], vpool[:, mask])
+    for b in (range(n_seqs) if check_seqs is None else check_seqs):
+        L = int(lay.seq_lens[b])
+        kc = oracle.paged_gather_f16(kpool, lay.page_table[b], 16, L)
+        vc = oracle.paged_gather_f16(vpool, lay.page_table[b], 16, L)
+        wout, wk, wv = _oracle_step(oracle, q[b:b + 1], k[b:b + 1], v[b:b + 1], qn, kn, np.array([L - 1], np.int32),
+                                    kc, vc, L - 1, s)
+        ulp_k = f16_ulp_diff(gk[:, new_slots[b]], wk[:, L - 1])
+        ulp_v = f16_ulp_diff(gv[:, new_slots[b]], wv[:, L - 1])
+        assert ulp_k.max() <= 1 and ulp_v.max() <= 1
+        check_out(got[b], wout)
+
+
+def test_paged_decode_small(ctx, hip, oracle):
+    _paged_case(ctx, hip, oracle, 7, 1, 300, seed=5)
+
+
+def test_paged_decode_config4_geometry(ctx, hip, oracle):
+    _paged_case(ctx, hip, oracle, 32, 512, 16384, seed=0, check_seqs=(0, 13, 31))
+
+
+# ---------------------------------------------------------------------------
+# determinism
+# ---------------------------------------------------------------------------
+
+def test_decode_is_deterministic(ctx, hip):
+    s = synth.Shape()
+    q, k, v, qn, kn = synth.step_inputs(1, 3, 1, s)
+    kc, vc = synth.cache_f16(1, 3, s, 2048, 2047)
+    a = _run_step(ctx, hip, q, k, v, qn, kn, np.array([2047], np.int32), kc, vc, 2047, s, True)
+    b = _run_step(ctx, hip, q, k, v, qn, kn, np.array([2047], np.int32), kc, vc, 2047, s, True)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_config0_golden(ctx, hip, oracle, fused):
+    """The committed config-0 vectors (tests/golden/c0), run through the GPU."""
+    import os
+    from conftest import GOLDEN
+    L = lambda n: oracle.load_ds5t(os.path.join(GOLDEN, "c0", f"{n}.ds5t")).data
+    s = synth.CONFIGS[0]["shape"]
+    q, k, v = L("q"), L("k"), L("v")
+    kc, vc = L("k_cache_in"), L("v_cache_in")
+    out, gk, gv = _run_step(ctx, hip, q, k, v, L("q_norm"), L("k_norm"), L("positions"), kc, vc, 31, s, fused)
+    check_cache(gk, gv, L("k_cache_out"), L("v_cache_out"), kc, vc, 31, 1)
+    check_out(out, L("output"))
