@@ -209,3 +209,18 @@ DS5_DEVICE_INLINE f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
 DS5_DEVICE_INLINE float lane_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 DS5_DEVICE_INLINE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Correctly rounded f32 square root. The compiler lowers __fsqrt_rn and
+// sqrtf to v_sqrt_f32, which is only 1-ulp accurate, while the reference's
+// @sqrt (and the C library's sqrtf) round correctly. The root is taken in f64
+// and rounded to f32: rounding twice is innocuous for sqrt when the wide
+// format has at least 2*24+2 significand bits (53 here), and a 24-bit input's
+// square root lies at least 2^-51 (relative) away from every f32 midpoint, so
+// an f64 root within 1 f64 ulp still rounds to the correct f32.
+DS5_DEVICE_INLINE float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
+
+// 1 / sqrt(sumsq / dim + eps) with each operation correctly rounded, the
+// RMSNorm scale of kernels_a.zig:87.
+DS5_DEVICE_INLINE float rms_inv(float sumsq, float dim, float eps) {
+    return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sumsq, dim) + eps));
+}

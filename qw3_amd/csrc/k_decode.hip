@@ -87,7 +87,7 @@ __device__ __forceinline__ float row_inv_rms(const float* row, int dim, float ep
 #pragma clang fp contract(off)
     float sumsq = 0.0f;
     for (int i = 0; i < dim; i++) sumsq += row[i] * row[i];
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)dim) + eps));
+    return rms_inv(sumsq, (float)dim, eps);
 }
 
 __device__ __forceinline__ float norm_mul(float v, float inv, float w) {

@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void rms_norm_kernel(const float* x,
     const int lane = threadIdx.x;
     float sumsq;
     rows_sumsq(x, row0, n_rows, dim, tile, &sumsq);
-    s_inv[lane] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)dim) + eps));
+    s_inv[lane] = rms_inv(sumsq, (float)dim, eps);
     __syncthreads();
     // out may alias x: every element is read before the same thread writes it.
     for (int r = 0; r < kRowsPerBlock; r++) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void kv_prep_kernel(KvPrepLaunch a, 
     const int lane = threadIdx.x;
     float sumsq;
     rows_sumsq(a.k, row0, n_rows, dim, tile, &sumsq);
-    s_inv[lane] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)dim) + a.eps));
+    s_inv[lane] = rms_inv(sumsq, (float)dim, a.eps);
     __syncthreads();
     for (int r = 0; r < kRowsPerBlock; r++) {
         const uint32_t row = row0 + r;

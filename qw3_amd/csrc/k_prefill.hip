@@ -68,7 +68,7 @@ __device__ __forceinline__ void load_q_operands(const PrefillParams& p, const Ro
             sumsq += v.z * v.z;
             sumsq += v.w * v.w;
         }
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sumsq, (float)D) + p.eps));
+        const float inv = rms_inv(sumsq, (float)D, p.eps);
         const float tpos = (float)p.positions[t];
         // This lane holds dims ks*16 + 8*half_id + j; the rope partner of a
         // dim d < D/2 is d + D/2, which is k-step ks + D/32 of the same lane.

@@ -79,7 +79,8 @@ class RopeArgs(C.Structure):
                 ("head_dim", C.c_uint32), ("theta", C.c_float), ("freq_scale", C.c_float)]
 
     def __init__(self, *args, **kw):
-        kw.setdefault("freq_scale", 1.0)  # contracts.zig:237 default
+        if len(args) < len(self._fields_):
+            kw.setdefault("freq_scale", 1.0)  # contracts.zig:237 default
         super().__init__(*args, **kw)
 
 

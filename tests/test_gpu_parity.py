@@ -77,7 +77,9 @@ def test_rope_fixtures(ctx, hip, oracle, i):
 @pytest.mark.parametrize("kv_dtype", [0, 1])
 def test_attention_fixtures(ctx, hip, oracle, i, kv_dtype):
     """f32 caches: the reference fixture tolerance. f16 caches (MFMA decode and
-    prefill at head_dim 64): against the oracle's f16 branch."""
+    prefill at head_dim 64): against the oracle's f16 branch at the attention
+    gate (max-abs 2e-3, cosine 0.99999); prefill rounds q and p to f16 for the
+    MFMA products, which moves outputs by ~1e-4 on these fixtures."""
     c = _cases(oracle, "attention")[i]
     p, tol = c["params"], c["tolerance"]
     q, kc, vc, want = (_t(oracle, c, n) for n in ("q", "k_cache", "v_cache", "output"))
@@ -94,7 +96,7 @@ def test_attention_fixtures(ctx, hip, oracle, i, kv_dtype):
         r = oracle.compare(want, got, tol["atol"], tol["rtol"])
         assert r.passed, r
     else:
-        check_out(got, want, atol=1e-4)
+        check_out(got, want)
 
 
 @pytest.mark.parametrize("kv_dtype", [0, 1])
