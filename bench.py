@@ -14,7 +14,7 @@ synchronisation on both sides and timed with HIP events on the context
 stream. Inputs are synthetic and already resident in HBM.
 
 value  = C1 algorithmic HBM bytes of the K sweeps / elapsed (GB/s)
-roofline.achieved = algorithmic bytes of one decode_splitk_kernel launch (one
+roofline.achieved = algorithmic bytes of one decode_split_kernel launch (one
          layer) / that kernel's mean device duration from HIP events around
          each launch on the context stream (a separate, eager pass)
 cpu_baseline = the CPU oracle (a line-by-line C restatement of the reference's
@@ -178,6 +178,18 @@ def kernel_mean_ns(ctx, work, kernel, reps):
     return (total / n if n else float("nan")), n
 
 
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/<kernel>_<workload>_traffic.json: FETCH_SIZE and WRITE_SIZE per
+    dispatch, scaled by the same counters' reading of a copy of known size),
+    or None when no summary is committed."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def cpu_baseline_c1(synth, seconds):
     """Oracle (single-threaded C restatement of kernels_a/b.zig) on C1 layers."""
     from oracle import oracle as O
@@ -209,6 +221,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", default="C1,C2,C3,C4", help="comma list of configs to run (C1 is the headline)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
+                         "the FETCH_SIZE / WRITE_SIZE traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -220,6 +235,13 @@ def main():
 
     only = set(args.only.upper().split(","))
     ctx = H.Ctx.init(0)
+    if args.calibrate_copy:
+        nb = args.calibrate_copy << 20
+        src, dst = ctx.createBuffer(nb), ctx.createBuffer(nb)
+        ctx.fill_normal_f16(src, nb // 2, seed=7)
+        ctx.copy_device(dst, src, nb)
+        ctx.submit()
+        log(f"[bench] calibration copy of {args.calibrate_copy} MiB done")
     extra = {}
     result = None
 
@@ -231,9 +253,9 @@ def main():
         us_layer = elapsed / layers * 1e6
         gbs = w.bytes_per_layer * layers / elapsed / 1e9
         log(f"[bench] C1 graph sweep: {us_layer:.3f} us/layer, {gbs:.1f} GB/s (wall {wall / layers * 1e6:.3f} us/layer)")
-        ns_split, n_split = kernel_mean_ns(ctx, w, "decode_splitk_kernel", max(2, args.steps // 10))
+        ns_split, n_split = kernel_mean_ns(ctx, w, "decode_split_kernel", max(2, args.steps // 10))
         achieved = w.bytes_per_layer / ns_split  # bytes/ns == GB/s
-        log(f"[bench] C1 decode_splitk_kernel mean {ns_split / 1e3:.3f} us over {n_split} launches -> {achieved:.1f} GB/s")
+        log(f"[bench] C1 decode_split_kernel mean {ns_split / 1e3:.3f} us over {n_split} launches -> {achieved:.1f} GB/s")
         ctx.submit()
         ctx.begin()
         for _ in range(args.steps):
@@ -253,8 +275,9 @@ def main():
             us_per_layer=round(us_layer, 4),
             us_per_layer_eager=round(eager_us, 4),
             roofline=dict(bound="hbm", achieved=round(achieved, 2), peak=HBM_PEAK_GBS, unit="GB/s",
-                          frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                          kernel="decode_splitk_kernel", kernel_mean_us=round(ns_split / 1e3, 4),
+                          frac=round(achieved / HBM_PEAK_GBS, 4),
+                          traffic=measured_traffic("decode_split_kernel", "c1"),
+                          kernel="decode_split_kernel", kernel_mean_us=round(ns_split / 1e3, 4),
                           algorithmic_bytes_per_launch=w.bytes_per_layer),
         )
         del w
@@ -279,7 +302,7 @@ def main():
         steps3 = max(5, args.steps // 4)
         elapsed, _ = time_graph(ctx, w, steps3, 2)
         us = elapsed / (w.layers * steps3) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "decode_splitk_kernel", 2)
+        ns_k, _ = kernel_mean_ns(ctx, w, "decode_split_kernel", 2)
         extra["C3_decode"] = dict(us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
                                   kernel_us=round(ns_k / 1e3, 3),
                                   kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),
@@ -293,7 +316,7 @@ def main():
         steps4 = max(3, args.steps // 10)
         elapsed, _ = time_graph(ctx, w, steps4, 1)
         us = elapsed / (w.layers * steps4) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "decode_splitk_kernel", 1)
+        ns_k, _ = kernel_mean_ns(ctx, w, "decode_split_kernel", 1)
         extra["C4_paged_decode"] = dict(us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
                                         kernel_us=round(ns_k / 1e3, 3),
                                         kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),

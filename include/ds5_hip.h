@@ -242,8 +242,11 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* args
  * One decode token per sequence: its q/k/v are normalised and rotated at
  * position seq_lens[b] - 1, k/v are appended into that slot, and the token
  * attends positions 0..seq_lens[b]-1. max_seq_len is a host-side upper bound
- * of seq_lens (it sizes the launch); sequences longer than it are rejected by
- * the kernel through the status buffer. */
+ * of seq_lens (it sizes the launch). page_size must be a multiple of 16 (a
+ * 16-position half-tile of the kernel never straddles pages). Entries the
+ * device finds out of range -- a sequence length outside [1, max_seq_len] or a
+ * page index outside [0, n_pages) -- are never dereferenced; that sequence's
+ * output rows are set to NaN instead. */
 typedef struct ds5_paged_decode_args {
     ds5_buf q;          /* f32 [n_seqs, n_q_heads, head_dim] (in/out: normalised + rotated) */
     ds5_buf k;          /* f32 [n_seqs, n_kv_heads, head_dim] (in/out) */
@@ -283,6 +286,11 @@ int ds5_hip_rope_table(float theta, uint32_t head_dim, float* out);
  * (seed, element index) on the device. Lets benchmarks build multi-GB caches
  * without host generation; results are deterministic for a given seed. */
 int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t seed);
+
+/* Device-to-device byte copy on the context stream (the runtime's plain copy
+ * kernel). The benchmark uses a copy of known size to calibrate the HBM
+ * traffic counters (FETCH_SIZE / WRITE_SIZE) it reports. */
+int ds5_hip_copy_device(ds5_hip_ctx* ctx, ds5_buf dst, ds5_buf src, uint64_t len);
 
 #ifdef __cplusplus
 }

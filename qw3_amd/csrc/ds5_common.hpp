@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -163,7 +164,6 @@ struct DecodeLaunch {
     uint32_t page_size, max_pages;
     uint32_t ctx_len;        // contiguous: attended positions (pos + 1)
     uint32_t max_len;        // upper bound of attended positions (sizes the grid)
-    int32_t* status;         // paged: device flag set when a sequence is out of range
     float* out;              // [n_seqs, n_q_heads * head_dim]
     uint32_t n_seqs, n_q_heads, n_kv_heads, head_dim;
     float scale, eps, freq_scale;

@@ -6,7 +6,7 @@
 //   rmsNorm       kernels_a.zig:68-91   -> rms_norm_kernel
 //   rope          kernels_a.zig:97-130  -> rope_kernel
 //   kvAppend      kernels_a.zig:169-217 -> kv_append_kernel
-//   gqaAttention  kernels_b.zig:29-133  -> decode_splitk_kernel (+ merge),
+//   gqaAttention  kernels_b.zig:29-133  -> decode_split_kernel (+ merge),
 //                                          prefill_kernel, or the generic kernel
 #include <math.h>
 
@@ -336,6 +336,8 @@ int ds5_hip_paged_decode(ds5_hip_ctx* ctx, const ds5_paged_decode_args* a) {
     if (hd != 64 && hd != 128) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: head_dim must be 64 or 128");
     if (a->page_size == 0 || a->n_pages == 0 || a->max_pages == 0)
         return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: empty page geometry");
+    if (a->page_size % 16 != 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: page_size must be a multiple of 16");
     if ((uint64_t)a->max_seq_len > (uint64_t)a->max_pages * a->page_size)
         return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "paged: max_seq_len exceeds max_pages * page_size");
     const uint64_t slots = (uint64_t)a->n_pages * a->page_size;
@@ -387,6 +389,14 @@ int ds5_hip_rope_table(float theta, uint32_t head_dim, float* out) {
     ds5_rope_table(theta, head_dim, &t);
     for (uint32_t i = 0; i < head_dim / 2; i++) out[i] = t.inv[i];
     return DS5_OK;
+}
+
+int ds5_hip_copy_device(ds5_hip_ctx* ctx, ds5_buf dst, ds5_buf src, uint64_t len) {
+    if (!covers(dst, len) || !covers(src, len)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "copy_device: view too small");
+    if (int rc = set_device(ctx)) return rc;
+    if (len == 0) return DS5_OK;
+    return ds5_hip_status(ctx, hipMemcpyAsync(ds5_ptr(dst), ds5_ptr(src), len, hipMemcpyDeviceToDevice, ctx->stream),
+                          "copy_device");
 }
 
 int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t seed) {

@@ -1,37 +1,50 @@
-// k_decode.hip -- split-K flash-decoding on gfx950 MFMA for one query token
-// per sequence over an f16 KV cache (contiguous or paged).
+// k_decode.hip -- split-K flash decoding on gfx950 MFMA: one query token per
+// sequence over an f16 KV cache (contiguous or paged).
 //
 // Semantics: kernels_b.zig:29-133 with n_tokens == 1 -- q head h attends
 // positions 0..L-1 of kv head h/group with softmax(scale * q.k) in f32.
 //
-// Work decomposition. One workgroup serves ALL q heads of one kv head (up to
-// 16 per workgroup; larger groups use several head subgroups) for one range
+// Work decomposition. A workgroup (4 wavefronts) serves up to 16 q heads of one
+// kv head -- the whole GQA group for the Qwen3 shapes -- over one range
 // ("split") of `chunk` positions, so each K/V byte is read from HBM once per
-// GQA group. A workgroup is WAVES wavefronts; each wavefront takes 32-position
-// tiles of the split in turn:
+// group. Each wavefront owns 32-position tiles of the split:
 //   S^T[32 pos x 16 heads] = K[32 pos x D] . Q^T      v_mfma_f32_16x16x32_f16
 //   O^T[D x 16 heads]     += V^T[D x 32 pos] . P^T    v_mfma_f32_16x16x32_f16
-// K goes from HBM straight into MFMA A-operand registers (16-byte loads, a
-// lane owns one position row and 8 consecutive dims per k-step). V is staged
-// through LDS (coalesced 16-byte loads, padded rows) and read back transposed
-// as the A operand of the P.V product. q and p are split into f16 hi + lo
-// parts (x = hi + lo exactly to ~22 bits), and both halves are accumulated
-// into the same f32 accumulator, so the products keep ~f32 accuracy while
-// K/V stay f16. Softmax runs in the log2 domain with running max / sum per
-// head; row reductions are lane exchanges inside the 16-lane groups.
-// Workgroup partials (max, sum, unnormalised O) go to a workspace and a merge
-// kernel combines the splits, unless one split covers the whole context.
+// K rows go from HBM straight into MFMA A-operand registers (16-byte loads);
+// V rows are staged through a wavefront-private LDS area and read back
+// transposed. q and p are split into f16 hi + lo halves accumulated into one
+// f32 accumulator, so the products keep ~22 significant bits while K/V stay
+// f16. Softmax runs in the log2 domain against a per-head reference that only
+// moves when a tile's maximum exceeds it by more than 2^8 (the lazy rescale),
+// so the O accumulators are rescaled rarely.
 //
-// Fused mode adds the step's prologue (forward.zig:345-396 order): the
-// workgroup normalises and rotates its q heads itself, and the workgroup whose
-// split holds the new position normalises and rotates k, appends k and v (f16)
-// to the cache, and feeds the new row to the tile from LDS. All of that uses
-// the reference's operation order (serial norm sum, (v*inv)*w, unfused rope).
+// Latency structure (a decode layer is ~2 us of HBM time, so the critical path
+// matters more than instruction counts): every wavefront issues its first
+// tile's K/V loads before anything else, the q prologue (load, norm, rope,
+// hi/lo split) runs while they are in flight, and later tiles are prefetched
+// one tile ahead. Workgroup barriers before the main loop are LDS-only, so
+// they never wait for the outstanding K/V loads.
+//
+// Splits combine through a workspace: each workgroup writes its unnormalised
+// O, its reference max and its sum; decode_merge_kernel combines the splits of
+// every (sequence, q head) with one load per split and lane. A single split
+// writes the output directly. Cross-workgroup combining inside one launch was
+// measured to be slower on this part than the second launch.
+//
+// Fused mode adds the step's prologue in the engine's op order
+// (forward.zig:345-396): the workgroup normalises and rotates its q heads
+// (serial-order f32 sum of squares, (v*inv)*w, unfused rotation), and the
+// workgroup whose split holds the new position normalises and rotates k,
+// appends k and v (f16) to the cache and substitutes the new row into its tile.
 #include "ds5_common.hpp"
 
 namespace {
 
-constexpr int kTile = 32;  // positions per wavefront tile
+constexpr int kTile = 32;   // positions per wavefront tile
+constexpr int kWaves = 4;   // wavefronts per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kHeads = 16;  // q heads per workgroup (the MFMA N dimension)
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (p <= 2^8 between rescales)
 
 struct DecodeParams {
     const float* q;
@@ -42,12 +55,12 @@ struct DecodeParams {
     const int32_t* positions;
     f16* k_cache;
     f16* v_cache;
-    uint64_t cache_stride;
+    uint64_t cache_stride;  // rows per kv head: max_ctx, or pool slots when paged
     const int32_t* page_table;
     const int32_t* seq_lens;
     float* out;
-    float* part_o;   // [n_seqs, n_q_heads, n_splits, D]
-    float* part_ml;  // [n_seqs, n_q_heads, n_splits, 2]
+    float* part_o;   // [n_seqs * n_q_heads, n_splits, D]
+    float* part_ml;  // [n_seqs * n_q_heads, n_splits, 2]: reference max (log2), sum
     uint32_t page_size, max_pages, n_pages;
     uint32_t ctx_len, max_len, chunk, n_splits;
     uint32_t n_q_heads, n_kv_heads, group, n_sub;
@@ -55,39 +68,201 @@ struct DecodeParams {
 };
 
 template <int D>
-struct Geometry {
-    static constexpr int KK = D / 32;                  // k-steps of the Q.K product
-    static constexpr int DT = D / 16;                  // 16-row tiles of O^T
-    static constexpr int ROW_BYTES = D * 2 + 8;        // LDS V row, padded: conflict-free transposed reads
-    static constexpr int ROW_CHUNKS = D / 8;           // 16-byte chunks per cache row
-    static constexpr int V_CHUNKS = kTile * ROW_CHUNKS / 64;  // 16-byte V loads per lane per tile
+struct Geo {
+    static constexpr int KK = D / 32;            // k-steps of the S product
+    static constexpr int DT = D / 16;            // 16-row blocks of O^T
+    static constexpr int RC = D / 8;             // 16-byte chunks per cache row
+    static constexpr int VC = kTile * RC / 64;   // V chunks per lane per tile
+    static constexpr int VROW = D * 2 + 16;      // bytes per staged V row (aligned, banks spread)
+    static constexpr int OROW = D + 4;           // floats per row of the cross-wave O buffer
 };
 
-__device__ __forceinline__ u32x4 load16(const f16* p) { return *(const u32x4*)p; }
+template <int D>
+struct TileRegs {
+    u32x4 k[2][Geo<D>::KK];  // [half-tile][k-step]: row c16 of the half, dims kk*32 + 8g .. +8
+    u32x4 v[Geo<D>::VC];     // chunk r: row (lane + 64r) / RC, dims ((lane + 64r) % RC) * 8 .. +8
+};
 
-template <bool PAGED>
-__device__ __forceinline__ int64_t cache_row(const DecodeParams& p, uint32_t b, uint32_t pos) {
-    if (!PAGED) return pos;
-    const int32_t page = p.page_table[(uint64_t)b * p.max_pages + pos / p.page_size];
-    if (page < 0 || (uint32_t)page >= p.n_pages) return -1;
-    return (int64_t)page * p.page_size + pos % p.page_size;
+// Barrier for LDS traffic only: outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Serial-order f32 row norm + NeoX rope of one row held in LDS (in place);
-// row_inv is the row's 1/rms computed by one thread.
-__device__ __forceinline__ void rope_pair(float x0, float x1, float angle, float& y0, float& y1) {
-#pragma clang fp contract(off)
-    const float c = cosf(angle);
-    const float s = sinf(angle);
-    y0 = x0 * c - x1 * s;
-    y1 = x0 * s + x1 * c;
+__device__ __forceinline__ u32x4 ld16(const f16* ptr) { return *(const u32x4*)ptr; }
+
+// gfx950 LDS transpose read (ds_read_b64_tr_b16) of 4 halves; see its use below.
+__device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_byte_ptr) {
+    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4h;
+    typedef __attribute__((address_space(3))) v4h lds_v4h;
+    const v4h r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4h*)(lds_byte_ptr));
+    return __builtin_bit_cast(f16x4, r);
 }
 
-__device__ __forceinline__ float row_inv_rms(const float* row, int dim, float eps) {
+// Page of sequence b holding position pos; out-of-range entries read page 0
+// and raise `bad` (the workgroup then poisons its output).
+__device__ __forceinline__ uint64_t page_base(const DecodeParams& p, uint32_t b, uint32_t pos, bool& bad) {
+    const int32_t pg = p.page_table[(uint64_t)b * p.max_pages + pos / p.page_size];
+    const bool ok = (uint32_t)pg < p.n_pages;
+    bad |= !ok;
+    return (uint64_t)(ok ? pg : 0) * p.page_size;
+}
+
+// Issues the K/V loads of tile [p0, p0 + 32) of a split ending at `end`.
+// Rows at or past `end` are redirected to valid memory (clamped for the
+// contiguous cache, kept inside the same page when paged); their scores are
+// masked and their V rows zeroed before use.
+template <int D, bool PAGED>
+__device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p, const f16* kbase, const f16* vbase,
+                                           uint32_t b, uint32_t p0, uint32_t end, int g, int c16, int lane,
+                                           bool& bad) {
+    using G = Geo<D>;
+    uint64_t rowA = 0, rowB = 0;  // paged: first slot of each 16-position half-tile
+    if constexpr (PAGED) {
+        // page_size is a multiple of 16 and p0 a multiple of 32: each half is inside one page
+        const uint32_t posB = min(p0 + 16, end - 1);
+        rowA = page_base(p, b, p0, bad) + p0 % p.page_size;
+        rowB = page_base(p, b, posB, bad) + (p0 + 16) % p.page_size;
+    }
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+        uint64_t row;
+        if constexpr (PAGED)
+            row = (st ? rowB : rowA) + c16;
+        else
+            row = min((uint32_t)(p0 + 16 * st + c16), end - 1);
+#pragma unroll
+        for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = ld16(kbase + row * D + kk * 32 + 8 * g);
+    }
+#pragma unroll
+    for (int r = 0; r < G::VC; r++) {
+        const int c = lane + 64 * r;
+        const int tr = c / G::RC;  // row within the tile
+        uint64_t row;
+        if constexpr (PAGED)
+            row = (r < G::VC / 2 ? rowA : rowB) + (tr & 15);
+        else
+            row = min((uint32_t)(p0 + tr), end - 1);
+        T.v[r] = ld16(vbase + row * D + (c % G::RC) * 8);
+    }
+}
+
+// Splits x into f16 hi + lo with x ~= hi + lo to ~22 significant bits.
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+template <int D, bool FUSED>
+__device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32_t end, int g, int c16, int lane,
+                                             const f16x8 (&qh)[Geo<D>::KK], const f16x8 (&ql)[Geo<D>::KK],
+                                             f32x4 (&O)[Geo<D>::DT], float& m_ref, float& l_sum, char* vlds,
+                                             int new_row, const f16* s_knew, const f16* s_vnew, float scale_log2,
+                                             bool first) {
+    using G = Geo<D>;
+    // Fused: the tile holding the new position takes the freshly appended row from LDS.
+    if (FUSED && new_row >= 0) {
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+            if (16 * st + c16 == new_row)
+#pragma unroll
+                for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = *(const u32x4*)(s_knew + kk * 32 + 8 * g);
+#pragma unroll
+        for (int r = 0; r < G::VC; r++) {
+            const int c = lane + 64 * r;
+            if (c / G::RC == new_row) T.v[r] = *(const u32x4*)(s_vnew + (c % G::RC) * 8);
+        }
+    }
+    const bool partial = p0 + kTile > end;  // wave-uniform
+
+    // S^T = K . Q^T with q = hi + lo
+    f32x4 S[2];
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < G::KK; kk++) {
+            const f16x8 a = __builtin_bit_cast(f16x8, T.k[st][kk]);
+            acc = mfma_16x16x32(a, qh[kk], acc);
+            acc = mfma_16x16x32(a, ql[kk], acc);
+        }
+        S[st] = acc;
+    }
+    // this lane: head c16, positions p0 + 16*st + 4g + i (score j = 4*st + i)
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) s[j] = S[j / 4][j % 4] * scale_log2;
+    if (partial) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (p0 + 16 * (j / 4) + 4 * g + (j % 4) >= end) s[j] = -INFINITY;
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) mx = fmaxf(mx, s[j]);
+    mx = fmaxf(mx, lane_xor(mx, 16));
+    mx = fmaxf(mx, lane_xor(mx, 32));
+    // Lazy rescale: move the reference only when the tile max exceeds it by > 2^8.
+    if (first) {
+        m_ref = mx;  // O and l are still zero
+    } else if (__ballot(mx > m_ref + kRescaleLog2) != 0) {
+        const bool move = mx > m_ref + kRescaleLog2;
+        const float m_new = move ? mx : m_ref;
+        const float alpha = fast_exp2(m_ref - m_new);  // 1 for heads that keep their reference
+        l_sum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; dt++) O[dt] *= alpha;
+        m_ref = m_new;
+    }
+    f16x8 ph, pl;
+    float psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float pj = fast_exp2(s[j] - m_ref);
+        psum += pj;
+        _Float16 hi, lo;
+        split_f16(pj, hi, lo);
+        ph[j] = hi;
+        pl[j] = lo;
+    }
+    l_sum += psum;
+
+    // V tile -> wavefront LDS area (rows past the split end zeroed: p is 0 there, V may be garbage)
+#pragma unroll
+    for (int r = 0; r < G::VC; r++) {
+        const int c = lane + 64 * r;
+        u32x4 v = T.v[r];
+        if (partial && p0 + c / G::RC >= end) v = u32x4{0u, 0u, 0u, 0u};
+        *(u32x4*)(vlds + (c / G::RC) * G::VROW + (c % G::RC) * 16) = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // O^T += V^T . P^T; k-slot (g, j) <-> tile row 4g + j (j < 4), 16 + 4g + j - 4 (j >= 4).
+    // ds_read_b64_tr_b16: within each 16-lane group, lane i reads 4 halves at row
+    // base + i/4, columns c0 + 4*(i%4); lane j then holds column c0 + j of those 4 rows.
+#pragma unroll
+    for (int dt = 0; dt < G::DT; dt++) {
+        const int col = dt * 16 + 4 * (c16 & 3);
+        const f16x4 lo4 = lds_read_tr16(vlds + (4 * g + (c16 >> 2)) * G::VROW + col * 2);
+        const f16x4 hi4 = lds_read_tr16(vlds + (16 + 4 * g + (c16 >> 2)) * G::VROW + col * 2);
+        const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        O[dt] = mfma_16x16x32(a, ph, O[dt]);
+        O[dt] = mfma_16x16x32(a, pl, O[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float serial_sumsq(const float* row, int dim) {
 #pragma clang fp contract(off)
-    float sumsq = 0.0f;
-    for (int i = 0; i < dim; i++) sumsq += row[i] * row[i];
-    return rms_inv(sumsq, (float)dim, eps);
+    float acc = 0.0f;
+    for (int i = 0; i < dim; i += 4) {
+        const float4 v = *(const float4*)(row + i);
+        acc += v.x * v.x;
+        acc += v.y * v.y;
+        acc += v.z * v.z;
+        acc += v.w * v.w;
+    }
+    return acc;
 }
 
 __device__ __forceinline__ float norm_mul(float v, float inv, float w) {
@@ -95,297 +270,313 @@ __device__ __forceinline__ float norm_mul(float v, float inv, float w) {
     return v * inv * w;
 }
 
+__device__ __forceinline__ void rotate(float x0, float x1, float c, float s, float& y0, float& y1) {
+#pragma clang fp contract(off)
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+
 __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float inv) {
 #pragma clang fp contract(off)
     return pos * freq_scale * inv;
 }
 
-template <int D, int WAVES, bool FUSED, bool PAGED>
-__global__ __launch_bounds__(WAVES * 64) void decode_splitk_kernel(DecodeParams p, RopeTable table) {
-    using Gm = Geometry<D>;
-    constexpr int KK = Gm::KK, DT = Gm::DT, VC = Gm::V_CHUNKS, RC = Gm::ROW_CHUNKS;
-    constexpr int NT = WAVES * 64;
-
-    // LDS: V staging per wavefront, reused for the cross-wave reduction.
-    constexpr int V_BYTES = WAVES * kTile * Gm::ROW_BYTES;
-    constexpr int O_STRIDE = D + 4;  // padded row of the cross-wave O buffer
-    constexpr int O_BYTES = WAVES * 16 * O_STRIDE * 4;
-    __shared__ __attribute__((aligned(16))) char s_raw[V_BYTES > O_BYTES ? V_BYTES : O_BYTES];
-    __shared__ float s_m[WAVES][16], s_l[WAVES][16];
-    __shared__ float s_q[FUSED ? 16 : 1][FUSED ? D : 1];
-    __shared__ float s_krow[FUSED ? D : 1];
-    __shared__ float s_inv[17];
+template <int D, bool FUSED, bool PAGED>
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, RopeTable table) {
+    using G = Geo<D>;
+    constexpr int KK = G::KK, DT = G::DT;
+    constexpr int V_BYTES = kWaves * kTile * G::VROW;
+    constexpr int O_BYTES = kWaves * kHeads * G::OROW * 4;
+    __shared__ __attribute__((aligned(16))) char s_big[V_BYTES > O_BYTES ? V_BYTES : O_BYTES];
+    __shared__ __attribute__((aligned(16))) float s_q[kHeads][G::OROW];
+    __shared__ __attribute__((aligned(16))) float s_krow[FUSED ? D : 4];
+    __shared__ float s_qn[FUSED ? D : 1], s_kn[FUSED ? D : 1], s_cos[FUSED ? D / 2 : 1], s_sin[FUSED ? D / 2 : 1];
     __shared__ __attribute__((aligned(16))) f16 s_knew[FUSED ? D : 8];
     __shared__ __attribute__((aligned(16))) f16 s_vnew[FUSED ? D : 8];
+    __shared__ float s_m[kWaves][kHeads], s_l[kWaves][kHeads];
+    __shared__ int s_badw[kWaves];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
     const uint32_t split = blockIdx.x;
     const uint32_t kvh = blockIdx.y / p.n_sub, sub = blockIdx.y % p.n_sub;
     const uint32_t b = blockIdx.z;
-    const uint32_t n0 = sub * 16;
-    const int NS = (int)min(16u, p.group - n0);
+    const uint32_t n0 = sub * kHeads;
+    const int NS = (int)min((uint32_t)kHeads, p.group - n0);
     const uint32_t hq0 = kvh * p.group + n0;  // first q head of this workgroup
+    const uint64_t qrow0 = (uint64_t)b * p.n_q_heads + hq0;
 
     uint32_t L = p.ctx_len;
-    if (PAGED) {
+    if constexpr (PAGED) {
         const int32_t len = p.seq_lens[b];
         if (len < 1 || (uint32_t)len > p.max_len) {
             // Out-of-range sequence: poison its output (written once) and skip it.
             if (split == 0)
-                for (int i = tid; i < NS * D; i += NT)
-                    p.out[((uint64_t)b * p.n_q_heads + hq0) * D + i] = __builtin_nanf("");
+                for (int i = tid; i < NS * D; i += kThreads) p.out[qrow0 * D + i] = __builtin_nanf("");
             return;
         }
         L = (uint32_t)len;
     }
     const uint32_t start = split * p.chunk;
-    if (start >= L) return;  // whole workgroup idle (uniform)
+    if (start >= L) return;  // uniform: this split is past the sequence
     const uint32_t end = min(L, start + p.chunk);
     const uint32_t n_tiles = (end - start + kTile - 1) / kTile;
     const uint32_t newpos = L - 1;
     const bool has_new = FUSED && newpos >= start && newpos < end;
 
-    const uint64_t head_base = (uint64_t)kvh * p.cache_stride;  // in rows
-    const f16* kbase = p.k_cache + head_base * D;
-    const f16* vbase = p.v_cache + head_base * D;
+    const uint64_t head_base = (uint64_t)kvh * p.cache_stride;  // rows
+    f16* const kbase = p.k_cache + head_base * D;
+    f16* const vbase = p.v_cache + head_base * D;
+    bool bad = false;
 
-    // ---------------- fused prologue: q/k norm + rope, k/v append ----------
+    // ---- 1. small loads first: vmcnt retires loads in issue order, so a load
+    //         issued after the K/V tile could only be used once the whole tile
+    //         has arrived. q rows, norm weights, position and the new k/v row.
+    constexpr int QV = (kHeads * D / 4 + kThreads - 1) / kThreads;  // q-row float4s per thread
+    // Every load here is unconditional with a clamped (valid) address: loads
+    // under divergent branches make the compiler wait for all outstanding
+    // loads at the join, which would include the K/V tile.
+    static_assert(QV == 1 || QV == 2, "q staging assumes at most two float4 per thread");
+    auto q_at = [&](int k) -> const float4* {
+        const int i = tid + k * kThreads, n = min(i / (D / 4), NS - 1);
+        return (const float4*)(p.q + (qrow0 + n) * D + (i % (D / 4)) * 4);
+    };
+    const float4 qv0 = *q_at(0);
+    const float4 qv1 = QV > 1 ? *q_at(QV - 1) : qv0;
+    const uint64_t kv_off = ((uint64_t)b * p.n_kv_heads + kvh) * D;
+    float wq = 0.f, wk = 0.f, kr = 0.f, vr = 0.f, inv_freq = 0.f;
+    int32_t pos_raw = 0;
     if constexpr (FUSED) {
-        const float* qsrc = p.q + ((uint64_t)b * p.n_q_heads + hq0) * D;
-        for (int i = tid; i < NS * D; i += NT) s_q[i / D][i % D] = qsrc[i];
-        const uint64_t kv_off = ((uint64_t)b * p.n_kv_heads + kvh) * D;
-        if (has_new)
-            for (int i = tid; i < D; i += NT) s_krow[i] = p.k_new[kv_off + i];
-        __syncthreads();
-        if (tid < NS) s_inv[tid] = row_inv_rms(s_q[tid], D, p.eps);
-        if (has_new && tid == 16) s_inv[16] = row_inv_rms(s_krow, D, p.eps);
-        __syncthreads();
-        const float qpos = PAGED ? (float)newpos : (float)p.positions[0];
-        for (int i = tid; i < NS * (D / 2); i += NT) {
-            const int n = i / (D / 2), j = i % (D / 2);
-            const float inv = s_inv[n];
-            const float x0 = norm_mul(s_q[n][j], inv, p.q_norm[j]);
-            const float x1 = norm_mul(s_q[n][j + D / 2], inv, p.q_norm[j + D / 2]);
-            float y0, y1;
-            rope_pair(x0, x1, rope_angle(qpos, p.freq_scale, table.inv[j]), y0, y1);
-            s_q[n][j] = y0;
-            s_q[n][j + D / 2] = y1;
+        const int i = tid % D;
+        wq = p.q_norm[i];
+        wk = p.k_norm[i];
+        kr = p.k_new[kv_off + i];
+        vr = p.v_new[kv_off + i];
+        inv_freq = table.inv[tid % (D / 2)];
+        if (!PAGED) pos_raw = p.positions[0];
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. the first tile's K/V loads
+    // Unconditional (a wavefront without a tile loads the split's last tile and
+    // drops it): a branch around the loads would make the compiler's wait
+    // counts at the join assume nothing was issued.
+    TileRegs<D> TA, TB;
+    uint32_t it = wave;
+    issue_tile<D, PAGED>(TA, p, kbase, vbase, b, start + min(it, n_tiles - 1) * kTile, end, g, c16, lane, bad);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. q operands (hi/lo f16) from the LDS copy, built while the tile is in flight
+#pragma unroll
+    for (int k = 0; k < QV; k++) {
+        const int i = tid + k * kThreads, n = i / (D / 4);
+        if (n < NS) *(float4*)&s_q[n][(i % (D / 4)) * 4] = k == 0 ? qv0 : qv1;
+    }
+    f16x8 qh[KK], ql[KK];
+    const int qn_row = c16 < NS ? c16 : 0;
+    // Fused: the wavefront that owns the tile holding the new position
+    // normalises, rotates and appends the new k row itself (no extra barrier).
+    const int new_wave = has_new ? (int)(((newpos - start) / kTile) % kWaves) : -1;
+    float x[KK][8];
+    if constexpr (FUSED) {
+        const float qpos = PAGED ? (float)newpos : (float)pos_raw;
+        if (tid < D) {
+            s_qn[tid] = wq;
+            if (has_new) {
+                s_krow[tid] = kr;
+                s_kn[tid] = wk;
+            }
         }
-        if (has_new) {
-            const int64_t row = cache_row<PAGED>(p, b, newpos);
-            f16* kdst = row >= 0 ? p.k_cache + (head_base + row) * D : nullptr;
-            f16* vdst = row >= 0 ? p.v_cache + (head_base + row) * D : nullptr;
-            for (int j = tid; j < D / 2; j += NT) {
-                const float inv = s_inv[16];
-                const float x0 = norm_mul(s_krow[j], inv, p.k_norm[j]);
-                const float x1 = norm_mul(s_krow[j + D / 2], inv, p.k_norm[j + D / 2]);
+        if (tid < D / 2) {
+            const float ang = rope_angle(qpos, p.freq_scale, inv_freq);
+            s_cos[tid] = cosf(ang);
+            s_sin[tid] = sinf(ang);
+        }
+        if (has_new && tid < D) {
+            // v: f16 append (round to nearest even) into the cache and the tile
+            bool pbad = false;
+            const uint64_t vslot = PAGED ? page_base(p, b, newpos, pbad) + newpos % p.page_size : newpos;
+            const f16 hv = (f16)vr;
+            s_vnew[tid] = hv;
+            if (!pbad) vbase[vslot * D + tid] = hv;
+        }
+        lds_barrier();  // the prologue's only workgroup barrier
+        if (wave == new_wave) {
+            // k row: serial-order sum of squares (kernels_a.zig:85-86) in one lane,
+            // then norm + rope of pair (lane, lane + D/2) and the f16 append.
+            bool pbad = false;
+            const uint64_t kslot = PAGED ? page_base(p, b, newpos, pbad) + newpos % p.page_size : newpos;
+            bad |= pbad;
+            float kinv = lane == 0 ? rms_inv(serial_sumsq(s_krow, D), (float)D, p.eps) : 0.0f;
+            kinv = __shfl(kinv, 0, 64);
+            for (int i = lane; i < D / 2; i += 64) {
+                const float x0 = norm_mul(s_krow[i], kinv, s_kn[i]);
+                const float x1 = norm_mul(s_krow[i + D / 2], kinv, s_kn[i + D / 2]);
                 float y0, y1;
-                rope_pair(x0, x1, rope_angle(qpos, p.freq_scale, table.inv[j]), y0, y1);
+                rotate(x0, x1, s_cos[i], s_sin[i], y0, y1);
                 const f16 h0 = (f16)y0, h1 = (f16)y1;
-                s_knew[j] = h0;
-                s_knew[j + D / 2] = h1;
-                if (kdst) {
-                    kdst[j] = h0;
-                    kdst[j + D / 2] = h1;
+                s_knew[i] = h0;
+                s_knew[i + D / 2] = h1;
+                if (!pbad) {
+                    kbase[kslot * D + i] = h0;
+                    kbase[kslot * D + i + D / 2] = h1;
                 }
             }
-            for (int j = tid; j < D; j += NT) {
-                const f16 hv = (f16)p.v_new[kv_off + j];
-                s_vnew[j] = hv;
-                if (vdst) vdst[j] = hv;
-            }
         }
-        __syncthreads();
-    }
-
-    // ---------------- Q^T operands (B of the S product), hi + lo ------------
-    f16x8 qh[KK], ql[KK];
-    {
-        const bool valid = c16 < NS;
-        const float* qrow = p.q + ((uint64_t)b * p.n_q_heads + hq0 + (valid ? c16 : 0)) * D;
+        // q: this lane holds dims kk*32 + 8g + j of head c16; the head's sum of
+        // squares is the lane's partial sum reduced over the 4 lanes of the head
+        // (q only feeds attention, so the summation order is free).
+        float ss = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
+            const float4 a4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g];
+            const float4 c4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g + 4];
+            const float r[8] = {a4.x, a4.y, a4.z, a4.w, c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                x[kk][j] = r[j];
+                ss += r[j] * r[j];
+            }
+        }
+        ss += lane_xor(ss, 16);
+        ss += lane_xor(ss, 32);
+        const float inv = rms_inv(ss, (float)D, p.eps);
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[kk][j] = norm_mul(x[kk][j], inv, s_qn[kk * 32 + 8 * g + j]);
+#pragma unroll
+        for (int kk = 0; kk < KK / 2; kk++)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int d = kk * 32 + 8 * g + j;
-                float x = 0.0f;
-                if (valid) {
-                    if constexpr (FUSED)
-                        x = s_q[c16][d];
-                    else
-                        x = qrow[d];
-                }
-                const f16 hi = (f16)x;
-                qh[kk][j] = hi;
-                ql[kk][j] = (f16)(x - (float)hi);
+                float y0, y1;
+                rotate(x[kk][j], x[kk + KK / 2][j], s_cos[d], s_sin[d], y0, y1);
+                x[kk][j] = y0;
+                x[kk + KK / 2][j] = y1;
             }
+    } else {
+        lds_barrier();
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            const float4 a4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g];
+            const float4 c4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g + 4];
+            const float r[8] = {a4.x, a4.y, a4.z, a4.w, c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[kk][j] = r[j];
         }
     }
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 hi, lo;
+            split_f16(c16 < NS ? x[kk][j] : 0.0f, hi, lo);
+            qh[kk][j] = hi;
+            ql[kk][j] = lo;
+        }
 
-    // ---------------- main loop over this wavefront's tiles -----------------
-    char* vlds = s_raw + wave * kTile * Gm::ROW_BYTES;
+    // ---- 4. main loop: prefetch one tile ahead, two register sets
     f32x4 O[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_lane = 0.0f;
-
-    for (uint32_t it = wave; it < n_tiles; it += WAVES) {
-        const uint32_t p0 = start + it * kTile;
-        // K rows straight into A operands: lane row c16 of each 16-row half.
-        u32x4 kop[2][KK];
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            const uint32_t pos = p0 + 16 * st + c16;
-            const int64_t row = pos < end ? cache_row<PAGED>(p, b, pos) : -1;
-#pragma unroll
-            for (int kk = 0; kk < KK; kk++) {
-                u32x4 v = u32x4{0u, 0u, 0u, 0u};
-                if (row >= 0) {
-                    if (FUSED && pos == newpos)
-                        v = *(const u32x4*)(s_knew + kk * 32 + 8 * g);
-                    else
-                        v = load16(kbase + (uint64_t)row * D + kk * 32 + 8 * g);
-                }
-                kop[st][kk] = v;
+    float m_ref = -INFINITY, l_sum = 0.0f;
+    char* vlds = s_big + wave * kTile * G::VROW;
+    auto new_row_of = [&](uint32_t p0) -> int {
+        return (FUSED && has_new && newpos >= p0 && newpos < p0 + kTile) ? (int)(newpos - p0) : -1;
+    };
+    // Every compute path sees a fixed set of outstanding loads (the next tile's
+    // or none), so the compiler's wait before a tile's first use never covers
+    // the prefetch.
+    if (it < n_tiles) {
+        bool first = true;
+        for (;;) {
+            uint32_t nx = it + kWaves;
+            uint32_t p0 = start + it * kTile;
+            if (nx >= n_tiles) {
+                compute_tile<D, FUSED>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                                       s_vnew, p.scale_log2, first);
+                break;
             }
-        }
-        // V tile -> LDS (row-major, padded). Rows past the split end are zero.
-        u32x4 vreg[VC];
-#pragma unroll
-        for (int r = 0; r < VC; r++) {
-            const int c = lane + 64 * r;
-            const uint32_t pos = p0 + c / RC;
-            const int64_t row = pos < end ? cache_row<PAGED>(p, b, pos) : -1;
-            u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if (row >= 0) {
-                if (FUSED && pos == newpos)
-                    v = *(const u32x4*)(s_vnew + (c % RC) * 8);
-                else
-                    v = load16(vbase + (uint64_t)row * D + (c % RC) * 8);
+            issue_tile<D, PAGED>(TB, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
+            compute_tile<D, FUSED>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                                   s_vnew, p.scale_log2, first);
+            first = false;
+            it = nx;
+            nx = it + kWaves;
+            p0 = start + it * kTile;
+            if (nx >= n_tiles) {
+                compute_tile<D, FUSED>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                                       s_vnew, p.scale_log2, false);
+                break;
             }
-            vreg[r] = v;
+            issue_tile<D, PAGED>(TA, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
+            compute_tile<D, FUSED>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                                   s_vnew, p.scale_log2, false);
+            it = nx;
         }
-#pragma unroll
-        for (int r = 0; r < VC; r++) {
-            const int c = lane + 64 * r;
-            uint32_t* dst = (uint32_t*)(vlds + (c / RC) * Gm::ROW_BYTES + (c % RC) * 16);
-            *(uint2*)dst = uint2{vreg[r][0], vreg[r][1]};
-            *(uint2*)(dst + 2) = uint2{vreg[r][2], vreg[r][3]};
-        }
-
-        // S^T = K . Q^T (hi and lo halves into one accumulator)
-        f32x4 S[2];
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KK; kk++) {
-                const f16x8 a = __builtin_bit_cast(f16x8, kop[st][kk]);
-                acc = mfma_16x16x32(a, qh[kk], acc);
-                acc = mfma_16x16x32(a, ql[kk], acc);
-            }
-            S[st] = acc;
-        }
-        // Scores of this lane: head c16, positions p0 + 16*st + 4*g + i.
-        float sc[8];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < 2; st++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t pos = p0 + 16 * st + 4 * g + i;
-                const float s = pos < end ? S[st][i] * p.scale_log2 : -INFINITY;
-                sc[st * 4 + i] = s;
-                mx = fmaxf(mx, s);
-            }
-        mx = fmaxf(mx, lane_xor(mx, 16));
-        mx = fmaxf(mx, lane_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        f16x8 ph, pl;
-        float psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float pj = fast_exp2(sc[j] - m_new);
-            psum += pj;
-            const f16 hi = (f16)pj;
-            ph[j] = hi;
-            pl[j] = (f16)(pj - (float)hi);
-        }
-        l_lane = l_lane * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
-
-        // O^T += V^T . P^T. k-slot (g, j) <-> tile row 4g+j (j<4), 16+4g+j-4.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const f16* vl = (const f16*)vlds;
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            f16x8 a;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int r = (j < 4) ? 4 * g + j : 16 + 4 * g + (j - 4);
-                a[j] = vl[r * (Gm::ROW_BYTES / 2) + dt * 16 + c16];
-            }
-            O[dt] = mfma_16x16x32(a, ph, O[dt]);
-            O[dt] = mfma_16x16x32(a, pl, O[dt]);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
-    // ---------------- combine wavefronts, emit partial or output ------------
-    float l_w = l_lane + lane_xor(l_lane, 16);
+    // ---- 5. combine the wavefronts, then write the partial (or the output)
+    float l_w = l_sum + lane_xor(l_sum, 16);
     l_w += lane_xor(l_w, 32);
-    __syncthreads();  // every wavefront is done with its V staging area
-    float* s_o = (float*)s_raw;  // [WAVES][16][O_STRIDE]
+    __syncthreads();  // all wavefronts are done with their V staging areas
+    float* s_o = (float*)s_big;  // [kWaves][kHeads][OROW]
     if (g == 0) {
-        s_m[wave][c16] = m_run;
+        s_m[wave][c16] = m_ref;
         s_l[wave][c16] = l_w;
     }
+    if (lane == 0) s_badw[wave] = bad ? 1 : 0;  // page lookups are wave-uniform
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) s_o[(wave * 16 + c16) * O_STRIDE + dt * 16 + 4 * g + i] = O[dt][i];
+        for (int i = 0; i < 4; i++) s_o[(wave * kHeads + c16) * G::OROW + dt * 16 + 4 * g + i] = O[dt][i];
     __syncthreads();
 
+    bool poison = false;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) poison |= s_badw[w] != 0;
     const bool single = p.n_splits == 1;
-    for (int idx = tid; idx < NS * D; idx += NT) {
-        const int n = idx / D, d = idx % D;
-        float M = -INFINITY;
+    for (int q4 = tid; q4 < NS * (D / 4); q4 += kThreads) {
+        const int n = q4 / (D / 4), d0 = (q4 % (D / 4)) * 4;
+        float M = s_m[0][n];
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) M = fmaxf(M, s_m[w][n]);
-        float acc = 0.0f, lt = 0.0f;
+        for (int w = 1; w < kWaves; w++) M = fmaxf(M, s_m[w][n]);
+        float4 acc = {0.f, 0.f, 0.f, 0.f};
+        float lt = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) {
-            const float f = fast_exp2(s_m[w][n] - M);
-            acc += s_o[(w * 16 + n) * O_STRIDE + d] * f;
+        for (int w = 0; w < kWaves; w++) {
+            const float f = fast_exp2(s_m[w][n] - M);  // 0 for a wavefront without tiles
+            const float4 o = *(const float4*)&s_o[(w * kHeads + n) * G::OROW + d0];
+            acc.x += o.x * f;
+            acc.y += o.y * f;
+            acc.z += o.z * f;
+            acc.w += o.w * f;
             lt += s_l[w][n] * f;
         }
-        const uint64_t qh_idx = (uint64_t)b * p.n_q_heads + hq0 + n;
+        if (poison) acc.x = acc.y = acc.z = acc.w = __builtin_nanf("");
+        const uint64_t qi = qrow0 + n;
         if (single) {
-            p.out[qh_idx * D + d] = acc / lt;
+            *(float4*)(p.out + qi * D + d0) = float4{acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
         } else {
-            p.part_o[(qh_idx * p.n_splits + split) * D + d] = acc;
-            if (d == 0) {
-                p.part_ml[(qh_idx * p.n_splits + split) * 2 + 0] = M;
-                p.part_ml[(qh_idx * p.n_splits + split) * 2 + 1] = lt;
-            }
+            *(float4*)(p.part_o + (qi * p.n_splits + split) * D + d0) = acc;
+            if (d0 == 0) *(float2*)(p.part_ml + (qi * p.n_splits + split) * 2) = float2{M, lt};
         }
     }
 }
 
-// Merge of the split partials: one workgroup per (sequence, q head), one
-// thread per output dim.
+// Split merge: block = 4 wavefronts = 4 groups of 4 output dims of one
+// (sequence, q head); lane s holds split s (n_splits <= 64). One load per
+// lane, then fixed-order lane reductions, so results are deterministic.
 template <int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(DecodeParams p) {
-    const uint32_t b = blockIdx.x / p.n_q_heads;
-    const uint64_t qh_idx = blockIdx.x;
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+    const uint64_t qi = blockIdx.x;  // sequence * n_q_heads + head
+    const uint32_t b = (uint32_t)(qi / p.n_q_heads);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d0 = (blockIdx.y * 4 + wave) * 4;
     uint32_t L = p.ctx_len;
     if (p.seq_lens) {
         const int32_t len = p.seq_lens[b];
@@ -393,58 +584,75 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(DecodeParams p) {
         L = (uint32_t)len;
     }
     const uint32_t ns = (L + p.chunk - 1) / p.chunk;
-    const float* ml = p.part_ml + qh_idx * p.n_splits * 2;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < ns; s++) M = fmaxf(M, ml[2 * s]);
-    float acc = 0.0f, lt = 0.0f;
-    const float* po = p.part_o + qh_idx * p.n_splits * D + threadIdx.x;
-    for (uint32_t s = 0; s < ns; s++) {
-        const float f = fast_exp2(ml[2 * s] - M);
-        acc += po[(uint64_t)s * D] * f;
-        lt += ml[2 * s + 1] * f;
+    float m = -INFINITY, l = 0.0f;
+    float4 o = {0.f, 0.f, 0.f, 0.f};
+    if ((uint32_t)lane < ns) {
+        const float2 ml = *(const float2*)(p.part_ml + (qi * p.n_splits + lane) * 2);
+        m = ml.x;
+        l = ml.y;
+        o = *(const float4*)(p.part_o + (qi * p.n_splits + lane) * D + d0);
     }
-    p.out[qh_idx * D + threadIdx.x] = acc / lt;
+    float M = m;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) M = fmaxf(M, lane_xor(M, s));
+    const float w = (uint32_t)lane < ns ? fast_exp2(m - M) : 0.0f;
+    l *= w;
+    o.x *= w;
+    o.y *= w;
+    o.z *= w;
+    o.w *= w;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        l += lane_xor(l, s);
+        o.x += lane_xor(o.x, s);
+        o.y += lane_xor(o.y, s);
+        o.z += lane_xor(o.z, s);
+        o.w += lane_xor(o.w, s);
+    }
+    if (lane == 0) *(float4*)(p.out + qi * D + d0) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
 }
 
-template <int D, int WAVES>
+template <int D>
 int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams& prm, dim3 grid) {
-    const dim3 block(WAVES * 64);
+    const dim3 block(kThreads);
     const bool paged = a.page_table != nullptr;
+    const RopeTable& tab = a.fused ? *a.table : RopeTable{};
     if (a.fused && paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_splitk_kernel", (decode_splitk_kernel<D, WAVES, true, true>), grid, block, 0, ctx->stream, prm, *a.table);
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, true>), grid, block, 0, ctx->stream, prm, tab);
     else if (a.fused)
-        DS5_TIMED_LAUNCH(ctx, "decode_splitk_kernel", (decode_splitk_kernel<D, WAVES, true, false>), grid, block, 0, ctx->stream, prm, *a.table);
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, false>), grid, block, 0, ctx->stream, prm, tab);
     else if (paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_splitk_kernel", (decode_splitk_kernel<D, WAVES, false, true>), grid, block, 0, ctx->stream, prm, RopeTable{});
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, true>), grid, block, 0, ctx->stream, prm, tab);
     else
-        DS5_TIMED_LAUNCH(ctx, "decode_splitk_kernel", (decode_splitk_kernel<D, WAVES, false, false>), grid, block, 0, ctx->stream, prm, RopeTable{});
-    int rc = ds5_after_launch(ctx, "decode_splitk_kernel");
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, false>), grid, block, 0, ctx->stream, prm, tab);
+    int rc = ds5_after_launch(ctx, "decode_split_kernel");
     if (rc || prm.n_splits == 1) return rc;
-    DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", decode_merge_kernel<D>, dim3(a.n_seqs * a.n_q_heads), dim3(D), 0, ctx->stream, prm);
+    DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", decode_merge_kernel<D>, dim3(a.n_seqs * a.n_q_heads, D / 16), dim3(256), 0,
+                     ctx->stream, prm);
     return ds5_after_launch(ctx, "decode_merge_kernel");
 }
 
 }  // namespace
 
 int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
-    constexpr int WAVES = 4;
     const uint32_t group = a.n_q_heads / a.n_kv_heads;
-    const uint32_t n_sub = (group + 15) / 16;
+    const uint32_t n_sub = (group + kHeads - 1) / kHeads;
     const uint32_t max_len = a.max_len;
     if (a.n_seqs == 0 || max_len == 0) return DS5_OK;
 
-    // Positions per split: enough workgroups to cover the CUs about twice,
-    // never fewer than one 32-position tile per wavefront.
+    // Positions per split: about four workgroups per CU over the longest
+    // sequence, whole 128-position steps (one 32-position tile per wavefront),
+    // at most 64 splits (the merge kernel's lane count).
+    constexpr uint32_t kStep = kWaves * kTile;
     uint32_t chunk = ctx->decode_chunk;
     if (chunk == 0) {
         const uint64_t units = (uint64_t)a.n_seqs * a.n_kv_heads * n_sub;
-        const uint64_t target = 2ull * (ctx->cu_count > 0 ? ctx->cu_count : 256);
-        const uint64_t per_unit = (target + units - 1) / units;  // splits wanted per (seq, kv head)
-        uint64_t c = (max_len + per_unit - 1) / per_unit;
-        c = c < 128 ? 128 : c;
-        chunk = (uint32_t)c;
+        const uint64_t target = 4ull * (ctx->cu_count > 0 ? ctx->cu_count : 256);
+        chunk = (uint32_t)std::min<uint64_t>((max_len * units + target - 1) / target, max_len);
     }
-    chunk = (chunk + kTile - 1) / kTile * kTile;
+    chunk = std::max<uint32_t>((chunk + kStep - 1) / kStep * kStep, kStep);
+    chunk = std::max<uint32_t>(chunk, (max_len + 63) / 64);
+    chunk = (chunk + kStep - 1) / kStep * kStep;
     const uint32_t n_splits = (max_len + chunk - 1) / chunk;
 
     DecodeParams prm{};
@@ -483,6 +691,6 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
         prm.part_ml = prm.part_o + n_part * a.head_dim;
     }
     const dim3 grid(n_splits, a.n_kv_heads * n_sub, a.n_seqs);
-    if (a.head_dim == 128) return launch_decode_d<128, WAVES>(ctx, a, prm, grid);
-    return launch_decode_d<64, WAVES>(ctx, a, prm, grid);
+    if (a.head_dim == 128) return launch_decode_d<128>(ctx, a, prm, grid);
+    return launch_decode_d<64>(ctx, a, prm, grid);
 }

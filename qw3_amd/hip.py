@@ -140,6 +140,7 @@ SIGNATURES = {
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
     "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
+    "ds5_hip_copy_device": ([_P, Buf, Buf, C.c_uint64], C.c_int),
 }
 
 
@@ -269,6 +270,9 @@ class Ctx:
 
     def fill_normal_f16(self, buf: Buf, n: int, seed: int) -> None:
         self.check(LIB.ds5_hip_fill_normal_f16(self._h, buf, n, seed))
+
+    def copy_device(self, dst: Buf, src: Buf, length: int) -> None:
+        self.check(LIB.ds5_hip_copy_device(self._h, dst, src, length))
 
 
 class Graph:
