@@ -288,7 +288,7 @@ def main():
         elapsed, _ = time_graph(ctx, p, max(5, args.steps // 5), 2)
         n_rep = max(5, args.steps // 5)
         e2e_us = elapsed / n_rep * 1e6
-        ns_pf, _ = kernel_mean_ns(ctx, p, "prefill_kernel", 5)
+        ns_pf, _ = kernel_mean_ns(ctx, p, "prefill_attention_kernel", 5)
         tf = p.flops / ns_pf / 1e3
         extra["C2_prefill"] = dict(prefill_kernel_us=round(ns_pf / 1e3, 3), tflops=round(tf, 2),
                                    frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(e2e_us, 3),

@@ -38,15 +38,17 @@ int ds5_after_launch(ds5_hip_ctx* ctx, const char* what) {
 
 int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->workspace_bytes) {
-        // The old workspace may still be read by enqueued kernels.
+        // A larger workspace is a new allocation; the old one stays owned by the
+        // context until deinit, because enqueued kernels and captured graphs may
+        // still reference it.
         int rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "workspace sync");
         if (rc) return rc;
-        if (ctx->workspace) (void)hipFree(ctx->workspace);
-        ctx->workspace = nullptr;
-        ctx->workspace_bytes = 0;
         const size_t want = std::max<size_t>(bytes, 4u << 20);
-        rc = ds5_hip_status(ctx, hipMalloc(&ctx->workspace, want), "workspace alloc");
+        void* p = nullptr;
+        rc = ds5_hip_status(ctx, hipMalloc(&p, want), "workspace alloc");
         if (rc) return rc;
+        if (ctx->workspace) ctx->owned.push_back(ctx->workspace);
+        ctx->workspace = p;
         ctx->workspace_bytes = want;
     }
     *out = ctx->workspace;

@@ -275,40 +275,43 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             l.table = table;
             return launch_decode(ctx, l);
         }
-        KvPrepLaunch kp{};
-        kp.k = (const float*)ds5_ptr(a->k);
-        kp.v = (const float*)ds5_ptr(a->v);
-        kp.k_norm = (const float*)ds5_ptr(a->k_norm);
-        kp.positions = (const int32_t*)ds5_ptr(a->positions);
-        kp.k_cache = (f16*)ds5_ptr(a->k_cache);
-        kp.v_cache = (f16*)ds5_ptr(a->v_cache);
-        kp.pos = a->pos;
-        kp.n_tokens = a->n_tokens;
-        kp.n_kv_heads = a->n_kv_heads;
-        kp.head_dim = a->head_dim;
-        kp.max_ctx = a->max_ctx;
-        kp.eps = a->eps;
-        kp.freq_scale = a->freq_scale;
-        kp.table = table;
-        if (int rc = launch_kv_prep(ctx, kp)) return rc;
-        PrefillLaunch l{};
-        l.q = (const float*)ds5_ptr(a->q);
-        l.q_norm = (const float*)ds5_ptr(a->q_norm);
-        l.positions = (const int32_t*)ds5_ptr(a->positions);
-        l.k_cache = (const f16*)ds5_ptr(a->k_cache);
-        l.v_cache = (const f16*)ds5_ptr(a->v_cache);
-        l.out = (float*)ds5_ptr(a->out);
-        l.pos = a->pos;
-        l.n_tokens = a->n_tokens;
-        l.n_q_heads = a->n_q_heads;
-        l.n_kv_heads = a->n_kv_heads;
-        l.head_dim = a->head_dim;
-        l.max_ctx = a->max_ctx;
-        l.scale = a->scale;
-        l.eps = a->eps;
-        l.freq_scale = a->freq_scale;
-        l.table = table;
-        return launch_prefill(ctx, l);
+        if (prefill_prep_supported(a->n_kv_heads, a->head_dim)) {
+            // q rotation table of the pre-pass: [n_tokens, head_dim / 2] float4 in the workspace
+            void* ws = nullptr;
+            if (int rc = ds5_workspace(ctx, (size_t)T * (hd / 2) * sizeof(float4), &ws)) return rc;
+            KvPrepLaunch kp{};
+            kp.k = (const float*)ds5_ptr(a->k);
+            kp.v = (const float*)ds5_ptr(a->v);
+            kp.k_norm = (const float*)ds5_ptr(a->k_norm);
+            kp.q_norm = (const float*)ds5_ptr(a->q_norm);
+            kp.positions = (const int32_t*)ds5_ptr(a->positions);
+            kp.k_cache = (f16*)ds5_ptr(a->k_cache);
+            kp.v_cache = (f16*)ds5_ptr(a->v_cache);
+            kp.pos = a->pos;
+            kp.n_tokens = a->n_tokens;
+            kp.n_kv_heads = a->n_kv_heads;
+            kp.head_dim = a->head_dim;
+            kp.max_ctx = a->max_ctx;
+            kp.eps = a->eps;
+            kp.freq_scale = a->freq_scale;
+            kp.table = table;
+            if (int rc = launch_kv_prep(ctx, kp, (float4*)ws)) return rc;
+            PrefillLaunch l{};
+            l.q = (const float*)ds5_ptr(a->q);
+            l.q_rot = (const float4*)ws;
+            l.k_cache = (const f16*)ds5_ptr(a->k_cache);
+            l.v_cache = (const f16*)ds5_ptr(a->v_cache);
+            l.out = (float*)ds5_ptr(a->out);
+            l.pos = a->pos;
+            l.n_tokens = a->n_tokens;
+            l.n_q_heads = a->n_q_heads;
+            l.n_kv_heads = a->n_kv_heads;
+            l.head_dim = a->head_dim;
+            l.max_ctx = a->max_ctx;
+            l.scale = a->scale;
+            l.eps = a->eps;
+            return launch_prefill(ctx, l);
+        }
     }
 
     // Other shapes: the six separate device ops, in place on q and k.

@@ -1,5 +1,4 @@
-// k_norm_rope.hip -- rmsNorm, rope and kvAppend on gfx950, plus the prefill
-// k/v pre-pass (norm + rope of k, append of k and v) of the fused step.
+// k_norm_rope.hip -- rmsNorm, rope and kvAppend on gfx950 (the separate ops).
 //
 // Arithmetic follows the reference CPU path operation for operation so that
 // results are bit-exact where the operations are IEEE-exact:
@@ -120,42 +119,6 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
     }
 }
 
-// Prefill pre-pass of the fused step: 64 k rows (row = t*n_kv_heads + h) per
-// block: serial-order norm, rope at positions[t], f16 append; v rows are
-// converted and appended. k and v inputs are not modified.
-__global__ __launch_bounds__(kRowsPerBlock) void kv_prep_kernel(KvPrepLaunch a, RopeTable table) {
-    __shared__ float tile[kRowsPerBlock][kColTile + 1];
-    __shared__ float s_inv[kRowsPerBlock];
-    const uint32_t n_rows = a.n_tokens * a.n_kv_heads;
-    const uint32_t dim = a.head_dim, half = dim / 2;
-    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
-    const int lane = threadIdx.x;
-    float sumsq;
-    rows_sumsq(a.k, row0, n_rows, dim, tile, &sumsq);
-    s_inv[lane] = rms_inv(sumsq, (float)dim, a.eps);
-    __syncthreads();
-    for (int r = 0; r < kRowsPerBlock; r++) {
-        const uint32_t row = row0 + r;
-        if (row >= n_rows) break;
-        const uint32_t t = row / a.n_kv_heads, h = row % a.n_kv_heads;
-        const float inv = s_inv[r];
-        const float pos = (float)a.positions[t];
-        const float* src = a.k + (uint64_t)row * dim;
-        const uint64_t dst = ((uint64_t)h * a.max_ctx + a.pos + t) * dim;
-        for (uint32_t i = lane; i < half; i += kRowsPerBlock) {
-            const float x0 = src[i] * inv * a.k_norm[i];
-            const float x1 = src[i + half] * inv * a.k_norm[i + half];
-            const float angle = pos * a.freq_scale * table.inv[i];
-            const float c = cosf(angle);
-            const float s = sinf(angle);
-            a.k_cache[dst + i] = (f16)(x0 * c - x1 * s);
-            a.k_cache[dst + i + half] = (f16)(x0 * s + x1 * c);
-        }
-        const float* vsrc = a.v + (uint64_t)row * dim;
-        for (uint32_t c = lane; c < dim; c += kRowsPerBlock) a.v_cache[dst + c] = (f16)vsrc[c];
-    }
-}
-
 inline uint32_t grid_for(uint64_t total, uint32_t block) {
     const uint64_t g = (total + block - 1) / block;
     return (uint32_t)(g > 65535u * 16u ? 65535u * 16u : (g ? g : 1));
@@ -193,12 +156,4 @@ int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a) {
                            a.max_ctx);
     }
     return ds5_after_launch(ctx, "kv_append_kernel");
-}
-
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a) {
-    const uint32_t n_rows = a.n_tokens * a.n_kv_heads;
-    if (n_rows == 0) return DS5_OK;
-    const uint32_t blocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    DS5_TIMED_LAUNCH(ctx, "kv_prep_kernel", kv_prep_kernel, dim3(blocks), dim3(kRowsPerBlock), 0, ctx->stream, a, *a.table);
-    return ds5_after_launch(ctx, "kv_prep_kernel");
 }
