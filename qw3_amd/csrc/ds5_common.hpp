@@ -118,15 +118,13 @@ struct KvAppendLaunch {
 };
 int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a);
 
-// Prefill pre-pass of the fused step: per token, the q rotation table (rope
-// cos/sin with the q_norm weights folded in) and the norm + rope + f16 append
-// of every kv head's k row, f16 append of v.
+// Prefill pre-pass of the fused step: per token, the rope cos/sin table and
+// the norm + rope + f16 append of every kv head's k row, f16 append of v.
 // Leaves q untouched. Supported while n_kv_heads * head_dim <= 2048.
 struct KvPrepLaunch {
     const float* k;
     const float* v;
     const float* k_norm;
-    const float* q_norm;
     const int32_t* positions;
     f16* k_cache;
     f16* v_cache;
@@ -135,7 +133,7 @@ struct KvPrepLaunch {
     const RopeTable* table;
 };
 bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim);
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float4* q_rot);
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float2* rope_cs);
 
 // Generic causal GQA attention (any head_dim <= 512, f32 or f16 cache).
 struct GenericAttnLaunch {
@@ -179,7 +177,8 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a);
 // Causal flash-attention prefill on f16 MFMA (head_dim 128 or 64).
 struct PrefillLaunch {
     const float* q;          // [n_tokens, n_q_heads, head_dim]
-    const float4* q_rot;     // non-null: q is raw; [n_tokens, head_dim / 2] rotation table of the pre-pass
+    const float* q_norm;     // fused only: [head_dim]
+    const float2* rope_cs;   // non-null: q is raw; [n_tokens, head_dim / 2] (cos, sin) of the pre-pass
     const f16* k_cache;
     const f16* v_cache;
     float* out;

@@ -276,14 +276,13 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             return launch_decode(ctx, l);
         }
         if (prefill_prep_supported(a->n_kv_heads, a->head_dim)) {
-            // q rotation table of the pre-pass: [n_tokens, head_dim / 2] float4 in the workspace
+            // cos/sin table of the pre-pass: [n_tokens, head_dim / 2] float2 in the workspace
             void* ws = nullptr;
-            if (int rc = ds5_workspace(ctx, (size_t)T * (hd / 2) * sizeof(float4), &ws)) return rc;
+            if (int rc = ds5_workspace(ctx, (size_t)T * (hd / 2) * sizeof(float2), &ws)) return rc;
             KvPrepLaunch kp{};
             kp.k = (const float*)ds5_ptr(a->k);
             kp.v = (const float*)ds5_ptr(a->v);
             kp.k_norm = (const float*)ds5_ptr(a->k_norm);
-            kp.q_norm = (const float*)ds5_ptr(a->q_norm);
             kp.positions = (const int32_t*)ds5_ptr(a->positions);
             kp.k_cache = (f16*)ds5_ptr(a->k_cache);
             kp.v_cache = (f16*)ds5_ptr(a->v_cache);
@@ -295,10 +294,11 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             kp.eps = a->eps;
             kp.freq_scale = a->freq_scale;
             kp.table = table;
-            if (int rc = launch_kv_prep(ctx, kp, (float4*)ws)) return rc;
+            if (int rc = launch_kv_prep(ctx, kp, (float2*)ws)) return rc;
             PrefillLaunch l{};
             l.q = (const float*)ds5_ptr(a->q);
-            l.q_rot = (const float4*)ws;
+            l.q_norm = (const float*)ds5_ptr(a->q_norm);
+            l.rope_cs = (const float2*)ws;
             l.k_cache = (const f16*)ds5_ptr(a->k_cache);
             l.v_cache = (const f16*)ds5_ptr(a->v_cache);
             l.out = (float*)ds5_ptr(a->out);

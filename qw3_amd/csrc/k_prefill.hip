@@ -5,19 +5,25 @@
 // position pos + t) of q head h attends cache positions 0..pos+t of kv head
 // h / group; softmax(scale * q.k) in f32.
 //
-// prefill_attention_kernel. A workgroup is 4 wavefronts, one q head each, all
-// four heads from the same GQA group, so every K/V byte staged in LDS feeds
-// four heads. A wavefront owns 32 query rows of its head. Keys stream in
-// 64-position tiles through a double-buffered LDS stage (the next tile's global
-// loads are in flight while the current one is consumed):
-//   S^T[32 keys x 32 q] = K . Q^T         v_mfma_f32_32x32x16_f16 (x2 per tile)
+// prefill_attention_kernel. A workgroup serves 4 q heads of one GQA group
+// with 8 wavefronts: two sets of four (one head each), set s taking the key
+// tiles 2r + s, so each SIMD runs two wavefronts whose MFMA, exponential and
+// LDS phases overlap. A wavefront owns 32 query rows of its head. Each set
+// streams 64-position K/V tiles into its own pair of LDS stages with gfx950's
+// direct-to-LDS loads (global_load_lds_dwordx4, no register staging); the next
+// tile's loads are in flight while the current one is consumed. Per tile:
+//   S^T[32 keys x 32 q] = K . Q^T         v_mfma_f32_32x32x16_f16 (x2)
 //   O^T[D x 32 q]      += V^T . P^T       v_mfma_f32_32x32x16_f16
 // With S transposed a lane holds 16 scores of one query row, so row max/sum
-// need one lane exchange, and the P^T operand is the lane's own scores. V^T
-// operands come from LDS through gfx950's transpose read (ds_read_b64_tr_b16).
-// q and p are rounded to f16 for the products; softmax state is f32 in the
-// log2 domain with a lazy reference max (rescale only on growth > 2^8).
-// Causal masking runs only on tiles that cross the diagonal.
+// need one lane swap (v_permlane32_swap), and the P^T operand is the lane's
+// own scores. V^T operands come from LDS through the transpose read
+// (ds_read_b64_tr_b16). LDS rows are unpadded with XOR-swizzled 16-byte
+// chunks so both read patterns are bank-conflict free. q (pre-scaled by
+// scale * log2 e) and p are rounded to f16 for the products; the softmax state
+// is f32 in the log2 domain with a lazy reference max (rescale only on growth
+// > 2^8); the row sum adds the f16 weights the products use. Causal masking
+// runs only on tiles that cross the diagonal. The two sets' (max, sum, O)
+// merge through LDS at the end of a q tile.
 //
 // Load balance: q tiles are paired heaviest with lightest (tile NQ-1-i with
 // tile i) so every workgroup carries the same number of key tiles, and the
@@ -25,11 +31,10 @@
 // XCD b % 8), so each XCD's L2 holds one kv head's K/V.
 //
 // Fused mode: the pre-pass (prefill_prep_kernel) writes the normalised,
-// rotated f16 k rows and the f16 v rows into the cache, and a q rotation table
-// per (token, pair) with the q_norm weights folded in; the attention kernel
-// takes raw q, applies the per-head RMSNorm scale (the row's sum of squares
-// reduced across the two lanes that hold it) and the rotation, and rounds q to
-// f16.
+// rotated f16 k rows and the f16 v rows into the cache and a (cos, sin) table
+// per (token, pair); the attention kernel takes raw q, applies the per-head
+// RMSNorm (the row's sum of squares reduced across the two lanes that hold
+// it) and the rotation, and rounds q to f16.
 #include "ds5_common.hpp"
 
 namespace {
@@ -69,10 +74,10 @@ __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float i
     return pos * freq_scale * inv;
 }
 
-// Token t: cos/sin of its rope angles (kernels_a.zig:119-122), the q rotation
-// table with the q_norm weights folded in, then every kv head's k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX
+// Token t: cos/sin of its rope angles (kernels_a.zig:119-122) into the table,
+// then every kv head's k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX
 // rotation (:125-126), f16 append at slot pos + t (:196-210); v rows f16.
-__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, float4* q_rot, RopeTable table) {
+__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, float2* rope_cs, RopeTable table) {
     __shared__ __attribute__((aligned(16))) float s_k[kPrepMaxRow];
     __shared__ float s_cos[DS5_MAX_ROPE_HALF], s_sin[DS5_MAX_ROPE_HALF];
     __shared__ float s_inv[kPrepMaxRow / 64];
@@ -84,9 +89,7 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
         const float c = cosf(ang), s = sinf(ang);
         s_cos[i] = c;
         s_sin[i] = s;
-        // q: norm weights folded into the rotation (see load_q)
-        const float w0 = a.q_norm[i], w1 = a.q_norm[i + half];
-        q_rot[(uint64_t)t * half + i] = float4{w0 * c, w1 * s, w0 * s, w1 * c};
+        rope_cs[(uint64_t)t * half + i] = float2{c, s};
     }
     const float* krow = a.k + (uint64_t)t * H * D;
     for (uint32_t e = tid; e < H * D; e += kPrepThreads) s_k[e] = krow[e];
@@ -114,133 +117,127 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
 // ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
-constexpr int kWaves = 4;      // q heads per workgroup, one per wavefront
+constexpr int kHeads = 4;      // q heads per workgroup
+constexpr int kSets = 2;       // wavefront sets, each takes every other key tile
+constexpr int kWaves = kHeads * kSets;
 constexpr int kThreads = kWaves * 64;
-constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA M)
+constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA N)
 constexpr int kKTile = 64;     // keys per LDS stage
 constexpr float kRescaleLog2 = 8.0f;
 
 struct PrefillParams {
     const float* q;
-    const float4* q_rot;    // fused only: [n_tokens, head_dim / 2] (w0 cos, w1 sin, w0 sin, w1 cos)
+    const float* q_norm;     // fused only: [head_dim]
+    const float2* rope_cs;   // fused only: [n_tokens, head_dim / 2] (cos, sin)
     const f16* k_cache;
     const f16* v_cache;
     float* out;
     uint32_t pos, n_tokens, n_q_heads, group, max_ctx;
     uint32_t n_qtiles, n_pairs, n_hgroups, n_items, items_per_xcd;
-    float scale_log2, eps;
+    float q_scale;           // softmax scale * log2(e), folded into the f16 q operand
+    float eps;
 };
 
 template <int D>
 struct PGeo {
     static constexpr int KS = D / 16;              // k-steps of the S product
     static constexpr int DT = D / 32;              // 32-row blocks of O^T
-    static constexpr int ROW = D + 8;              // LDS row stride in halves (16-byte pad)
-    static constexpr int STAGE = kKTile * ROW;     // halves per K (or V) stage
-    static constexpr int CPT = kKTile * D / 8 / kThreads;  // 16-byte chunks per thread per K (or V) tile
+    static constexpr int RB = D * 2;               // bytes per K / V row in LDS (unpadded, chunk-swizzled)
+    static constexpr int STAGE = kKTile * RB;      // bytes per K (or V) stage
+    static constexpr int CPT = STAGE / 1024 / kHeads;  // 1 KiB direct-to-LDS loads per wavefront per stage
 };
 
-__device__ __forceinline__ f16x4 lds_read_tr16(const f16* lds_ptr) {
+__device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_ptr) {
     typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4h;
     typedef __attribute__((address_space(3))) v4h lds_v4h;
     const v4h r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4h*)(lds_ptr));
     return __builtin_bit_cast(f16x4, r);
 }
 
-// Global loads of the K and V tile starting at key0 (rows past kv_end are
-// clamped to valid memory; their V rows are zeroed when staged).
+// Workgroup barrier that orders LDS only: global loads stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Wait until at most n vector-memory operations of this wavefront are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// max / sum of v over lanes l and l ^ 32 (one VALU swap, no LDS round trip)
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// LDS rows are unpadded; the 16-byte chunk c of row r sits in slot c ^ swz(r).
+// Eight consecutive rows at one chunk (the S operand reads) and four
+// consecutive rows at two adjacent chunks (the V transpose reads) then fall in
+// distinct banks.
+__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+
+// Direct-to-LDS loads of the 64 K (or V) rows starting at key0 into one stage.
+// Load u of this wavefront fills bytes [1024 (wave CPT + u), +1024) of the
+// stage, lane L the 16 bytes at +16 L, i.e. row r = byte / RB, slot s; it
+// fetches chunk s ^ swz(r) of cache row key0 + r (rows past kv_end are clamped
+// to kv_end - 1: valid memory, weighted 0). DmaLane holds the lane's rows and
+// chunk offsets; the LDS destination is wave-uniform.
 template <int D>
-__device__ __forceinline__ void load_tile(u32x4 (&kr)[PGeo<D>::CPT], u32x4 (&vr)[PGeo<D>::CPT], const f16* kc,
-                                          const f16* vc, uint32_t key0, uint32_t kv_end, int tid) {
+struct DmaLane {
+    uint32_t row[PGeo<D>::CPT];
+    uint32_t col[PGeo<D>::CPT];  // halves
+    __device__ __forceinline__ DmaLane(int wave, int lane) {
+        using G = PGeo<D>;
 #pragma unroll
-    for (int u = 0; u < PGeo<D>::CPT; u++) {
-        const int c = tid + kThreads * u;
-        const uint32_t key = min(key0 + (uint32_t)(c / (D / 8)), kv_end - 1);
-        const int col = (c % (D / 8)) * 8;
-        kr[u] = *(const u32x4*)(kc + (uint64_t)key * D + col);
-        vr[u] = *(const u32x4*)(vc + (uint64_t)key * D + col);
+        for (int u = 0; u < G::CPT; u++) {
+            const int byte = 1024 * (wave * G::CPT + u) + 16 * lane;
+            const int r = byte / G::RB, slot = (byte % G::RB) / 16;
+            row[u] = (uint32_t)r;
+            col[u] = (uint32_t)(8 * (slot ^ swz(r)));
+        }
+    }
+};
+
+template <int D>
+__device__ __forceinline__ void dma_tile(uint32_t stage_lds, const f16* base, uint32_t key0, uint32_t kv_end,
+                                         const DmaLane<D>& dl, int wave) {
+    using G = PGeo<D>;
+#pragma unroll
+    for (int u = 0; u < G::CPT; u++) {
+        const uint32_t key = min(key0 + dl.row[u], kv_end - 1);
+        const f16* src = base + (uint64_t)key * D + dl.col[u];
+        // Issued as inline asm: the compiler would otherwise make every later
+        // LDS read wait for all such loads (it cannot tell the stages apart).
+        // Completion is awaited explicitly (wait_vm) before the barrier that
+        // publishes a stage.
+        const uint32_t lds = stage_lds + 1024 * (wave * G::CPT + u);
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
     }
 }
 
-template <int D>
-__device__ __forceinline__ void store_tile(f16* sk, f16* sv, const u32x4 (&kr)[PGeo<D>::CPT],
-                                           const u32x4 (&vr)[PGeo<D>::CPT], uint32_t key0, uint32_t kv_end, int tid) {
-#pragma unroll
-    for (int u = 0; u < PGeo<D>::CPT; u++) {
-        const int c = tid + kThreads * u;
-        const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-        *(u32x4*)(sk + row * PGeo<D>::ROW + col) = kr[u];
-        *(u32x4*)(sv + row * PGeo<D>::ROW + col) = key0 + row < kv_end ? vr[u] : u32x4{0u, 0u, 0u, 0u};
-    }
-}
-
-// q operands of one lane: row t of head hq, dims ks*16 + 8h .. +8 for every k-step.
-// Fused: two passes over the row so that few values are live at once -- the
-// sum of squares (the two lanes of a row hold complementary halves), then
-// each rope pair of 8-dim chunks (ks, ks + KS/2) is reloaded, normalised,
-// rotated with the cos/sin table and rounded to f16.
-template <int D, bool FUSED>
-__device__ __forceinline__ void load_q(const PrefillParams& p, uint32_t t, uint32_t hq, bool live,
-                                       int h, f16x8 (&qop)[PGeo<D>::KS]) {
-    constexpr int KS = PGeo<D>::KS;
-    const uint32_t tc = min(t, p.n_tokens - 1);
-    const bool keep = live && t < p.n_tokens;
-    const float* row = p.q + ((uint64_t)tc * p.n_q_heads + hq) * D;
-    auto chunk = [&](int ks, float (&x)[8]) {
-        const float4 a = *(const float4*)(row + ks * 16 + 8 * h);
-        const float4 b = *(const float4*)(row + ks * 16 + 8 * h + 4);
-        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    };
-    if constexpr (FUSED) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            float x[8];
-            chunk(ks, x);
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss += x[j] * x[j];
-        }
-        ss += lane_xor(ss, 32);
-        const float inv = rms_inv(ss, (float)D, p.eps);
-        // y0 = inv (x0 w0 c - x1 w1 s), y1 = inv (x0 w0 s + x1 w1 c): the RMSNorm weights
-        // folded into the rotation table (q only feeds attention; reassociating
-        // moves it by a few f32 ulp before the f16 rounding)
-        const float4* rot = p.q_rot + (uint64_t)tc * (D / 2);
-#pragma unroll
-        for (int ks = 0; ks < KS / 2; ks++) {
-            float x0[8], x1[8];
-            chunk(ks, x0);
-            chunk(ks + KS / 2, x1);
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float4 r = rot[ks * 16 + 8 * h + j];
-                const float y0 = inv * (x0[j] * r.x - x1[j] * r.y);
-                const float y1 = inv * (x0[j] * r.z + x1[j] * r.w);
-                qop[ks][j] = (f16)(keep ? y0 : 0.0f);
-                qop[ks + KS / 2][j] = (f16)(keep ? y1 : 0.0f);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            float x[8];
-            chunk(ks, x);
-#pragma unroll
-            for (int j = 0; j < 8; j++) qop[ks][j] = (f16)(keep ? x[j] : 0.0f);
-        }
-    }
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p;
 }
 
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
-    constexpr int KS = G::KS, DT = G::DT, CPT = G::CPT;
-    __shared__ __attribute__((aligned(16))) f16 s_k[2 * G::STAGE];
-    __shared__ __attribute__((aligned(16))) f16 s_v[2 * G::STAGE];
+    constexpr int KS = G::KS, DT = G::DT, RB = G::RB;
+    // LDS: K stages [set][2] then V stages [set][2]; reused by the set merge
+    __shared__ __attribute__((aligned(1024))) char s_kv[2 * kSets * 2 * G::STAGE];
+    __shared__ __attribute__((aligned(16))) float s_qn[FUSED ? D : 4];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int set = wave / kHeads, hw = wave % kHeads;  // key-tile set, head slot
     const int r32 = lane & 31, h = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
 
     // workgroup -> (kv head, head group, q-tile pair); one kv head per XCD where possible
@@ -249,26 +246,109 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const uint32_t pair = item % p.n_pairs;
     const uint32_t hg = (item / p.n_pairs) % p.n_hgroups;
     const uint32_t kvh = item / (p.n_pairs * p.n_hgroups);
-    const uint32_t hin = hg * kWaves + wave;  // head index inside the group
+    const uint32_t hin = hg * kHeads + hw;  // head index inside the group
     const bool live = hin < p.group;
     const uint32_t hq = kvh * p.group + (live ? hin : 0);
     const f16* kc = p.k_cache + (uint64_t)kvh * p.max_ctx * D;
     const f16* vc = p.v_cache + (uint64_t)kvh * p.max_ctx * D;
+    if constexpr (FUSED) {
+        for (int i = tid; i < D; i += kThreads) s_qn[i] = p.q_norm[i];
+    }
 
+    // this set's stages
+    char* const k_st = s_kv + set * 2 * G::STAGE;
+    char* const v_st = s_kv + (kSets + set) * 2 * G::STAGE;
+    const uint32_t k_lds = lds_addr(k_st), v_lds = lds_addr(v_st);
 
-    u32x4 kr[CPT], vr[CPT];
+    // Per-lane LDS byte offsets. S operand (row 32 kh + r32, chunk 2 ks + h) is in
+    // slot (2 ks + h) ^ swz(r32) = 2 ks ^ (h ^ swz(r32)); for ks >= 4 that is
+    // 8 + (2 (ks - 4) ^ ...), i.e. 128 bytes further, so four offsets cover all ks.
+    int kofs[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) kofs[i] = r32 * RB + 16 * ((2 * i) ^ h ^ swz(r32));
+    // V transpose read: lane i16 of group g16 reads row 16 m + 4 hh + i16 / 4 (+ 8),
+    // halves dt*32 + 16 (g16 & 1) + 4 (i16 & 3): chunk 4 dt + 2 (g16 & 1) + (i16 & 3) / 2,
+    // byte 8 (i16 & 1) inside it; swz of that row is 2 (i16 / 4) + (hh & 1).
+    int vofs[DT];
+    {
+        const int hh = g16 >> 1;
+        const int v_x = 2 * (i16 >> 2) + (hh & 1);
+        const int v_c = 2 * (g16 & 1) + ((i16 & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vofs[dt] = (4 * hh + (i16 >> 2)) * RB + 8 * (i16 & 1) + 16 * ((4 * dt + v_c) ^ v_x);
+    }
+    const DmaLane<D> dl(hw, lane);
+
     const uint32_t heavy = p.n_qtiles - 1 - pair;
     for (int sel = 0; sel < 2; sel++) {
         const uint32_t qt = sel == 0 ? heavy : pair;
         if (sel == 1 && qt >= heavy) break;  // the middle tile of an odd count is processed once
         const uint32_t q0 = qt * kQRows;
         const uint32_t t = q0 + r32;
+        const uint32_t tc = min(t, p.n_tokens - 1);
+        const bool keep = live && t < p.n_tokens;
         const uint64_t t_abs = (uint64_t)p.pos + t;
         const uint32_t kv_end = p.pos + min(p.n_tokens, q0 + kQRows);  // keys this tile needs (exclusive)
         const uint32_t n_kt = (kv_end + kKTile - 1) / kKTile;
+        const uint32_t n_full = (p.pos + q0 + 1) / kKTile;             // tiles with no masked key
+        const uint32_t n_rounds = (n_kt + 1) / 2;                      // set s takes tiles 2 r + s
 
+        // ---- q row loads first (vmcnt retires in issue order), then the first tile
+        // lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
+        const float* qrow = p.q + ((uint64_t)tc * p.n_q_heads + hq) * D;
+        float4 xq[KS][2];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            xq[ks][0] = *(const float4*)(qrow + ks * 16 + 8 * h);
+            xq[ks][1] = *(const float4*)(qrow + ks * 16 + 8 * h + 4);
+        }
+        float4 cs[FUSED ? KS / 2 : 1][4];  // (cos, sin) of pairs 16 ks + 8 h + [0, 8)
+        if constexpr (FUSED) {
+            const float2* tab = p.rope_cs + (uint64_t)tc * (D / 2);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ks++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) cs[ks][e] = *(const float4*)(tab + ks * 16 + 8 * h + 2 * e);
+        }
+        dma_tile<D>(k_lds, kc, set * kKTile, kv_end, dl, hw);
+        dma_tile<D>(v_lds, vc, set * kKTile, kv_end, dl, hw);
+
+        // ---- q operand: RMSNorm + rotation (fused), scale * log2(e), f16
         f16x8 qop[KS];
-        load_q<D, FUSED>(p, t, hq, live, h, qop);
+        {
+            float x[KS][8];
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                x[ks][0] = xq[ks][0].x; x[ks][1] = xq[ks][0].y; x[ks][2] = xq[ks][0].z; x[ks][3] = xq[ks][0].w;
+                x[ks][4] = xq[ks][1].x; x[ks][5] = xq[ks][1].y; x[ks][6] = xq[ks][1].z; x[ks][7] = xq[ks][1].w;
+            }
+            if constexpr (FUSED) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) ss += x[ks][j] * x[ks][j];
+                ss = sum_xor32(ss);
+                const float inv = rms_inv(ss, (float)D, p.eps) * p.q_scale;
+#pragma unroll
+                for (int ks = 0; ks < KS / 2; ks++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int d0 = ks * 16 + 8 * h + j;
+                        const float c = (j & 1) ? cs[ks][j / 2].z : cs[ks][j / 2].x;
+                        const float sn = (j & 1) ? cs[ks][j / 2].w : cs[ks][j / 2].y;
+                        const float a0 = x[ks][j] * s_qn[d0];
+                        const float a1 = x[ks + KS / 2][j] * s_qn[d0 + D / 2];
+                        qop[ks][j] = (f16)(keep ? (a0 * c - a1 * sn) * inv : 0.0f);
+                        qop[ks + KS / 2][j] = (f16)(keep ? (a0 * sn + a1 * c) * inv : 0.0f);
+                    }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) qop[ks][j] = (f16)(keep ? x[ks][j] * p.q_scale : 0.0f);
+            }
+        }
 
         f32x16 O[DT];
 #pragma unroll
@@ -277,105 +357,125 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
         float m_ref = -INFINITY, l_sum = 0.0f;
 
-        load_tile<D>(kr, vr, kc, vc, 0, kv_end, tid);
-        store_tile<D>(s_k, s_v, kr, vr, 0, kv_end, tid);
-        __syncthreads();
-
-        for (uint32_t j = 0; j < n_kt; j++) {
-            const uint32_t key0 = j * kKTile;
-            const bool more = j + 1 < n_kt;
-            if (more) load_tile<D>(kr, vr, kc, vc, key0 + kKTile, kv_end, tid);
-            const f16* sk = s_k + (j & 1) * G::STAGE;
-            const f16* sv = s_v + (j & 1) * G::STAGE;
-
-            // S^T for the two 32-key halves of the tile
-            f32x16 S[2];
+        wait_vm<0>();
+        lds_sync();
+        // Round r: this set's tile j = 2 r + set sits in its stage r % 2; the
+        // tile of round r + 1 streams into the other stage meanwhile (that stage
+        // was last read in round r - 1, before the previous barrier).
+        for (uint32_t r = 0; r < n_rounds; r++) {
+            const uint32_t j = 2 * r + set;
+            const uint32_t cur = (r & 1) * G::STAGE, nxt = G::STAGE - cur;
+            dma_tile<D>(k_lds + nxt, kc, (j + 2) * kKTile, kv_end, dl, hw);
+            dma_tile<D>(v_lds + nxt, vc, (j + 2) * kKTile, kv_end, dl, hw);
+            if (j < n_kt) {
+                const uint32_t key0 = j * kKTile;
+                const char* sk = k_st + cur;
+                f32x16 S[2];  // S^T of the tile's two 32-key halves
 #pragma unroll
-            for (int kh = 0; kh < 2; kh++) {
-                f32x16 acc;
+                for (int kh = 0; kh < 2; kh++) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+                    for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    const f16x8 a = *(const f16x8*)(sk + (32 * kh + r32) * G::ROW + ks * 16 + 8 * h);
-                    acc = mfma_32x32x16(a, qop[ks], acc);
+                    for (int ks = 0; ks < KS; ks++) {
+                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RB + kofs[ks & 3] + 128 * (ks >> 2));
+                        S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
+                    }
                 }
-                S[kh] = acc;
-            }
-            // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
-            // Softmax in place on the accumulators (log2 domain).
+                // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
+                if (j >= n_full) {  // causal mask on tiles that reach past the first row
 #pragma unroll
-            for (int kh = 0; kh < 2; kh++) S[kh] *= p.scale_log2;
-            if (key0 + kKTile - 1 > (uint64_t)p.pos + q0) {  // tile crosses the diagonal (uniform)
+                    for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) {
+                            const uint64_t key = key0 + 32 * kh + 8 * (i / 4) + 4 * h + (i % 4);
+                            if (key > t_abs) S[kh][i] = -INFINITY;
+                        }
+                }
+                float mx = S[0][0];
 #pragma unroll
                 for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const uint64_t key = key0 + 32 * kh + 8 * (r / 4) + 4 * h + (r % 4);
-                        if (key > t_abs) S[kh][r] = -INFINITY;
+                    for (int i = 0; i < 16; i++) mx = fmaxf(mx, S[kh][i]);
+                mx = max_xor32(mx);
+                if (__ballot(mx > m_ref + kRescaleLog2) != 0) {  // lazy rescale (also the first tile)
+                    const float m_new = mx > m_ref + kRescaleLog2 ? mx : m_ref;
+                    const float alpha = m_new == m_ref ? 1.0f : fast_exp2(m_ref - m_new);  // -inf - -inf would be NaN
+                    l_sum *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
+                    m_ref = m_new;
+                }
+                // A row with every key so far masked (possible in set 1, whose first
+                // tile is key tile 1) keeps m_ref = -inf; its weights are 0.
+                const float m_exp = m_ref == -INFINITY ? 0.0f : m_ref;
+                f16x8 pop[4];  // P^T operand of key step m: scores i = 8 (m % 2) + jj of half m / 2
+#pragma unroll
+                for (int m = 0; m < 4; m++)
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj++) pop[m][jj] = (f16)fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
+                // row sum of the f16 weights, as the products use them
+                struct H4 { f16x2 v[4]; };
+                const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const H4 pr = __builtin_bit_cast(H4, pop[m]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) l_sum = __builtin_amdgcn_fdot2(pr.v[e], ones, l_sum, false);
+                }
+                // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
+                // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
+                // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
+                const char* sv = v_st + cur;
+#pragma unroll
+                for (int m = 0; m < 4; m++)
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) {
+                        const f16x4 lo = lds_read_tr16(sv + vofs[dt] + 16 * m * RB);
+                        const f16x4 hi = lds_read_tr16(sv + vofs[dt] + (16 * m + 8) * RB);
+                        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
                     }
             }
-            float mx = S[0][0];
-#pragma unroll
-            for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, S[kh][r]);
-            mx = fmaxf(mx, lane_xor(mx, 32));
-            if (j == 0) {
-                m_ref = mx;  // key 0 is always visible, so mx is finite
-            } else if (__ballot(mx > m_ref + kRescaleLog2) != 0) {
-                const float m_new = mx > m_ref + kRescaleLog2 ? mx : m_ref;
-                const float alpha = fast_exp2(m_ref - m_new);
-                l_sum *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
-                m_ref = m_new;
-            }
-            f16x8 pop[4];  // P^T operand of key step m: scores r = 8(m%2) + jj of half m/2
-            float psum = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const float pv = fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_ref);
-                    psum += pv;
-                    pop[m][jj] = (f16)pv;
-                }
-            l_sum += psum;
-
-            // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
-            // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
-            // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    const int col = dt * 32 + 16 * (g16 & 1) + 4 * (i16 & 3);
-                    const int hh = g16 >> 1;
-                    const f16x4 lo = lds_read_tr16(sv + (16 * m + 4 * hh + (i16 >> 2)) * G::ROW + col);
-                    const f16x4 hi = lds_read_tr16(sv + (16 * m + 8 + 4 * hh + (i16 >> 2)) * G::ROW + col);
-                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
-                }
-
-            if (more) store_tile<D>(s_k + ((j + 1) & 1) * G::STAGE, s_v + ((j + 1) & 1) * G::STAGE, kr, vr,
-                                    key0 + kKTile, kv_end, tid);
-            __syncthreads();
+            wait_vm<0>();
+            lds_sync();
         }
 
-        if (live && t < p.n_tokens) {
-            float l = l_sum + lane_xor(l_sum, 32);
-            const float inv_l = 1.0f / l;
-            float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
+        // ---- merge set 1 into set 0 through LDS: [head slot][value][lane] floats
+        constexpr int NV = DT * 16 + 2;
+        float* mrg = (float*)s_kv + hw * NV * 64 + lane;
+        if (set == 1) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                for (int i4 = 0; i4 < 4; i4++) {
-                    const int d = dt * 32 + 8 * i4 + 4 * h;
-                    *(float4*)(out + d) = float4{O[dt][i4 * 4 + 0] * inv_l, O[dt][i4 * 4 + 1] * inv_l,
-                                                 O[dt][i4 * 4 + 2] * inv_l, O[dt][i4 * 4 + 3] * inv_l};
-                }
+                for (int i = 0; i < 16; i++) mrg[(dt * 16 + i) * 64] = O[dt][i];
+            mrg[DT * 16 * 64] = m_ref;
+            mrg[(DT * 16 + 1) * 64] = l_sum;
         }
+        lds_sync();
+        if (set == 0) {
+            const float m1 = mrg[DT * 16 * 64], l1 = mrg[(DT * 16 + 1) * 64];
+            const float m = fmaxf(m_ref, m1);  // m_ref is finite (key 0 is visible to set 0)
+            const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(m1 - m);  // set 1 with no tile: m1 = -inf, a1 = 0
+            const float l = sum_xor32(l_sum * a0 + l1 * a1);
+            if (keep) {
+                const float inv_l = 1.0f / l;
+                float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; i4++) {
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int i = i4 * 4 + e;
+                            v[e] = (O[dt][i] * a0 + mrg[(dt * 16 + i) * 64] * a1) * inv_l;
+                        }
+                        const int d = dt * 32 + 8 * i4 + 4 * h;
+                        *(float4*)(out + d) = float4{v[0], v[1], v[2], v[3]};
+                    }
+            }
+        }
+        lds_sync();  // the merge area is the next tile's stages
     }
 }
 
@@ -385,10 +485,10 @@ bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim) {
     return (uint64_t)n_kv_heads * head_dim <= kPrepMaxRow && head_dim % 4 == 0;
 }
 
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float4* q_rot) {
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float2* rope_cs) {
     if (a.n_tokens == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel, dim3(a.n_tokens), dim3(kPrepThreads), 0, ctx->stream, a,
-                     q_rot, *a.table);
+                     rope_cs, *a.table);
     return ds5_after_launch(ctx, "prefill_prep_kernel");
 }
 
@@ -396,7 +496,8 @@ int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
     PrefillParams p{};
     p.q = a.q;
-    p.q_rot = a.q_rot;
+    p.q_norm = a.q_norm;
+    p.rope_cs = a.rope_cs;
     p.k_cache = a.k_cache;
     p.v_cache = a.v_cache;
     p.out = a.out;
@@ -407,13 +508,13 @@ int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     p.max_ctx = a.max_ctx;
     p.n_qtiles = (a.n_tokens + kQRows - 1) / kQRows;
     p.n_pairs = (p.n_qtiles + 1) / 2;
-    p.n_hgroups = (p.group + kWaves - 1) / kWaves;
+    p.n_hgroups = (p.group + kHeads - 1) / kHeads;
     p.n_items = a.n_kv_heads * p.n_hgroups * p.n_pairs;
     p.items_per_xcd = p.n_items % 8 == 0 ? p.n_items / 8 : 0;
-    p.scale_log2 = a.scale * 1.4426950408889634f;
+    p.q_scale = a.scale * 1.4426950408889634f;
     p.eps = a.eps;
     const dim3 grid(p.n_items);
-    const bool fused = a.q_rot != nullptr;
+    const bool fused = a.rope_cs != nullptr;
     if (a.head_dim == 128) {
         if (fused)
             DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<128, true>), grid, dim3(kThreads), 0,

@@ -294,9 +294,18 @@ def test_decode_step_configs(ctx, hip, oracle, config, layer, fused):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("T,pos,hd", [(300, 0, 128), (130, 100, 128), (77, 5, 64), (2, 0, 128)])
-def test_prefill_step(ctx, hip, oracle, T, pos, hd, fused):
-    s = synth.Shape(head_dim=hd)
+@pytest.mark.parametrize("T,pos,hd,hq,hkv", [
+    (300, 0, 128, 32, 4),   # 10 q tiles, masked last key tile
+    (130, 100, 128, 32, 4),  # chunked continuation: the mask spans two key tiles
+    (77, 5, 64, 32, 4),     # head_dim 64
+    (2, 0, 128, 32, 4),     # one key tile: the second wavefront set idles
+    (97, 0, 128, 32, 4),    # odd q-tile count: the middle tile runs once
+    (200, 31, 128, 64, 4),  # 16-head group: four head groups per kv head
+    (96, 3, 128, 6, 3),     # 2-head group: half the wavefronts have no head
+    (65, 0, 64, 8, 8),      # no grouping, head_dim 64
+])
+def test_prefill_step(ctx, hip, oracle, T, pos, hd, hq, hkv, fused):
+    s = synth.Shape(n_q_heads=hq, n_kv_heads=hkv, head_dim=hd)
     cap = pos + T + 7
     q, k, v, qn, kn = synth.step_inputs(2, T, T, s, f16_exact=True)
     kc, vc = synth.cache_f16(2, T, s, cap, pos)
