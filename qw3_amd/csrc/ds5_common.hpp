@@ -118,22 +118,28 @@ struct KvAppendLaunch {
 };
 int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a);
 
-// Prefill pre-pass of the fused step: per token, the rope cos/sin table and
-// the norm + rope + f16 append of every kv head's k row, f16 append of v.
-// Leaves q untouched. Supported while n_kv_heads * head_dim <= 2048.
+// Prefill pre-pass of the fused step: per token, the norm + rope + f16 append
+// of every kv head's k row, f16 append of v, and the attention kernel's q
+// operand: q RMSNorm + rope, times q_scale, f16 into q16 [n_tokens, n_q_heads, head_dim].
+constexpr float kLog2e = 1.4426950408889634f;  // softmax runs in the log2 domain
+
 struct KvPrepLaunch {
     const float* k;
     const float* v;
     const float* k_norm;
+    const float* q;
+    const float* q_norm;
     const int32_t* positions;
     f16* k_cache;
     f16* v_cache;
-    uint32_t pos, n_tokens, n_kv_heads, head_dim, max_ctx;
-    float eps, freq_scale;
+    uint32_t pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
+    float eps, freq_scale, q_scale;
     const RopeTable* table;
 };
 bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim);
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float2* rope_cs);
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, f16* q16);
+// Separate-op prefill: q16 = f16(q * q_scale) for n values (n % 8 == 0).
+int launch_q_pack(ds5_hip_ctx* ctx, const float* q, f16* q16, uint64_t n, float q_scale);
 
 // Generic causal GQA attention (any head_dim <= 512, f32 or f16 cache).
 struct GenericAttnLaunch {
@@ -176,14 +182,11 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a);
 
 // Causal flash-attention prefill on f16 MFMA (head_dim 128 or 64).
 struct PrefillLaunch {
-    const float* q;          // [n_tokens, n_q_heads, head_dim]
-    const float* q_norm;     // fused only: [head_dim]
-    const float2* rope_cs;   // non-null: q is raw; [n_tokens, head_dim / 2] (cos, sin) of the pre-pass
+    const f16* q16;          // [n_tokens, n_q_heads, head_dim], already scaled by softmax scale * log2(e)
     const f16* k_cache;
     const f16* v_cache;
     float* out;
     uint32_t pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
-    float scale, eps;
 };
 int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a);
 

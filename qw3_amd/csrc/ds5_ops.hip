@@ -207,8 +207,13 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
             l.scale = a->scale;
             return launch_decode(ctx, l);
         }
+        // f16 q operand (scaled by scale * log2 e) in the workspace
+        const uint64_t nq = (uint64_t)a->n_tokens * a->n_q_heads * a->head_dim;
+        void* ws = nullptr;
+        if (int rc = ds5_workspace(ctx, nq * sizeof(uint16_t), &ws)) return rc;
+        if (int rc = launch_q_pack(ctx, (const float*)ds5_ptr(a->q), (f16*)ws, nq, a->scale * kLog2e)) return rc;
         PrefillLaunch l{};
-        l.q = (const float*)ds5_ptr(a->q);
+        l.q16 = (const f16*)ws;
         l.k_cache = (const f16*)ds5_ptr(a->k_cache);
         l.v_cache = (const f16*)ds5_ptr(a->v_cache);
         l.out = (float*)ds5_ptr(a->out);
@@ -218,7 +223,6 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
         l.n_kv_heads = a->n_kv_heads;
         l.head_dim = a->head_dim;
         l.max_ctx = a->max_ctx;
-        l.scale = a->scale;
         return launch_prefill(ctx, l);
     }
     GenericAttnLaunch g{(const float*)ds5_ptr(a->q), ds5_ptr(a->k_cache), ds5_ptr(a->v_cache), (float*)ds5_ptr(a->out),
@@ -276,29 +280,31 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             return launch_decode(ctx, l);
         }
         if (prefill_prep_supported(a->n_kv_heads, a->head_dim)) {
-            // cos/sin table of the pre-pass: [n_tokens, head_dim / 2] float2 in the workspace
+            // the pre-pass's f16 q operand [n_tokens, n_q_heads, head_dim] in the workspace
             void* ws = nullptr;
-            if (int rc = ds5_workspace(ctx, (size_t)T * (hd / 2) * sizeof(float2), &ws)) return rc;
+            if (int rc = ds5_workspace(ctx, (size_t)T * hq * hd * sizeof(uint16_t), &ws)) return rc;
             KvPrepLaunch kp{};
             kp.k = (const float*)ds5_ptr(a->k);
             kp.v = (const float*)ds5_ptr(a->v);
             kp.k_norm = (const float*)ds5_ptr(a->k_norm);
+            kp.q = (const float*)ds5_ptr(a->q);
+            kp.q_norm = (const float*)ds5_ptr(a->q_norm);
             kp.positions = (const int32_t*)ds5_ptr(a->positions);
             kp.k_cache = (f16*)ds5_ptr(a->k_cache);
             kp.v_cache = (f16*)ds5_ptr(a->v_cache);
             kp.pos = a->pos;
             kp.n_tokens = a->n_tokens;
+            kp.n_q_heads = a->n_q_heads;
             kp.n_kv_heads = a->n_kv_heads;
             kp.head_dim = a->head_dim;
             kp.max_ctx = a->max_ctx;
             kp.eps = a->eps;
             kp.freq_scale = a->freq_scale;
+            kp.q_scale = a->scale * kLog2e;
             kp.table = table;
-            if (int rc = launch_kv_prep(ctx, kp, (float2*)ws)) return rc;
+            if (int rc = launch_kv_prep(ctx, kp, (f16*)ws)) return rc;
             PrefillLaunch l{};
-            l.q = (const float*)ds5_ptr(a->q);
-            l.q_norm = (const float*)ds5_ptr(a->q_norm);
-            l.rope_cs = (const float2*)ws;
+            l.q16 = (const f16*)ws;
             l.k_cache = (const f16*)ds5_ptr(a->k_cache);
             l.v_cache = (const f16*)ds5_ptr(a->v_cache);
             l.out = (float*)ds5_ptr(a->out);
@@ -308,8 +314,6 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             l.n_kv_heads = a->n_kv_heads;
             l.head_dim = a->head_dim;
             l.max_ctx = a->max_ctx;
-            l.scale = a->scale;
-            l.eps = a->eps;
             return launch_prefill(ctx, l);
         }
     }

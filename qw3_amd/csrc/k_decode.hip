@@ -679,7 +679,7 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
     prm.n_kv_heads = a.n_kv_heads;
     prm.group = group;
     prm.n_sub = n_sub;
-    prm.scale_log2 = a.scale * 1.4426950408889634f;
+    prm.scale_log2 = a.scale * kLog2e;
     prm.eps = a.eps;
     prm.freq_scale = a.freq_scale;
     if (n_splits > 1) {

@@ -74,22 +74,25 @@ __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float i
     return pos * freq_scale * inv;
 }
 
-// Token t: cos/sin of its rope angles (kernels_a.zig:119-122) into the table,
-// then every kv head's k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX
-// rotation (:125-126), f16 append at slot pos + t (:196-210); v rows f16.
-__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, float2* rope_cs, RopeTable table) {
+// Token t: cos/sin of its rope angles (kernels_a.zig:119-122); every kv head's
+// k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX rotation (:125-126),
+// f16 append at slot pos + t (:196-210); v rows f16. Then the q rows of every
+// head: RMSNorm, rotation, times softmax scale * log2(e), rounded to f16 into
+// q16 [n_tokens, n_q_heads, head_dim] (the attention kernel's operand). q only
+// feeds the attention products, so its sum of squares is a lane reduction.
+template <int D>
+__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, f16* q16, RopeTable table) {
     __shared__ __attribute__((aligned(16))) float s_k[kPrepMaxRow];
-    __shared__ float s_cos[DS5_MAX_ROPE_HALF], s_sin[DS5_MAX_ROPE_HALF];
+    __shared__ float s_cos[D / 2], s_sin[D / 2];
     __shared__ float s_inv[kPrepMaxRow / 64];
+    constexpr uint32_t half = D / 2;
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const uint32_t D = a.head_dim, half = D / 2, H = a.n_kv_heads;
+    const uint32_t H = a.n_kv_heads;
     const float pos = (float)a.positions[t];
     for (uint32_t i = tid; i < half; i += kPrepThreads) {
         const float ang = rope_angle(pos, a.freq_scale, table.inv[i]);
-        const float c = cosf(ang), s = sinf(ang);
-        s_cos[i] = c;
-        s_sin[i] = s;
-        rope_cs[(uint64_t)t * half + i] = float2{c, s};
+        s_cos[i] = cosf(ang);
+        s_sin[i] = sinf(ang);
     }
     const float* krow = a.k + (uint64_t)t * H * D;
     for (uint32_t e = tid; e < H * D; e += kPrepThreads) s_k[e] = krow[e];
@@ -112,6 +115,46 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
         const uint32_t h = e / D, i = e % D;
         a.v_cache[((uint64_t)h * a.max_ctx + a.pos + t) * D + i] = (f16)vrow[e];
     }
+    // q: D / 16 threads per head, thread k takes dims 8k + [0, 8) and half + 8k + [0, 8)
+    constexpr uint32_t TPH = D / 16;
+    for (uint32_t e = tid; e < a.n_q_heads * TPH; e += kPrepThreads) {
+        const uint32_t hq = e / TPH, k8 = 8 * (e % TPH);
+        const float* row = a.q + ((uint64_t)t * a.n_q_heads + hq) * D;
+        float x0[8], x1[8];
+        *(float4*)&x0[0] = *(const float4*)(row + k8);
+        *(float4*)&x0[4] = *(const float4*)(row + k8 + 4);
+        *(float4*)&x1[0] = *(const float4*)(row + half + k8);
+        *(float4*)&x1[4] = *(const float4*)(row + half + k8 + 4);
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss += x0[j] * x0[j] + x1[j] * x1[j];
+#pragma unroll
+        for (uint32_t m = 1; m < TPH; m <<= 1) ss += __shfl_xor(ss, (int)m, 64);
+        const float inv = rms_inv(ss, (float)D, a.eps);
+        f16x8 y0v, y1v;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t i = k8 + j;
+            float y0, y1;
+            rotate(norm_mul(x0[j], inv, a.q_norm[i]), norm_mul(x1[j], inv, a.q_norm[i + half]), s_cos[i], s_sin[i], y0,
+                   y1);
+            y0v[j] = (f16)(y0 * a.q_scale);
+            y1v[j] = (f16)(y1 * a.q_scale);
+        }
+        f16* dst = q16 + ((uint64_t)t * a.n_q_heads + hq) * D;
+        *(f16x8*)(dst + k8) = y0v;
+        *(f16x8*)(dst + half + k8) = y1v;
+    }
+}
+
+// Separate-op path: q already normalised and rotated; q16 = f16(q * q_scale).
+__global__ __launch_bounds__(256) void q_pack_kernel(const float* q, f16* q16, uint64_t n8, float q_scale) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n8; i += (uint64_t)gridDim.x * 256) {
+        const float4 a = *(const float4*)(q + 8 * i), b = *(const float4*)(q + 8 * i + 4);
+        const f16x8 y = {(f16)(a.x * q_scale), (f16)(a.y * q_scale), (f16)(a.z * q_scale), (f16)(a.w * q_scale),
+                         (f16)(b.x * q_scale), (f16)(b.y * q_scale), (f16)(b.z * q_scale), (f16)(b.w * q_scale)};
+        *(f16x8*)(q16 + 8 * i) = y;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -126,16 +169,12 @@ constexpr int kKTile = 64;     // keys per LDS stage
 constexpr float kRescaleLog2 = 8.0f;
 
 struct PrefillParams {
-    const float* q;
-    const float* q_norm;     // fused only: [head_dim]
-    const float2* rope_cs;   // fused only: [n_tokens, head_dim / 2] (cos, sin)
+    const f16* q16;          // [n_tokens, n_q_heads, head_dim], scaled by softmax scale * log2(e)
     const f16* k_cache;
     const f16* v_cache;
     float* out;
     uint32_t pos, n_tokens, n_q_heads, group, max_ctx;
     uint32_t n_qtiles, n_pairs, n_hgroups, n_items, items_per_xcd;
-    float q_scale;           // softmax scale * log2(e), folded into the f16 q operand
-    float eps;
 };
 
 template <int D>
@@ -227,13 +266,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p;
 }
 
-template <int D, bool FUSED>
+template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
     constexpr int KS = G::KS, DT = G::DT, RB = G::RB;
     // LDS: K stages [set][2] then V stages [set][2]; reused by the set merge
     __shared__ __attribute__((aligned(1024))) char s_kv[2 * kSets * 2 * G::STAGE];
-    __shared__ __attribute__((aligned(16))) float s_qn[FUSED ? D : 4];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -251,10 +289,6 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const uint32_t hq = kvh * p.group + (live ? hin : 0);
     const f16* kc = p.k_cache + (uint64_t)kvh * p.max_ctx * D;
     const f16* vc = p.v_cache + (uint64_t)kvh * p.max_ctx * D;
-    if constexpr (FUSED) {
-        for (int i = tid; i < D; i += kThreads) s_qn[i] = p.q_norm[i];
-    }
-
     // this set's stages
     char* const k_st = s_kv + set * 2 * G::STAGE;
     char* const v_st = s_kv + (kSets + set) * 2 * G::STAGE;
@@ -293,61 +327,17 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         const uint32_t n_full = (p.pos + q0 + 1) / kKTile;             // tiles with no masked key
         const uint32_t n_rounds = (n_kt + 1) / 2;                      // set s takes tiles 2 r + s
 
-        // ---- q row loads first (vmcnt retires in issue order), then the first tile
+        // ---- q operand first (vmcnt retires in issue order), then the first tile.
         // lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
-        const float* qrow = p.q + ((uint64_t)tc * p.n_q_heads + hq) * D;
-        float4 xq[KS][2];
+        const f16* qrow = p.q16 + ((uint64_t)tc * p.n_q_heads + hq) * D + 8 * h;
+        f16x8 qop[KS];
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            xq[ks][0] = *(const float4*)(qrow + ks * 16 + 8 * h);
-            xq[ks][1] = *(const float4*)(qrow + ks * 16 + 8 * h + 4);
-        }
-        float4 cs[FUSED ? KS / 2 : 1][4];  // (cos, sin) of pairs 16 ks + 8 h + [0, 8)
-        if constexpr (FUSED) {
-            const float2* tab = p.rope_cs + (uint64_t)tc * (D / 2);
-#pragma unroll
-            for (int ks = 0; ks < KS / 2; ks++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) cs[ks][e] = *(const float4*)(tab + ks * 16 + 8 * h + 2 * e);
-        }
+        for (int ks = 0; ks < KS; ks++) qop[ks] = *(const f16x8*)(qrow + 16 * ks);
         dma_tile<D>(k_lds, kc, set * kKTile, kv_end, dl, hw);
         dma_tile<D>(v_lds, vc, set * kKTile, kv_end, dl, hw);
-
-        // ---- q operand: RMSNorm + rotation (fused), scale * log2(e), f16
-        f16x8 qop[KS];
-        {
-            float x[KS][8];
+        if (!keep) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                x[ks][0] = xq[ks][0].x; x[ks][1] = xq[ks][0].y; x[ks][2] = xq[ks][0].z; x[ks][3] = xq[ks][0].w;
-                x[ks][4] = xq[ks][1].x; x[ks][5] = xq[ks][1].y; x[ks][6] = xq[ks][1].z; x[ks][7] = xq[ks][1].w;
-            }
-            if constexpr (FUSED) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-                    for (int j = 0; j < 8; j++) ss += x[ks][j] * x[ks][j];
-                ss = sum_xor32(ss);
-                const float inv = rms_inv(ss, (float)D, p.eps) * p.q_scale;
-#pragma unroll
-                for (int ks = 0; ks < KS / 2; ks++)
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const int d0 = ks * 16 + 8 * h + j;
-                        const float c = (j & 1) ? cs[ks][j / 2].z : cs[ks][j / 2].x;
-                        const float sn = (j & 1) ? cs[ks][j / 2].w : cs[ks][j / 2].y;
-                        const float a0 = x[ks][j] * s_qn[d0];
-                        const float a1 = x[ks + KS / 2][j] * s_qn[d0 + D / 2];
-                        qop[ks][j] = (f16)(keep ? (a0 * c - a1 * sn) * inv : 0.0f);
-                        qop[ks + KS / 2][j] = (f16)(keep ? (a0 * sn + a1 * c) * inv : 0.0f);
-                    }
-            } else {
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-                    for (int j = 0; j < 8; j++) qop[ks][j] = (f16)(keep ? x[ks][j] * p.q_scale : 0.0f);
-            }
+            for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
         }
 
         f32x16 O[DT];
@@ -365,8 +355,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         for (uint32_t r = 0; r < n_rounds; r++) {
             const uint32_t j = 2 * r + set;
             const uint32_t cur = (r & 1) * G::STAGE, nxt = G::STAGE - cur;
-            dma_tile<D>(k_lds + nxt, kc, (j + 2) * kKTile, kv_end, dl, hw);
-            dma_tile<D>(v_lds + nxt, vc, (j + 2) * kKTile, kv_end, dl, hw);
+            // The next tile's loads are issued in two halves inside the round (a
+            // burst from all eight wavefronts right after the barrier would stall
+            // their issue); with no tile this round there is none next round.
             if (j < n_kt) {
                 const uint32_t key0 = j * kKTile;
                 const char* sk = k_st + cur;
@@ -381,6 +372,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                         S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
                     }
                 }
+                dma_tile<D>(k_lds + nxt, kc, (j + 2) * kKTile, kv_end, dl, hw);
                 // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
                 if (j >= n_full) {  // causal mask on tiles that reach past the first row
 #pragma unroll
@@ -422,6 +414,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
 #pragma unroll
                     for (int e = 0; e < 4; e++) l_sum = __builtin_amdgcn_fdot2(pr.v[e], ones, l_sum, false);
                 }
+                dma_tile<D>(v_lds + nxt, vc, (j + 2) * kKTile, kv_end, dl, hw);
                 // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
                 // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
                 // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
@@ -482,22 +475,32 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
 }  // namespace
 
 bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim) {
-    return (uint64_t)n_kv_heads * head_dim <= kPrepMaxRow && head_dim % 4 == 0;
+    return (uint64_t)n_kv_heads * head_dim <= kPrepMaxRow && (head_dim == 64 || head_dim == 128);
 }
 
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, float2* rope_cs) {
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, f16* q16) {
     if (a.n_tokens == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel, dim3(a.n_tokens), dim3(kPrepThreads), 0, ctx->stream, a,
-                     rope_cs, *a.table);
+    if (a.head_dim == 128)
+        DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel<128>, dim3(a.n_tokens), dim3(kPrepThreads), 0,
+                         ctx->stream, a, q16, *a.table);
+    else
+        DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel<64>, dim3(a.n_tokens), dim3(kPrepThreads), 0,
+                         ctx->stream, a, q16, *a.table);
     return ds5_after_launch(ctx, "prefill_prep_kernel");
+}
+
+int launch_q_pack(ds5_hip_ctx* ctx, const float* q, f16* q16, uint64_t n, float q_scale) {
+    if (n == 0) return DS5_OK;
+    const uint64_t n8 = n / 8;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n8 + 255) / 256, 2048);
+    DS5_TIMED_LAUNCH(ctx, "q_pack_kernel", q_pack_kernel, dim3(blocks), dim3(256), 0, ctx->stream, q, q16, n8, q_scale);
+    return ds5_after_launch(ctx, "q_pack_kernel");
 }
 
 int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
     PrefillParams p{};
-    p.q = a.q;
-    p.q_norm = a.q_norm;
-    p.rope_cs = a.rope_cs;
+    p.q16 = a.q16;
     p.k_cache = a.k_cache;
     p.v_cache = a.v_cache;
     p.out = a.out;
@@ -511,24 +514,12 @@ int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     p.n_hgroups = (p.group + kHeads - 1) / kHeads;
     p.n_items = a.n_kv_heads * p.n_hgroups * p.n_pairs;
     p.items_per_xcd = p.n_items % 8 == 0 ? p.n_items / 8 : 0;
-    p.q_scale = a.scale * 1.4426950408889634f;
-    p.eps = a.eps;
     const dim3 grid(p.n_items);
-    const bool fused = a.rope_cs != nullptr;
-    if (a.head_dim == 128) {
-        if (fused)
-            DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<128, true>), grid, dim3(kThreads), 0,
-                             ctx->stream, p);
-        else
-            DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<128, false>), grid, dim3(kThreads), 0,
-                             ctx->stream, p);
-    } else {
-        if (fused)
-            DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<64, true>), grid, dim3(kThreads), 0,
-                             ctx->stream, p);
-        else
-            DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<64, false>), grid, dim3(kThreads), 0,
-                             ctx->stream, p);
-    }
+    if (a.head_dim == 128)
+        DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", prefill_attention_kernel<128>, grid, dim3(kThreads), 0,
+                         ctx->stream, p);
+    else
+        DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", prefill_attention_kernel<64>, grid, dim3(kThreads), 0,
+                         ctx->stream, p);
     return ds5_after_launch(ctx, "prefill_attention_kernel");
 }
