@@ -218,10 +218,20 @@ __device__ __forceinline__ float sum_xor32(float v) {
 }
 
 // LDS rows are unpadded; the 16-byte chunk c of row r sits in slot c ^ swz(r).
-// Eight consecutive rows at one chunk (the S operand reads) and four
-// consecutive rows at two adjacent chunks (the V transpose reads) then fall in
-// distinct banks.
-__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+// The LDS serves 256 bytes (64 banks) per cycle: 16 lanes of a 16-byte read, 32
+// of an 8-byte one. The S operand read puts 16 consecutive rows at one chunk
+// in a cycle, the V transpose read 4 consecutive rows x 4 adjacent chunks
+// (aligned to 4); swz makes both hit 16 distinct 16-byte bank groups.
+//   D = 128 (256-byte rows, one per bank period): swz(r) = 4 (r % 4) + (r / 4) % 4,
+//     a permutation of r % 16 whose high two bits separate any 4 consecutive rows.
+//   D = 64 (128-byte rows, two per period): rows of equal parity share a period
+//     half, so swz(r) = 4 ((r / 2) % 2) + (r / 4) % 4 permutes r / 2 % 8 and
+//     separates rows 4a and 4a + 2.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
+    else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
 
 // Direct-to-LDS loads of the 64 K (or V) rows starting at key0 into one stage.
 // Load u of this wavefront fills bytes [1024 (wave CPT + u), +1024) of the
@@ -240,7 +250,7 @@ struct DmaLane {
             const int byte = 1024 * (wave * G::CPT + u) + 16 * lane;
             const int r = byte / G::RB, slot = (byte % G::RB) / 16;
             row[u] = (uint32_t)r;
-            col[u] = (uint32_t)(8 * (slot ^ swz(r)));
+            col[u] = (uint32_t)(8 * (slot ^ swz<D>(r)));
         }
     }
 };
@@ -294,22 +304,25 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     char* const v_st = s_kv + (kSets + set) * 2 * G::STAGE;
     const uint32_t k_lds = lds_addr(k_st), v_lds = lds_addr(v_st);
 
-    // Per-lane LDS byte offsets. S operand (row 32 kh + r32, chunk 2 ks + h) is in
-    // slot (2 ks + h) ^ swz(r32) = 2 ks ^ (h ^ swz(r32)); for ks >= 4 that is
-    // 8 + (2 (ks - 4) ^ ...), i.e. 128 bytes further, so four offsets cover all ks.
-    int kofs[4];
+    // Per-lane LDS byte offsets. S operand of k-step ks: row 32 kh + r32, chunk
+    // 2 ks + h (swz of row 32 kh + r32 equals swz(r32)).
+    int kofs[KS];
 #pragma unroll
-    for (int i = 0; i < 4; i++) kofs[i] = r32 * RB + 16 * ((2 * i) ^ h ^ swz(r32));
-    // V transpose read: lane i16 of group g16 reads row 16 m + 4 hh + i16 / 4 (+ 8),
-    // halves dt*32 + 16 (g16 & 1) + 4 (i16 & 3): chunk 4 dt + 2 (g16 & 1) + (i16 & 3) / 2,
-    // byte 8 (i16 & 1) inside it; swz of that row is 2 (i16 / 4) + (hh & 1).
-    int vofs[DT];
+    for (int ks = 0; ks < KS; ks++) kofs[ks] = r32 * RB + 16 * ((2 * ks + h) ^ swz<D>(r32));
+    // V transpose read: lane i16 of group g16 reads row 16 m + 4 hh + i16 / 4 (+ 8 for
+    // the upper half), halves dt*32 + 16 (g16 & 1) + 4 (i16 & 3): chunk
+    // 4 dt + 2 (g16 & 1) + (i16 & 3) / 2, byte 8 (i16 & 1) inside it. 16 m leaves
+    // swz unchanged, so the offsets depend on (dt, half) only.
+    int vofs[2][DT];
     {
         const int hh = g16 >> 1;
-        const int v_x = 2 * (i16 >> 2) + (hh & 1);
         const int v_c = 2 * (g16 & 1) + ((i16 & 3) >> 1);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vofs[dt] = (4 * hh + (i16 >> 2)) * RB + 8 * (i16 & 1) + 16 * ((4 * dt + v_c) ^ v_x);
+        for (int hi = 0; hi < 2; hi++) {
+            const int row = 8 * hi + 4 * hh + (i16 >> 2);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vofs[hi][dt] = row * RB + 8 * (i16 & 1) + 16 * ((4 * dt + v_c) ^ swz<D>(row));
+        }
     }
     const DmaLane<D> dl(hw, lane);
 
@@ -368,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                     for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
 #pragma unroll
                     for (int ks = 0; ks < KS; ks++) {
-                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RB + kofs[ks & 3] + 128 * (ks >> 2));
+                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RB + kofs[ks]);
                         S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
                     }
                 }
@@ -423,8 +436,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                 for (int m = 0; m < 4; m++)
 #pragma unroll
                     for (int dt = 0; dt < DT; dt++) {
-                        const f16x4 lo = lds_read_tr16(sv + vofs[dt] + 16 * m * RB);
-                        const f16x4 hi = lds_read_tr16(sv + vofs[dt] + (16 * m + 8) * RB);
+                        const f16x4 lo = lds_read_tr16(sv + vofs[0][dt] + 16 * m * RB);
+                        const f16x4 hi = lds_read_tr16(sv + vofs[1][dt] + 16 * m * RB);
                         const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                         O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
                     }
