@@ -446,23 +446,23 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             lds_sync();
         }
 
-        // ---- merge set 1 into set 0 through LDS: [head slot][value][lane] floats
-        constexpr int NV = DT * 16 + 2;
-        float* mrg = (float*)s_kv + hw * NV * 64 + lane;
+        // ---- merge set 1 into set 0 through LDS: [head slot][float4 index][lane]
+        constexpr int NV4 = DT * 4 + 1;  // O as float4s, then (m, l, -, -)
+        float4* mrg = (float4*)s_kv + hw * NV4 * 64 + lane;
         if (set == 1) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) mrg[(dt * 16 + i) * 64] = O[dt][i];
-            mrg[DT * 16 * 64] = m_ref;
-            mrg[(DT * 16 + 1) * 64] = l_sum;
+                for (int i4 = 0; i4 < 4; i4++)
+                    mrg[(dt * 4 + i4) * 64] = float4{O[dt][4 * i4], O[dt][4 * i4 + 1], O[dt][4 * i4 + 2], O[dt][4 * i4 + 3]};
+            mrg[DT * 4 * 64] = float4{m_ref, l_sum, 0.0f, 0.0f};
         }
         lds_sync();
         if (set == 0) {
-            const float m1 = mrg[DT * 16 * 64], l1 = mrg[(DT * 16 + 1) * 64];
-            const float m = fmaxf(m_ref, m1);  // m_ref is finite (key 0 is visible to set 0)
-            const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(m1 - m);  // set 1 with no tile: m1 = -inf, a1 = 0
-            const float l = sum_xor32(l_sum * a0 + l1 * a1);
+            const float4 ml = mrg[DT * 4 * 64];
+            const float m = fmaxf(m_ref, ml.x);  // m_ref is finite (key 0 is visible to set 0)
+            const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(ml.x - m);  // set 1 with no tile: m1 = -inf, a1 = 0
+            const float l = sum_xor32(l_sum * a0 + ml.y * a1);
             if (keep) {
                 const float inv_l = 1.0f / l;
                 float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
@@ -470,14 +470,12 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                 for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                     for (int i4 = 0; i4 < 4; i4++) {
-                        float v[4];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int i = i4 * 4 + e;
-                            v[e] = (O[dt][i] * a0 + mrg[(dt * 16 + i) * 64] * a1) * inv_l;
-                        }
+                        const float4 o1 = mrg[(dt * 4 + i4) * 64];
                         const int d = dt * 32 + 8 * i4 + 4 * h;
-                        *(float4*)(out + d) = float4{v[0], v[1], v[2], v[3]};
+                        *(float4*)(out + d) = float4{(O[dt][4 * i4] * a0 + o1.x * a1) * inv_l,
+                                                     (O[dt][4 * i4 + 1] * a0 + o1.y * a1) * inv_l,
+                                                     (O[dt][4 * i4 + 2] * a0 + o1.z * a1) * inv_l,
+                                                     (O[dt][4 * i4 + 3] * a0 + o1.w * a1) * inv_l};
                     }
             }
         }
