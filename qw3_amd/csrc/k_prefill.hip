@@ -86,45 +86,50 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
     __shared__ float s_cos[D / 2], s_sin[D / 2];
     __shared__ float s_inv[kPrepMaxRow / 64];
     constexpr uint32_t half = D / 2;
+    constexpr uint32_t TPH = D / 16;  // q: threads per head, thread k takes dims 8k + [0, 8) and half + 8k + [0, 8)
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const uint32_t H = a.n_kv_heads;
+    const uint32_t H = a.n_kv_heads, HQ = a.n_q_heads;
+    // Every global load of the token is issued up front (k to LDS, the first q
+    // chunk and v quad of this thread to registers), so one memory round trip
+    // covers them all.
+    const float* krow = a.k + (uint64_t)t * H * D;
+    for (uint32_t e = tid; e < H * D / 4; e += kPrepThreads) ((float4*)s_k)[e] = ((const float4*)krow)[e];
+    const float* qbase = a.q + (uint64_t)t * HQ * D;
+    float x0[8], x1[8];
+    if (tid < HQ * TPH) {
+        const float* row = qbase + (tid / TPH) * D + 8 * (tid % TPH);
+        *(float4*)&x0[0] = *(const float4*)(row);
+        *(float4*)&x0[4] = *(const float4*)(row + 4);
+        *(float4*)&x1[0] = *(const float4*)(row + half);
+        *(float4*)&x1[4] = *(const float4*)(row + half + 4);
+    }
+    const float4* vrow = (const float4*)(a.v + (uint64_t)t * H * D);
+    float4 v0 = tid < H * D / 4 ? vrow[tid] : float4{};
     const float pos = (float)a.positions[t];
     for (uint32_t i = tid; i < half; i += kPrepThreads) {
         const float ang = rope_angle(pos, a.freq_scale, table.inv[i]);
         s_cos[i] = cosf(ang);
         s_sin[i] = sinf(ang);
     }
-    const float* krow = a.k + (uint64_t)t * H * D;
-    for (uint32_t e = tid; e < H * D; e += kPrepThreads) s_k[e] = krow[e];
     __syncthreads();
     for (uint32_t h = tid; h < H; h += kPrepThreads) s_inv[h] = rms_inv(serial_sumsq(s_k + h * D, (int)D), (float)D, a.eps);
-    __syncthreads();
-    for (uint32_t e = tid; e < H * half; e += kPrepThreads) {
-        const uint32_t h = e / half, i = e % half;
-        const float inv = s_inv[h];
-        const float x0 = norm_mul(s_k[h * D + i], inv, a.k_norm[i]);
-        const float x1 = norm_mul(s_k[h * D + i + half], inv, a.k_norm[i + half]);
-        float y0, y1;
-        rotate(x0, x1, s_cos[i], s_sin[i], y0, y1);
-        f16* dst = a.k_cache + ((uint64_t)h * a.max_ctx + a.pos + t) * D;
-        dst[i] = (f16)y0;
-        dst[i + half] = (f16)y1;
+    // v rows: f16 append
+    for (uint32_t e = tid; e < H * D / 4; e += kPrepThreads) {
+        const float4 v = e == tid ? v0 : vrow[e];
+        const uint32_t h = (4 * e) / D, i = (4 * e) % D;
+        const f16x4 y = {(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
+        *(f16x4*)(a.v_cache + ((uint64_t)h * a.max_ctx + a.pos + t) * D + i) = y;
     }
-    const float* vrow = a.v + (uint64_t)t * H * D;
-    for (uint32_t e = tid; e < H * D; e += kPrepThreads) {
-        const uint32_t h = e / D, i = e % D;
-        a.v_cache[((uint64_t)h * a.max_ctx + a.pos + t) * D + i] = (f16)vrow[e];
-    }
-    // q: D / 16 threads per head, thread k takes dims 8k + [0, 8) and half + 8k + [0, 8)
-    constexpr uint32_t TPH = D / 16;
-    for (uint32_t e = tid; e < a.n_q_heads * TPH; e += kPrepThreads) {
+    // q rows: RMSNorm (lane-reduced sum of squares), rotation, scale, f16
+    for (uint32_t e = tid; e < HQ * TPH; e += kPrepThreads) {
         const uint32_t hq = e / TPH, k8 = 8 * (e % TPH);
-        const float* row = a.q + ((uint64_t)t * a.n_q_heads + hq) * D;
-        float x0[8], x1[8];
-        *(float4*)&x0[0] = *(const float4*)(row + k8);
-        *(float4*)&x0[4] = *(const float4*)(row + k8 + 4);
-        *(float4*)&x1[0] = *(const float4*)(row + half + k8);
-        *(float4*)&x1[4] = *(const float4*)(row + half + k8 + 4);
+        if (e != tid) {
+            const float* row = qbase + hq * D + k8;
+            *(float4*)&x0[0] = *(const float4*)(row);
+            *(float4*)&x0[4] = *(const float4*)(row + 4);
+            *(float4*)&x1[0] = *(const float4*)(row + half);
+            *(float4*)&x1[4] = *(const float4*)(row + half + 4);
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) ss += x0[j] * x0[j] + x1[j] * x1[j];
@@ -141,9 +146,22 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
             y0v[j] = (f16)(y0 * a.q_scale);
             y1v[j] = (f16)(y1 * a.q_scale);
         }
-        f16* dst = q16 + ((uint64_t)t * a.n_q_heads + hq) * D;
+        f16* dst = q16 + ((uint64_t)t * HQ + hq) * D;
         *(f16x8*)(dst + k8) = y0v;
         *(f16x8*)(dst + half + k8) = y1v;
+    }
+    __syncthreads();
+    // k rows: serial-order RMSNorm, rotation, f16 append
+    for (uint32_t e = tid; e < H * half; e += kPrepThreads) {
+        const uint32_t h = e / half, i = e % half;
+        const float inv = s_inv[h];
+        const float y0n = norm_mul(s_k[h * D + i], inv, a.k_norm[i]);
+        const float y1n = norm_mul(s_k[h * D + i + half], inv, a.k_norm[i + half]);
+        float y0, y1;
+        rotate(y0n, y1n, s_cos[i], s_sin[i], y0, y1);
+        f16* dst = a.k_cache + ((uint64_t)h * a.max_ctx + a.pos + t) * D;
+        dst[i] = (f16)y0;
+        dst[i + half] = (f16)y1;
     }
 }
 
