@@ -209,8 +209,46 @@ DS5_DEVICE_INLINE f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Lane exchange within the 64-wide wavefront (ds_bpermute based).
+// Lane exchange within the 64-wide wavefront (ds_bpermute based: an LDS round trip).
 DS5_DEVICE_INLINE float lane_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// VALU-only cross-lane operations (no LDS round trip).
+// DPP move within rows of 16 lanes; CTRL is a DPP control word.
+template <int CTRL>
+DS5_DEVICE_INLINE float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// op(v[l], v[l ^ 16]) and op(v[l], v[l ^ 32]): v_permlane16_swap / v_permlane32_swap
+// with both operands v return (own, partner) in some order, so a commutative op
+// of the pair gives the combined value on every lane.
+template <class F>
+DS5_DEVICE_INLINE float swap16_op(float v, F op) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <class F>
+DS5_DEVICE_INLINE float swap32_op(float v, F op) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// All-reduce over the 64 lanes in a fixed order: xor 1 and xor 2 (quad_perm),
+// the quads of 8 lanes (row_half_mirror), the halves of 16 (row_mirror), then
+// rows (permlane16 swap) and halves of the wave (permlane32 swap).
+template <class F>
+DS5_DEVICE_INLINE float wave_allreduce(float v, F op) {
+    v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_mov<0x140>(v));  // row_mirror
+    v = swap16_op(v, op);
+    return swap32_op(v, op);
+}
+struct OpAdd {
+    DS5_DEVICE_INLINE float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    DS5_DEVICE_INLINE float operator()(float a, float b) const { return fmaxf(a, b); }
+};
 
 DS5_DEVICE_INLINE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -201,8 +201,7 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
     float mx = s[0];
 #pragma unroll
     for (int j = 1; j < 8; j++) mx = fmaxf(mx, s[j]);
-    mx = fmaxf(mx, lane_xor(mx, 16));
-    mx = fmaxf(mx, lane_xor(mx, 32));
+    mx = swap32_op(swap16_op(mx, OpMax{}), OpMax{});
     // Lazy rescale: move the reference only when the tile max exceeds it by > 2^8.
     if (first) {
         m_ref = mx;  // O and l are still zero
@@ -441,8 +440,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
                 ss += r[j] * r[j];
             }
         }
-        ss += lane_xor(ss, 16);
-        ss += lane_xor(ss, 32);
+        ss = swap32_op(swap16_op(ss, OpAdd{}), OpAdd{});
         const float inv = rms_inv(ss, (float)D, p.eps);
 #pragma unroll
         for (int kk = 0; kk < KK; kk++)
@@ -521,8 +519,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     }
 
     // ---- 5. combine the wavefronts, then write the partial (or the output)
-    float l_w = l_sum + lane_xor(l_sum, 16);
-    l_w += lane_xor(l_w, 32);
+    const float l_w = swap32_op(swap16_op(l_sum, OpAdd{}), OpAdd{});
     __syncthreads();  // all wavefronts are done with their V staging areas
     float* s_o = (float*)s_big;  // [kWaves][kHeads][OROW]
     if (g == 0) {
@@ -570,7 +567,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 
 // Split merge: block = 4 wavefronts = 4 groups of 4 output dims of one
 // (sequence, q head); lane s holds split s (n_splits <= 64). One load per
-// lane, then fixed-order lane reductions, so results are deterministic.
+// lane, then fixed-order DPP / permlane reductions (VALU only), so results are
+// deterministic.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     const uint64_t qi = blockIdx.x;  // sequence * n_q_heads + head
@@ -592,23 +590,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
         l = ml.y;
         o = *(const float4*)(p.part_o + (qi * p.n_splits + lane) * D + d0);
     }
-    float M = m;
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) M = fmaxf(M, lane_xor(M, s));
+    const float M = wave_allreduce(m, OpMax{});
     const float w = (uint32_t)lane < ns ? fast_exp2(m - M) : 0.0f;
     l *= w;
     o.x *= w;
     o.y *= w;
     o.z *= w;
     o.w *= w;
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        l += lane_xor(l, s);
-        o.x += lane_xor(o.x, s);
-        o.y += lane_xor(o.y, s);
-        o.z += lane_xor(o.z, s);
-        o.w += lane_xor(o.w, s);
-    }
+    l = wave_allreduce(l, OpAdd{});
+    o.x = wave_allreduce(o.x, OpAdd{});
+    o.y = wave_allreduce(o.y, OpAdd{});
+    o.z = wave_allreduce(o.z, OpAdd{});
+    o.w = wave_allreduce(o.w, OpAdd{});
     if (lane == 0) *(float4*)(p.out + qi * D + d0) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
 }
 
