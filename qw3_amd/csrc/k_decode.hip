@@ -73,7 +73,7 @@ struct Geo {
     static constexpr int DT = D / 16;            // 16-row blocks of O^T
     static constexpr int RC = D / 8;             // 16-byte chunks per cache row
     static constexpr int VC = kTile * RC / 64;   // V chunks per lane per tile
-    static constexpr int VROW = D * 2 + 16;      // bytes per staged V row (aligned, banks spread)
+    static constexpr int VROW = D * 2;           // bytes per staged V row (chunks swizzled, see vswz)
     static constexpr int OROW = D + 4;           // floats per row of the cross-wave O buffer
 };
 
@@ -148,13 +148,24 @@ __device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p
     }
 }
 
+// Staged V rows are unpadded; 16-byte chunk c of row r sits in slot c ^ vswz(r).
+// A transpose read serves 32 lanes (256 bytes, all 64 banks) per cycle: 8
+// consecutive rows x 2 adjacent chunks; vswz sends them to 16 distinct slots
+// (D = 128: one row per bank period; D = 64: two rows per period, so only rows
+// of equal parity need distinct offsets).
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+    if constexpr (D == 128) return 2 * (r & 7);
+    else return 2 * ((r >> 1) & 3);
+}
+
 // Splits x into f16 hi + lo with x ~= hi + lo to ~22 significant bits.
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
 }
 
-template <int D, bool FUSED>
+template <int D, bool FUSED, bool PACK>
 __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32_t end, int g, int c16, int lane,
                                              const f16x8 (&qh)[Geo<D>::KK], const f16x8 (&ql)[Geo<D>::KK],
                                              f32x4 (&O)[Geo<D>::DT], float& m_ref, float& l_sum, char* vlds,
@@ -176,7 +187,9 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
     }
     const bool partial = p0 + kTile > end;  // wave-uniform
 
-    // S^T = K . Q^T with q = hi + lo
+    // S^T = K . Q^T with q = hi + lo. Packed (group <= 8): columns 0-7 carry the
+    // hi halves of heads 0-7 and columns 8-15 the lo halves, so one product
+    // covers both and lanes c16, c16 ^ 8 add their columns (DPP row_ror:8).
     f32x4 S[2];
 #pragma unroll
     for (int st = 0; st < 2; st++) {
@@ -185,7 +198,11 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
         for (int kk = 0; kk < G::KK; kk++) {
             const f16x8 a = __builtin_bit_cast(f16x8, T.k[st][kk]);
             acc = mfma_16x16x32(a, qh[kk], acc);
-            acc = mfma_16x16x32(a, ql[kk], acc);
+            if constexpr (!PACK) acc = mfma_16x16x32(a, ql[kk], acc);
+        }
+        if constexpr (PACK) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += dpp_mov<0x128>(acc[i]);
         }
         S[st] = acc;
     }
@@ -214,7 +231,7 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
         for (int dt = 0; dt < G::DT; dt++) O[dt] *= alpha;
         m_ref = m_new;
     }
-    f16x8 ph, pl;
+    f16x8 ph, pl;  // packed: ph alone, hi halves in columns 0-7 and lo halves in 8-15
     float psum = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -222,8 +239,12 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
         psum += pj;
         _Float16 hi, lo;
         split_f16(pj, hi, lo);
-        ph[j] = hi;
-        pl[j] = lo;
+        if constexpr (PACK) {
+            ph[j] = c16 >= 8 ? lo : hi;
+        } else {
+            ph[j] = hi;
+            pl[j] = lo;
+        }
     }
     l_sum += psum;
 
@@ -233,20 +254,22 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
         const int c = lane + 64 * r;
         u32x4 v = T.v[r];
         if (partial && p0 + c / G::RC >= end) v = u32x4{0u, 0u, 0u, 0u};
-        *(u32x4*)(vlds + (c / G::RC) * G::VROW + (c % G::RC) * 16) = v;
+        *(u32x4*)(vlds + (c / G::RC) * G::VROW + ((c % G::RC) ^ vswz<D>(c / G::RC)) * 16) = v;
     }
     __builtin_amdgcn_wave_barrier();
     // O^T += V^T . P^T; k-slot (g, j) <-> tile row 4g + j (j < 4), 16 + 4g + j - 4 (j >= 4).
     // ds_read_b64_tr_b16: within each 16-lane group, lane i reads 4 halves at row
     // base + i/4, columns c0 + 4*(i%4); lane j then holds column c0 + j of those 4 rows.
+    // Halves dt*16 + 4 (c16 & 3) are chunk 2 dt + (c16 & 3) / 2, byte 8 (c16 & 1) inside it.
+    const int r_lo = 4 * g + (c16 >> 2), r_hi = 16 + r_lo;
 #pragma unroll
     for (int dt = 0; dt < G::DT; dt++) {
-        const int col = dt * 16 + 4 * (c16 & 3);
-        const f16x4 lo4 = lds_read_tr16(vlds + (4 * g + (c16 >> 2)) * G::VROW + col * 2);
-        const f16x4 hi4 = lds_read_tr16(vlds + (16 + 4 * g + (c16 >> 2)) * G::VROW + col * 2);
+        const int ch = 2 * dt + ((c16 & 3) >> 1);
+        const f16x4 lo4 = lds_read_tr16(vlds + r_lo * G::VROW + (ch ^ vswz<D>(r_lo)) * 16 + 8 * (c16 & 1));
+        const f16x4 hi4 = lds_read_tr16(vlds + r_hi * G::VROW + (ch ^ vswz<D>(r_hi)) * 16 + 8 * (c16 & 1));
         const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
         O[dt] = mfma_16x16x32(a, ph, O[dt]);
-        O[dt] = mfma_16x16x32(a, pl, O[dt]);
+        if constexpr (!PACK) O[dt] = mfma_16x16x32(a, pl, O[dt]);
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -280,7 +303,7 @@ __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float i
     return pos * freq_scale * inv;
 }
 
-template <int D, bool FUSED, bool PAGED>
+template <int D, bool FUSED, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, RopeTable table) {
     using G = Geo<D>;
     constexpr int KK = G::KK, DT = G::DT;
@@ -375,7 +398,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
         if (n < NS) *(float4*)&s_q[n][(i % (D / 4)) * 4] = k == 0 ? qv0 : qv1;
     }
     f16x8 qh[KK], ql[KK];
-    const int qn_row = c16 < NS ? c16 : 0;
+    const int hcol = PACK ? (c16 & 7) : c16;  // head of this lane's MFMA column
+    const int qn_row = hcol < NS ? hcol : 0;
     // Fused: the wavefront that owns the tile holding the new position
     // normalises, rotates and appends the new k row itself (no extra barrier).
     const int new_wave = has_new ? (int)(((newpos - start) / kTile) % kWaves) : -1;
@@ -472,9 +496,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             _Float16 hi, lo;
-            split_f16(c16 < NS ? x[kk][j] : 0.0f, hi, lo);
-            qh[kk][j] = hi;
-            ql[kk][j] = lo;
+            split_f16(hcol < NS ? x[kk][j] : 0.0f, hi, lo);
+            if constexpr (PACK) {
+                qh[kk][j] = c16 >= 8 ? lo : hi;
+            } else {
+                qh[kk][j] = hi;
+                ql[kk][j] = lo;
+            }
         }
 
     // ---- 4. main loop: prefetch one tile ahead, two register sets
@@ -495,27 +523,35 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
             uint32_t nx = it + kWaves;
             uint32_t p0 = start + it * kTile;
             if (nx >= n_tiles) {
-                compute_tile<D, FUSED>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
                                        s_vnew, p.scale_log2, first);
                 break;
             }
             issue_tile<D, PAGED>(TB, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
-            compute_tile<D, FUSED>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+            compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
                                    s_vnew, p.scale_log2, first);
             first = false;
             it = nx;
             nx = it + kWaves;
             p0 = start + it * kTile;
             if (nx >= n_tiles) {
-                compute_tile<D, FUSED>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                compute_tile<D, FUSED, PACK>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
                                        s_vnew, p.scale_log2, false);
                 break;
             }
             issue_tile<D, PAGED>(TA, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
-            compute_tile<D, FUSED>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+            compute_tile<D, FUSED, PACK>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
                                    s_vnew, p.scale_log2, false);
             it = nx;
         }
+    }
+
+    // packed: columns c16 and c16 ^ 8 hold the hi and lo parts of one head
+    if constexpr (PACK) {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) O[dt][i] += dpp_mov<0x128>(O[dt][i]);
     }
 
     // ---- 5. combine the wavefronts, then write the partial (or the output)
@@ -605,19 +641,32 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     if (lane == 0) *(float4*)(p.out + qi * D + d0) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
 }
 
+template <int D, bool PACK>
+void launch_split(ds5_hip_ctx* ctx, bool fused, bool paged, const DecodeParams& prm, const RopeTable& tab, dim3 grid) {
+    const dim3 block(kThreads);
+    if (fused && paged)
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, true, PACK>), grid, block, 0, ctx->stream,
+                         prm, tab);
+    else if (fused)
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, false, PACK>), grid, block, 0, ctx->stream,
+                         prm, tab);
+    else if (paged)
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, true, PACK>), grid, block, 0, ctx->stream,
+                         prm, tab);
+    else
+        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, false, PACK>), grid, block, 0,
+                         ctx->stream, prm, tab);
+}
+
 template <int D>
 int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams& prm, dim3 grid) {
-    const dim3 block(kThreads);
     const bool paged = a.page_table != nullptr;
     const RopeTable& tab = a.fused ? *a.table : RopeTable{};
-    if (a.fused && paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, true>), grid, block, 0, ctx->stream, prm, tab);
-    else if (a.fused)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, false>), grid, block, 0, ctx->stream, prm, tab);
-    else if (paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, true>), grid, block, 0, ctx->stream, prm, tab);
+    // groups of at most 8 heads use the packed hi/lo columns (half the products)
+    if (prm.group <= kHeads / 2)
+        launch_split<D, true>(ctx, a.fused, paged, prm, tab, grid);
     else
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, false>), grid, block, 0, ctx->stream, prm, tab);
+        launch_split<D, false>(ctx, a.fused, paged, prm, tab, grid);
     int rc = ds5_after_launch(ctx, "decode_split_kernel");
     if (rc || prm.n_splits == 1) return rc;
     DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", decode_merge_kernel<D>, dim3(a.n_seqs * a.n_q_heads, D / 16), dim3(256), 0,
