@@ -148,6 +148,9 @@ def test_step_and_paged_preconditions(hip):
     bad = hip.PagedDecodeArgs.from_buffer_copy(pg)
     bad.head_dim = 96
     assert rc_of(hip, "ds5_hip_paged_decode", bad) == 1
+    bad = hip.PagedDecodeArgs.from_buffer_copy(pg)
+    bad.page_size = 8  # a 16-position half tile must not straddle pages
+    assert rc_of(hip, "ds5_hip_paged_decode", bad) == 1
 
 
 def test_rope_table_is_the_oracle_pow(hip, oracle):

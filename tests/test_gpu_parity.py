@@ -59,6 +59,21 @@ def test_rmsnorm_fixtures_bit_exact(ctx, hip, oracle, i):
     assert np.array_equal(got, oracle.rms_norm(x, w, p["eps"], p["n_rows"], p["dim"]))
 
 
+@pytest.mark.parametrize("dim,scale", [(128, 1.0), (64, 1e-3), (128, 3e4), (4, 1.0)])
+def test_rmsnorm_random_rows_bit_exact(ctx, hip, oracle, dim, scale):
+    """rmsNorm over 5000 seeded rows of widely varying magnitude, bit-identical to
+    the oracle (the scale 1/sqrt(mean + eps) must be correctly rounded)."""
+    g = np.random.default_rng(dim + int(scale))
+    n = 5000
+    x = (g.standard_normal((n, dim)) * scale * np.exp(g.uniform(-4, 4, (n, 1)))).astype(np.float32)
+    w = (1.0 + 0.02 * g.standard_normal(dim)).astype(np.float32)
+    xb, out = dev(ctx, x), ctx.createBuffer(x.nbytes)
+    hip.rmsNorm(ctx, hip.RmsNormArgs(xb, dev(ctx, w), out, n, dim, 1e-6))
+    got = ctx.to_numpy(out, np.float32, x.shape)
+    want = oracle.rms_norm(x, w, 1e-6, n, dim)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("i", range(3))
 def test_rope_fixtures(ctx, hip, oracle, i):
     c = _cases(oracle, "rope")[i]
@@ -384,6 +399,40 @@ def test_paged_decode_small(ctx, hip, oracle):
 
 def test_paged_decode_config4_geometry(ctx, hip, oracle):
     _paged_case(ctx, hip, oracle, 32, 512, 16384, seed=0, check_seqs=(0, 13, 31))
+
+
+def test_paged_decode_invalid_entries(ctx, hip, oracle):
+    """Device-side entries the host cannot check: a page id outside the pool and
+    sequence lengths outside [1, max_seq_len] are never dereferenced; those
+    sequences' outputs are NaN, every other sequence is unaffected."""
+    s = synth.Shape()
+    n_seqs, hq, hkv, hd = 5, s.n_q_heads, s.n_kv_heads, s.head_dim
+    lay = synth.paged_layout(n_seqs, 40, 300, 16, seed=11)
+    slots = lay.n_pages * 16
+    g = np.random.default_rng(11)
+    kpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
+    vpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
+    q, k, v, qn, kn = synth.step_inputs(4, 11, n_seqs, s)
+    max_len = int(lay.seq_lens.max())
+    table, lens = lay.page_table.copy(), lay.seq_lens.copy()
+    table[1, 0] = lay.n_pages + 3          # page outside the pool
+    lens[2] = 0                            # empty sequence
+    lens[3] = max_len + 1                  # longer than max_seq_len
+    out = ctx.createBuffer(n_seqs * hq * hd * 4)
+    hip.pagedDecode(ctx, hip.PagedDecodeArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), dev(ctx, qn), dev(ctx, kn),
+                                             dev(ctx, kpool), dev(ctx, vpool), dev(ctx, table), dev(ctx, lens), out,
+                                             n_seqs, hq, hkv, hd, 16, lay.n_pages, lay.max_pages, max_len, s.eps,
+                                             s.theta, 1.0, s.scale))
+    got = ctx.to_numpy(out, np.float32).reshape(n_seqs, hq * hd)
+    for b in (1, 2, 3):
+        assert np.all(np.isnan(got[b])), b
+    for b in (0, 4):
+        L = int(lens[b])
+        kc = oracle.paged_gather_f16(kpool, table[b], 16, L)
+        vc = oracle.paged_gather_f16(vpool, table[b], 16, L)
+        wout, _, _ = _oracle_step(oracle, q[b:b + 1], k[b:b + 1], v[b:b + 1], qn, kn, np.array([L - 1], np.int32),
+                                  kc, vc, L - 1, s)
+        check_out(got[b], wout)
 
 
 # ---------------------------------------------------------------------------
