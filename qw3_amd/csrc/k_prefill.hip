@@ -199,9 +199,21 @@ template <int D>
 struct PGeo {
     static constexpr int KS = D / 16;              // k-steps of the S product
     static constexpr int DT = D / 32;              // 32-row blocks of O^T
-    static constexpr int RB = D * 2;               // bytes per K / V row in LDS (unpadded, chunk-swizzled)
-    static constexpr int STAGE = kKTile * RB;      // bytes per K (or V) stage
-    static constexpr int CPT = STAGE / 1024 / kHeads;  // 1 KiB direct-to-LDS loads per wavefront per stage
+    static constexpr int RB = D * 2;               // data bytes per cache row
+    // LDS row strides, padded so the two read patterns are bank-conflict free
+    // on the 64-bank LDS (256 bytes = 16 chunk slots per cycle): the S-operand
+    // read puts 16 consecutive K rows at one chunk in a cycle, so the K stride
+    // is 1 (mod 16) chunks; the V transpose read puts 4 consecutive rows x 4
+    // adjacent chunks in a cycle, so the V stride is 4 (mod 16) chunks. Every
+    // read address is then a per-lane base plus an immediate.
+    static constexpr int RSK = RB + 16;
+    static constexpr int RSV = RB + 64;
+    static constexpr int KSTAGE = kKTile * RSK;    // bytes per K stage
+    static constexpr int VSTAGE = kKTile * RSV;    // bytes per V stage
+    static constexpr int NBK = KSTAGE / 1024, NBV = VSTAGE / 1024;  // 1 KiB direct-to-LDS loads per stage
+    static_assert(KSTAGE % 1024 == 0 && VSTAGE % 1024 == 0, "stages are whole 1 KiB loads");
+    static constexpr int BK = (NBK + kHeads - 1) / kHeads, BV = (NBV + kHeads - 1) / kHeads;  // per wavefront
+    static constexpr int SET_BYTES = 2 * (KSTAGE + VSTAGE);  // double-buffered K and V of one wavefront set
 };
 
 __device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_ptr) {
@@ -235,58 +247,51 @@ __device__ __forceinline__ float sum_xor32(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// LDS rows are unpadded; the 16-byte chunk c of row r sits in slot c ^ swz(r).
-// The LDS serves 256 bytes (64 banks) per cycle: 16 lanes of a 16-byte read, 32
-// of an 8-byte one. The S operand read puts 16 consecutive rows at one chunk
-// in a cycle, the V transpose read 4 consecutive rows x 4 adjacent chunks
-// (aligned to 4); swz makes both hit 16 distinct 16-byte bank groups.
-//   D = 128 (256-byte rows, one per bank period): swz(r) = 4 (r % 4) + (r / 4) % 4,
-//     a permutation of r % 16 whose high two bits separate any 4 consecutive rows.
-//   D = 64 (128-byte rows, two per period): rows of equal parity share a period
-//     half, so swz(r) = 4 ((r / 2) % 2) + (r / 4) % 4 permutes r / 2 % 8 and
-//     separates rows 4a and 4a + 2.
-template <int D>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (D == 128) return 4 * (r & 3) + ((r >> 2) & 3);
-    else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
-}
-
-// Direct-to-LDS loads of the 64 K (or V) rows starting at key0 into one stage.
-// Load u of this wavefront fills bytes [1024 (wave CPT + u), +1024) of the
-// stage, lane L the 16 bytes at +16 L, i.e. row r = byte / RB, slot s; it
-// fetches chunk s ^ swz(r) of cache row key0 + r (rows past kv_end are clamped
-// to kv_end - 1: valid memory, weighted 0). DmaLane holds the lane's rows and
-// chunk offsets; the LDS destination is wave-uniform.
-template <int D>
-struct DmaLane {
-    uint32_t row[PGeo<D>::CPT];
-    uint32_t col[PGeo<D>::CPT];  // halves
-    __device__ __forceinline__ DmaLane(int wave, int lane) {
-        using G = PGeo<D>;
+// Direct-to-LDS loads of the 64 K (or V) rows starting at key0 into one stage
+// with row stride RS. Load b fills stage bytes [1024 b, +1024), lane L the 16
+// bytes at 1024 b + 16 L: row r, chunk slot c of that row, or the row padding
+// (such a lane re-reads the row's first chunk; the padding is never read).
+// Loads b = wave, wave + 4, ... are this wavefront's. DmaPlan keeps the lane's
+// byte offset inside the tile for each of its loads: whole tiles (all 64 rows
+// below kv_end) are fetched with a scalar tile base plus that offset; the last
+// tile clamps rows past kv_end to kv_end - 1 (valid memory, weighted 0).
+template <int D, int RS, int B>
+struct DmaPlan {
+    uint32_t off[B];
+    __device__ __forceinline__ DmaPlan(int wave, int lane) {
 #pragma unroll
-        for (int u = 0; u < G::CPT; u++) {
-            const int byte = 1024 * (wave * G::CPT + u) + 16 * lane;
-            const int r = byte / G::RB, slot = (byte % G::RB) / 16;
-            row[u] = (uint32_t)r;
-            col[u] = (uint32_t)(8 * (slot ^ swz<D>(r)));
+        for (int i = 0; i < B; i++) {
+            const int pos = 1024 * (wave + kHeads * i) + 16 * lane;
+            const int r = pos / RS, c = (pos % RS) / 16;
+            off[i] = (uint32_t)(r * 2 * D + (c < D / 8 ? 16 * c : 0));
         }
     }
 };
 
-template <int D>
+template <int D, int RS, int B>
 __device__ __forceinline__ void dma_tile(uint32_t stage_lds, const f16* base, uint32_t key0, uint32_t kv_end,
-                                         const DmaLane<D>& dl, int wave) {
-    using G = PGeo<D>;
+                                         const DmaPlan<D, RS, B>& dp, int wave, int lane) {
+    constexpr int NB = kKTile * RS / 1024;
+    const char* tile = (const char*)(base + (uint64_t)key0 * D);
+    const bool whole = key0 + kKTile <= kv_end;  // uniform
 #pragma unroll
-    for (int u = 0; u < G::CPT; u++) {
-        const uint32_t key = min(key0 + dl.row[u], kv_end - 1);
-        const f16* src = base + (uint64_t)key * D + dl.col[u];
+    for (int i = 0; i < B; i++) {
+        const int b = wave + kHeads * i;
+        if (B * kHeads > NB && b >= NB) break;  // uniform: this wavefront has fewer loads
+        const uint32_t lds = stage_lds + 1024 * b;
         // Issued as inline asm: the compiler would otherwise make every later
         // LDS read wait for all such loads (it cannot tell the stages apart).
         // Completion is awaited explicitly (wait_vm) before the barrier that
         // publishes a stage.
-        const uint32_t lds = stage_lds + 1024 * (wave * G::CPT + u);
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
+        if (whole) {
+            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(dp.off[i]), "s"(tile), "s"(lds)
+                         : "m0");
+        } else {
+            const uint32_t r = dp.off[i] / (2 * D), col = dp.off[i] % (2 * D);
+            const uint32_t key = min(key0 + r, kv_end - 1);
+            const char* src = (const char*)(base + (uint64_t)key * D) + col;
+            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
+        }
     }
 }
 
@@ -297,9 +302,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
-    constexpr int KS = G::KS, DT = G::DT, RB = G::RB;
-    // LDS: K stages [set][2] then V stages [set][2]; reused by the set merge
-    __shared__ __attribute__((aligned(1024))) char s_kv[2 * kSets * 2 * G::STAGE];
+    constexpr int KS = G::KS, DT = G::DT, RSK = G::RSK, RSV = G::RSV;
+    // LDS: per set, K stages 0 and 1 then V stages 0 and 1; reused by the set merge
+    __shared__ __attribute__((aligned(1024))) char s_kv[kSets * G::SET_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -318,31 +323,19 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const f16* kc = p.k_cache + (uint64_t)kvh * p.max_ctx * D;
     const f16* vc = p.v_cache + (uint64_t)kvh * p.max_ctx * D;
     // this set's stages
-    char* const k_st = s_kv + set * 2 * G::STAGE;
-    char* const v_st = s_kv + (kSets + set) * 2 * G::STAGE;
+    char* const k_st = s_kv + set * G::SET_BYTES;
+    char* const v_st = k_st + 2 * G::KSTAGE;
     const uint32_t k_lds = lds_addr(k_st), v_lds = lds_addr(v_st);
 
-    // Per-lane LDS byte offsets. S operand of k-step ks: row 32 kh + r32, chunk
-    // 2 ks + h (swz of row 32 kh + r32 equals swz(r32)).
-    int kofs[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) kofs[ks] = r32 * RB + 16 * ((2 * ks + h) ^ swz<D>(r32));
-    // V transpose read: lane i16 of group g16 reads row 16 m + 4 hh + i16 / 4 (+ 8 for
-    // the upper half), halves dt*32 + 16 (g16 & 1) + 4 (i16 & 3): chunk
-    // 4 dt + 2 (g16 & 1) + (i16 & 3) / 2, byte 8 (i16 & 1) inside it. 16 m leaves
-    // swz unchanged, so the offsets depend on (dt, half) only.
-    int vofs[2][DT];
-    {
-        const int hh = g16 >> 1;
-        const int v_c = 2 * (g16 & 1) + ((i16 & 3) >> 1);
-#pragma unroll
-        for (int hi = 0; hi < 2; hi++) {
-            const int row = 8 * hi + 4 * hh + (i16 >> 2);
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) vofs[hi][dt] = row * RB + 8 * (i16 & 1) + 16 * ((4 * dt + v_c) ^ swz<D>(row));
-        }
-    }
-    const DmaLane<D> dl(hw, lane);
+    // Per-lane LDS byte bases; every read adds an immediate. S operand of
+    // (half kh, k-step ks): row 32 kh + r32, bytes 32 ks + 16 h of the row.
+    const int kb = r32 * RSK + 16 * h;
+    // V transpose read of (key step m, dim block dt, upper half hi): lane i16 of
+    // group g16 reads row 16 m + 8 hi + 4 hh + i16 / 4, halves dt*32 + 16 (g16 & 1)
+    // + 4 (i16 & 3), i.e. bytes 64 dt + 32 (g16 & 1) + 8 (i16 & 3) of the row.
+    const int vb = (4 * (g16 >> 1) + (i16 >> 2)) * RSV + 32 * (g16 & 1) + 8 * (i16 & 3);
+    const DmaPlan<D, RSK, G::BK> dk(hw, lane);
+    const DmaPlan<D, RSV, G::BV> dv(hw, lane);
 
     const uint32_t heavy = p.n_qtiles - 1 - pair;
     for (int sel = 0; sel < 2; sel++) {
@@ -364,8 +357,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         f16x8 qop[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qop[ks] = *(const f16x8*)(qrow + 16 * ks);
-        dma_tile<D>(k_lds, kc, set * kKTile, kv_end, dl, hw);
-        dma_tile<D>(v_lds, vc, set * kKTile, kv_end, dl, hw);
+        dma_tile(k_lds, kc, set * kKTile, kv_end, dk, hw, lane);
+        dma_tile(v_lds, vc, set * kKTile, kv_end, dv, hw, lane);
         if (!keep) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
@@ -385,13 +378,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         // was last read in round r - 1, before the previous barrier).
         for (uint32_t r = 0; r < n_rounds; r++) {
             const uint32_t j = 2 * r + set;
-            const uint32_t cur = (r & 1) * G::STAGE, nxt = G::STAGE - cur;
+            const uint32_t kcur = (r & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
+            const uint32_t vcur = (r & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
             // The next tile's loads are issued in two halves inside the round (a
             // burst from all eight wavefronts right after the barrier would stall
             // their issue); with no tile this round there is none next round.
             if (j < n_kt) {
                 const uint32_t key0 = j * kKTile;
-                const char* sk = k_st + cur;
+                const char* sk = k_st + kcur + kb;
                 f32x16 S[2];  // S^T of the tile's two 32-key halves
 #pragma unroll
                 for (int kh = 0; kh < 2; kh++) {
@@ -399,11 +393,11 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                     for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
 #pragma unroll
                     for (int ks = 0; ks < KS; ks++) {
-                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RB + kofs[ks]);
+                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RSK + 32 * ks);
                         S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
                     }
                 }
-                dma_tile<D>(k_lds + nxt, kc, (j + 2) * kKTile, kv_end, dl, hw);
+                dma_tile(k_lds + knxt, kc, (j + 2) * kKTile, kv_end, dk, hw, lane);
                 // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
                 if (j >= n_full) {  // causal mask on tiles that reach past the first row
 #pragma unroll
@@ -445,17 +439,17 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
 #pragma unroll
                     for (int e = 0; e < 4; e++) l_sum = __builtin_amdgcn_fdot2(pr.v[e], ones, l_sum, false);
                 }
-                dma_tile<D>(v_lds + nxt, vc, (j + 2) * kKTile, kv_end, dl, hw);
+                dma_tile(v_lds + vnxt, vc, (j + 2) * kKTile, kv_end, dv, hw, lane);
                 // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
                 // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
                 // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
-                const char* sv = v_st + cur;
+                const char* sv = v_st + vcur + vb;
 #pragma unroll
                 for (int m = 0; m < 4; m++)
 #pragma unroll
                     for (int dt = 0; dt < DT; dt++) {
-                        const f16x4 lo = lds_read_tr16(sv + vofs[0][dt] + 16 * m * RB);
-                        const f16x4 hi = lds_read_tr16(sv + vofs[1][dt] + 16 * m * RB);
+                        const f16x4 lo = lds_read_tr16(sv + 16 * m * RSV + 64 * dt);
+                        const f16x4 hi = lds_read_tr16(sv + (16 * m + 8) * RSV + 64 * dt);
                         const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                         O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
                     }
