@@ -272,13 +272,20 @@ template <int D, int RS, int B>
 __device__ __forceinline__ void dma_tile(uint32_t stage_lds, const f16* base, uint32_t key0, uint32_t kv_end,
                                          const DmaPlan<D, RS, B>& dp, int wave, int lane) {
     constexpr int NB = kKTile * RS / 1024;
-    const char* tile = (const char*)(base + (uint64_t)key0 * D);
+    // wave-uniform operands made explicitly scalar (else the compiler wraps each
+    // asm statement in a loop over the distinct lane values)
+    // (readfirstlane returns int: each half goes through uint32_t so that the low
+    // half is zero-extended, not sign-extended, when the pointer is rebuilt)
+    const uint64_t tb = (uint64_t)(base + (uint64_t)key0 * D);
+    const uint32_t tb_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(tb >> 32));
+    const uint32_t tb_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)tb);
+    const uint64_t tile = ((uint64_t)tb_hi << 32) | (uint64_t)tb_lo;
     const bool whole = key0 + kKTile <= kv_end;  // uniform
 #pragma unroll
     for (int i = 0; i < B; i++) {
         const int b = wave + kHeads * i;
         if (B * kHeads > NB && b >= NB) break;  // uniform: this wavefront has fewer loads
-        const uint32_t lds = stage_lds + 1024 * b;
+        const uint32_t lds = __builtin_amdgcn_readfirstlane(stage_lds + 1024 * b);
         // Issued as inline asm: the compiler would otherwise make every later
         // LDS read wait for all such loads (it cannot tell the stages apart).
         // Completion is awaited explicitly (wait_vm) before the barrier that
