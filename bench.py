@@ -290,10 +290,10 @@ def main():
         e2e_us = elapsed / n_rep * 1e6
         ns_pf, _ = kernel_mean_ns(ctx, p, "prefill_attention_kernel", 5)
         tf = p.flops / ns_pf / 1e3
-        extra["C2_prefill"] = dict(prefill_kernel_us=round(ns_pf / 1e3, 3), tflops=round(tf, 2),
+        extra["C2_prefill"] = dict(kernel="prefill_attention_kernel", kernel_us=round(ns_pf / 1e3, 3), tflops=round(tf, 2),
                                    frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(e2e_us, 3),
                                    flops=p.flops, peak_tflops=F16_MFMA_PEAK_TFLOPS)
-        log(f"[bench] C2 prefill_kernel {ns_pf / 1e3:.2f} us -> {tf:.1f} TFLOP/s; end-to-end {e2e_us:.2f} us")
+        log(f"[bench] C2 prefill_attention_kernel {ns_pf / 1e3:.2f} us -> {tf:.1f} TFLOP/s; end-to-end {e2e_us:.2f} us")
         del p
 
     if "C3" in only:

@@ -7,7 +7,8 @@
 //   rope          kernels_a.zig:97-130  -> rope_kernel
 //   kvAppend      kernels_a.zig:169-217 -> kv_append_kernel
 //   gqaAttention  kernels_b.zig:29-133  -> decode_split_kernel (+ merge),
-//                                          prefill_kernel, or the generic kernel
+//                                          q_pack_kernel + prefill_attention_kernel,
+//                                          or the generic kernel
 #include <math.h>
 
 #include "ds5_common.hpp"
