@@ -274,15 +274,31 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
     __builtin_amdgcn_wave_barrier();
 }
 
-__device__ __forceinline__ float serial_sumsq(const float* row, int dim) {
+__device__ __forceinline__ float sq(float v) {
+#pragma clang fp contract(off)
+    return v * v;
+}
+
+// Sum of the D squares in index order with f32 rounding after each add -- the
+// reference's serial sum of squares (kernels_a.zig:85-86), the products having
+// been rounded on their own. Every lane reads the same LDS words (broadcast) and
+// computes the same sum; reads go in batches of eight 16-byte chunks.
+template <int D>
+__device__ __forceinline__ float serial_sum(const float* sq_row) {
 #pragma clang fp contract(off)
     float acc = 0.0f;
-    for (int i = 0; i < dim; i += 4) {
-        const float4 v = *(const float4*)(row + i);
-        acc += v.x * v.x;
-        acc += v.y * v.y;
-        acc += v.z * v.z;
-        acc += v.w * v.w;
+#pragma unroll
+    for (int b = 0; b < D / 32; b++) {
+        float4 c[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) c[j] = *(const float4*)(sq_row + 32 * b + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            acc += c[j].x;
+            acc += c[j].y;
+            acc += c[j].z;
+            acc += c[j].w;
+        }
     }
     return acc;
 }
@@ -307,11 +323,16 @@ template <int D, bool FUSED, bool PAGED, bool PACK>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, RopeTable table) {
     using G = Geo<D>;
     constexpr int KK = G::KK, DT = G::DT;
-    constexpr int V_BYTES = kWaves * kTile * G::VROW;
-    constexpr int O_BYTES = kWaves * kHeads * G::OROW * 4;
-    __shared__ __attribute__((aligned(16))) char s_big[V_BYTES > O_BYTES ? V_BYTES : O_BYTES];
+    // One area per wavefront: its V staging tile, later its O for the cross-wavefront
+    // combine (a wavefront overwrites only its own staging, so no barrier is needed
+    // between its last transpose read and its O writes).
+    constexpr int V_BYTES = kTile * G::VROW;
+    constexpr int O_BYTES = kHeads * G::OROW * 4;
+    constexpr int AREA = V_BYTES > O_BYTES ? V_BYTES : O_BYTES;
+    __shared__ __attribute__((aligned(16))) char s_big[kWaves * AREA];
     __shared__ __attribute__((aligned(16))) float s_q[kHeads][G::OROW];
     __shared__ __attribute__((aligned(16))) float s_krow[FUSED ? D : 4];
+    __shared__ __attribute__((aligned(16))) float s_ksq[FUSED ? D : 4];  // squares of the new k row
     __shared__ float s_qn[FUSED ? D : 1], s_kn[FUSED ? D : 1], s_cos[FUSED ? D / 2 : 1], s_sin[FUSED ? D / 2 : 1];
     __shared__ __attribute__((aligned(16))) f16 s_knew[FUSED ? D : 8];
     __shared__ __attribute__((aligned(16))) f16 s_vnew[FUSED ? D : 8];
@@ -410,6 +431,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
             s_qn[tid] = wq;
             if (has_new) {
                 s_krow[tid] = kr;
+                s_ksq[tid] = sq(kr);
                 s_kn[tid] = wk;
             }
         }
@@ -433,8 +455,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
             bool pbad = false;
             const uint64_t kslot = PAGED ? page_base(p, b, newpos, pbad) + newpos % p.page_size : newpos;
             bad |= pbad;
-            float kinv = lane == 0 ? rms_inv(serial_sumsq(s_krow, D), (float)D, p.eps) : 0.0f;
-            kinv = __shfl(kinv, 0, 64);
+            const float kinv = rms_inv(serial_sum<D>(s_ksq), (float)D, p.eps);
             for (int i = lane; i < D / 2; i += 64) {
                 const float x0 = norm_mul(s_krow[i], kinv, s_kn[i]);
                 const float x1 = norm_mul(s_krow[i + D / 2], kinv, s_kn[i + D / 2]);
@@ -510,7 +531,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -INFINITY, l_sum = 0.0f;
-    char* vlds = s_big + wave * kTile * G::VROW;
+    char* vlds = s_big + wave * AREA;
     auto new_row_of = [&](uint32_t p0) -> int {
         return (FUSED && has_new && newpos >= p0 && newpos < p0 + kTile) ? (int)(newpos - p0) : -1;
     };
@@ -556,8 +577,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 
     // ---- 5. combine the wavefronts, then write the partial (or the output)
     const float l_w = swap32_op(swap16_op(l_sum, OpAdd{}), OpAdd{});
-    __syncthreads();  // all wavefronts are done with their V staging areas
-    float* s_o = (float*)s_big;  // [kWaves][kHeads][OROW]
+    float* s_o = (float*)s_big;  // wavefront w's O: [w * AREA / 4 + head * OROW + dim]
     if (g == 0) {
         s_m[wave][c16] = m_ref;
         s_l[wave][c16] = l_w;
@@ -566,7 +586,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) s_o[(wave * kHeads + c16) * G::OROW + dt * 16 + 4 * g + i] = O[dt][i];
+        for (int i = 0; i < 4; i++) s_o[wave * (AREA / 4) + c16 * G::OROW + dt * 16 + 4 * g + i] = O[dt][i];
     __syncthreads();
 
     bool poison = false;
@@ -583,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
             const float f = fast_exp2(s_m[w][n] - M);  // 0 for a wavefront without tiles
-            const float4 o = *(const float4*)&s_o[(w * kHeads + n) * G::OROW + d0];
+            const float4 o = *(const float4*)&s_o[w * (AREA / 4) + n * G::OROW + d0];
             acc.x += o.x * f;
             acc.y += o.y * f;
             acc.z += o.z * f;

@@ -433,19 +433,18 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                 // tile is key tile 1) keeps m_ref = -inf; its weights are 0.
                 const float m_exp = m_ref == -INFINITY ? 0.0f : m_ref;
                 f16x8 pop[4];  // P^T operand of key step m: scores i = 8 (m % 2) + jj of half m / 2
+                // Row sum in f32 adds of the f32 weights: v_dot2 of the f16 weights would
+                // share the matrix core with the other wavefront's products on this SIMD.
+                float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int m = 0; m < 4; m++)
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) pop[m][jj] = (f16)fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
-                // row sum of the f16 weights, as the products use them
-                struct H4 { f16x2 v[4]; };
-                const f16x2 ones = {(f16)1.0f, (f16)1.0f};
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const H4 pr = __builtin_bit_cast(H4, pop[m]);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) l_sum = __builtin_amdgcn_fdot2(pr.v[e], ones, l_sum, false);
-                }
+                    for (int jj = 0; jj < 8; jj++) {
+                        const float e = fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
+                        pop[m][jj] = (f16)e;
+                        ps[m] += e;
+                    }
+                l_sum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
                 dma_tile(v_lds + vnxt, vc, (j + 2) * kKTile, kv_end, dv, hw, lane);
                 // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
                 // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
