@@ -319,7 +319,11 @@ __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float i
     return pos * freq_scale * inv;
 }
 
-template <int D, bool FUSED, bool PAGED, bool PACK>
+// ONE: every wavefront has at most one tile (chunk <= kWaves * kTile). That case
+// gets a kernel of its own without the prefetch loop: the loop's four tile
+// bodies double the code, and a decode launch is short enough for instruction
+// fetch to show in its duration.
+template <int D, bool FUSED, bool PAGED, bool PACK, bool ONE>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, RopeTable table) {
     using G = Geo<D>;
     constexpr int KK = G::KK, DT = G::DT;
@@ -538,7 +542,13 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     // Every compute path sees a fixed set of outstanding loads (the next tile's
     // or none), so the compiler's wait before a tile's first use never covers
     // the prefetch.
-    if (it < n_tiles) {
+    if constexpr (ONE) {
+        if (it < n_tiles) {
+            const uint32_t p0 = start + it * kTile;
+            compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
+                                         s_vnew, p.scale_log2, true);
+        }
+    } else if (it < n_tiles) {
         bool first = true;
         for (;;) {
             uint32_t nx = it + kWaves;
@@ -661,21 +671,22 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     if (lane == 0) *(float4*)(p.out + qi * D + d0) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
 }
 
-template <int D, bool PACK>
+template <int D, bool FUSED, bool PAGED, bool PACK, bool ONE>
+void launch_split_k(ds5_hip_ctx* ctx, const DecodeParams& prm, const RopeTable& tab, dim3 grid) {
+    DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, FUSED, PAGED, PACK, ONE>), grid, dim3(kThreads), 0,
+                     ctx->stream, prm, tab);
+}
+
+template <int D, bool PACK, bool ONE>
 void launch_split(ds5_hip_ctx* ctx, bool fused, bool paged, const DecodeParams& prm, const RopeTable& tab, dim3 grid) {
-    const dim3 block(kThreads);
     if (fused && paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, true, PACK>), grid, block, 0, ctx->stream,
-                         prm, tab);
+        launch_split_k<D, true, true, PACK, ONE>(ctx, prm, tab, grid);
     else if (fused)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, true, false, PACK>), grid, block, 0, ctx->stream,
-                         prm, tab);
+        launch_split_k<D, true, false, PACK, ONE>(ctx, prm, tab, grid);
     else if (paged)
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, true, PACK>), grid, block, 0, ctx->stream,
-                         prm, tab);
+        launch_split_k<D, false, true, PACK, ONE>(ctx, prm, tab, grid);
     else
-        DS5_TIMED_LAUNCH(ctx, "decode_split_kernel", (decode_split_kernel<D, false, false, PACK>), grid, block, 0,
-                         ctx->stream, prm, tab);
+        launch_split_k<D, false, false, PACK, ONE>(ctx, prm, tab, grid);
 }
 
 template <int D>
@@ -683,10 +694,15 @@ int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams&
     const bool paged = a.page_table != nullptr;
     const RopeTable& tab = a.fused ? *a.table : RopeTable{};
     // groups of at most 8 heads use the packed hi/lo columns (half the products)
-    if (prm.group <= kHeads / 2)
-        launch_split<D, true>(ctx, a.fused, paged, prm, tab, grid);
+    const bool pack = prm.group <= kHeads / 2, one = prm.chunk <= kWaves * kTile;
+    if (pack && one)
+        launch_split<D, true, true>(ctx, a.fused, paged, prm, tab, grid);
+    else if (pack)
+        launch_split<D, true, false>(ctx, a.fused, paged, prm, tab, grid);
+    else if (one)
+        launch_split<D, false, true>(ctx, a.fused, paged, prm, tab, grid);
     else
-        launch_split<D, false>(ctx, a.fused, paged, prm, tab, grid);
+        launch_split<D, false, false>(ctx, a.fused, paged, prm, tab, grid);
     int rc = ds5_after_launch(ctx, "decode_split_kernel");
     if (rc || prm.n_splits == 1) return rc;
     DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", decode_merge_kernel<D>, dim3(a.n_seqs * a.n_q_heads, D / 16), dim3(256), 0,
