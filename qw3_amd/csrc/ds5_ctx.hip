@@ -40,8 +40,16 @@ int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->workspace_bytes) {
         // A larger workspace is a new allocation; the old one stays owned by the
         // context until deinit, because enqueued kernels and captured graphs may
-        // still reference it.
-        int rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "workspace sync");
+        // still reference it. Growing it needs a synchronise and an allocation,
+        // neither of which a stream capture allows.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        int rc = ds5_hip_status(ctx, hipStreamIsCapturing(ctx->stream, &cap), "workspace capture query");
+        if (rc) return rc;
+        if (cap != hipStreamCaptureStatusNone)
+            return ds5_fail(ctx, DS5_DEVICE_FAILURE,
+                            "workspace must grow to %zu bytes during a stream capture: run the same call once "
+                            "before capturing it", bytes);
+        rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "workspace sync");
         if (rc) return rc;
         const size_t want = std::max<size_t>(bytes, 4u << 20);
         void* p = nullptr;

@@ -461,3 +461,72 @@ def test_config0_golden(ctx, hip, oracle, fused):
     out, gk, gv = _run_step(ctx, hip, q, k, v, L("q_norm"), L("k_norm"), L("positions"), kc, vc, 31, s, fused)
     check_cache(gk, gv, L("k_cache_out"), L("v_cache_out"), kc, vc, 31, 1)
     check_out(out, L("output"))
+
+
+# ---------------------------------------------------------------------------
+# graph capture: every replay equals the eager call
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind,T,cap,hd", [
+    ("decode", 1, 2048, 128),     # one tile per wavefront (16 splits + merge)
+    ("decode", 1, 16384, 128),    # two tiles per wavefront (prefetch loop)
+    ("prefill", 300, 307, 128),   # pre-pass + attention
+    ("prefill", 77, 84, 64),
+])
+def test_graph_replays_match_eager(ctx, hip, kind, T, cap, hd):
+    """The fused step captured into a HIP graph, replayed three times with eager
+    work and synchronisations between the replays: each replay's output is
+    bit-identical to the eager call's."""
+    s = synth.Shape(n_q_heads=32, n_kv_heads=4, head_dim=hd)
+    pos = cap - T if kind == "decode" else cap - T - 7
+    config = 1 if kind == "decode" else 2
+    q, k, v, qn, kn = synth.step_inputs(config, T, T, s, f16_exact=(kind == "prefill"))
+    kc, vc = synth.cache_f16(config, T, s, cap, pos)
+    positions = np.arange(pos, pos + T, dtype=np.int32)
+    bufs = [dev(ctx, a) for a in (q, k, v, qn, kn, positions, kc, vc)]
+    out, other = ctx.createBuffer(T * 32 * hd * 4), ctx.createBuffer(T * 32 * hd * 4)
+    args = lambda o: hip.AttentionStepArgs(*bufs, o, 1, pos, T, 32, 4, hd, cap, s.eps, s.theta, 1.0, s.scale)
+    hip.attentionStep(ctx, args(out))  # eager; also sizes the workspace before the capture
+    want = ctx.to_numpy(out, np.float32)
+    g = ctx.capture(lambda: hip.attentionStep(ctx, args(out)))
+    try:
+        zeros = np.zeros(T * 32 * hd, np.float32)
+        for r in range(3):
+            ctx.upload(out, 0, zeros)
+            hip.attentionStep(ctx, args(other))  # eager work between replays
+            ctx.submit()
+            g.launch()
+            ctx.submit()
+            got = ctx.to_numpy(out, np.float32)
+            print(f"  replay {r}: bit-identical={np.array_equal(got, want)}", flush=True)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(ctx.to_numpy(other, np.float32).view(np.uint32), want.view(np.uint32))
+    finally:
+        g.destroy()
+
+
+def test_capture_before_workspace_sized_fails_cleanly(hip):
+    """A call whose workspace would have to grow inside a stream capture fails with a
+    DeviceFailure that says to run it once first; the context stays usable."""
+    c = hip.Ctx.init(0)
+    try:
+        s = synth.Shape()
+        T, cap = 64, 64
+        q, k, v, qn, kn = synth.step_inputs(2, T, T, s, f16_exact=True)
+        kc, vc = synth.cache_f16(2, T, s, cap, 0)
+        bufs = [c.from_numpy(np.ascontiguousarray(a)) for a in (q, k, v, qn, kn, np.arange(T, dtype=np.int32), kc, vc)]
+        out = c.createBuffer(T * 32 * 128 * 4)
+        args = hip.AttentionStepArgs(*bufs, out, 1, 0, T, 32, 4, 128, cap, s.eps, s.theta, 1.0, s.scale)
+        with pytest.raises(hip.DeviceFailure, match="before capturing"):
+            c.capture(lambda: hip.attentionStep(c, args))
+        hip.attentionStep(c, args)  # eager: grows the workspace
+        eager = c.to_numpy(out, np.float32)
+        assert np.all(np.isfinite(eager))
+        g = c.capture(lambda: hip.attentionStep(c, args))
+        c.upload(out, 0, np.zeros_like(eager))
+        g.launch()
+        c.submit()
+        assert np.array_equal(c.to_numpy(out, np.float32).view(np.uint32), eager.view(np.uint32))
+        g.destroy()
+    finally:
+        c.deinit()
