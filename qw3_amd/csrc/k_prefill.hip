@@ -345,9 +345,23 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const DmaPlan<D, RSV, G::BV> dv(hw, lane);
 
     const uint32_t heavy = p.n_qtiles - 1 - pair;
+    const bool has_light = pair < heavy;  // the middle tile of an odd count is processed once
+    // Keys of the light q tile, and the stage parity its first round starts on for
+    // this set (its first tile is loaded during the heavy tile's last round).
+    const uint32_t kv_end_light = p.pos + min(p.n_tokens, pair * kQRows + kQRows);
+    const uint32_t n_kt_light = (kv_end_light + kKTile - 1) / kKTile;
+    const uint32_t n_kt_heavy = (p.pos + min(p.n_tokens, heavy * kQRows + kQRows) + kKTile - 1) / kKTile;
+    // Stage parity of set s's first round in q tile sel: 0 for the heavy tile; for the
+    // light tile, the stage its first tile was loaded into (the one after the heavy
+    // tile's last round of set s).
+    auto sb_of = [&](int sel, int s) -> uint32_t {
+        if (sel == 0) return 0;
+        const uint32_t rl = n_kt_heavy > (uint32_t)s ? (n_kt_heavy - 1 - s) / 2 : 0;
+        return (rl + 1) & 1;
+    };
     for (int sel = 0; sel < 2; sel++) {
         const uint32_t qt = sel == 0 ? heavy : pair;
-        if (sel == 1 && qt >= heavy) break;  // the middle tile of an odd count is processed once
+        if (sel == 1 && !has_light) break;
         const uint32_t q0 = qt * kQRows;
         const uint32_t t = q0 + r32;
         const uint32_t tc = min(t, p.n_tokens - 1);
@@ -357,6 +371,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         const uint32_t n_kt = (kv_end + kKTile - 1) / kKTile;
         const uint32_t n_full = (p.pos + q0 + 1) / kKTile;             // tiles with no masked key
         const uint32_t n_rounds = (n_kt + 1) / 2;                      // set s takes tiles 2 r + s
+        const uint32_t sb = sb_of(sel, set);
+        // in its last round the set loads the light tile's first tile (set 0: key tile 0, set 1: 1)
+        const bool prefetch_light = sel == 0 && has_light && (uint32_t)set < n_kt_light;
 
         // ---- q operand first (vmcnt retires in issue order), then the first tile.
         // lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
@@ -364,8 +381,10 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         f16x8 qop[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) qop[ks] = *(const f16x8*)(qrow + 16 * ks);
-        dma_tile(k_lds, kc, set * kKTile, kv_end, dk, hw, lane);
-        dma_tile(v_lds, vc, set * kKTile, kv_end, dv, hw, lane);
+        if (sel == 0) {  // the light tile's first tiles are already in LDS
+            dma_tile(k_lds, kc, set * kKTile, kv_end, dk, hw, lane);
+            dma_tile(v_lds, vc, set * kKTile, kv_end, dv, hw, lane);
+        }
         if (!keep) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
@@ -380,13 +399,18 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
 
         wait_vm<0>();
         lds_sync();
-        // Round r: this set's tile j = 2 r + set sits in its stage r % 2; the
+        // Round r: this set's tile j = 2 r + set sits in its stage (r + sb) % 2; the
         // tile of round r + 1 streams into the other stage meanwhile (that stage
-        // was last read in round r - 1, before the previous barrier).
+        // was last read in round r - 1, before the previous barrier). In the set's
+        // last round the other stage receives the light q tile's first tile instead.
         for (uint32_t r = 0; r < n_rounds; r++) {
             const uint32_t j = 2 * r + set;
-            const uint32_t kcur = (r & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
-            const uint32_t vcur = (r & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
+            const uint32_t kcur = ((r + sb) & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
+            const uint32_t vcur = ((r + sb) & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
+            const bool own_next = j + 2 < n_kt;
+            const bool load_next = own_next || prefetch_light;
+            const uint32_t nkey0 = own_next ? (j + 2) * kKTile : (uint32_t)set * kKTile;
+            const uint32_t nend = own_next ? kv_end : kv_end_light;
             // The next tile's loads are issued in two halves inside the round (a
             // burst from all eight wavefronts right after the barrier would stall
             // their issue); with no tile this round there is none next round.
@@ -404,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                         S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
                     }
                 }
-                dma_tile(k_lds + knxt, kc, (j + 2) * kKTile, kv_end, dk, hw, lane);
+                if (load_next) dma_tile(k_lds + knxt, kc, nkey0, nend, dk, hw, lane);
                 // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
                 if (j >= n_full) {  // causal mask on tiles that reach past the first row
 #pragma unroll
@@ -445,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                         ps[m] += e;
                     }
                 l_sum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-                dma_tile(v_lds + vnxt, vc, (j + 2) * kKTile, kv_end, dv, hw, lane);
+                if (load_next) dma_tile(v_lds + vnxt, vc, nkey0, nend, dv, hw, lane);
                 // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
                 // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
                 // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
@@ -464,9 +488,18 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             lds_sync();
         }
 
-        // ---- merge set 1 into set 0 through LDS: [head slot][float4 index][lane]
+        // ---- merge set 1 into set 0 through LDS: head slot hw uses a stage freed by
+        // the last round (slots 0, 1: set 0's K and V stages of its last round's
+        // parity; 2, 3: set 1's), so the light tile's prefetched stages stay intact.
+        // [float4 index][lane]
         constexpr int NV4 = DT * 4 + 1;  // O as float4s, then (m, l, -, -)
-        float4* mrg = (float4*)s_kv + hw * NV4 * 64 + lane;
+        static_assert(NV4 * 64 * 16 <= G::KSTAGE && G::KSTAGE <= G::VSTAGE, "a merge slot fits a stage");
+        const int ms = hw >> 1;  // set whose stage holds this slot
+        const uint32_t r_last_ms = n_kt > (uint32_t)ms ? (n_kt - 1 - ms) / 2 : 0;
+        const uint32_t lp_ms = (r_last_ms + sb_of(sel, ms)) & 1;
+        char* const slot = s_kv + ms * G::SET_BYTES +
+                           ((hw & 1) == 0 ? lp_ms * G::KSTAGE : 2 * G::KSTAGE + lp_ms * G::VSTAGE);
+        float4* mrg = (float4*)slot + lane;
         if (set == 1) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
@@ -497,7 +530,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                     }
             }
         }
-        lds_sync();  // the merge area is the next tile's stages
+        lds_sync();  // the merge slots are stages again for the light tile
     }
 }
 
