@@ -90,6 +90,32 @@ class DecodeSweep:
             self.H.attentionStep(self.ctx, a)
 
 
+class ProjSweep:
+    """The q/k/v projection of a decode step (the matmul before the attention path,
+    forward.zig:337-339): n_layers of x [1, hidden] . W^T with W Q8_0 [n_q_heads*d +
+    2*n_kv_heads*d, hidden]; distinct random weights per layer (the 256 MB MALL cannot
+    hold the sweep)."""
+
+    def __init__(self, H, ctx, layers=48, hidden=2048, hq=32, hkv=4, d=128, seed=7):
+        self.H, self.ctx, self.layers = H, ctx, layers
+        self.n, self.k = hq * d + 2 * hkv * d, hidden
+        nb = self.k // 32
+        g = np.random.default_rng(seed)
+        self.args = []
+        for _ in range(layers):
+            w = g.integers(0, 256, (self.n, nb, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
+            x = g.standard_normal((1, self.k)).astype(np.float32)
+            out = ctx.createBuffer(self.n * 4)
+            self.args.append(H.MatmulArgs(ctx.from_numpy(x), ctx.from_numpy(w.reshape(self.n, nb * 34)),
+                                          H.DTYPE_Q8_0, out, 1, self.n, self.k))
+        self.bytes_per_layer = self.n * nb * 34 + self.k * 4 + self.n * 4
+
+    def sweep(self):
+        for a in self.args:
+            self.H.matmul(self.ctx, a)
+
+
 class PagedSweep:
     """C4: n_layers of batched paged decode (32 sequences, 16-token pages)."""
 
@@ -220,7 +246,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="C1,C2,C3,C4", help="comma list of configs to run (C1 is the headline)")
+    ap.add_argument("--only", default="C1,C2,C3,C4,QKV",
+                    help="comma list of configs to run (C1 is the headline; QKV: the decode q/k/v projection)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -323,6 +350,20 @@ def main():
                                         bytes_per_layer=w.bytes_per_layer,
                                         total_tokens=int(w.lay.seq_lens.sum()))
         log(f"[bench] C4 {us:.3f} us/layer; kernel {ns_k / 1e3:.3f} us")
+        del w
+
+    if "QKV" in only:
+        log("[bench] QKV: decode q/k/v projection, Q8_0 [5120 x 2048], 48 layers")
+        w = ProjSweep(H, ctx)
+        stepsq = max(5, args.steps // 4)
+        elapsed, _ = time_graph(ctx, w, stepsq, 2)
+        us = elapsed / (w.layers * stepsq) * 1e6
+        ns_k, _ = kernel_mean_ns(ctx, w, "matmul_rows_kernel", 2)
+        extra["qkv_projection_decode"] = dict(
+            kernel="matmul_rows_kernel", us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
+            kernel_us=round(ns_k / 1e3, 3), kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),
+            bytes_per_layer=w.bytes_per_layer, shape="m 1, n 5120, k 2048, Q8_0")
+        log(f"[bench] QKV {us:.3f} us/layer ({w.bytes_per_layer / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us")
         del w
 
     if result is None:

@@ -12,8 +12,9 @@
  *      src/kernels/cpu/ctx.zig and src/metal/metal.zig implement;
  *   2. the kernel-provider ops of the attention path, replacing
  *      rmsNorm / rope / kvAppend / gqaAttention of contracts.assertKernelApi
- *      (src/shared/contracts.zig:358-367), plus fused and paged extensions
- *      that the engine may pick up with @hasDecl.
+ *      (src/shared/contracts.zig:358-367), plus the matmul of the projections
+ *      on either side of it, and fused and paged extensions that the engine
+ *      may pick up with @hasDecl.
  *
  * Status codes are contracts.KernelError (src/shared/contracts.zig:201-206):
  * every precondition the reference checks is checked here before any launch.
@@ -36,9 +37,10 @@ extern "C" {
 #define DS5_DEVICE_FAILURE 3    /* KernelError.DeviceFailure: any HIP error */
 #define DS5_OUT_OF_MEMORY 4     /* KernelError.OutOfMemory */
 
-/* ---- dtypes: contracts.zig:22-24 (GGML type ids) ------------------------ */
+/* ---- dtypes: contracts.zig:22-29 (GGML type ids) ------------------------ */
 #define DS5_DTYPE_F32 0u
 #define DS5_DTYPE_F16 1u
+#define DS5_DTYPE_Q8_0 8u /* 32-element blocks of 34 bytes: f16 scale, 32 x int8 (contracts.zig:57,74) */
 
 /* contracts.zig:210-214 `Buf = extern struct { handle, offset, len }`, 24 B.
  * handle = base of a device allocation owned by the context; offset and len
@@ -190,6 +192,27 @@ typedef struct ds5_attn_args {
     float scale; /* 1/sqrt(head_dim) in the engine (forward.zig:308) */
 } ds5_attn_args;
 int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* args);
+
+/* contracts.zig:242-250 MatmulArgs. out[m, n] = x[m, k] . W^T with W a
+ * GGUF-layout weight, n rows of k elements (ne = {k, n}): f32, or Q8_0 blocks
+ * (value = f32(f16 scale) * int8 q, contracts.zig:194). Replaces
+ * kernels_a.zig:136-163 matmul -- the q/k/v projections feeding the attention
+ * step (forward.zig:337-339) and the output projection after it (:416-418).
+ * Weight dtypes other than f32 / Q8_0 are UnsupportedDtype; k must be a
+ * positive multiple of the dtype's block (32 for Q8_0). Each output is the
+ * same dot product as the reference's serial one, summed as a fixed tree of
+ * per-block partial sums, so it agrees to rounding (the generic path, used for
+ * unaligned views or k > 8192, keeps the serial order and is bit-identical). */
+typedef struct ds5_matmul_args {
+    ds5_buf x;        /* f32 [m, k] */
+    ds5_buf w;        /* w_dtype: n rows of k elements */
+    uint32_t w_dtype; /* DS5_DTYPE_F32 or DS5_DTYPE_Q8_0 */
+    ds5_buf out;      /* f32 [m, n] */
+    uint32_t m;
+    uint32_t n;
+    uint32_t k;
+} ds5_matmul_args;
+int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* args);
 
 /* ========================================================================
  * 3. Fused extensions (optional decls; the engine uses them via @hasDecl)

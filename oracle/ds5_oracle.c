@@ -154,6 +154,47 @@ float ds5o_zig_powf(float x, float y) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* matmul -- kernels_a.zig:136-163: out[m, n] = x[m, k] . W^T, one serial    */
+/* f32 dot per (row, output) (dotRow, kernels_a.zig:39-62): f32 weights add */
+/* w*x in k order; Q8_0 adds (f32(scale) * f32(q)) * x block by block, in   */
+/* k order.                                                                 */
+/* ------------------------------------------------------------------------ */
+
+static float dot_row(const float* x, const uint8_t* row, uint32_t w_dtype, uint64_t k) {
+    float acc = 0.0f;
+    if (w_dtype == DS5O_F32) {
+        const float* w = (const float*)row;
+        for (uint64_t i = 0; i < k; i++) acc += w[i] * x[i];
+    } else { /* DS5O_Q8_0 */
+        for (uint64_t b = 0; b < k / 32; b++) {
+            const uint8_t* blk = row + b * 34;
+            const float scale = ds5o_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))); /* little endian */
+            const int8_t* qs = (const int8_t*)(blk + 2);
+            for (int i = 0; i < 32; i++) acc += (scale * (float)qs[i]) * x[b * 32 + i];
+        }
+    }
+    return acc;
+}
+
+int ds5o_matmul(const ds5o_matmul_args* a) {
+    if (a->w_dtype != DS5O_F32 && a->w_dtype != DS5O_Q8_0) return DS5O_UNSUPPORTED_DTYPE;
+    const uint64_t m = a->m, n = a->n, k = a->k;
+    const uint64_t block = a->w_dtype == DS5O_Q8_0 ? 32 : 1;
+    if (k == 0 || k % block != 0) return DS5O_SHAPE_MISMATCH;
+    if (a->x.len < m * k * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->out.len < m * n * 4) return DS5O_SHAPE_MISMATCH;
+    const uint64_t row_bytes = a->w_dtype == DS5O_Q8_0 ? k / 32 * 34 : k * 4;
+    if (a->w.len < n * row_bytes) return DS5O_SHAPE_MISMATCH;
+
+    const float* x = (const float*)view(a->x);
+    const uint8_t* w = (const uint8_t*)view(a->w);
+    float* out = (float*)view(a->out);
+    for (uint64_t mi = 0; mi < m; mi++)
+        for (uint64_t ni = 0; ni < n; ni++) out[mi * n + ni] = dot_row(x + mi * k, w + ni * row_bytes, a->w_dtype, k);
+    return DS5O_OK;
+}
+
+/* ------------------------------------------------------------------------ */
 /* rmsNorm -- kernels_a.zig:68-91                                            */
 /* ------------------------------------------------------------------------ */
 

@@ -13,6 +13,7 @@
  *   ds5o_rope           src/kernels/cpu/kernels_a.zig:97-130
  *   ds5o_kv_append      src/kernels/cpu/kernels_a.zig:169-217
  *   ds5o_gqa_attention  src/kernels/cpu/kernels_b.zig:29-133
+ *   ds5o_matmul         src/kernels/cpu/kernels_a.zig:136-163 (row dot :39-62)
  *
  * Argument structs mirror src/shared/contracts.zig:210-286 (Buf and the
  * RmsNorm/Rope/KvAppend/Attn args); buffer views honour offset and len as
@@ -40,8 +41,9 @@ enum {
     DS5O_OUT_OF_MEMORY = 4,
 };
 
-/* contracts.zig:22-24 Dtype ids (GGML type ids). */
-enum { DS5O_F32 = 0, DS5O_F16 = 1 };
+/* contracts.zig:22-29 Dtype ids (GGML type ids). Q8_0 blocks: 32 elements in 34
+ * bytes, an f16 scale then 32 int8 (contracts.zig:57,74); value = f32(scale) * q. */
+enum { DS5O_F32 = 0, DS5O_F16 = 1, DS5O_Q8_0 = 8 };
 
 /* contracts.zig:210-214 Buf: handle is a host pointer for this oracle. */
 typedef struct ds5o_buf {
@@ -49,6 +51,14 @@ typedef struct ds5o_buf {
     uint64_t offset;
     uint64_t len;
 } ds5o_buf;
+
+typedef struct ds5o_matmul_args { /* contracts.zig:242-250 MatmulArgs */
+    ds5o_buf x;       /* f32 [m, k] */
+    ds5o_buf w;       /* w_dtype: n rows of k elements (GGUF layout, ne = {k, n}) */
+    uint32_t w_dtype; /* DS5O_F32 or DS5O_Q8_0 */
+    ds5o_buf out;     /* f32 [m, n] */
+    uint32_t m, n, k;
+} ds5o_matmul_args;
 
 typedef struct ds5o_rms_norm_args { /* contracts.zig:218-225 */
     ds5o_buf x, weight, out;
@@ -75,6 +85,7 @@ typedef struct ds5o_attn_args { /* contracts.zig:272-286 */
     float scale;
 } ds5o_attn_args;
 
+int ds5o_matmul(const ds5o_matmul_args* a);
 int ds5o_rms_norm(const ds5o_rms_norm_args* a);
 int ds5o_rope(const ds5o_rope_args* a);
 int ds5o_kv_append(const ds5o_kv_append_args* a);

@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(HERE, "build", "libds5oracle.so")
 
 OK, SHAPE_MISMATCH, UNSUPPORTED_DTYPE, DEVICE_FAILURE, OUT_OF_MEMORY = 0, 1, 2, 3, 4
 F32, F16, I32 = 0, 1, 26
+Q8_0 = 8  # contracts.zig:29; 32-element blocks of 34 bytes (f16 scale, 32 x int8)
 ERRORS = {1: "ShapeMismatch", 2: "UnsupportedDtype", 3: "DeviceFailure", 4: "OutOfMemory"}
 
 
@@ -37,6 +38,11 @@ class KernelError(Exception):
 
 class Buf(C.Structure):
     _fields_ = [("handle", C.c_void_p), ("offset", C.c_uint64), ("len", C.c_uint64)]
+
+
+class MatmulArgs(C.Structure):  # contracts.zig:242-250
+    _fields_ = [("x", Buf), ("w", Buf), ("w_dtype", C.c_uint32), ("out", Buf),
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
 class RmsNormArgs(C.Structure):
@@ -86,7 +92,7 @@ def lib() -> C.CDLL:
         L = C.CDLL(LIB_PATH)
         for name, argt in (("ds5o_rms_norm", RmsNormArgs), ("ds5o_rope", RopeArgs),
                            ("ds5o_kv_append", KvAppendArgs), ("ds5o_gqa_attention", AttnArgs),
-                           ("ds5o_attention_step", StepArgs)):
+                           ("ds5o_attention_step", StepArgs), ("ds5o_matmul", MatmulArgs)):
             f = getattr(L, name)
             f.argtypes = [C.POINTER(argt)]
             f.restype = C.c_int
@@ -123,6 +129,44 @@ def _check(rc: int) -> None:
 # --------------------------------------------------------------------------
 # Op wrappers (reference semantics, f32 numpy in/out, f16 caches as uint16)
 # --------------------------------------------------------------------------
+
+def matmul(x: np.ndarray, w: np.ndarray, w_dtype: int, m: int, n: int, k: int) -> np.ndarray:
+    """out[m, n] = x[m, k] . W^T (kernels_a.zig:136-163). w: f32 [n, k], or the raw Q8_0
+    rows as uint8 [n, k / 32 * 34]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w)
+    out = np.empty((m, n), np.float32)
+    _check(lib().ds5o_matmul(MatmulArgs(buf(x), buf(w), w_dtype, buf(out), m, n, k)))
+    return out
+
+
+def q8_0_quantize(w: np.ndarray) -> np.ndarray:
+    """Q8_0 rows from f32 rows [n, k] (k a multiple of 32): per 32-element block the
+    scale d = f16(max|w| / 127) and q = round(w / d) clipped to [-127, 127]. Test-input
+    helper (quantising with the stored f16 scale); the reference only dequantises
+    (contracts.zig:194)."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    blocks = w.reshape(n, k // 32, 32)
+    amax = np.abs(blocks).max(axis=2, keepdims=True)
+    d = (amax / 127.0).astype(np.float16).astype(np.float32)
+    inv = np.where(d > 0, 1.0 / np.where(d > 0, d, 1.0), 0.0)
+    q = np.clip(np.rint(blocks * inv), -127, 127).astype(np.int8)
+    out = np.empty((n, k // 32, 34), np.uint8)
+    out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, k // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(n, k // 32 * 34)
+
+
+def q8_0_dequantize(rows: np.ndarray, k: int) -> np.ndarray:
+    """f32 [n, k] from Q8_0 rows: f32(f16 scale) * q, exactly (contracts.zig:194)."""
+    rows = np.ascontiguousarray(rows, np.uint8)
+    n = rows.shape[0]
+    blk = rows.reshape(n, k // 32, 34)
+    scale = blk[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    q = blk[:, :, 2:].copy().view(np.int8).astype(np.float32)
+    return (scale * q).reshape(n, k)
+
 
 def rms_norm(x: np.ndarray, w: np.ndarray, eps: float, n_rows: int | None = None,
              dim: int | None = None, out: np.ndarray | None = None) -> np.ndarray:
@@ -237,9 +281,17 @@ def load_ds5t(path: str) -> Tensor:
         raise ValueError("BadMagic")
     if version != 1:
         raise ValueError("BadVersion")
+    ne = (ne0, ne1, ne2, ne3)
+    if dtype == Q8_0:  # raw rows of 34-byte blocks: uint8 [rows, ne0 / 32 * 34]
+        if ne0 % 32 or n_dims != 2:
+            raise ValueError("SizeMismatch")
+        row_bytes = ne0 // 32 * 34
+        if row_bytes * ne1 != data_bytes or len(raw) < 64 + data_bytes:
+            raise ValueError("SizeMismatch")
+        arr = np.frombuffer(raw, dtype=np.uint8, count=data_bytes, offset=64).copy()
+        return Tensor(dtype, ne[:n_dims], arr.reshape(ne1, row_bytes))
     if dtype not in _NP_DTYPE:
         raise ValueError(f"BadDtype {dtype}")
-    ne = (ne0, ne1, ne2, ne3)
     n = ne0 * ne1 * ne2 * ne3
     itemsize = np.dtype(_NP_DTYPE[dtype]).itemsize
     if n * itemsize != data_bytes or len(raw) < 64 + data_bytes:

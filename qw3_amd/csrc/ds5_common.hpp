@@ -91,6 +91,18 @@ static inline void* ds5_ptr(ds5_buf b) { return (char*)b.handle + b.offset; }
 // ---------------------------------------------------------------------------
 // Launchers exported by the kernel files (preconditions already checked)
 // ---------------------------------------------------------------------------
+// Projection matmul (k_matmul.hip): out[m, n] = x[m, k] . W^T, W f32 or Q8_0 rows.
+struct MatmulLaunch {
+    const float* x;
+    const uint8_t* w;
+    bool q8;
+    float* out;
+    uint32_t m, n, k;
+};
+bool matmul_rows_supported(const MatmulLaunch& a, uintptr_t x_addr, uintptr_t out_addr, uintptr_t w_addr,
+                           uint64_t w_len);
+int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, bool rows_path);
+
 struct RmsNormLaunch {
     const float* x;
     const float* w;

@@ -129,6 +129,27 @@ int ds5_hip_rms_norm(ds5_hip_ctx* ctx, const ds5_rms_norm_args* a) {
     return launch_rms_norm(ctx, l);
 }
 
+// kernels_a.zig:136-150: dtype first, then k, then the three buffer sizes.
+int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const bool q8 = a->w_dtype == DS5_DTYPE_Q8_0;
+    if (!q8 && a->w_dtype != DS5_DTYPE_F32)
+        return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "matmul: w_dtype %u (f32 and q8_0 are supported)", a->w_dtype);
+    const uint64_t m = a->m, n = a->n, k = a->k;
+    if (k == 0 || k % (q8 ? 32 : 1) != 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: k = %u is not a positive multiple of the weight block", a->k);
+    if (!covers(a->x, m * k * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: x too small");
+    if (!covers(a->out, m * n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: out too small");
+    const uint64_t row_bytes = q8 ? k / 32 * 34 : k * 4;
+    if (!covers(a->w, n * row_bytes)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: w too small");
+    if (m == 0 || n == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), q8, (float*)ds5_ptr(a->out),
+                         a->m, a->n, a->k};
+    const bool rows = matmul_rows_supported(l, (uintptr_t)l.x, (uintptr_t)l.out, (uintptr_t)l.w, a->w.len);
+    return launch_matmul(ctx, l, rows);
+}
+
 int ds5_hip_rope(ds5_hip_ctx* ctx, const ds5_rope_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
     const uint64_t T = a->n_tokens, H = a->n_heads, hd = a->head_dim;

@@ -29,6 +29,7 @@ LIB_PATH = os.path.join(PKG, "libds5hip.so")
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
+DTYPE_Q8_0 = 8
 
 
 # ---------------------------------------------------------------------------
@@ -90,6 +91,11 @@ class KvAppendArgs(C.Structure):
                 ("head_dim", C.c_uint32), ("max_ctx", C.c_uint32)]
 
 
+class MatmulArgs(C.Structure):
+    _fields_ = [("x", Buf), ("w", Buf), ("w_dtype", C.c_uint32), ("out", Buf), ("m", C.c_uint32),
+                ("n", C.c_uint32), ("k", C.c_uint32)]
+
+
 class AttnArgs(C.Structure):
     _fields_ = [("q", Buf), ("k_cache", Buf), ("v_cache", Buf), ("kv_dtype", C.c_uint32), ("out", Buf),
                 ("pos", C.c_uint32), ("n_tokens", C.c_uint32), ("n_q_heads", C.c_uint32),
@@ -136,6 +142,7 @@ SIGNATURES = {
     "ds5_hip_rope": ([_P, C.POINTER(RopeArgs)], C.c_int),
     "ds5_hip_kv_append": ([_P, C.POINTER(KvAppendArgs)], C.c_int),
     "ds5_hip_gqa_attention": ([_P, C.POINTER(AttnArgs)], C.c_int),
+    "ds5_hip_matmul": ([_P, C.POINTER(MatmulArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
@@ -307,6 +314,11 @@ def kvAppend(ctx: Ctx, args: KvAppendArgs) -> None:
 
 def gqaAttention(ctx: Ctx, args: AttnArgs) -> None:
     ctx.check(LIB.ds5_hip_gqa_attention(ctx.handle, C.byref(args)))
+
+
+def matmul(ctx: Ctx, args: MatmulArgs) -> None:
+    """out[m, n] = x[m, k] . W^T, W f32 or Q8_0 rows (kernels_a.zig:136-163)."""
+    ctx.check(LIB.ds5_hip_matmul(ctx.handle, C.byref(args)))
 
 
 def attentionStep(ctx: Ctx, args: AttentionStepArgs) -> None:

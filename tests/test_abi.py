@@ -36,6 +36,7 @@ STRUCTS = {
     "ds5_buf": "Buf", "ds5_rms_norm_args": "RmsNormArgs", "ds5_rope_args": "RopeArgs",
     "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
     "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
+    "ds5_matmul_args": "MatmulArgs",
 }
 
 
@@ -81,6 +82,21 @@ def test_rms_norm_preconditions(hip):
     for bad in (hip.RmsNormArgs(B(64), B(16), B(64), 4, 0, 1e-6), hip.RmsNormArgs(B(60), B(16), B(64), 4, 4, 1e-6),
                 hip.RmsNormArgs(B(64), B(16), B(60), 4, 4, 1e-6), hip.RmsNormArgs(B(64), B(12), B(64), 4, 4, 1e-6)):
         assert rc_of(hip, "ds5_hip_rms_norm", bad) == 1
+
+
+def test_matmul_preconditions(hip):
+    """kernels_a.zig:138-150: unsupported weight dtype, then k, then buffer sizes."""
+    M = lambda x, w, dt, out, m, n, k: hip.MatmulArgs(B(x), B(w), dt, B(out), m, n, k)
+    q8 = hip.DTYPE_Q8_0
+    assert rc_of(hip, "ds5_hip_matmul", M(4 * 64, 2 * 68, q8, 8, 1, 2, 64)) == 3  # valid: no device
+    assert rc_of(hip, "ds5_hip_matmul", M(4 * 3, 4 * 6, hip.DTYPE_F32, 8, 1, 2, 3)) == 3  # f32: any k
+    assert rc_of(hip, "ds5_hip_matmul", M(0, 0, q8, 0, 0, 0, 64)) == 0  # empty product: nothing to do
+    for dt in (hip.DTYPE_F16, 12, 9):  # f16, q4_k, q8_1
+        assert rc_of(hip, "ds5_hip_matmul", M(4 * 64, 2 * 68, dt, 8, 1, 2, 64)) == 2
+    for bad in (M(4 * 64, 2 * 68, q8, 8, 1, 2, 0), M(4 * 64, 2 * 68, q8, 8, 1, 2, 48),
+                M(4 * 64 - 4, 2 * 68, q8, 8, 1, 2, 64), M(4 * 64, 2 * 68 - 1, q8, 8, 1, 2, 64),
+                M(4 * 64, 2 * 68, q8, 4, 1, 2, 64), M(4 * 3, 4 * 6 - 4, hip.DTYPE_F32, 8, 1, 2, 3)):
+        assert rc_of(hip, "ds5_hip_matmul", bad) == 1
 
 
 def test_rope_preconditions(hip):

@@ -530,3 +530,99 @@ def test_capture_before_workspace_sized_fails_cleanly(hip):
         g.destroy()
     finally:
         c.deinit()
+
+
+# ---------------------------------------------------------------------------
+# matmul (the projection step before the path): kernels_a.zig:136-163
+# ---------------------------------------------------------------------------
+
+def _gpu_matmul(ctx, hip, x, w, w_dtype, m, n, k, x_off=0, w_off=0, out_off=0, w_pad=0):
+    """Runs ds5_hip_matmul on views at the given byte offsets into fresh buffers."""
+    xb = ctx.createBuffer(x.nbytes + x_off)
+    wb = ctx.createBuffer(w.nbytes + w_off + w_pad)
+    ob = ctx.createBuffer(m * n * 4 + out_off)
+    ctx.upload(xb, x_off, np.ascontiguousarray(x))
+    ctx.upload(wb, w_off, np.ascontiguousarray(w))
+    view = lambda b, off, ln: hip.Buf(b.handle, b.offset + off, ln)
+    hip.matmul(ctx, hip.MatmulArgs(view(xb, x_off, x.nbytes), view(wb, w_off, w.nbytes + w_pad), w_dtype,
+                                   view(ob, out_off, m * n * 4), m, n, k))
+    return ctx.to_numpy(ob, np.float32, (m, n), offset=out_off)
+
+
+def _dot_bound(x, wf):
+    """|a - b| allowed between two f32 evaluations of x . W^T in different orders."""
+    return 1e-5 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T) + 1e-30
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_matmul_quant_fixtures(ctx, hip, oracle, i):
+    """kernels_a.zig:395-458 through the GPU: the case tolerance, and the oracle's
+    value within the reordering bound."""
+    c = _cases(oracle, "matmul_quant")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w, want = (_t(oracle, c, n) for n in ("input", "weight", "output"))
+    got = _gpu_matmul(ctx, hip, x, w, hip.DTYPE_Q8_0, p["m"], p["n"], p["k"])
+    r = oracle.compare(want, got, tol["atol"], tol["rtol"])
+    print(f"  fixture max_abs={r.max_abs_diff:.3e} max_rel={r.max_rel_diff:.3e}", flush=True)
+    assert r.passed, r
+    orc = oracle.matmul(x, w, oracle.Q8_0, p["m"], p["n"], p["k"])
+    assert np.all(np.abs(got - orc) <= _dot_bound(x, oracle.q8_0_dequantize(w, p["k"])))
+
+
+def test_matmul_f32_hand_case(ctx, hip):
+    """kernels_a.zig:524-553."""
+    x = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    w = np.array([[1, 0, 2], [0, -1, 1]], np.float32)
+    got = _gpu_matmul(ctx, hip, x, w, hip.DTYPE_F32, 2, 2, 3)
+    assert np.array_equal(got, np.array([[7, 1], [16, 1]], np.float32))
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1, 5120, 2048),   # decode q/k/v projection, Qwen3-30B-A3B (hidden 2048 -> 32*128 + 2*4*128)
+    (1, 2048, 4096),   # decode output projection (32*128 -> 2048)
+    (3, 301, 4096),    # two blocks per lane, a 2-token pass plus a 1-token pass
+    (2, 77, 8192),     # four blocks per lane
+    (17, 256, 256),    # fixture shape: 4-token passes and a remainder
+    (5, 33, 96),       # three blocks, odd row count
+])
+def test_matmul_q8_0_and_f32_vs_oracle(ctx, hip, oracle, m, n, k):
+    """Q8_0 rows and their dequantised f32 rows against the oracle, within the bound
+    for summing the same products in another order."""
+    g = np.random.default_rng(m * 7 + n + k)
+    rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32) * 0.05)
+    wf = oracle.q8_0_dequantize(rows, k)
+    x = g.standard_normal((m, k)).astype(np.float32)
+    bound = _dot_bound(x, wf)
+    for w, dt, odt in ((rows, hip.DTYPE_Q8_0, oracle.Q8_0), (wf, hip.DTYPE_F32, oracle.F32)):
+        got = _gpu_matmul(ctx, hip, x, w, dt, m, n, k)
+        want = oracle.matmul(x, w, odt, m, n, k)
+        err = np.abs(got - want)
+        print(f"  dtype {dt}: max |gpu - oracle| = {err.max():.3e} (bound {bound.min():.3e}..)", flush=True)
+        assert np.all(np.isfinite(got)) and np.all(err <= bound)
+
+
+@pytest.mark.parametrize("case", ["x_unaligned", "w_unaligned", "k_gt_8192", "q8_tail_no_slack", "q8_tail_slack"])
+def test_matmul_generic_path_is_bit_exact(ctx, hip, oracle, case):
+    """Views the row kernel does not take (unaligned x or weights, k > 8192, a Q8_0
+    buffer whose last block would be over-read) run the serial kernel: bit-identical
+    to the oracle. With 2 bytes of slack after the weights, the row kernel runs."""
+    g = np.random.default_rng(len(case))
+    m, n, k = (2, 5, 8224) if case == "k_gt_8192" else ((1, 3, 32) if case.startswith("q8_tail") else (3, 9, 256))
+    rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32))
+    x = g.standard_normal((m, k)).astype(np.float32)
+    kw = dict(x_off=4) if case == "x_unaligned" else dict(w_off=2) if case == "w_unaligned" else \
+        dict(w_pad=2) if case == "q8_tail_slack" else {}
+    got = _gpu_matmul(ctx, hip, x, rows, hip.DTYPE_Q8_0, m, n, k, **kw)
+    want = oracle.matmul(x, rows, oracle.Q8_0, m, n, k)
+    if case == "q8_tail_slack":
+        assert np.all(np.abs(got - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)))
+    else:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_matmul_device_errors(ctx, hip):
+    x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
+    with pytest.raises(hip.UnsupportedDtype):
+        hip.matmul(ctx, hip.MatmulArgs(x, w, 12, out, 1, 2, 64))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.matmul(ctx, hip.MatmulArgs(x, w, hip.DTYPE_Q8_0, out, 1, 2, 48))

@@ -32,10 +32,25 @@ def _t(O, case, name):
 
 
 def test_fixture_case_counts(oracle):
-    # kernels_a.zig:335 (6 rmsnorm), :376 (3 rope); kernels_b.zig:225 (6 attention)
+    # kernels_a.zig:335 (6 rmsnorm), :376 (3 rope), :457 (4 matmul_quant); kernels_b.zig:225 (6 attention)
     assert len(_cases(oracle, "rmsnorm")) == 6
     assert len(_cases(oracle, "rope")) == 3
     assert len(_cases(oracle, "attention")) == 6
+    assert len(_cases(oracle, "matmul_quant")) == 4
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_matmul_quant_fixtures(oracle, i):
+    """kernels_a.zig:395-458: Q8_0 matmul within the case tolerance; the tensors'
+    shapes as the reference test checks them (input ne {k, m}, weight {k, n}, output {n, m})."""
+    c = _cases(oracle, "matmul_quant")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w, want = (_t(oracle, c, n) for n in ("input", "weight", "output"))
+    assert x.ne == (p["k"], p["m"]) and w.ne == (p["k"], p["n"]) and want.ne == (p["n"], p["m"])
+    assert w.dtype == oracle.Q8_0 and p["w_dtype"] == "q8_0"
+    got = oracle.matmul(x.data, w.data, oracle.Q8_0, p["m"], p["n"], p["k"])
+    r = oracle.compare(want.data, got, tol["atol"], tol["rtol"])
+    assert r.passed, r
 
 
 @pytest.mark.parametrize("i", range(6))
@@ -398,3 +413,74 @@ def test_config0_golden_vectors_reproduce(oracle):
         t = oracle.load_ds5t(os.path.join(GOLDEN, "c0", f"{name}.ds5t"))
         assert t.dtype == dt
         assert np.array_equal(t.data.reshape(arr.shape).view(np.uint8), np.ascontiguousarray(arr).view(np.uint8)), name
+
+
+# ---------------------------------------------------------------------------
+# matmul (the projection step before the path): kernels_a.zig:136-163
+# ---------------------------------------------------------------------------
+
+
+def test_matmul_f32_hand_case(oracle):
+    """kernels_a.zig:524-553: x [2,3] . W^T with rows {1,0,2} and {0,-1,1}."""
+    x = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    w = np.array([[1, 0, 2], [0, -1, 1]], np.float32)
+    got = oracle.matmul(x, w, oracle.F32, 2, 2, 3)
+    assert np.array_equal(got, np.array([[7, 1], [16, 1]], np.float32))
+
+
+def test_matmul_q8_0_equals_dequantized_f32(oracle):
+    """kernels_a.zig:555-602: the Q8_0 path equals the f32 path on the dequantised
+    weights (f32(scale) * q is exact in f32, so the serial sums match bit for bit)."""
+    g = np.random.default_rng(3)
+    k, n = 64, 3
+    rows = np.zeros((n, 2, 34), np.uint8)
+    for r in range(n):
+        for b in range(2):
+            rows[r, b, :2] = np.array([0.005 + 0.01 * (r + b)], np.float16).view(np.uint8)
+            rows[r, b, 2:] = g.integers(-127, 128, 32).astype(np.int8).view(np.uint8)
+    rows = rows.reshape(n, 68)
+    x = g.standard_normal((2, k)).astype(np.float32)
+    a = oracle.matmul(x, rows, oracle.Q8_0, 2, n, k)
+    b = oracle.matmul(x, oracle.q8_0_dequantize(rows, k), oracle.F32, 2, n, k)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 40, 2048), (5, 17, 96), (3, 9, 32)])
+def test_matmul_matches_float64(oracle, m, n, k):
+    """Q8_0 and f32 weights against a float64 product of the dequantised weights."""
+    g = np.random.default_rng(m * 1000 + n)
+    rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32) * 0.05)
+    wf = oracle.q8_0_dequantize(rows, k)
+    x = g.standard_normal((m, k)).astype(np.float32)
+    want = x.astype(np.float64) @ wf.astype(np.float64).T
+    bound = 1e-6 * k * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T) + 1e-30
+    for w, dt in ((rows, oracle.Q8_0), (wf, oracle.F32)):
+        got = oracle.matmul(x, w, dt, m, n, k).astype(np.float64)
+        assert np.all(np.abs(got - want) <= bound)
+
+
+def test_q8_0_quantize_roundtrip(oracle):
+    """The test helper's quantiser: |w - dequant(quant(w))| <= scale / 2 per element
+    (the f16 scale is within 2^-11 of max|w| / 127, so max|w| / scale stays below 127.5)."""
+    g = np.random.default_rng(11)
+    w = g.standard_normal((7, 128)).astype(np.float32)
+    rows = oracle.q8_0_quantize(w)
+    back = oracle.q8_0_dequantize(rows, 128)
+    d = rows.reshape(7, 4, 34)[:, :, :2].copy().view(np.float16).astype(np.float32)
+    assert np.all(np.abs(w - back).reshape(7, 4, 32) <= d * 0.5 * (1 + 1e-6))
+
+
+def test_matmul_rejections(oracle):
+    """kernels_a.zig:138-150 and :604-617: unsupported dtype first, then k and buffer sizes."""
+    x, w = np.zeros((1, 64), np.float32), np.zeros((2, 68), np.uint8)
+    out = np.zeros(2, np.float32)
+    call = lambda xa, wa, dt, m, n, k, o=out: oracle.lib().ds5o_matmul(
+        oracle.MatmulArgs(oracle.buf(xa), oracle.buf(wa), dt, oracle.buf(o), m, n, k))
+    assert call(x, w, 12, 1, 1, 256) == oracle.UNSUPPORTED_DTYPE  # q4_k
+    assert call(x, w, oracle.F16, 1, 2, 64) == oracle.UNSUPPORTED_DTYPE
+    assert call(x, w, oracle.Q8_0, 1, 2, 0) == oracle.SHAPE_MISMATCH
+    assert call(x, w, oracle.Q8_0, 1, 2, 48) == oracle.SHAPE_MISMATCH  # not a block multiple
+    assert call(x, w, oracle.Q8_0, 2, 2, 64) == oracle.SHAPE_MISMATCH  # x too small
+    assert call(x, w, oracle.Q8_0, 1, 3, 64) == oracle.SHAPE_MISMATCH  # w too small (and out)
+    assert call(x, w, oracle.Q8_0, 1, 2, 64, np.zeros(1, np.float32)) == oracle.SHAPE_MISMATCH
+    assert call(x, w, oracle.Q8_0, 1, 2, 64) == oracle.OK
