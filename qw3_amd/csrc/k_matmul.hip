@@ -9,29 +9,28 @@
 //
 // Decode-shaped products (m = a few tokens) are weight-bandwidth bound: every
 // weight byte is read once per pass of up to MT tokens. matmul_rows_kernel
-// streams whole weight rows: lane L of a wavefront owns the 32-element blocks
-// b = L + 64 j of every row (so a 2048-wide Q8_0 row, 64 blocks, is one load
-// sweep of the wavefront), keeps the x values of its blocks in registers for
-// all rows, and the wavefront reduces each row's partial sums. Q8_0 blocks are
-// only 2-byte aligned: a lane reads the nine dwords covering its block from
-// the dword boundary below it and realigns the bytes in registers.
+// gives each wavefront one weight row: lane L owns the 32-element blocks
+// b = L + 64 j of the row (a 2048-wide Q8_0 row, 64 blocks, is one load sweep),
+// and the wavefront reduces the row's partial sums. The workgroup (8 rows)
+// stages the pass's x once in LDS: read per wavefront from L2 instead, x costs
+// as many bytes as the weights themselves. Q8_0 blocks are only 2-byte aligned:
+// a lane reads the nine dwords covering its block from the dword boundary below
+// it and realigns the bytes in registers.
 #include "ds5_common.hpp"
 
 namespace {
 
-constexpr int kMmThreads = 256;  // 4 wavefronts
+constexpr int kMmThreads = 512;  // 8 wavefronts, one weight row each
 constexpr int kQ8Bytes = 34;     // Q8_0 block: f16 scale + 32 x int8
-
-// Rows one wavefront streams, all loads of a row group issued before use.
-template <bool Q8>
-constexpr int rows_per_wave() { return Q8 ? 2 : 1; }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
 // The 32 int8 of a Q8_0 block as 8 dwords plus its f32 scale, from the nine
-// dwords d[0..8] read at (block address & ~3); sh = block address & 3 (0 or 2).
+// dwords d[0..8] read at (block offset & ~3); sh = block offset & 3 (0 or 2).
+// Both cases run the same instructions: a per-lane byte-permute selector picks
+// bytes 2..5 (sh = 0) or 4..7 (sh = 2) of each dword pair.
 struct Q8Block {
     uint32_t q[8];
     float scale;
@@ -39,15 +38,10 @@ struct Q8Block {
 
 __device__ __forceinline__ Q8Block q8_unpack(const uint32_t (&d)[9], uint32_t sh) {
     Q8Block r;
-    if (sh == 0) {  // scale in d[0] bits 0-15, q bytes start at byte 2
-        r.scale = f16_bits_to_f32(d[0] & 0xffffu);
+    r.scale = f16_bits_to_f32((d[0] >> (8 * sh)) & 0xffffu);
+    const uint32_t sel = sh ? 0x07060504u : 0x05040302u;
 #pragma unroll
-        for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], 2);
-    } else {        // scale in d[0] bits 16-31, q bytes are d[1..8]
-        r.scale = f16_bits_to_f32(d[0] >> 16);
-#pragma unroll
-        for (int i = 0; i < 8; i++) r.q[i] = d[i + 1];
-    }
+    for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_perm(d[i + 1], d[i], sel);
     return r;
 }
 
@@ -64,107 +58,115 @@ __device__ __forceinline__ float q8_dot(const uint32_t (&q)[8], const float (&x)
     return (s[0] + s[1]) + (s[2] + s[3]);
 }
 
-// MT tokens per pass (x in registers), JB blocks per lane (k <= 2048 * JB).
-// Launch: grid.x = ceil(n / (4 * rows_per_wave)), one pass of tokens m0..m0+MT-1.
+// MT tokens per pass, JB blocks per lane (k <= 2048 * JB).
+// Launch: grid.x = ceil(n / 8), one pass of tokens m0..m0+MT-1. Rows past n
+// (last workgroup) load row n - 1 and store nothing: every wavefront reaches
+// the barrier.
 template <int MT, int JB, bool Q8>
 __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const uint8_t* __restrict__ w,
                                                                  float* __restrict__ out, uint32_t m, uint32_t n,
                                                                  uint32_t k, uint32_t m0) {
-    constexpr int RPW = rows_per_wave<Q8>();
+    // x in LDS: float4 chunk i of block b of token t at t * kXChunks + 8 b + (i ^ (b & 7)),
+    // so the 16-byte reads of 8 consecutive lanes (one block each) hit distinct banks
+    constexpr int kXChunks = JB * 512;                                  // float4 chunks of one token's x
+    constexpr int kXPer = (kXChunks + kMmThreads - 1) / kMmThreads;     // chunks each thread stages
+    __shared__ float4 xs[MT * kXChunks];
+
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nb = k / 32;
+    const uint32_t row = min(blockIdx.x * (kMmThreads / 64) + (threadIdx.x >> 6), n - 1);
+    const uint32_t nb = k / 32, kc = k / 4;
     const uint64_t row_bytes = Q8 ? (uint64_t)nb * kQ8Bytes : (uint64_t)k * 4;
     const uint32_t mt = min((uint32_t)MT, m - m0);
 
-    // x of this lane's blocks for the pass's tokens (zero past the block count)
-    float xr[JB][MT][32];
+    // 1. this thread's share of x (tokens past mt re-read token mt - 1; never stored)
+    float4 xv[MT][kXPer];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int u = 0; u < kXPer; u++) {
+            const uint32_t e = min(threadIdx.x + (uint32_t)kMmThreads * u, kc - 1);
+            xv[t][u] = ((const float4*)x)[(uint64_t)(m0 + min((uint32_t)t, mt - 1)) * kc + e];
+        }
+
+    // 2. the row's weights, all in flight before x is needed (loads complete in
+    //    issue order, so staging x waits for x alone)
+    constexpr int kWDw = Q8 ? 9 : 32;  // dwords per lane and block
+    uint32_t d[JB][kWDw];
+    uint32_t sh[JB];
 #pragma unroll
     for (int j = 0; j < JB; j++) {
-        const uint32_t b = lane + 64 * j;
+        const uint32_t b = min(lane + 64u * j, nb - 1);
+        if constexpr (Q8) {
+            // byte offset from w (w is 4-byte aligned, so offset & 3 is the block's)
+            const uint64_t off = row * row_bytes + (uint64_t)b * kQ8Bytes;
+            sh[j] = (uint32_t)off & 3u;
+            const uint32_t* p = (const uint32_t*)(w + (off - sh[j]));
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const bool ok = b < nb && (uint32_t)t < mt;
-            const float4* src = (const float4*)(x + (uint64_t)(m0 + (ok ? t : 0)) * k + 32 * (ok ? b : 0));
+            for (int i = 0; i < 9; i++) d[j][i] = p[i];
+        } else {
+            const uint4* p = (const uint4*)(w + row * row_bytes + (uint64_t)b * 128);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float4 v = ok ? src[i] : float4{0.f, 0.f, 0.f, 0.f};
-                xr[j][t][4 * i] = v.x;
-                xr[j][t][4 * i + 1] = v.y;
-                xr[j][t][4 * i + 2] = v.z;
-                xr[j][t][4 * i + 3] = v.w;
+                const uint4 v = p[i];
+                d[j][4 * i] = v.x;
+                d[j][4 * i + 1] = v.y;
+                d[j][4 * i + 2] = v.z;
+                d[j][4 * i + 3] = v.w;
             }
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    const uint32_t row0 = (blockIdx.x * (kMmThreads / 64) + wave) * RPW;
-    if (row0 >= n) return;  // wave-uniform
-    float acc[RPW][MT];
+    // 3. stage x, then each lane takes the x of its blocks
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int t = 0; t < MT; t++) acc[r][t] = 0.0f;
-
-    if constexpr (Q8) {
-        // all loads of the row group first: nine dwords per (row, block)
-        uint32_t d[RPW][JB][9];
-        uint32_t sh[RPW][JB];
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
-#pragma unroll
-            for (int j = 0; j < JB; j++) {
-                const uint32_t row = min(row0 + r, n - 1);
-                const uint32_t b = min(lane + 64u * j, nb - 1);
-                const uintptr_t addr = (uintptr_t)(w + row * row_bytes + (uint64_t)b * kQ8Bytes);
-                sh[r][j] = (uint32_t)(addr & 3u);
-                const uint32_t* p = (const uint32_t*)(addr - sh[r][j]);
-#pragma unroll
-                for (int i = 0; i < 9; i++) d[r][j][i] = p[i];
-            }
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
-#pragma unroll
-            for (int j = 0; j < JB; j++) {
-                if (lane + 64u * j >= nb) continue;
-                const Q8Block blk = q8_unpack(d[r][j], sh[r][j]);
-#pragma unroll
-                for (int t = 0; t < MT; t++) acc[r][t] = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr[j][t]), acc[r][t]);
-            }
-    } else {
-        float4 wv[JB][8];
-#pragma unroll
-        for (int j = 0; j < JB; j++) {
-            const uint32_t b = min(lane + 64u * j, nb - 1);
-            const float4* p = (const float4*)(w + row0 * row_bytes + (uint64_t)b * 128);
-#pragma unroll
-            for (int i = 0; i < 8; i++) wv[j][i] = p[i];
+        for (int u = 0; u < kXPer; u++) {
+            const uint32_t e = threadIdx.x + (uint32_t)kMmThreads * u;
+            if (e < kc) xs[t * kXChunks + (e & ~7u) + ((e & 7u) ^ ((e >> 3) & 7u))] = xv[t][u];
         }
+    __syncthreads();
+
+    // 4. per-block partial sums (x of the lane's block read from LDS just before
+    //    use), then the wavefront's fixed-order reduction
+    float acc[MT];
 #pragma unroll
-        for (int j = 0; j < JB; j++) {
-            if (lane + 64u * j >= nb) continue;
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < JB; j++) {
+        const uint32_t b = min(lane + 64u * j, nb - 1);
+        float xr[MT][32];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 v = xs[t * kXChunks + 8 * b + (i ^ (b & 7))];
+                xr[t][4 * i] = v.x;
+                xr[t][4 * i + 1] = v.y;
+                xr[t][4 * i + 2] = v.z;
+                xr[t][4 * i + 3] = v.w;
+            }
+        if (lane + 64u * j >= nb) continue;
+        if constexpr (Q8) {
+            const Q8Block blk = q8_unpack(d[j], sh[j]);
+#pragma unroll
+            for (int t = 0; t < MT; t++) acc[t] = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr[t]), acc[t]);
+        } else {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
                 float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    s[0] = __builtin_fmaf(wv[j][i].x, xr[j][t][4 * i], s[0]);
-                    s[1] = __builtin_fmaf(wv[j][i].y, xr[j][t][4 * i + 1], s[1]);
-                    s[2] = __builtin_fmaf(wv[j][i].z, xr[j][t][4 * i + 2], s[2]);
-                    s[3] = __builtin_fmaf(wv[j][i].w, xr[j][t][4 * i + 3], s[3]);
-                }
-                acc[0][t] += (s[0] + s[1]) + (s[2] + s[3]);
+                for (int i = 0; i < 32; i++)
+                    s[i & 3] = __builtin_fmaf(__builtin_bit_cast(float, d[j][i]), xr[t][i], s[i & 3]);
+                acc[t] += (s[0] + s[1]) + (s[2] + s[3]);
             }
         }
     }
-
+    const bool live = blockIdx.x * (kMmThreads / 64) + (threadIdx.x >> 6) < n;
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const uint32_t row = row0 + r;
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const float v = wave_allreduce(acc[r][t], OpAdd{});
-            if (lane == 0 && row < n && (uint32_t)t < mt) out[(uint64_t)(m0 + t) * n + row] = v;
-        }
+    for (int t = 0; t < MT; t++) {
+        const float v = wave_allreduce(acc[t], OpAdd{});
+        if (lane == 0 && live && (uint32_t)t < mt) out[(uint64_t)(m0 + t) * n + row] = v;
     }
 }
 
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_generic_kernel(const float*
 
 template <int MT, int JB, bool Q8>
 int launch_rows(ds5_hip_ctx* ctx, const MatmulLaunch& a, uint32_t m0) {
-    const uint32_t rows_per_block = (kMmThreads / 64) * rows_per_wave<Q8>();
+    const uint32_t rows_per_block = kMmThreads / 64;
     const dim3 grid((a.n + rows_per_block - 1) / rows_per_block);
     DS5_TIMED_LAUNCH(ctx, "matmul_rows_kernel", (matmul_rows_kernel<MT, JB, Q8>), grid, dim3(kMmThreads), 0, ctx->stream,
                      a.x, a.w, a.out, a.m, a.n, a.k, m0);
