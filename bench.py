@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2516.6
+BF16_MFMA_PEAK_TFLOPS = 2516.6  # dense bf16 matrix-core peak (same as f16)
 LOG = sys.stderr
 
 
@@ -114,6 +115,26 @@ class ProjSweep:
     def sweep(self):
         for a in self.args:
             self.H.matmul(self.ctx, a)
+
+
+class ProjPrefill:
+    """The q/k/v projection of a 2048-token prefill (forward.zig:337-339 at m = T):
+    x [T, hidden] f32 . W^T with W Q8_0 [n_q_heads*d + 2*n_kv_heads*d, hidden]."""
+
+    def __init__(self, H, ctx, T=2048, hidden=2048, hq=32, hkv=4, d=128, seed=11):
+        self.H, self.ctx = H, ctx
+        self.m, self.n, self.k = T, hq * d + 2 * hkv * d, hidden
+        nb = self.k // 32
+        g = np.random.default_rng(seed)
+        w = g.integers(0, 256, (self.n, nb, 34), dtype=np.uint8)
+        w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
+        x = g.standard_normal((T, self.k)).astype(np.float32)
+        self.args = H.MatmulArgs(ctx.from_numpy(x), ctx.from_numpy(w.reshape(self.n, nb * 34)), H.DTYPE_Q8_0,
+                                 ctx.createBuffer(T * self.n * 4), T, self.n, self.k)
+        self.flops = 2 * self.m * self.n * self.k
+
+    def sweep(self):
+        self.H.matmul(self.ctx, self.args)
 
 
 class PagedSweep:
@@ -246,8 +267,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="C1,C2,C3,C4,QKV",
-                    help="comma list of configs to run (C1 is the headline; QKV: the decode q/k/v projection)")
+    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,QKVP",
+                    help="comma list of configs to run (C1 is the headline; QKV / QKVP: the decode / prefill "
+                         "q/k/v projection)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -365,6 +387,21 @@ def main():
             bytes_per_layer=w.bytes_per_layer, shape="m 1, n 5120, k 2048, Q8_0")
         log(f"[bench] QKV {us:.3f} us/layer ({w.bytes_per_layer / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us")
         del w
+
+    if "QKVP" in only:
+        log("[bench] QKVP: prefill q/k/v projection, 2048 tokens, Q8_0 [5120 x 2048]")
+        p = ProjPrefill(H, ctx)
+        n_rep = max(5, args.steps // 5)
+        elapsed, _ = time_graph(ctx, p, n_rep, 2)
+        ns_k, _ = kernel_mean_ns(ctx, p, "matmul_q8_mfma_kernel", 5)
+        tf = p.flops / ns_k / 1e3
+        extra["qkv_projection_prefill"] = dict(
+            kernel="matmul_q8_mfma_kernel", kernel_us=round(ns_k / 1e3, 3), tflops=round(tf, 2),
+            frac=round(tf / BF16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(elapsed / n_rep * 1e6, 3),
+            flops=p.flops, peak_tflops=BF16_MFMA_PEAK_TFLOPS,
+            shape="m 2048, n 5120, k 2048, Q8_0; x as three bf16 parts (3 matrix-core products per useful one)")
+        log(f"[bench] QKVP matmul_q8_mfma_kernel {ns_k / 1e3:.2f} us -> {tf:.1f} TFLOP/s (useful)")
+        del p
 
     if result is None:
         result = dict(metric="partial run", value=None, extra=extra)

@@ -99,9 +99,11 @@ struct MatmulLaunch {
     float* out;
     uint32_t m, n, k;
 };
-bool matmul_rows_supported(const MatmulLaunch& a, uintptr_t x_addr, uintptr_t out_addr, uintptr_t w_addr,
-                           uint64_t w_len);
-int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, bool rows_path);
+// Which kernel runs: the row (GEMV) kernel, the Q8_0 matrix-core GEMM, or the
+// serial one-thread-per-output kernel that takes any shape and alignment.
+enum class MatmulPath { Generic, Rows, Gemm };
+MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len);
+int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path);
 
 struct RmsNormLaunch {
     const float* x;

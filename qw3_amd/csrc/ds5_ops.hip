@@ -146,8 +146,7 @@ int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* a) {
     if (int rc = set_device(ctx)) return rc;
     const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), q8, (float*)ds5_ptr(a->out),
                          a->m, a->n, a->k};
-    const bool rows = matmul_rows_supported(l, (uintptr_t)l.x, (uintptr_t)l.out, (uintptr_t)l.w, a->w.len);
-    return launch_matmul(ctx, l, rows);
+    return launch_matmul(ctx, l, matmul_path(l, a->w.len));
 }
 
 int ds5_hip_rope(ds5_hip_ctx* ctx, const ds5_rope_args* a) {

@@ -170,6 +170,221 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill-shaped products (many tokens): Q8_0 GEMM on the f16 matrix cores.
+//
+// out[m, n] = sum_b scale[n, b] * sum_{e < 32} x[m, 32 b + e] * q[n, 32 b + e].
+// The int8 q are exact in f16. Each x row is first scaled by a power of two,
+// x' = x * 2^(14 - E) with 2^E <= max |x row| < 2^(E+1), so |x'| < 2^15 fits
+// f16, and split into two f16 parts, x' = hi + lo (lo the f16 rounding of
+// x' - hi): 22 significant bits, and no overflow or loss of range whatever
+// the row's magnitude. Per 32-element block and 16 x 16 output tile, two
+// v_mfma_f32_16x16x32_f16 (lo, then hi) into a zeroed temporary, then
+// acc += scale * tmp in f32 (the scale belongs to the weight row: one per lane
+// in the result layout); the epilogue undoes the row's power of two exactly.
+//
+// matmul_x_split_kernel writes the two planes and the row exponents into the
+// context workspace; matmul_q8_mfma_kernel then only copies x tiles.
+//
+// GEMM workgroup: BM tokens x BN weight rows, WM x WN wavefronts, each with
+// TM x TN tiles of 16 x 16. Per block, the workgroup stages x (hi and lo
+// planes) and q (as f16) and the BN scales in LDS, double-buffered: the next
+// block's global loads are in flight while the current block is multiplied.
+// LDS rows are 32 halves (four 16-byte chunks) with chunk c of row r stored at
+// c ^ ((r >> 2) & 3), so a 16-lane group reading one chunk of 16 rows hits 16
+// distinct bank groups.
+//
+// MFMA operand layout (16x16x32): lane l supplies row / column l % 16 and the
+// eight k of chunk l / 16; result element (4 (l / 16) + i, l % 16) is in
+// register i of lane l.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kSplitThreads = 256;
+constexpr int kXExpBias = 14;  // scaled rows have max |x'| in [2^14, 2^15)
+
+// Workspace bytes of the split x: hi and lo planes of m x k halves, m exponents.
+inline size_t x_split_bytes(uint32_t m, uint32_t k) { return (size_t)m * k * 4 + (size_t)m * 4; }
+
+// One workgroup per x row: max |x|, its exponent E, then hi / lo of x * 2^(14 - E).
+// A row of zeros (or with a non-finite maximum) keeps E = 0.
+__global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const float* __restrict__ x,
+                                                                       uint16_t* __restrict__ hi,
+                                                                       uint16_t* __restrict__ lo,
+                                                                       int* __restrict__ row_exp, uint32_t k) {
+    __shared__ float red[kSplitThreads / 64];
+    const uint64_t row = blockIdx.x;
+    const float4* xr = (const float4*)(x + row * k);
+    const uint32_t kc = k / 4;
+    float mx = 0.0f;
+    for (uint32_t c = threadIdx.x; c < kc; c += kSplitThreads) {
+        const float4 v = xr[c];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    mx = wave_allreduce(mx, OpMax{});
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // floor(log2 mx): frexp gives mx = f * 2^x with f in [0.5, 1)
+    const int e = (mx > 0.0f && mx <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(mx) - 1 : 0;
+    const int sh = kXExpBias - e;
+    if (threadIdx.x == 0) row_exp[row] = e;
+    uint2* h2 = (uint2*)(hi + row * k);
+    uint2* l2 = (uint2*)(lo + row * k);
+    for (uint32_t c = threadIdx.x; c < kc; c += kSplitThreads) {
+        const float4 v = xr[c];
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t hb[4], lb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float s = __builtin_ldexpf(f[i], sh);
+            const _Float16 h = (_Float16)s;
+            hb[i] = __builtin_bit_cast(uint16_t, h);
+            lb[i] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)h));
+        }
+        h2[c] = uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+        l2[c] = uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+    }
+}
+
+// Four int8 (one dword) as four f16: bytes biased to q + 128, placed under the
+// f16 pattern 0x64 (1024 + q + 128, exact), then 1152 subtracted in f16.
+__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t u) {
+    const uint32_t v = u ^ 0x80808080u;
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    const h2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2_t a = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)) - bias;
+    const h2_t b = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)) - bias;
+    return uint2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
+                                                                      const uint16_t* __restrict__ xlo,
+                                                                      const int* __restrict__ row_exp,
+                                                                      const uint8_t* __restrict__ w,
+                                                                      float* __restrict__ out, uint32_t m, uint32_t n,
+                                                                      uint32_t k) {
+    constexpr int kThreads = WM * WN * 64;
+    constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+    static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "tile split");
+    constexpr int kAPer = BM * 8 / kThreads;  // 16-byte x chunks (both planes) per thread and block
+    constexpr int kBPer = BN * 4 / kThreads;  // 8-byte q runs per thread and block
+    static_assert(kAPer >= 1 && kBPer >= 1, "at least one staging unit per thread");
+
+    __shared__ u32x4_t As[2][2][BM * 4];  // [buffer][hi, lo][row * 4 + swizzled chunk]
+    __shared__ u32x4_t Bs[2][BN * 4];
+    __shared__ float Ss[2][BN];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t nb = k / 32;
+    const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
+
+    // ---- staging: this thread's x chunks and q runs of one block -------------
+    u32x4_t xa[kAPer];
+    uint32_t qd[kBPer][3];
+    uint32_t qsh[kBPer];
+    uint32_t sbits[kBPer];  // scale bits of the run's block (read by part-0 threads)
+    auto load_block = [&](uint32_t b) {
+#pragma unroll
+        for (int u = 0; u < kAPer; u++) {
+            const uint32_t c = threadIdx.x + kThreads * u;  // plane c / (4 BM), row (c / 4) % BM, chunk c % 4
+            const uint32_t row = min(m0 + ((c >> 2) % BM), m - 1);
+            const uint16_t* src = c < 4 * BM ? xhi : xlo;
+            xa[u] = *(const u32x4_t*)(src + (uint64_t)row * k + 32 * b + 8 * (c & 3));
+        }
+#pragma unroll
+        for (int u = 0; u < kBPer; u++) {
+            const uint32_t c = threadIdx.x + kThreads * u;  // row c / 4, q bytes 8 (c % 4) ..
+            const uint32_t row = min(n0 + (c >> 2), n - 1);
+            const uint64_t blk = row * row_bytes + (uint64_t)b * kQ8Bytes;
+            const uint64_t s = blk + 2 + 8 * (c & 3);
+            qsh[u] = (uint32_t)s & 3u;  // w is 4-byte aligned: 0 or 2
+            const uint32_t* p = (const uint32_t*)(w + (s - qsh[u]));
+            qd[u][0] = p[0];
+            qd[u][1] = p[1];
+            qd[u][2] = qsh[u] ? p[2] : 0u;  // the third dword only when the run straddles it
+            sbits[u] = (c & 3) == 0 ? *(const uint16_t*)(w + blk) : 0u;
+        }
+    };
+    auto stage_block = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < kAPer; u++) {
+            const uint32_t c = threadIdx.x + kThreads * u;
+            const uint32_t row = (c >> 2) % BM;
+            As[buf][c < 4 * BM ? 0 : 1][row * 4 + ((c & 3) ^ ((row >> 2) & 3))] = xa[u];
+        }
+#pragma unroll
+        for (int u = 0; u < kBPer; u++) {
+            const uint32_t c = threadIdx.x + kThreads * u;
+            const uint32_t row = c >> 2, part = c & 3;
+            const uint32_t sel = qsh[u] ? 0x05040302u : 0x03020100u;
+            const uint2 a = i8x4_to_f16x4(__builtin_amdgcn_perm(qd[u][1], qd[u][0], sel));
+            const uint2 b = i8x4_to_f16x4(__builtin_amdgcn_perm(qd[u][2], qd[u][1], sel));
+            Bs[buf][row * 4 + (part ^ ((row >> 2) & 3))] = u32x4_t{a.x, a.y, b.x, b.y};
+            if (part == 0) Ss[buf][row] = f16_bits_to_f32(sbits[u]);
+        }
+    };
+
+    // ---- per-wavefront tiles ---------------------------------------------------
+    const int wm0 = (wave / WN) * (BM / WM), wn0 = (wave % WN) * (BN / WN);
+    const int r16 = lane & 15, grp = lane >> 4;
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    load_block(0);
+    stage_block(0);
+    __syncthreads();
+    for (uint32_t b = 0; b < nb; b++) {
+        const int cur = b & 1;
+        if (b + 1 < nb) load_block(b + 1);
+        f16x8_t bv[TN];
+        float sv[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int row = wn0 + 16 * j + r16;
+            bv[j] = __builtin_bit_cast(f16x8_t, Bs[cur][row * 4 + (grp ^ ((row >> 2) & 3))]);
+            sv[j] = Ss[cur][row];
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int row = wm0 + 16 * i + r16;
+            const int slot = row * 4 + (grp ^ ((row >> 2) & 3));
+            const f16x8_t ah = __builtin_bit_cast(f16x8_t, As[cur][0][slot]);
+            const f16x8_t al = __builtin_bit_cast(f16x8_t, As[cur][1][slot]);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv[j], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv[j], t, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = __builtin_fmaf(sv[j], t[e], acc[i][j][e]);
+            }
+        }
+        if (b + 1 < nb) stage_block(cur ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t row = m0 + wm0 + 16 * i + 4 * grp + e;
+            if (row >= m) continue;
+            const int sh = row_exp[row] - kXExpBias;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint32_t col = n0 + wn0 + 16 * j + r16;
+                if (col < n) out[(uint64_t)row * n + col] = __builtin_ldexpf(acc[i][j][e], sh);
+            }
+        }
+}
+
 // Any shape or alignment: one thread per output in the reference's serial order
 // with every product and sum rounded on its own (bit-identical to dotRow).
 __global__ __launch_bounds__(kMmThreads) void matmul_generic_kernel(const float* __restrict__ x, const uint8_t* __restrict__ w,
@@ -231,24 +446,54 @@ int launch_rows_q(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
     return launch_passes<4, Q8>(ctx, a);
 }
 
+template <int BM, int BN, int WM, int WN>
+int launch_gemm(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
+    void* ws = nullptr;
+    if (int rc = ds5_workspace(ctx, x_split_bytes(a.m, a.k), &ws)) return rc;
+    uint16_t* hi = (uint16_t*)ws;
+    uint16_t* lo = hi + (size_t)a.m * a.k;
+    int* row_exp = (int*)(lo + (size_t)a.m * a.k);
+    DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel, dim3(a.m), dim3(kSplitThreads), 0, ctx->stream,
+                     a.x, hi, lo, row_exp, a.k);
+    if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
+    const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN>), grid, dim3(WM * WN * 64), 0,
+                     ctx->stream, hi, lo, row_exp, a.w, a.out, a.m, a.n, a.k);
+    return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
+}
+
 }  // namespace
+
+// Tokens from which Q8_0 products run on the matrix cores (below, the row
+// kernel's passes of up to 4 tokens re-read the weights less often than the
+// GEMM wastes matrix-core work)
+constexpr uint32_t kGemmMinM = 16;
 
 // The row kernel needs x and out 16-byte aligned, k <= 8192, and f32 weights 16-byte
 // aligned or Q8_0 weights 4-byte aligned. A Q8_0 block is read as the nine dwords
 // from the dword boundary at or below it, which ends 2 bytes past the block when
 // the block starts on a dword boundary; for the last block that stays inside the
 // view only if the weights end on a dword boundary or the view has 2 more bytes.
-bool matmul_rows_supported(const MatmulLaunch& a, uintptr_t x_addr, uintptr_t out_addr, uintptr_t w_addr,
-                           uint64_t w_len) {
-    if (a.k % 32 != 0 || a.k / 32 > 256 || (x_addr & 15u) || (out_addr & 15u)) return false;
-    if (!a.q8) return (w_addr & 15u) == 0;
+// The GEMM reads x as float4 (x 16-byte aligned), stores single floats (out
+// 4-byte aligned) and reads q in 8-byte runs from the dword boundary at or below
+// them, with the same end condition.
+MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len) {
+    const uintptr_t x_addr = (uintptr_t)a.x, out_addr = (uintptr_t)a.out, w_addr = (uintptr_t)a.w;
+    if (a.k % 32 != 0 || (x_addr & 15u)) return MatmulPath::Generic;
+    if (!a.q8) return (a.k / 32 <= 256 && (out_addr & 15u) == 0 && (w_addr & 15u) == 0) ? MatmulPath::Rows
+                                                                                         : MatmulPath::Generic;
     const uint64_t end = (uint64_t)a.n * (a.k / 32) * kQ8Bytes;
-    return (w_addr & 3u) == 0 && ((w_addr + end) % 4 == 0 || w_len >= end + 2);
+    if ((w_addr & 3u) || !((w_addr + end) % 4 == 0 || w_len >= end + 2)) return MatmulPath::Generic;
+    if (a.m >= kGemmMinM && (out_addr & 3u) == 0) return MatmulPath::Gemm;
+    if (a.k / 32 <= 256 && (out_addr & 15u) == 0) return MatmulPath::Rows;
+    return (out_addr & 3u) == 0 ? MatmulPath::Gemm : MatmulPath::Generic;
 }
 
-int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, bool rows_path) {
+int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path) {
     if (a.m == 0 || a.n == 0) return DS5_OK;
-    if (rows_path) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
+    if (path == MatmulPath::Rows) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
+    if (path == MatmulPath::Gemm)
+        return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);
     const uint64_t total = (uint64_t)a.m * a.n;
     const dim3 grid((unsigned)((total + kMmThreads - 1) / kMmThreads));
     DS5_TIMED_LAUNCH(ctx, "matmul_generic_kernel", matmul_generic_kernel, grid, dim3(kMmThreads), 0, ctx->stream, a.x,

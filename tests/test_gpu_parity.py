@@ -582,8 +582,13 @@ def test_matmul_f32_hand_case(ctx, hip):
     (1, 2048, 4096),   # decode output projection (32*128 -> 2048)
     (3, 301, 4096),    # two blocks per lane, a 2-token pass plus a 1-token pass
     (2, 77, 8192),     # four blocks per lane
-    (17, 256, 256),    # fixture shape: 4-token passes and a remainder
-    (5, 33, 96),       # three blocks, odd row count
+    (5, 33, 96),       # three blocks, odd row count, 4-token pass plus one
+    (15, 40, 512),     # the most tokens the row kernel takes
+    (16, 64, 32),      # matrix-core GEMM from 16 tokens: one block
+    (17, 256, 256),    # fixture shape, small GEMM tile
+    (33, 130, 4096),   # small tiles, ragged tokens and rows
+    (128, 512, 2048),  # large tiles, exact
+    (200, 300, 2080),  # large tiles, ragged tokens, rows and an odd block count
 ])
 def test_matmul_q8_0_and_f32_vs_oracle(ctx, hip, oracle, m, n, k):
     """Q8_0 rows and their dequantised f32 rows against the oracle, within the bound
@@ -601,23 +606,52 @@ def test_matmul_q8_0_and_f32_vs_oracle(ctx, hip, oracle, m, n, k):
         assert np.all(np.isfinite(got)) and np.all(err <= bound)
 
 
-@pytest.mark.parametrize("case", ["x_unaligned", "w_unaligned", "k_gt_8192", "q8_tail_no_slack", "q8_tail_slack"])
-def test_matmul_generic_path_is_bit_exact(ctx, hip, oracle, case):
-    """Views the row kernel does not take (unaligned x or weights, k > 8192, a Q8_0
-    buffer whose last block would be over-read) run the serial kernel: bit-identical
-    to the oracle. With 2 bytes of slack after the weights, the row kernel runs."""
+def test_matmul_q8_0_wide_exponent_range(ctx, hip, oracle):
+    """x rows from 1e-30 to 1e30 and mixed magnitudes inside rows: the GEMM's
+    three-part bf16 split of x keeps f32 accuracy over the whole f32 range."""
+    g = np.random.default_rng(5)
+    m, n, k = 40, 96, 1024
+    rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32) * 0.05)
+    wf = oracle.q8_0_dequantize(rows, k)
+    x = g.standard_normal((m, k)) * 10.0 ** g.integers(-6, 7, (m, k))
+    x = (x * 10.0 ** np.linspace(-24, 24, m)[:, None]).astype(np.float32)
+    got = _gpu_matmul(ctx, hip, x, rows, hip.DTYPE_Q8_0, m, n, k)
+    want = oracle.matmul(x, rows, oracle.Q8_0, m, n, k)
+    assert np.all(np.isfinite(got)) and np.all(np.abs(got - want) <= _dot_bound(x, wf))
+
+
+# (case, kernel that must run): views the fast kernels do not take (unaligned x or
+# weights, a Q8_0 buffer whose last block would be over-read) run the serial
+# kernel, bit-identical to the oracle; 2 bytes of slack after the weights, or
+# k > 8192 (past the row kernel), take the fast kernels.
+_PATH_CASES = [("x_unaligned", "matmul_generic_kernel"), ("w_unaligned", "matmul_generic_kernel"),
+               ("q8_tail_no_slack", "matmul_generic_kernel"), ("q8_tail_slack", "matmul_rows_kernel"),
+               ("k_gt_8192", "matmul_q8_mfma_kernel"), ("decode", "matmul_rows_kernel"),
+               ("prefill", "matmul_q8_mfma_kernel")]
+
+
+@pytest.mark.parametrize("case,kernel", _PATH_CASES, ids=[c for c, _ in _PATH_CASES])
+def test_matmul_paths(ctx, hip, oracle, case, kernel):
     g = np.random.default_rng(len(case))
-    m, n, k = (2, 5, 8224) if case == "k_gt_8192" else ((1, 3, 32) if case.startswith("q8_tail") else (3, 9, 256))
+    m, n, k = {"k_gt_8192": (2, 5, 8224), "q8_tail_no_slack": (1, 3, 32), "q8_tail_slack": (1, 3, 32),
+               "decode": (1, 24, 2048), "prefill": (16, 24, 2048)}.get(case, (3, 9, 256))
     rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32))
     x = g.standard_normal((m, k)).astype(np.float32)
     kw = dict(x_off=4) if case == "x_unaligned" else dict(w_off=2) if case == "w_unaligned" else \
-        dict(w_pad=2) if case == "q8_tail_slack" else {}
-    got = _gpu_matmul(ctx, hip, x, rows, hip.DTYPE_Q8_0, m, n, k, **kw)
+        dict(w_pad=2) if case in ("q8_tail_slack", "k_gt_8192") else {}
+    ctx.set_kernel_timing(True)
+    try:
+        before = {kn: ctx.kernel_time(kn)[0] for _, kn in _PATH_CASES}
+        got = _gpu_matmul(ctx, hip, x, rows, hip.DTYPE_Q8_0, m, n, k, **kw)
+        ran = [kn for kn in before if ctx.kernel_time(kn)[0] > before[kn]]
+    finally:
+        ctx.set_kernel_timing(False)
+    assert ran == [kernel]
     want = oracle.matmul(x, rows, oracle.Q8_0, m, n, k)
-    if case == "q8_tail_slack":
-        assert np.all(np.abs(got - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)))
-    else:
+    if kernel == "matmul_generic_kernel":
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.all(np.abs(got - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)))
 
 
 def test_matmul_device_errors(ctx, hip):
