@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2516.6
 BF16_MFMA_PEAK_TFLOPS = 2516.6  # dense bf16 matrix-core peak (same as f16)
+QKV_BYTES = 5120 * 64 * 34 + 2048 * 4 + 5120 * 4  # Qwen3-30B-A3B q/k/v weights + x + out per layer
 LOG = sys.stderr
 
 
@@ -92,49 +93,64 @@ class DecodeSweep:
 
 
 class ProjSweep:
-    """The q/k/v projection of a decode step (the matmul before the attention path,
-    forward.zig:337-339): n_layers of x [1, hidden] . W^T with W Q8_0 [n_q_heads*d +
-    2*n_kv_heads*d, hidden]; distinct random weights per layer (the 256 MB MALL cannot
-    hold the sweep)."""
+    """The q/k/v projections of a decode step (the matmuls before the attention path,
+    forward.zig:337-339): n_layers of x [1, hidden] . W^T for the three Q8_0 weights
+    wq [n_q_heads*d, hidden], wk and wv [n_kv_heads*d, hidden], as one grouped call
+    (grouped=True) or as the engine's three matmul calls; distinct random weights per
+    layer (the 256 MB MALL cannot hold the sweep)."""
 
-    def __init__(self, H, ctx, layers=48, hidden=2048, hq=32, hkv=4, d=128, seed=7):
-        self.H, self.ctx, self.layers = H, ctx, layers
-        self.n, self.k = hq * d + 2 * hkv * d, hidden
+    def __init__(self, H, ctx, layers=48, hidden=2048, hq=32, hkv=4, d=128, seed=7, grouped=True):
+        self.H, self.ctx, self.layers, self.grouped = H, ctx, layers, grouped
+        self.ns, self.k = (hq * d, hkv * d, hkv * d), hidden
+        self.n = sum(self.ns)
         nb = self.k // 32
         g = np.random.default_rng(seed)
         self.args = []
         for _ in range(layers):
-            w = g.integers(0, 256, (self.n, nb, 34), dtype=np.uint8)
-            w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
-            x = g.standard_normal((1, self.k)).astype(np.float32)
-            out = ctx.createBuffer(self.n * 4)
-            self.args.append(H.MatmulArgs(ctx.from_numpy(x), ctx.from_numpy(w.reshape(self.n, nb * 34)),
-                                          H.DTYPE_Q8_0, out, 1, self.n, self.k))
+            x = ctx.from_numpy(g.standard_normal((1, self.k)).astype(np.float32))
+            entries = []
+            for n in self.ns:
+                w = g.integers(0, 256, (n, nb, 34), dtype=np.uint8)
+                w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
+                entries.append((ctx.from_numpy(w.reshape(n, nb * 34)), ctx.createBuffer(n * 4), n))
+            if grouped:
+                self.args.append(H.MatmulGroupArgs.of(x, H.DTYPE_Q8_0, 1, self.k, entries))
+            else:
+                self.args.append([H.MatmulArgs(x, w, H.DTYPE_Q8_0, o, 1, n, self.k) for w, o, n in entries])
         self.bytes_per_layer = self.n * nb * 34 + self.k * 4 + self.n * 4
 
     def sweep(self):
         for a in self.args:
-            self.H.matmul(self.ctx, a)
+            if self.grouped:
+                self.H.matmulGroup(self.ctx, a)
+            else:
+                for one in a:
+                    self.H.matmul(self.ctx, one)
 
 
 class ProjPrefill:
-    """The q/k/v projection of a 2048-token prefill (forward.zig:337-339 at m = T):
-    x [T, hidden] f32 . W^T with W Q8_0 [n_q_heads*d + 2*n_kv_heads*d, hidden]."""
+    """The q/k/v projections of a 2048-token prefill (forward.zig:337-339 at m = T):
+    x [T, hidden] f32 . W^T for wq [n_q_heads*d, hidden], wk and wv [n_kv_heads*d,
+    hidden], Q8_0, in one grouped call."""
 
     def __init__(self, H, ctx, T=2048, hidden=2048, hq=32, hkv=4, d=128, seed=11):
         self.H, self.ctx = H, ctx
-        self.m, self.n, self.k = T, hq * d + 2 * hkv * d, hidden
+        self.m, self.k = T, hidden
+        ns = (hq * d, hkv * d, hkv * d)
+        self.n = sum(ns)
         nb = self.k // 32
         g = np.random.default_rng(seed)
-        w = g.integers(0, 256, (self.n, nb, 34), dtype=np.uint8)
-        w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
-        x = g.standard_normal((T, self.k)).astype(np.float32)
-        self.args = H.MatmulArgs(ctx.from_numpy(x), ctx.from_numpy(w.reshape(self.n, nb * 34)), H.DTYPE_Q8_0,
-                                 ctx.createBuffer(T * self.n * 4), T, self.n, self.k)
+        x = ctx.from_numpy(g.standard_normal((T, self.k)).astype(np.float32))
+        entries = []
+        for n in ns:
+            w = g.integers(0, 256, (n, nb, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
+            entries.append((ctx.from_numpy(w.reshape(n, nb * 34)), ctx.createBuffer(T * n * 4), n))
+        self.args = H.MatmulGroupArgs.of(x, H.DTYPE_Q8_0, T, self.k, entries)
         self.flops = 2 * self.m * self.n * self.k
 
     def sweep(self):
-        self.H.matmul(self.ctx, self.args)
+        self.H.matmulGroup(self.ctx, self.args)
 
 
 class PagedSweep:
@@ -375,31 +391,40 @@ def main():
         del w
 
     if "QKV" in only:
-        log("[bench] QKV: decode q/k/v projection, Q8_0 [5120 x 2048], 48 layers")
-        w = ProjSweep(H, ctx)
+        log("[bench] QKV: decode q/k/v projections, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048], 48 layers")
         stepsq = max(5, args.steps // 4)
+        w = ProjSweep(H, ctx)
         elapsed, _ = time_graph(ctx, w, stepsq, 2)
         us = elapsed / (w.layers * stepsq) * 1e6
         ns_k, _ = kernel_mean_ns(ctx, w, "matmul_rows_kernel", 2)
-        extra["qkv_projection_decode"] = dict(
-            kernel="matmul_rows_kernel", us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
-            kernel_us=round(ns_k / 1e3, 3), kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),
-            bytes_per_layer=w.bytes_per_layer, shape="m 1, n 5120, k 2048, Q8_0")
-        log(f"[bench] QKV {us:.3f} us/layer ({w.bytes_per_layer / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us")
         del w
+        w = ProjSweep(H, ctx, grouped=False)
+        elapsed, _ = time_graph(ctx, w, stepsq, 2)
+        us_sep = elapsed / (w.layers * stepsq) * 1e6
+        del w
+        extra["qkv_projection_decode"] = dict(
+            kernel="matmul_rows_kernel", us_per_layer=round(us, 3), gbs=round(QKV_BYTES / (us * 1e3), 2),
+            kernel_us=round(ns_k / 1e3, 3), kernel_frac=round(QKV_BYTES / ns_k / HBM_PEAK_GBS, 4),
+            us_per_layer_three_calls=round(us_sep, 3), bytes_per_layer=QKV_BYTES,
+            shape="m 1, n 4096 + 512 + 512, k 2048, Q8_0; one grouped call (three matmul calls: us_per_layer_three_calls)")
+        log(f"[bench] QKV grouped {us:.3f} us/layer ({QKV_BYTES / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us; "
+            f"three calls {us_sep:.3f} us/layer")
 
     if "QKVP" in only:
-        log("[bench] QKVP: prefill q/k/v projection, 2048 tokens, Q8_0 [5120 x 2048]")
+        log("[bench] QKVP: prefill q/k/v projections, 2048 tokens, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048]")
         p = ProjPrefill(H, ctx)
         n_rep = max(5, args.steps // 5)
         elapsed, _ = time_graph(ctx, p, n_rep, 2)
         ns_k, _ = kernel_mean_ns(ctx, p, "matmul_q8_mfma_kernel", 5)
+        ns_split, _ = kernel_mean_ns(ctx, p, "matmul_x_split_kernel", 5)
         tf = p.flops / ns_k / 1e3
         extra["qkv_projection_prefill"] = dict(
             kernel="matmul_q8_mfma_kernel", kernel_us=round(ns_k / 1e3, 3), tflops=round(tf, 2),
             frac=round(tf / BF16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(elapsed / n_rep * 1e6, 3),
             flops=p.flops, peak_tflops=BF16_MFMA_PEAK_TFLOPS,
-            shape="m 2048, n 5120, k 2048, Q8_0; x as three bf16 parts (3 matrix-core products per useful one)")
+            split_us=round(ns_split / 1e3, 3),
+            shape="m 2048, n 4096 + 512 + 512, k 2048, Q8_0, one grouped call; x split into f16 hi and lo "
+                  "(2 matrix-core products per useful one)")
         log(f"[bench] QKVP matmul_q8_mfma_kernel {ns_k / 1e3:.2f} us -> {tf:.1f} TFLOP/s (useful)")
         del p
 

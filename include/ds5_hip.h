@@ -201,8 +201,10 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* args);
  * Weight dtypes other than f32 / Q8_0 are UnsupportedDtype; k must be a
  * positive multiple of the dtype's block (32 for Q8_0). Each output is the
  * same dot product as the reference's serial one, summed as a fixed tree of
- * per-block partial sums, so it agrees to rounding (the generic path, used for
- * unaligned views or k > 8192, keeps the serial order and is bit-identical). */
+ * per-block partial sums, so it agrees to rounding (the serial kernel, used for
+ * views the fast kernels cannot read, keeps the reference's order and is
+ * bit-identical). From 16 tokens a Q8_0 product uses 4*m*k bytes of the
+ * context workspace: run a shape once before capturing it in a graph. */
 typedef struct ds5_matmul_args {
     ds5_buf x;        /* f32 [m, k] */
     ds5_buf w;        /* w_dtype: n rows of k elements */
@@ -217,6 +219,26 @@ int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* args);
 /* ========================================================================
  * 3. Fused extensions (optional decls; the engine uses them via @hasDecl)
  * ======================================================================== */
+
+/* The engine's q, k and v projections (forward.zig:337-339: three matmul calls
+ * on the same x) as one call: entry e is exactly ds5_hip_matmul(x, w[e],
+ * w_dtype, out[e], m, n[e], k), same results bit for bit. All entries are
+ * checked (in order, each as matmul checks) before anything is enqueued. When
+ * every entry takes the same kernel the group is one launch per pass of tokens
+ * (from 16 Q8_0 tokens: one split of x, then one launch). count is
+ * 1..DS5_MATMUL_GROUP_MAX, else ShapeMismatch. */
+#define DS5_MATMUL_GROUP_MAX 4u
+typedef struct ds5_matmul_group_args {
+    ds5_buf x;        /* f32 [m, k], shared */
+    uint32_t w_dtype; /* DS5_DTYPE_F32 or DS5_DTYPE_Q8_0, shared */
+    uint32_t m;
+    uint32_t k;
+    uint32_t count;
+    ds5_buf w[DS5_MATMUL_GROUP_MAX];   /* entry e: n[e] rows of k elements */
+    ds5_buf out[DS5_MATMUL_GROUP_MAX]; /* entry e: f32 [m, n[e]] */
+    uint32_t n[DS5_MATMUL_GROUP_MAX];
+} ds5_matmul_group_args;
+int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* args);
 
 /* One layer's attention block in the engine's op order
  * (src/engine/forward.zig:345-412): per-head RMSNorm of q and k with

@@ -104,6 +104,18 @@ struct MatmulLaunch {
 enum class MatmulPath { Generic, Rows, Gemm };
 MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len);
 int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path);
+// Up to kMatmulGroupMax products sharing x (and m, k, the weight dtype).
+constexpr int kMatmulGroupMax = DS5_MATMUL_GROUP_MAX;
+struct MatmulGroupLaunch {
+    const float* x;
+    bool q8;
+    uint32_t m, k;
+    uint32_t count;
+    const uint8_t* w[kMatmulGroupMax];
+    float* out[kMatmulGroupMax];
+    uint32_t n[kMatmulGroupMax];
+};
+int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const MatmulPath* paths);
 
 struct RmsNormLaunch {
     const float* x;

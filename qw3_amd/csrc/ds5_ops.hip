@@ -130,23 +130,54 @@ int ds5_hip_rms_norm(ds5_hip_ctx* ctx, const ds5_rms_norm_args* a) {
 }
 
 // kernels_a.zig:136-150: dtype first, then k, then the three buffer sizes.
+static int check_matmul(ds5_hip_ctx* ctx, const char* op, ds5_buf x, ds5_buf w, uint32_t w_dtype, ds5_buf out,
+                        uint64_t m, uint64_t n, uint64_t k) {
+    const bool q8 = w_dtype == DS5_DTYPE_Q8_0;
+    if (!q8 && w_dtype != DS5_DTYPE_F32)
+        return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "%s: w_dtype %u (f32 and q8_0 are supported)", op, w_dtype);
+    if (k == 0 || k % (q8 ? 32 : 1) != 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: k = %llu is not a positive multiple of the weight block", op,
+                        (unsigned long long)k);
+    if (!covers(x, m * k * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: x too small", op);
+    if (!covers(out, m * n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: out too small", op);
+    const uint64_t row_bytes = q8 ? k / 32 * 34 : k * 4;
+    if (!covers(w, n * row_bytes)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: w too small", op);
+    return DS5_OK;
+}
+
 int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
-    const bool q8 = a->w_dtype == DS5_DTYPE_Q8_0;
-    if (!q8 && a->w_dtype != DS5_DTYPE_F32)
-        return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "matmul: w_dtype %u (f32 and q8_0 are supported)", a->w_dtype);
-    const uint64_t m = a->m, n = a->n, k = a->k;
-    if (k == 0 || k % (q8 ? 32 : 1) != 0)
-        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: k = %u is not a positive multiple of the weight block", a->k);
-    if (!covers(a->x, m * k * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: x too small");
-    if (!covers(a->out, m * n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: out too small");
-    const uint64_t row_bytes = q8 ? k / 32 * 34 : k * 4;
-    if (!covers(a->w, n * row_bytes)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul: w too small");
-    if (m == 0 || n == 0) return DS5_OK;
+    if (int rc = check_matmul(ctx, "matmul", a->x, a->w, a->w_dtype, a->out, a->m, a->n, a->k)) return rc;
+    if (a->m == 0 || a->n == 0) return DS5_OK;
     if (int rc = set_device(ctx)) return rc;
-    const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), q8, (float*)ds5_ptr(a->out),
-                         a->m, a->n, a->k};
+    const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), a->w_dtype == DS5_DTYPE_Q8_0,
+                         (float*)ds5_ptr(a->out), a->m, a->n, a->k};
     return launch_matmul(ctx, l, matmul_path(l, a->w.len));
+}
+
+int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (a->count == 0 || a->count > DS5_MATMUL_GROUP_MAX)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul_group: count = %u (1..%u)", a->count, DS5_MATMUL_GROUP_MAX);
+    for (uint32_t e = 0; e < a->count; e++)
+        if (int rc = check_matmul(ctx, "matmul_group", a->x, a->w[e], a->w_dtype, a->out[e], a->m, a->n[e], a->k))
+            return rc;
+    if (a->m == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    MatmulGroupLaunch g{};
+    g.x = (const float*)ds5_ptr(a->x);
+    g.q8 = a->w_dtype == DS5_DTYPE_Q8_0;
+    g.m = a->m;
+    g.k = a->k;
+    g.count = a->count;
+    MatmulPath paths[kMatmulGroupMax];
+    for (uint32_t e = 0; e < a->count; e++) {
+        g.w[e] = (const uint8_t*)ds5_ptr(a->w[e]);
+        g.out[e] = (float*)ds5_ptr(a->out[e]);
+        g.n[e] = a->n[e];
+        paths[e] = matmul_path(MatmulLaunch{g.x, g.w[e], g.q8, g.out[e], g.m, g.n[e], g.k}, a->w[e].len);
+    }
+    return launch_matmul_group(ctx, g, paths);
 }
 
 int ds5_hip_rope(ds5_hip_ctx* ctx, const ds5_rope_args* a) {

@@ -58,14 +58,36 @@ __device__ __forceinline__ float q8_dot(const uint32_t (&q)[8], const float (&x)
     return (s[0] + s[1]) + (s[2] + s[3]);
 }
 
+// Up to kMatmulGroupMax weight matrices sharing x, in one launch: entry e owns
+// the workgroups (row kernel) or column tiles (GEMM) [wg0[e], wg0[e + 1]).
+struct WeightGroup {
+    const uint8_t* w[kMatmulGroupMax];
+    float* out[kMatmulGroupMax];
+    uint32_t n[kMatmulGroupMax];
+    uint32_t wg0[kMatmulGroupMax];
+    uint32_t count;
+};
+
 // MT tokens per pass, JB blocks per lane (k <= 2048 * JB).
-// Launch: grid.x = ceil(n / 8), one pass of tokens m0..m0+MT-1. Rows past n
-// (last workgroup) load row n - 1 and store nothing: every wavefront reaches
-// the barrier.
+// Launch: grid.x = sum of ceil(n[e] / 8), one pass of tokens m0..m0+MT-1. Rows
+// past n (an entry's last workgroup) load row n - 1 and store nothing: every
+// wavefront reaches the barrier.
 template <int MT, int JB, bool Q8>
-__global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const uint8_t* __restrict__ w,
-                                                                 float* __restrict__ out, uint32_t m, uint32_t n,
-                                                                 uint32_t k, uint32_t m0) {
+__global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const WeightGroup g,
+                                                                 uint32_t m, uint32_t k, uint32_t m0) {
+    // this workgroup's entry (uniform; selected without indexing the argument arrays)
+    const uint8_t* __restrict__ w = g.w[0];
+    float* __restrict__ out = g.out[0];
+    uint32_t n = g.n[0], wg = blockIdx.x;
+#pragma unroll
+    for (int e = 1; e < kMatmulGroupMax; e++)
+        if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
+            w = g.w[e];
+            out = g.out[e];
+            n = g.n[e];
+            wg = blockIdx.x - g.wg0[e];
+        }
+
     // x in LDS: float4 chunk i of block b of token t at t * kXChunks + 8 b + (i ^ (b & 7)),
     // so the 16-byte reads of 8 consecutive lanes (one block each) hit distinct banks
     constexpr int kXChunks = JB * 512;                                  // float4 chunks of one token's x
@@ -73,7 +95,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
     __shared__ float4 xs[MT * kXChunks];
 
     const int lane = threadIdx.x & 63;
-    const uint32_t row = min(blockIdx.x * (kMmThreads / 64) + (threadIdx.x >> 6), n - 1);
+    const uint32_t row = min(wg * (kMmThreads / 64) + (threadIdx.x >> 6), n - 1);
     const uint32_t nb = k / 32, kc = k / 4;
     const uint64_t row_bytes = Q8 ? (uint64_t)nb * kQ8Bytes : (uint64_t)k * 4;
     const uint32_t mt = min((uint32_t)MT, m - m0);
@@ -162,7 +184,7 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
             }
         }
     }
-    const bool live = blockIdx.x * (kMmThreads / 64) + (threadIdx.x >> 6) < n;
+    const bool live = wg * (kMmThreads / 64) + (threadIdx.x >> 6) < n;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         const float v = wave_allreduce(acc[t], OpAdd{});
@@ -263,9 +285,19 @@ template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
-                                                                      const uint8_t* __restrict__ w,
-                                                                      float* __restrict__ out, uint32_t m, uint32_t n,
-                                                                      uint32_t k) {
+                                                                      const WeightGroup g, uint32_t m, uint32_t k) {
+    // this workgroup's entry and column tile (uniform)
+    const uint8_t* __restrict__ w = g.w[0];
+    float* __restrict__ out = g.out[0];
+    uint32_t n = g.n[0], tile = blockIdx.x;
+#pragma unroll
+    for (int e = 1; e < kMatmulGroupMax; e++)
+        if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
+            w = g.w[e];
+            out = g.out[e];
+            n = g.n[e];
+            tile = blockIdx.x - g.wg0[e];
+        }
     constexpr int kThreads = WM * WN * 64;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "tile split");
@@ -279,7 +311,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t m0 = blockIdx.y * BM, n0 = tile * BN;
     const uint32_t nb = k / 32;
     const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
 
@@ -411,18 +443,28 @@ __global__ __launch_bounds__(kMmThreads) void matmul_generic_kernel(const float*
 }
 
 template <int MT, int JB, bool Q8>
-int launch_rows(ds5_hip_ctx* ctx, const MatmulLaunch& a, uint32_t m0) {
-    const uint32_t rows_per_block = kMmThreads / 64;
-    const dim3 grid((a.n + rows_per_block - 1) / rows_per_block);
-    DS5_TIMED_LAUNCH(ctx, "matmul_rows_kernel", (matmul_rows_kernel<MT, JB, Q8>), grid, dim3(kMmThreads), 0, ctx->stream,
-                     a.x, a.w, a.out, a.m, a.n, a.k, m0);
+int launch_rows(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, uint32_t m0) {
+    constexpr uint32_t kRowsPerBlock = kMmThreads / 64;
+    WeightGroup g{};
+    uint32_t wgs = 0;
+    for (uint32_t e = 0; e < a.count; e++) {
+        g.w[g.count] = a.w[e];
+        g.out[g.count] = a.out[e];
+        g.n[g.count] = a.n[e];
+        g.wg0[g.count] = wgs;
+        wgs += (a.n[e] + kRowsPerBlock - 1) / kRowsPerBlock;
+        g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
+    }
+    if (wgs == 0) return DS5_OK;
+    DS5_TIMED_LAUNCH(ctx, "matmul_rows_kernel", (matmul_rows_kernel<MT, JB, Q8>), dim3(wgs), dim3(kMmThreads), 0,
+                     ctx->stream, a.x, g, a.m, a.k, m0);
     return ds5_after_launch(ctx, "matmul_rows_kernel");
 }
 
 // Tokens per pass: up to 4 / JB (the x registers hold MT * JB * 32 floats per lane),
 // and no more than the tokens there are (a 1-token decode runs MT = 1).
 template <int JB, bool Q8>
-int launch_passes(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
+int launch_passes(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     constexpr uint32_t kMaxMt = 4 / JB;
     const uint32_t mt = a.m >= kMaxMt ? kMaxMt : (a.m >= 2 ? 2 : 1);
     for (uint32_t m0 = 0; m0 < a.m; m0 += mt) {
@@ -439,15 +481,16 @@ int launch_passes(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
 }
 
 template <bool Q8>
-int launch_rows_q(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
+int launch_rows_q(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     const uint32_t nb = a.k / 32;
     if (nb <= 64) return launch_passes<1, Q8>(ctx, a);
     if (nb <= 128) return launch_passes<2, Q8>(ctx, a);
     return launch_passes<4, Q8>(ctx, a);
 }
 
+// The split x is made once and shared by the group's products.
 template <int BM, int BN, int WM, int WN>
-int launch_gemm(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
+int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, x_split_bytes(a.m, a.k), &ws)) return rc;
     uint16_t* hi = (uint16_t*)ws;
@@ -456,9 +499,19 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulLaunch& a) {
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel, dim3(a.m), dim3(kSplitThreads), 0, ctx->stream,
                      a.x, hi, lo, row_exp, a.k);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
-    const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM);
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN>), grid, dim3(WM * WN * 64), 0,
-                     ctx->stream, hi, lo, row_exp, a.w, a.out, a.m, a.n, a.k);
+    WeightGroup g{};
+    uint32_t tiles = 0;
+    for (uint32_t e = 0; e < a.count; e++) {
+        g.w[g.count] = a.w[e];
+        g.out[g.count] = a.out[e];
+        g.n[g.count] = a.n[e];
+        g.wg0[g.count] = tiles;
+        tiles += (a.n[e] + BN - 1) / BN;
+        g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
+    }
+    if (tiles == 0) return DS5_OK;
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN>), dim3(tiles, (a.m + BM - 1) / BM),
+                     dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
 
@@ -489,14 +542,56 @@ MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len) {
     return (out_addr & 3u) == 0 ? MatmulPath::Gemm : MatmulPath::Generic;
 }
 
-int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path) {
-    if (a.m == 0 || a.n == 0) return DS5_OK;
+static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bool q8, float* out, uint32_t m,
+                          uint32_t n, uint32_t k) {
+    const uint64_t total = (uint64_t)m * n;
+    const dim3 grid((unsigned)((total + kMmThreads - 1) / kMmThreads));
+    DS5_TIMED_LAUNCH(ctx, "matmul_generic_kernel", matmul_generic_kernel, grid, dim3(kMmThreads), 0, ctx->stream, x, w,
+                     (uint32_t)q8, out, m, n, k);
+    return ds5_after_launch(ctx, "matmul_generic_kernel");
+}
+
+static int launch_same_path(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, MatmulPath path) {
     if (path == MatmulPath::Rows) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
     if (path == MatmulPath::Gemm)
         return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);
-    const uint64_t total = (uint64_t)a.m * a.n;
-    const dim3 grid((unsigned)((total + kMmThreads - 1) / kMmThreads));
-    DS5_TIMED_LAUNCH(ctx, "matmul_generic_kernel", matmul_generic_kernel, grid, dim3(kMmThreads), 0, ctx->stream, a.x,
-                     a.w, (uint32_t)a.q8, a.out, a.m, a.n, a.k);
-    return ds5_after_launch(ctx, "matmul_generic_kernel");
+    for (uint32_t e = 0; e < a.count; e++)
+        if (a.n[e])
+            if (int rc = launch_generic(ctx, a.x, a.w[e], a.q8, a.out[e], a.m, a.n[e], a.k)) return rc;
+    return DS5_OK;
+}
+
+int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path) {
+    MatmulGroupLaunch g{};
+    g.x = a.x;
+    g.q8 = a.q8;
+    g.m = a.m;
+    g.k = a.k;
+    g.count = 1;
+    g.w[0] = a.w;
+    g.out[0] = a.out;
+    g.n[0] = a.n;
+    return launch_matmul_group(ctx, g, &path);
+}
+
+// One launch for the whole group when every entry takes the same kernel;
+// otherwise each entry on its own kernel, in order.
+int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const MatmulPath* paths) {
+    if (a.m == 0 || a.count == 0) return DS5_OK;
+    bool same = true;
+    for (uint32_t e = 1; e < a.count; e++) same = same && paths[e] == paths[0];
+    if (same) return launch_same_path(ctx, a, paths[0]);
+    for (uint32_t e = 0; e < a.count; e++) {
+        MatmulGroupLaunch one{};
+        one.x = a.x;
+        one.q8 = a.q8;
+        one.m = a.m;
+        one.k = a.k;
+        one.count = 1;
+        one.w[0] = a.w[e];
+        one.out[0] = a.out[e];
+        one.n[0] = a.n[e];
+        if (int rc = launch_same_path(ctx, one, paths[e])) return rc;
+    }
+    return DS5_OK;
 }

@@ -96,6 +96,22 @@ class MatmulArgs(C.Structure):
                 ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
+MATMUL_GROUP_MAX = 4
+
+
+class MatmulGroupArgs(C.Structure):
+    _fields_ = [("x", Buf), ("w_dtype", C.c_uint32), ("m", C.c_uint32), ("k", C.c_uint32), ("count", C.c_uint32),
+                ("w", Buf * MATMUL_GROUP_MAX), ("out", Buf * MATMUL_GROUP_MAX), ("n", C.c_uint32 * MATMUL_GROUP_MAX)]
+
+    @classmethod
+    def of(cls, x: Buf, w_dtype: int, m: int, k: int, entries) -> "MatmulGroupArgs":
+        """entries: (w, out, n) triples, at most MATMUL_GROUP_MAX."""
+        a = cls(x=x, w_dtype=w_dtype, m=m, k=k, count=len(entries))
+        for e, (w, out, n) in enumerate(entries):
+            a.w[e], a.out[e], a.n[e] = w, out, n
+        return a
+
+
 class AttnArgs(C.Structure):
     _fields_ = [("q", Buf), ("k_cache", Buf), ("v_cache", Buf), ("kv_dtype", C.c_uint32), ("out", Buf),
                 ("pos", C.c_uint32), ("n_tokens", C.c_uint32), ("n_q_heads", C.c_uint32),
@@ -143,6 +159,7 @@ SIGNATURES = {
     "ds5_hip_kv_append": ([_P, C.POINTER(KvAppendArgs)], C.c_int),
     "ds5_hip_gqa_attention": ([_P, C.POINTER(AttnArgs)], C.c_int),
     "ds5_hip_matmul": ([_P, C.POINTER(MatmulArgs)], C.c_int),
+    "ds5_hip_matmul_group": ([_P, C.POINTER(MatmulGroupArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
@@ -319,6 +336,12 @@ def gqaAttention(ctx: Ctx, args: AttnArgs) -> None:
 def matmul(ctx: Ctx, args: MatmulArgs) -> None:
     """out[m, n] = x[m, k] . W^T, W f32 or Q8_0 rows (kernels_a.zig:136-163)."""
     ctx.check(LIB.ds5_hip_matmul(ctx.handle, C.byref(args)))
+
+
+def matmulGroup(ctx: Ctx, args: MatmulGroupArgs) -> None:
+    """Up to 4 matmuls on the same x (the engine's q/k/v projections,
+    forward.zig:337-339) in one call; each entry equals ds5_hip_matmul bit for bit."""
+    ctx.check(LIB.ds5_hip_matmul_group(ctx.handle, C.byref(args)))
 
 
 def attentionStep(ctx: Ctx, args: AttentionStepArgs) -> None:

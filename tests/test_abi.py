@@ -36,7 +36,7 @@ STRUCTS = {
     "ds5_buf": "Buf", "ds5_rms_norm_args": "RmsNormArgs", "ds5_rope_args": "RopeArgs",
     "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
     "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
-    "ds5_matmul_args": "MatmulArgs",
+    "ds5_matmul_args": "MatmulArgs", "ds5_matmul_group_args": "MatmulGroupArgs",
 }
 
 
@@ -97,6 +97,24 @@ def test_matmul_preconditions(hip):
                 M(4 * 64 - 4, 2 * 68, q8, 8, 1, 2, 64), M(4 * 64, 2 * 68 - 1, q8, 8, 1, 2, 64),
                 M(4 * 64, 2 * 68, q8, 4, 1, 2, 64), M(4 * 3, 4 * 6 - 4, hip.DTYPE_F32, 8, 1, 2, 3)):
         assert rc_of(hip, "ds5_hip_matmul", bad) == 1
+
+
+def test_matmul_group_preconditions(hip):
+    """count in 1..4, then every entry checked as matmul checks, before anything runs."""
+    q8 = hip.DTYPE_Q8_0
+    G = lambda x, dt, m, k, entries: hip.MatmulGroupArgs.of(B(x), dt, m, k, [(B(w), B(o), n) for w, o, n in entries])
+    ok = (2 * 68, 8, 2)
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 64, [ok, ok, ok])) == 3  # valid: no device
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 64, [])) == 1
+    bad = hip.MatmulGroupArgs.of(B(4 * 64), q8, 1, 64, [])
+    bad.count = 5
+    assert rc_of(hip, "ds5_hip_matmul_group", bad) == 1
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, hip.DTYPE_F16, 1, 64, [ok])) == 2
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 48, [ok])) == 1
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 64, [ok, (2 * 68 - 1, 8, 2)])) == 1  # entry 1's w
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 64, [ok, ok, (2 * 68, 4, 2)])) == 1  # entry 2's out
+    assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64 - 4, q8, 1, 64, [ok])) == 1  # x
+    assert rc_of(hip, "ds5_hip_matmul_group", G(0, q8, 0, 64, [(5 * 68, 0, 5)])) == 0  # no tokens: nothing to do
 
 
 def test_rope_preconditions(hip):

@@ -654,6 +654,57 @@ def test_matmul_paths(ctx, hip, oracle, case, kernel):
         assert np.all(np.abs(got - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)))
 
 
+_GROUP_CASES = {
+    # name: (m, k, rows per entry, weight dtype, byte offset of entry 1's weights, kernel launches)
+    "decode_qkv": (1, 2048, (4096, 512, 512), "q8", 0, {"matmul_rows_kernel": 1}),
+    "prefill_qkv": (40, 1024, (256, 64, 64), "q8", 0, {"matmul_x_split_kernel": 1, "matmul_q8_mfma_kernel": 1}),
+    "prefill_large_tiles": (130, 512, (300, 100), "q8", 0, {"matmul_x_split_kernel": 1, "matmul_q8_mfma_kernel": 1}),
+    "f32_passes": (6, 256, (40, 8, 8, 24), "f32", 0, {"matmul_rows_kernel": 2}),
+    "empty_entry": (2, 512, (33, 0, 17), "q8", 0, {"matmul_rows_kernel": 1}),
+    "mixed_kernels": (4, 256, (20, 9, 7), "q8", 2, {"matmul_rows_kernel": 2, "matmul_generic_kernel": 1}),
+}
+
+
+@pytest.mark.parametrize("case", list(_GROUP_CASES))
+def test_matmul_group_equals_separate_calls(ctx, hip, oracle, case):
+    """ds5_hip_matmul_group: every entry bit-identical to its own ds5_hip_matmul call;
+    one launch when every entry takes the same kernel (the split x made once for the GEMM)."""
+    m, k, ns, dt, w1_off, launches = _GROUP_CASES[case]
+    g = np.random.default_rng(len(case) * 31 + m)
+    x = g.standard_normal((m, k)).astype(np.float32)
+    xb = ctx.from_numpy(x)
+    dtype = hip.DTYPE_Q8_0 if dt == "q8" else hip.DTYPE_F32
+    entries, ws = [], []
+    for e, n in enumerate(ns):
+        wf = g.standard_normal((n, k)).astype(np.float32) * 0.05
+        w = oracle.q8_0_quantize(wf) if dt == "q8" else wf
+        off = w1_off if e == 1 else 0
+        wb = ctx.createBuffer(w.nbytes + off + 4)
+        if w.nbytes:
+            ctx.upload(wb, off, np.ascontiguousarray(w))
+        wv = hip.Buf(wb.handle, wb.offset + off, w.nbytes)
+        entries.append((wv, ctx.createBuffer(max(m * n * 4, 4)), n))
+        ws.append(w)
+    ctx.set_kernel_timing(True)
+    try:
+        hip.matmulGroup(ctx, hip.MatmulGroupArgs.of(xb, dtype, m, k, entries))
+        ctx.submit()
+        counts = {kn: ctx.kernel_time(kn)[0] for kn in ("matmul_rows_kernel", "matmul_x_split_kernel",
+                                                         "matmul_q8_mfma_kernel", "matmul_generic_kernel")}
+    finally:
+        ctx.set_kernel_timing(False)
+    assert {kn: c for kn, c in counts.items() if c} == launches
+    for (wv, ob, n), w in zip(entries, ws):
+        got = ctx.to_numpy(ob, np.float32, (m, n))
+        sep = ctx.createBuffer(max(m * n * 4, 4))
+        hip.matmul(ctx, hip.MatmulArgs(xb, wv, dtype, hip.Buf(sep.handle, sep.offset, m * n * 4), m, n, k))
+        assert np.array_equal(got.view(np.uint32), ctx.to_numpy(sep, np.float32, (m, n)).view(np.uint32))
+        if n:
+            want = oracle.matmul(x, w, oracle.Q8_0 if dt == "q8" else oracle.F32, m, n, k)
+            wf = oracle.q8_0_dequantize(w, k) if dt == "q8" else w
+            assert np.all(np.abs(got - want) <= _dot_bound(x, wf))
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):
