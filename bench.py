@@ -128,6 +128,40 @@ class ProjSweep:
                     self.H.matmul(self.ctx, one)
 
 
+class WoSweep:
+    """The output projection and residual of a decode step (forward.zig:416-418):
+    n_layers of x[1, hidden] += attn[1, n_q_heads*d] . Wo^T, Wo Q8_0 [hidden, n_q_heads*d],
+    as one matmul_add call (fused=True) or as the engine's matmul then add."""
+
+    def __init__(self, H, ctx, layers=48, hidden=2048, hq=32, d=128, seed=5, fused=True):
+        self.H, self.ctx, self.layers, self.fused = H, ctx, layers, fused
+        self.n, self.k = hidden, hq * d
+        nb = self.k // 32
+        g = np.random.default_rng(seed)
+        self.x = ctx.from_numpy(g.standard_normal((1, hidden)).astype(np.float32))  # the residual stream
+        self.args = []
+        for _ in range(layers):
+            attn = ctx.from_numpy(g.standard_normal((1, self.k)).astype(np.float32))
+            w = g.integers(0, 256, (self.n, nb, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.002], np.float16).view(np.uint8)
+            wb = ctx.from_numpy(w.reshape(self.n, nb * 34))
+            if fused:
+                self.args.append(H.MatmulAddArgs(attn, wb, H.DTYPE_Q8_0, self.x, self.x, 1, self.n, self.k))
+            else:
+                proj = ctx.createBuffer(self.n * 4)
+                self.args.append((H.MatmulArgs(attn, wb, H.DTYPE_Q8_0, proj, 1, self.n, self.k),
+                                  H.AddArgs(self.x, proj, self.x, self.n)))
+        self.bytes_per_layer = self.n * nb * 34 + self.k * 4 + 2 * self.n * 4
+
+    def sweep(self):
+        for a in self.args:
+            if self.fused:
+                self.H.matmulAdd(self.ctx, a)
+            else:
+                self.H.matmul(self.ctx, a[0])
+                self.H.add(self.ctx, a[1])
+
+
 class ProjPrefill:
     """The q/k/v projections of a 2048-token prefill (forward.zig:337-339 at m = T):
     x [T, hidden] f32 . W^T for wq [n_q_heads*d, hidden], wk and wv [n_kv_heads*d,
@@ -283,9 +317,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,QKVP",
+    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,WO,QKVP",
                     help="comma list of configs to run (C1 is the headline; QKV / QKVP: the decode / prefill "
-                         "q/k/v projection)")
+                         "q/k/v projections; WO: the decode output projection and residual)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -409,6 +443,28 @@ def main():
             shape="m 1, n 4096 + 512 + 512, k 2048, Q8_0; one grouped call (three matmul calls: us_per_layer_three_calls)")
         log(f"[bench] QKV grouped {us:.3f} us/layer ({QKV_BYTES / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us; "
             f"three calls {us_sep:.3f} us/layer")
+
+    if "WO" in only:
+        log("[bench] WO: decode output projection + residual, Q8_0 wo [2048 x 4096], 48 layers")
+        stepsw = max(5, args.steps // 4)
+        w = WoSweep(H, ctx)
+        elapsed, _ = time_graph(ctx, w, stepsw, 2)
+        us = elapsed / (w.layers * stepsw) * 1e6
+        ns_k, _ = kernel_mean_ns(ctx, w, "matmul_rows_kernel", 2)
+        bpl = w.bytes_per_layer
+        del w
+        w = WoSweep(H, ctx, fused=False)
+        elapsed, _ = time_graph(ctx, w, stepsw, 2)
+        us_sep = elapsed / (w.layers * stepsw) * 1e6
+        del w
+        extra["wo_projection_residual_decode"] = dict(
+            kernel="matmul_rows_kernel", us_per_layer=round(us, 3), gbs=round(bpl / (us * 1e3), 2),
+            kernel_us=round(ns_k / 1e3, 3), kernel_frac=round(bpl / ns_k / HBM_PEAK_GBS, 4),
+            us_per_layer_matmul_then_add=round(us_sep, 3), bytes_per_layer=bpl,
+            shape="m 1, n 2048, k 4096, Q8_0, residual added in the epilogue (matmul then add: "
+                  "us_per_layer_matmul_then_add)")
+        log(f"[bench] WO fused {us:.3f} us/layer ({bpl / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us; "
+            f"matmul then add {us_sep:.3f} us/layer")
 
     if "QKVP" in only:
         log("[bench] QKVP: prefill q/k/v projections, 2048 tokens, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048]")

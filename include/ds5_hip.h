@@ -216,9 +216,40 @@ typedef struct ds5_matmul_args {
 } ds5_matmul_args;
 int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* args);
 
+/* contracts.zig:334-339 AddArgs. out = x + y over n_elems f32 (replaces
+ * kernels_a.zig:223-233 add: the residual adds, forward.zig:418 after the
+ * attention block). x, y, then out too small are ShapeMismatch, in that order;
+ * out may be the same view as x or y. Bit-identical to the reference. */
+typedef struct ds5_add_args {
+    ds5_buf x;
+    ds5_buf y;
+    ds5_buf out;
+    uint64_t n_elems;
+} ds5_add_args;
+int ds5_hip_add(ds5_hip_ctx* ctx, const ds5_add_args* args);
+
 /* ========================================================================
  * 3. Fused extensions (optional decls; the engine uses them via @hasDecl)
  * ======================================================================== */
+
+/* The output projection and residual of forward.zig:416-418 as one call:
+ * out = residual + x . W^T, bit-identical to ds5_hip_matmul(x, w -> proj)
+ * then ds5_hip_add(residual, proj -> out) for the same views, without the
+ * proj buffer or the add launch. Checked as matmul (dtype, k, x, out, w),
+ * then residual too small; residual and out must be 4-byte aligned views
+ * (ShapeMismatch otherwise). out may be the same view as residual (the
+ * engine's x = x + proj); it must not overlap x or w otherwise. */
+typedef struct ds5_matmul_add_args {
+    ds5_buf x;        /* f32 [m, k] */
+    ds5_buf w;        /* w_dtype: n rows of k elements */
+    uint32_t w_dtype; /* DS5_DTYPE_F32 or DS5_DTYPE_Q8_0 */
+    ds5_buf residual; /* f32 [m, n] */
+    ds5_buf out;      /* f32 [m, n] */
+    uint32_t m;
+    uint32_t n;
+    uint32_t k;
+} ds5_matmul_add_args;
+int ds5_hip_matmul_add(ds5_hip_ctx* ctx, const ds5_matmul_add_args* args);
 
 /* The engine's q, k and v projections (forward.zig:337-339: three matmul calls
  * on the same x) as one call: entry e is exactly ds5_hip_matmul(x, w[e],

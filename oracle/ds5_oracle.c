@@ -195,6 +195,22 @@ int ds5o_matmul(const ds5o_matmul_args* a) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* add -- kernels_a.zig:223-233: the three sizes in order, then out = x + y   */
+/* ------------------------------------------------------------------------ */
+
+int ds5o_add(const ds5o_add_args* a) {
+    const uint64_t n = a->n_elems;
+    if (a->x.len < n * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->y.len < n * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->out.len < n * 4) return DS5O_SHAPE_MISMATCH;
+    const float* x = (const float*)view(a->x);
+    const float* y = (const float*)view(a->y);
+    float* out = (float*)view(a->out);
+    for (uint64_t i = 0; i < n; i++) out[i] = x[i] + y[i]; /* element i read before written */
+    return DS5O_OK;
+}
+
+/* ------------------------------------------------------------------------ */
 /* rmsNorm -- kernels_a.zig:68-91                                            */
 /* ------------------------------------------------------------------------ */
 

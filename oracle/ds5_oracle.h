@@ -14,6 +14,7 @@
  *   ds5o_kv_append      src/kernels/cpu/kernels_a.zig:169-217
  *   ds5o_gqa_attention  src/kernels/cpu/kernels_b.zig:29-133
  *   ds5o_matmul         src/kernels/cpu/kernels_a.zig:136-163 (row dot :39-62)
+ *   ds5o_add            src/kernels/cpu/kernels_a.zig:223-233
  *
  * Argument structs mirror src/shared/contracts.zig:210-286 (Buf and the
  * RmsNorm/Rope/KvAppend/Attn args); buffer views honour offset and len as
@@ -86,6 +87,12 @@ typedef struct ds5o_attn_args { /* contracts.zig:272-286 */
 } ds5o_attn_args;
 
 int ds5o_matmul(const ds5o_matmul_args* a);
+
+typedef struct ds5o_add_args { /* contracts.zig:334-339 AddArgs */
+    ds5o_buf x, y, out;        /* f32 [n_elems] each; out may alias x */
+    uint64_t n_elems;
+} ds5o_add_args;
+int ds5o_add(const ds5o_add_args* a);
 int ds5o_rms_norm(const ds5o_rms_norm_args* a);
 int ds5o_rope(const ds5o_rope_args* a);
 int ds5o_kv_append(const ds5o_kv_append_args* a);

@@ -45,6 +45,10 @@ class MatmulArgs(C.Structure):  # contracts.zig:242-250
                 ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
+class AddArgs(C.Structure):  # contracts.zig:334-339
+    _fields_ = [("x", Buf), ("y", Buf), ("out", Buf), ("n_elems", C.c_uint64)]
+
+
 class RmsNormArgs(C.Structure):
     _fields_ = [("x", Buf), ("weight", Buf), ("out", Buf), ("n_rows", C.c_uint32),
                 ("dim", C.c_uint32), ("eps", C.c_float)]
@@ -92,7 +96,8 @@ def lib() -> C.CDLL:
         L = C.CDLL(LIB_PATH)
         for name, argt in (("ds5o_rms_norm", RmsNormArgs), ("ds5o_rope", RopeArgs),
                            ("ds5o_kv_append", KvAppendArgs), ("ds5o_gqa_attention", AttnArgs),
-                           ("ds5o_attention_step", StepArgs), ("ds5o_matmul", MatmulArgs)):
+                           ("ds5o_attention_step", StepArgs), ("ds5o_matmul", MatmulArgs),
+                           ("ds5o_add", AddArgs)):
             f = getattr(L, name)
             f.argtypes = [C.POINTER(argt)]
             f.restype = C.c_int
@@ -129,6 +134,15 @@ def _check(rc: int) -> None:
 # --------------------------------------------------------------------------
 # Op wrappers (reference semantics, f32 numpy in/out, f16 caches as uint16)
 # --------------------------------------------------------------------------
+
+def add(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """out = x + y elementwise in f32 (kernels_a.zig:223-233)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    out = np.empty_like(x)
+    _check(lib().ds5o_add(AddArgs(buf(x), buf(y), buf(out), x.size)))
+    return out
+
 
 def matmul(x: np.ndarray, w: np.ndarray, w_dtype: int, m: int, n: int, k: int) -> np.ndarray:
     """out[m, n] = x[m, k] . W^T (kernels_a.zig:136-163). w: f32 [n, k], or the raw Q8_0

@@ -98,6 +98,7 @@ struct MatmulLaunch {
     bool q8;
     float* out;
     uint32_t m, n, k;
+    const float* res = nullptr;  // out = res + x . W^T when set (res may be out itself)
 };
 // Which kernel runs: the row (GEMV) kernel, the Q8_0 matrix-core GEMM, or the
 // serial one-thread-per-output kernel that takes any shape and alignment.
@@ -113,9 +114,12 @@ struct MatmulGroupLaunch {
     uint32_t count;
     const uint8_t* w[kMatmulGroupMax];
     float* out[kMatmulGroupMax];
+    const float* res[kMatmulGroupMax];  // per entry, as MatmulLaunch::res
     uint32_t n[kMatmulGroupMax];
 };
 int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const MatmulPath* paths);
+// Residual add out = x + y over n f32 elements (any views; out may be x or y).
+int launch_add(ds5_hip_ctx* ctx, const void* x, const void* y, void* out, uint64_t n);
 
 struct RmsNormLaunch {
     const float* x;

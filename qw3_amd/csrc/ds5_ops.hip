@@ -155,6 +155,33 @@ int ds5_hip_matmul(ds5_hip_ctx* ctx, const ds5_matmul_args* a) {
     return launch_matmul(ctx, l, matmul_path(l, a->w.len));
 }
 
+// kernels_a.zig:223-233: x, y, out sizes in order.
+int ds5_hip_add(ds5_hip_ctx* ctx, const ds5_add_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t n = a->n_elems;
+    if (!covers(a->x, n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "add: x too small");
+    if (!covers(a->y, n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "add: y too small");
+    if (!covers(a->out, n * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "add: out too small");
+    if (n == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    return launch_add(ctx, ds5_ptr(a->x), ds5_ptr(a->y), ds5_ptr(a->out), n);
+}
+
+int ds5_hip_matmul_add(ds5_hip_ctx* ctx, const ds5_matmul_add_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (int rc = check_matmul(ctx, "matmul_add", a->x, a->w, a->w_dtype, a->out, a->m, a->n, a->k)) return rc;
+    if (!covers(a->residual, (uint64_t)a->m * a->n * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul_add: residual too small");
+    if ((((uintptr_t)ds5_ptr(a->residual) | (uintptr_t)ds5_ptr(a->out)) & 3u) != 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "matmul_add: residual and out must be 4-byte aligned views");
+    if (a->m == 0 || a->n == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), a->w_dtype == DS5_DTYPE_Q8_0,
+                   (float*)ds5_ptr(a->out), a->m, a->n, a->k};
+    l.res = (const float*)ds5_ptr(a->residual);
+    return launch_matmul(ctx, l, matmul_path(l, a->w.len));
+}
+
 int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
     if (a->count == 0 || a->count > DS5_MATMUL_GROUP_MAX)

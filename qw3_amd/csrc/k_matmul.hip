@@ -63,6 +63,7 @@ __device__ __forceinline__ float q8_dot(const uint32_t (&q)[8], const float (&x)
 struct WeightGroup {
     const uint8_t* w[kMatmulGroupMax];
     float* out[kMatmulGroupMax];
+    const float* res[kMatmulGroupMax];  // residual added to out (nullptr: none)
     uint32_t n[kMatmulGroupMax];
     uint32_t wg0[kMatmulGroupMax];
     uint32_t count;
@@ -76,14 +77,17 @@ template <int MT, int JB, bool Q8>
 __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const WeightGroup g,
                                                                  uint32_t m, uint32_t k, uint32_t m0) {
     // this workgroup's entry (uniform; selected without indexing the argument arrays)
+    // (out may be the residual itself: each output is read, then written, by one lane)
     const uint8_t* __restrict__ w = g.w[0];
-    float* __restrict__ out = g.out[0];
+    float* out = g.out[0];
+    const float* res = g.res[0];
     uint32_t n = g.n[0], wg = blockIdx.x;
 #pragma unroll
     for (int e = 1; e < kMatmulGroupMax; e++)
         if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
             w = g.w[e];
             out = g.out[e];
+            res = g.res[e];
             n = g.n[e];
             wg = blockIdx.x - g.wg0[e];
         }
@@ -188,7 +192,10 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         const float v = wave_allreduce(acc[t], OpAdd{});
-        if (lane == 0 && live && (uint32_t)t < mt) out[(uint64_t)(m0 + t) * n + row] = v;
+        if (lane == 0 && live && (uint32_t)t < mt) {
+            const uint64_t o = (uint64_t)(m0 + t) * n + row;
+            out[o] = res ? res[o] + v : v;  // the reference's add(residual, proj)
+        }
     }
 }
 
@@ -286,15 +293,17 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
                                                                       const WeightGroup g, uint32_t m, uint32_t k) {
-    // this workgroup's entry and column tile (uniform)
+    // this workgroup's entry and column tile (uniform); out may be the residual itself
     const uint8_t* __restrict__ w = g.w[0];
-    float* __restrict__ out = g.out[0];
+    float* out = g.out[0];
+    const float* res = g.res[0];
     uint32_t n = g.n[0], tile = blockIdx.x;
 #pragma unroll
     for (int e = 1; e < kMatmulGroupMax; e++)
         if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
             w = g.w[e];
             out = g.out[e];
+            res = g.res[e];
             n = g.n[e];
             tile = blockIdx.x - g.wg0[e];
         }
@@ -412,7 +421,11 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint32_t col = n0 + wn0 + 16 * j + r16;
-                if (col < n) out[(uint64_t)row * n + col] = __builtin_ldexpf(acc[i][j][e], sh);
+                if (col < n) {
+                    const uint64_t o = (uint64_t)row * n + col;
+                    const float v = __builtin_ldexpf(acc[i][j][e], sh);
+                    out[o] = res ? res[o] + v : v;
+                }
             }
         }
 }
@@ -420,7 +433,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 // Any shape or alignment: one thread per output in the reference's serial order
 // with every product and sum rounded on its own (bit-identical to dotRow).
 __global__ __launch_bounds__(kMmThreads) void matmul_generic_kernel(const float* __restrict__ x, const uint8_t* __restrict__ w,
-                                                                    uint32_t q8, float* __restrict__ out, uint32_t m,
+                                                                    uint32_t q8, float* out, const float* res, uint32_t m,
                                                                     uint32_t n, uint32_t k) {
 #pragma clang fp contract(off)
     const uint64_t i = (uint64_t)blockIdx.x * kMmThreads + threadIdx.x;
@@ -439,7 +452,24 @@ __global__ __launch_bounds__(kMmThreads) void matmul_generic_kernel(const float*
         const float* row = (const float*)w + ni * k;
         for (uint32_t e = 0; e < k; e++) acc += row[e] * xr[e];
     }
-    out[i] = acc;
+    out[i] = res ? res[i] + acc : acc;
+}
+
+// out = x + y elementwise (kernels_a.zig:223-233): out may be x or y. Views that
+// are not all 4-byte aligned go through byte copies.
+__global__ __launch_bounds__(kMmThreads) void add_kernel(const uint8_t* x, const uint8_t* y, uint8_t* out, uint64_t n,
+                                                         uint32_t aligned) {
+    const uint64_t i = (uint64_t)blockIdx.x * kMmThreads + threadIdx.x;
+    if (i >= n) return;
+    if (aligned) {
+        ((float*)out)[i] = ((const float*)x)[i] + ((const float*)y)[i];
+    } else {
+        float a, b;
+        __builtin_memcpy(&a, x + 4 * i, 4);
+        __builtin_memcpy(&b, y + 4 * i, 4);
+        const float c = a + b;
+        __builtin_memcpy(out + 4 * i, &c, 4);
+    }
 }
 
 template <int MT, int JB, bool Q8>
@@ -450,6 +480,7 @@ int launch_rows(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, uint32_t m0) {
     for (uint32_t e = 0; e < a.count; e++) {
         g.w[g.count] = a.w[e];
         g.out[g.count] = a.out[e];
+        g.res[g.count] = a.res[e];
         g.n[g.count] = a.n[e];
         g.wg0[g.count] = wgs;
         wgs += (a.n[e] + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -460,6 +491,7 @@ int launch_rows(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, uint32_t m0) {
                      ctx->stream, a.x, g, a.m, a.k, m0);
     return ds5_after_launch(ctx, "matmul_rows_kernel");
 }
+
 
 // Tokens per pass: up to 4 / JB (the x registers hold MT * JB * 32 floats per lane),
 // and no more than the tokens there are (a 1-token decode runs MT = 1).
@@ -504,6 +536,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     for (uint32_t e = 0; e < a.count; e++) {
         g.w[g.count] = a.w[e];
         g.out[g.count] = a.out[e];
+        g.res[g.count] = a.res[e];
         g.n[g.count] = a.n[e];
         g.wg0[g.count] = tiles;
         tiles += (a.n[e] + BN - 1) / BN;
@@ -542,12 +575,12 @@ MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len) {
     return (out_addr & 3u) == 0 ? MatmulPath::Gemm : MatmulPath::Generic;
 }
 
-static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bool q8, float* out, uint32_t m,
-                          uint32_t n, uint32_t k) {
+static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bool q8, float* out, const float* res,
+                          uint32_t m, uint32_t n, uint32_t k) {
     const uint64_t total = (uint64_t)m * n;
     const dim3 grid((unsigned)((total + kMmThreads - 1) / kMmThreads));
     DS5_TIMED_LAUNCH(ctx, "matmul_generic_kernel", matmul_generic_kernel, grid, dim3(kMmThreads), 0, ctx->stream, x, w,
-                     (uint32_t)q8, out, m, n, k);
+                     (uint32_t)q8, out, res, m, n, k);
     return ds5_after_launch(ctx, "matmul_generic_kernel");
 }
 
@@ -557,7 +590,7 @@ static int launch_same_path(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, Matmul
         return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);
     for (uint32_t e = 0; e < a.count; e++)
         if (a.n[e])
-            if (int rc = launch_generic(ctx, a.x, a.w[e], a.q8, a.out[e], a.m, a.n[e], a.k)) return rc;
+            if (int rc = launch_generic(ctx, a.x, a.w[e], a.q8, a.out[e], a.res[e], a.m, a.n[e], a.k)) return rc;
     return DS5_OK;
 }
 
@@ -570,8 +603,18 @@ int launch_matmul(ds5_hip_ctx* ctx, const MatmulLaunch& a, MatmulPath path) {
     g.count = 1;
     g.w[0] = a.w;
     g.out[0] = a.out;
+    g.res[0] = a.res;
     g.n[0] = a.n;
     return launch_matmul_group(ctx, g, &path);
+}
+
+int launch_add(ds5_hip_ctx* ctx, const void* x, const void* y, void* out, uint64_t n) {
+    if (n == 0) return DS5_OK;
+    const uint32_t aligned = (((uintptr_t)x | (uintptr_t)y | (uintptr_t)out) & 3u) == 0;
+    const dim3 grid((unsigned)((n + kMmThreads - 1) / kMmThreads));
+    DS5_TIMED_LAUNCH(ctx, "add_kernel", add_kernel, grid, dim3(kMmThreads), 0, ctx->stream, (const uint8_t*)x,
+                     (const uint8_t*)y, (uint8_t*)out, n, aligned);
+    return ds5_after_launch(ctx, "add_kernel");
 }
 
 // One launch for the whole group when every entry takes the same kernel;
@@ -590,6 +633,7 @@ int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const Matm
         one.count = 1;
         one.w[0] = a.w[e];
         one.out[0] = a.out[e];
+        one.res[0] = a.res[e];
         one.n[0] = a.n[e];
         if (int rc = launch_same_path(ctx, one, paths[e])) return rc;
     }

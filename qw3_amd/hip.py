@@ -96,6 +96,15 @@ class MatmulArgs(C.Structure):
                 ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
+class AddArgs(C.Structure):
+    _fields_ = [("x", Buf), ("y", Buf), ("out", Buf), ("n_elems", C.c_uint64)]
+
+
+class MatmulAddArgs(C.Structure):
+    _fields_ = [("x", Buf), ("w", Buf), ("w_dtype", C.c_uint32), ("residual", Buf), ("out", Buf),
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
+
+
 MATMUL_GROUP_MAX = 4
 
 
@@ -160,6 +169,8 @@ SIGNATURES = {
     "ds5_hip_gqa_attention": ([_P, C.POINTER(AttnArgs)], C.c_int),
     "ds5_hip_matmul": ([_P, C.POINTER(MatmulArgs)], C.c_int),
     "ds5_hip_matmul_group": ([_P, C.POINTER(MatmulGroupArgs)], C.c_int),
+    "ds5_hip_add": ([_P, C.POINTER(AddArgs)], C.c_int),
+    "ds5_hip_matmul_add": ([_P, C.POINTER(MatmulAddArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
@@ -336,6 +347,16 @@ def gqaAttention(ctx: Ctx, args: AttnArgs) -> None:
 def matmul(ctx: Ctx, args: MatmulArgs) -> None:
     """out[m, n] = x[m, k] . W^T, W f32 or Q8_0 rows (kernels_a.zig:136-163)."""
     ctx.check(LIB.ds5_hip_matmul(ctx.handle, C.byref(args)))
+
+
+def add(ctx: Ctx, args: AddArgs) -> None:
+    """out = x + y over n_elems f32 (kernels_a.zig:223-233); out may alias x or y."""
+    ctx.check(LIB.ds5_hip_add(ctx.handle, C.byref(args)))
+
+
+def matmulAdd(ctx: Ctx, args: MatmulAddArgs) -> None:
+    """out = residual + x . W^T (forward.zig:416-418's matmul then add, one launch)."""
+    ctx.check(LIB.ds5_hip_matmul_add(ctx.handle, C.byref(args)))
 
 
 def matmulGroup(ctx: Ctx, args: MatmulGroupArgs) -> None:

@@ -36,7 +36,8 @@ STRUCTS = {
     "ds5_buf": "Buf", "ds5_rms_norm_args": "RmsNormArgs", "ds5_rope_args": "RopeArgs",
     "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
     "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
-    "ds5_matmul_args": "MatmulArgs", "ds5_matmul_group_args": "MatmulGroupArgs",
+    "ds5_matmul_args": "MatmulArgs", "ds5_matmul_group_args": "MatmulGroupArgs", "ds5_add_args": "AddArgs",
+    "ds5_matmul_add_args": "MatmulAddArgs",
 }
 
 
@@ -115,6 +116,27 @@ def test_matmul_group_preconditions(hip):
     assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64, q8, 1, 64, [ok, ok, (2 * 68, 4, 2)])) == 1  # entry 2's out
     assert rc_of(hip, "ds5_hip_matmul_group", G(4 * 64 - 4, q8, 1, 64, [ok])) == 1  # x
     assert rc_of(hip, "ds5_hip_matmul_group", G(0, q8, 0, 64, [(5 * 68, 0, 5)])) == 0  # no tokens: nothing to do
+
+
+def test_add_preconditions(hip):
+    """kernels_a.zig:225-227: x, y, out sizes in order."""
+    A = lambda x, y, o, n: hip.AddArgs(B(x), B(y), B(o), n)
+    assert rc_of(hip, "ds5_hip_add", A(40, 40, 40, 10)) == 3
+    assert rc_of(hip, "ds5_hip_add", A(0, 0, 0, 0)) == 0
+    for bad in (A(36, 40, 40, 10), A(40, 36, 40, 10), A(40, 40, 36, 10)):
+        assert rc_of(hip, "ds5_hip_add", bad) == 1
+
+
+def test_matmul_add_preconditions(hip):
+    """matmul's checks, then the residual's size, then 4-byte aligned residual / out."""
+    q8 = hip.DTYPE_Q8_0
+    M = lambda x, w, dt, r, o, m, n, k: hip.MatmulAddArgs(B(x), B(w), dt, r if isinstance(r, hip.Buf) else B(r),
+                                                          B(o), m, n, k)
+    assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, 8, 8, 1, 2, 64)) == 3
+    assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, hip.DTYPE_F16, 8, 8, 1, 2, 64)) == 2
+    assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, 8, 8, 1, 2, 48)) == 1
+    assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, 4, 8, 1, 2, 64)) == 1  # residual
+    assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, hip.Buf(FAKE, 2, 8), 8, 1, 2, 64)) == 1  # unaligned
 
 
 def test_rope_preconditions(hip):

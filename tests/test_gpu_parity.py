@@ -705,6 +705,49 @@ def test_matmul_group_equals_separate_calls(ctx, hip, oracle, case):
             assert np.all(np.abs(got - want) <= _dot_bound(x, wf))
 
 
+@pytest.mark.parametrize("n,off", [(97, 0), (2048 * 3, 0), (1000, 2)])
+def test_add_bit_exact(ctx, hip, oracle, n, off):
+    """kernels_a.zig:703-724 through the GPU: out = x + y bit for bit (specials included),
+    out aliasing x; views at a 2-byte offset take the byte-copy path."""
+    g = np.random.default_rng(n + off)
+    x = g.standard_normal(n).astype(np.float32)
+    y = g.standard_normal(n).astype(np.float32)
+    x[:5] = [np.inf, -np.inf, np.nan, -0.0, 3.4e38]
+    y[:5] = [-np.inf, 1.0, 1.0, -0.0, 3.4e38]
+    want = oracle.add(x, y)
+    xb, yb = ctx.createBuffer(4 * n + off), ctx.createBuffer(4 * n + off)
+    ctx.upload(xb, off, x)
+    ctx.upload(yb, off, y)
+    xv, yv = hip.Buf(xb.handle, xb.offset + off, 4 * n), hip.Buf(yb.handle, yb.offset + off, 4 * n)
+    hip.add(ctx, hip.AddArgs(xv, yv, xv, n))
+    got = ctx.to_numpy(xb, np.float32, (n,), offset=off)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n,k,w_off", [(1, 2048, 4096, 0), (3, 300, 2048, 0), (40, 200, 1024, 0), (2, 17, 256, 2)])
+def test_matmul_add_equals_matmul_then_add(ctx, hip, oracle, m, n, k, w_off):
+    """forward.zig:416-418: residual + x . Wo^T in one call equals ds5_hip_matmul into a
+    projection buffer then ds5_hip_add, bit for bit, in place on the residual (row
+    kernel, GEMM, and the serial kernel for weights at a 2-byte offset)."""
+    g = np.random.default_rng(m * 13 + n + w_off)
+    rows = oracle.q8_0_quantize(g.standard_normal((n, k)).astype(np.float32) * 0.05)
+    x = g.standard_normal((m, k)).astype(np.float32)
+    r = g.standard_normal((m, n)).astype(np.float32)
+    xb = ctx.from_numpy(x)
+    wb = ctx.createBuffer(rows.nbytes + w_off + 4)
+    ctx.upload(wb, w_off, rows)
+    wv = hip.Buf(wb.handle, wb.offset + w_off, rows.nbytes)
+    res = ctx.from_numpy(r)
+    hip.matmulAdd(ctx, hip.MatmulAddArgs(xb, wv, hip.DTYPE_Q8_0, res, res, m, n, k))
+    fused = ctx.to_numpy(res, np.float32, (m, n))
+    proj, res2 = ctx.createBuffer(m * n * 4), ctx.from_numpy(r)
+    hip.matmul(ctx, hip.MatmulArgs(xb, wv, hip.DTYPE_Q8_0, proj, m, n, k))
+    hip.add(ctx, hip.AddArgs(res2, proj, res2, m * n))
+    assert np.array_equal(fused.view(np.uint32), ctx.to_numpy(res2, np.float32, (m, n)).view(np.uint32))
+    want = oracle.add(r, oracle.matmul(x, rows, oracle.Q8_0, m, n, k))
+    assert np.all(np.abs(fused - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)) + 1e-6 * np.abs(r))
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):

@@ -484,3 +484,30 @@ def test_matmul_rejections(oracle):
     assert call(x, w, oracle.Q8_0, 1, 3, 64) == oracle.SHAPE_MISMATCH  # w too small (and out)
     assert call(x, w, oracle.Q8_0, 1, 2, 64, np.zeros(1, np.float32)) == oracle.SHAPE_MISMATCH
     assert call(x, w, oracle.Q8_0, 1, 2, 64) == oracle.OK
+
+
+def test_add_matches_ieee_and_aliases(oracle):
+    """kernels_a.zig:703-724: out = x + y elementwise (an odd size), out aliasing x
+    allowed; f32 addition is exactly numpy's IEEE float32 add, specials included."""
+    g = np.random.default_rng(11)
+    x = g.standard_normal(97).astype(np.float32)
+    y = g.standard_normal(97).astype(np.float32)
+    x[:6] = [np.inf, -np.inf, np.nan, 0.0, -0.0, 3.4e38]
+    y[:6] = [-np.inf, 1.0, 1.0, -0.0, -0.0, 3.4e38]
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = x + y
+    assert np.array_equal(oracle.add(x, y), want, equal_nan=True)
+    xa = x.copy()
+    assert oracle.lib().ds5o_add(oracle.AddArgs(oracle.buf(xa), oracle.buf(y), oracle.buf(xa), 97)) == oracle.OK
+    assert np.array_equal(xa.view(np.uint32), want.view(np.uint32))
+
+
+def test_add_rejections(oracle):
+    """kernels_a.zig:225-227: x, then y, then out too small."""
+    a, b = np.zeros(8, np.float32), np.zeros(7, np.float32)
+    call = lambda x, y, o, n: oracle.lib().ds5o_add(oracle.AddArgs(oracle.buf(x), oracle.buf(y), oracle.buf(o), n))
+    assert call(a, a, a, 8) == oracle.OK
+    assert call(b, a, a, 8) == oracle.SHAPE_MISMATCH
+    assert call(a, b, a, 8) == oracle.SHAPE_MISMATCH
+    assert call(a, a, b, 8) == oracle.SHAPE_MISMATCH
+    assert call(b, b, b, 0) == oracle.OK
