@@ -165,6 +165,9 @@ static float dot_row(const float* x, const uint8_t* row, uint32_t w_dtype, uint6
     if (w_dtype == DS5O_F32) {
         const float* w = (const float*)row;
         for (uint64_t i = 0; i < k; i++) acc += w[i] * x[i];
+    } else if (w_dtype == DS5O_F16) { /* kernels_c.zig:47-52 (router weights only) */
+        for (uint64_t i = 0; i < k; i++)
+            acc += ds5o_f16_to_f32((uint16_t)(row[2 * i] | (row[2 * i + 1] << 8))) * x[i];
     } else { /* DS5O_Q8_0 */
         for (uint64_t b = 0; b < k / 32; b++) {
             const uint8_t* blk = row + b * 34;
@@ -191,6 +194,124 @@ int ds5o_matmul(const ds5o_matmul_args* a) {
     float* out = (float*)view(a->out);
     for (uint64_t mi = 0; mi < m; mi++)
         for (uint64_t ni = 0; ni < n; ni++) out[mi * n + ni] = dot_row(x + mi * k, w + ni * row_bytes, a->w_dtype, k);
+    return DS5O_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* routerTopK -- kernels_c.zig:80-155                                         */
+/* logits = x . W^T (f32, serial), softmax over all experts, the top_k largest */
+/* probabilities descending with ties to the lower id (ascending scan, strict  */
+/* >), then optionally divided by their sum.                                   */
+/* ------------------------------------------------------------------------ */
+
+int ds5o_router_topk(const ds5o_router_args* a) {
+    if (a->w_dtype != DS5O_F32 && a->w_dtype != DS5O_F16 && a->w_dtype != DS5O_Q8_0) return DS5O_UNSUPPORTED_DTYPE;
+    const uint64_t T = a->n_tokens, dim = a->dim, E = a->n_experts, K = a->top_k;
+    const uint64_t block = a->w_dtype == DS5O_Q8_0 ? 32 : 1;
+    if (K == 0 || K > E) return DS5O_SHAPE_MISMATCH;
+    if (dim == 0 || dim % block != 0) return DS5O_SHAPE_MISMATCH;
+    if (a->out_ids_len != T * K) return DS5O_SHAPE_MISMATCH;
+    if (a->out_weights_len != T * K) return DS5O_SHAPE_MISMATCH;
+    if (a->x.len < T * dim * 4) return DS5O_SHAPE_MISMATCH;
+    const uint64_t row_bytes = a->w_dtype == DS5O_Q8_0 ? dim / 32 * 34 : dim * (a->w_dtype == DS5O_F16 ? 2 : 4);
+    if (a->w.len < E * row_bytes) return DS5O_SHAPE_MISMATCH;
+
+    float* probs = (float*)malloc(E * sizeof(float));
+    unsigned char* taken = (unsigned char*)malloc(E);
+    if (!probs || !taken) {
+        free(probs);
+        free(taken);
+        return DS5O_OUT_OF_MEMORY;
+    }
+    const float* x = (const float*)view(a->x);
+    const uint8_t* w = (const uint8_t*)view(a->w);
+    for (uint64_t t = 0; t < T; t++) {
+        const float* xr = x + t * dim;
+        float mx = -INFINITY;
+        for (uint64_t e = 0; e < E; e++) {
+            probs[e] = dot_row(xr, w + e * row_bytes, a->w_dtype, dim);
+            mx = fmaxf(mx, probs[e]);
+        }
+        float sum = 0.0f;
+        for (uint64_t e = 0; e < E; e++) {
+            probs[e] = expf(probs[e] - mx);
+            sum += probs[e];
+        }
+        const float inv_sum = 1.0f / sum;
+        for (uint64_t e = 0; e < E; e++) probs[e] *= inv_sum;
+        memset(taken, 0, E);
+        float picked = 0.0f;
+        for (uint64_t j = 0; j < K; j++) {
+            uint64_t best = 0;
+            float best_p = -1.0f;
+            for (uint64_t e = 0; e < E; e++)
+                if (!taken[e] && probs[e] > best_p) {
+                    best = e;
+                    best_p = probs[e];
+                }
+            taken[best] = 1;
+            a->out_ids[t * K + j] = (uint16_t)best;
+            a->out_weights[t * K + j] = best_p;
+            picked += best_p;
+        }
+        if (a->norm_topk_prob) {
+            const float inv = 1.0f / picked;
+            for (uint64_t j = 0; j < K; j++) a->out_weights[t * K + j] *= inv;
+        }
+    }
+    free(probs);
+    free(taken);
+    return DS5O_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* expertMlpSwiglu -- kernels_c.zig:157-214                                   */
+/* per pair, in list order: h = silu(gate . x) * (up . x) over ffn_dim, then   */
+/* out[token] += weight * (down . h); silu(v) = v / (1 + exp(-v)). A pair out  */
+/* of range is ShapeMismatch when it is reached (earlier pairs already added). */
+/* ------------------------------------------------------------------------ */
+
+int ds5o_expert_mlp_swiglu(const ds5o_expert_mlp_args* a) {
+    if (a->w_dtype != DS5O_F32 && a->w_dtype != DS5O_Q8_0) return DS5O_UNSUPPORTED_DTYPE;
+    const uint64_t dim = a->dim, ffn = a->ffn_dim, T = a->n_tokens;
+    const uint64_t block = a->w_dtype == DS5O_Q8_0 ? 32 : 1;
+    if (dim == 0 || ffn == 0) return DS5O_SHAPE_MISMATCH;
+    if (dim % block != 0 || ffn % block != 0) return DS5O_SHAPE_MISMATCH;
+    if (a->x.len < T * dim * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->out.len < T * dim * 4) return DS5O_SHAPE_MISMATCH;
+    const uint64_t row_h = a->w_dtype == DS5O_Q8_0 ? dim / 32 * 34 : dim * 4;  /* gate / up rows */
+    const uint64_t row_f = a->w_dtype == DS5O_Q8_0 ? ffn / 32 * 34 : ffn * 4;  /* down rows */
+    const uint64_t gate_stride = row_h * ffn, down_stride = row_f * dim;
+    if (a->gate.len < a->n_experts * gate_stride) return DS5O_SHAPE_MISMATCH;
+    if (a->up.len < a->n_experts * gate_stride) return DS5O_SHAPE_MISMATCH;
+    if (a->down.len < a->n_experts * down_stride) return DS5O_SHAPE_MISMATCH;
+
+    float* h = (float*)malloc((ffn ? ffn : 1) * sizeof(float));
+    if (!h) return DS5O_OUT_OF_MEMORY;
+    const float* x = (const float*)view(a->x);
+    float* out = (float*)view(a->out);
+    const uint8_t* gate = (const uint8_t*)view(a->gate);
+    const uint8_t* up = (const uint8_t*)view(a->up);
+    const uint8_t* down = (const uint8_t*)view(a->down);
+    for (uint64_t p = 0; p < a->n_pairs; p++) {
+        const ds5o_pair pr = a->pairs[p];
+        if (pr.token >= T || pr.expert >= a->n_experts) {
+            free(h);
+            return DS5O_SHAPE_MISMATCH;
+        }
+        const float* xr = x + (uint64_t)pr.token * dim;
+        const uint8_t* g = gate + (uint64_t)pr.expert * gate_stride;
+        const uint8_t* u = up + (uint64_t)pr.expert * gate_stride;
+        const uint8_t* d = down + (uint64_t)pr.expert * down_stride;
+        for (uint64_t j = 0; j < ffn; j++) {
+            const float gv = dot_row(xr, g + j * row_h, a->w_dtype, dim);
+            const float uv = dot_row(xr, u + j * row_h, a->w_dtype, dim);
+            h[j] = gv / (1.0f + expf(-gv)) * uv;
+        }
+        float* orow = out + (uint64_t)pr.token * dim;
+        for (uint64_t i = 0; i < dim; i++) orow[i] += pr.weight * dot_row(h, d + i * row_f, a->w_dtype, ffn);
+    }
+    free(h);
     return DS5O_OK;
 }
 

@@ -15,6 +15,8 @@
  *   ds5o_gqa_attention  src/kernels/cpu/kernels_b.zig:29-133
  *   ds5o_matmul         src/kernels/cpu/kernels_a.zig:136-163 (row dot :39-62)
  *   ds5o_add            src/kernels/cpu/kernels_a.zig:223-233
+ *   ds5o_router_topk    src/kernels/cpu/kernels_c.zig:80-155
+ *   ds5o_expert_mlp_swiglu  src/kernels/cpu/kernels_c.zig:157-214
  *
  * Argument structs mirror src/shared/contracts.zig:210-286 (Buf and the
  * RmsNorm/Rope/KvAppend/Attn args); buffer views honour offset and len as
@@ -93,6 +95,36 @@ typedef struct ds5o_add_args { /* contracts.zig:334-339 AddArgs */
     uint64_t n_elems;
 } ds5o_add_args;
 int ds5o_add(const ds5o_add_args* a);
+
+typedef struct ds5o_router_args { /* contracts.zig:293-304 RouterArgs */
+    ds5o_buf x;                   /* f32 [n_tokens, dim] */
+    ds5o_buf w;                   /* w_dtype (f32, f16, q8_0): n_experts rows of dim */
+    uint32_t w_dtype;
+    uint32_t n_tokens, dim, n_experts, top_k;
+    uint32_t norm_topk_prob;      /* bool */
+    uint16_t* out_ids;            /* host [n_tokens * top_k] */
+    uint64_t out_ids_len;
+    float* out_weights;           /* host [n_tokens * top_k] */
+    uint64_t out_weights_len;
+} ds5o_router_args;
+int ds5o_router_topk(const ds5o_router_args* a);
+
+typedef struct ds5o_pair { /* contracts.zig:308-312 PairDispatch (extern struct) */
+    uint32_t token;
+    uint32_t expert;
+    float weight;
+} ds5o_pair;
+
+typedef struct ds5o_expert_mlp_args { /* contracts.zig:319-331 ExpertMlpArgs */
+    ds5o_buf x;                       /* f32 [n_tokens, dim] */
+    ds5o_buf gate, up, down;          /* expert banks: gate/up n_experts x ffn rows of dim, down x dim rows of ffn */
+    uint32_t w_dtype;                 /* f32 or q8_0 */
+    const ds5o_pair* pairs;           /* host */
+    uint64_t n_pairs;
+    ds5o_buf out;                     /* f32 [n_tokens, dim], accumulated into */
+    uint32_t n_tokens, dim, ffn_dim, n_experts;
+} ds5o_expert_mlp_args;
+int ds5o_expert_mlp_swiglu(const ds5o_expert_mlp_args* a);
 int ds5o_rms_norm(const ds5o_rms_norm_args* a);
 int ds5o_rope(const ds5o_rope_args* a);
 int ds5o_kv_append(const ds5o_kv_append_args* a);

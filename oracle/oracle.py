@@ -49,6 +49,26 @@ class AddArgs(C.Structure):  # contracts.zig:334-339
     _fields_ = [("x", Buf), ("y", Buf), ("out", Buf), ("n_elems", C.c_uint64)]
 
 
+class RouterArgs(C.Structure):  # contracts.zig:293-304
+    _fields_ = [("x", Buf), ("w", Buf), ("w_dtype", C.c_uint32), ("n_tokens", C.c_uint32), ("dim", C.c_uint32),
+                ("n_experts", C.c_uint32), ("top_k", C.c_uint32), ("norm_topk_prob", C.c_uint32),
+                ("out_ids", C.POINTER(C.c_uint16)), ("out_ids_len", C.c_uint64),
+                ("out_weights", C.POINTER(C.c_float)), ("out_weights_len", C.c_uint64)]
+
+
+class Pair(C.Structure):  # contracts.zig:308-312 PairDispatch
+    _fields_ = [("token", C.c_uint32), ("expert", C.c_uint32), ("weight", C.c_float)]
+
+
+PAIR_DTYPE = np.dtype([("token", np.uint32), ("expert", np.uint32), ("weight", np.float32)])
+
+
+class ExpertMlpArgs(C.Structure):  # contracts.zig:319-331
+    _fields_ = [("x", Buf), ("gate", Buf), ("up", Buf), ("down", Buf), ("w_dtype", C.c_uint32),
+                ("pairs", C.c_void_p), ("n_pairs", C.c_uint64), ("out", Buf), ("n_tokens", C.c_uint32),
+                ("dim", C.c_uint32), ("ffn_dim", C.c_uint32), ("n_experts", C.c_uint32)]
+
+
 class RmsNormArgs(C.Structure):
     _fields_ = [("x", Buf), ("weight", Buf), ("out", Buf), ("n_rows", C.c_uint32),
                 ("dim", C.c_uint32), ("eps", C.c_float)]
@@ -97,7 +117,8 @@ def lib() -> C.CDLL:
         for name, argt in (("ds5o_rms_norm", RmsNormArgs), ("ds5o_rope", RopeArgs),
                            ("ds5o_kv_append", KvAppendArgs), ("ds5o_gqa_attention", AttnArgs),
                            ("ds5o_attention_step", StepArgs), ("ds5o_matmul", MatmulArgs),
-                           ("ds5o_add", AddArgs)):
+                           ("ds5o_add", AddArgs), ("ds5o_router_topk", RouterArgs),
+                           ("ds5o_expert_mlp_swiglu", ExpertMlpArgs)):
             f = getattr(L, name)
             f.argtypes = [C.POINTER(argt)]
             f.restype = C.c_int
@@ -141,6 +162,41 @@ def add(x: np.ndarray, y: np.ndarray) -> np.ndarray:
     y = np.ascontiguousarray(y, dtype=np.float32)
     out = np.empty_like(x)
     _check(lib().ds5o_add(AddArgs(buf(x), buf(y), buf(out), x.size)))
+    return out
+
+
+def router_topk(x, w, w_dtype: int, n_tokens: int, dim: int, n_experts: int, top_k: int, norm_topk_prob: bool):
+    """(ids uint16 [n_tokens, top_k], weights f32 [n_tokens, top_k]) (kernels_c.zig:80-155)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w)
+    ids = np.zeros((n_tokens, top_k), np.uint16)
+    wts = np.zeros((n_tokens, top_k), np.float32)
+    _check(lib().ds5o_router_topk(RouterArgs(
+        buf(x), buf(w), w_dtype, n_tokens, dim, n_experts, top_k, int(norm_topk_prob),
+        ids.ctypes.data_as(C.POINTER(C.c_uint16)), ids.size, wts.ctypes.data_as(C.POINTER(C.c_float)), wts.size)))
+    return ids, wts
+
+
+def pairs_from_router(ids: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """Token-major dispatch pairs from a router's outputs (kernels_c.zig:361-373)."""
+    T, K = ids.shape
+    p = np.zeros(T * K, PAIR_DTYPE)
+    p["token"] = np.repeat(np.arange(T, dtype=np.uint32), K)
+    p["expert"] = ids.reshape(-1)
+    p["weight"] = weights.reshape(-1)
+    return p
+
+
+def expert_mlp_swiglu(x, gate, up, down, w_dtype: int, pairs: np.ndarray, n_tokens: int, dim: int, ffn_dim: int,
+                      n_experts: int, out=None) -> np.ndarray:
+    """out[token] += weight * down(silu(gate(x)) * up(x)) per pair (kernels_c.zig:157-214);
+    out starts at zero unless given."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros((n_tokens, dim), np.float32) if out is None else np.array(out, np.float32, copy=True)
+    pairs = np.ascontiguousarray(pairs, dtype=PAIR_DTYPE)
+    _check(lib().ds5o_expert_mlp_swiglu(ExpertMlpArgs(
+        buf(x), buf(np.ascontiguousarray(gate)), buf(np.ascontiguousarray(up)), buf(np.ascontiguousarray(down)),
+        w_dtype, pairs.ctypes.data if pairs.size else None, pairs.size, buf(out), n_tokens, dim, ffn_dim, n_experts)))
     return out
 
 
@@ -296,14 +352,15 @@ def load_ds5t(path: str) -> Tensor:
     if version != 1:
         raise ValueError("BadVersion")
     ne = (ne0, ne1, ne2, ne3)
-    if dtype == Q8_0:  # raw rows of 34-byte blocks: uint8 [rows, ne0 / 32 * 34]
-        if ne0 % 32 or n_dims != 2:
+    if dtype == Q8_0:  # raw rows of 34-byte blocks: uint8 [rows, ne0 / 32 * 34] (3-D banks: rows = ne1 * ne2)
+        if ne0 % 32 or n_dims not in (2, 3):
             raise ValueError("SizeMismatch")
         row_bytes = ne0 // 32 * 34
-        if row_bytes * ne1 != data_bytes or len(raw) < 64 + data_bytes:
+        rows = ne1 * (ne2 if n_dims == 3 else 1)
+        if row_bytes * rows != data_bytes or len(raw) < 64 + data_bytes:
             raise ValueError("SizeMismatch")
         arr = np.frombuffer(raw, dtype=np.uint8, count=data_bytes, offset=64).copy()
-        return Tensor(dtype, ne[:n_dims], arr.reshape(ne1, row_bytes))
+        return Tensor(dtype, ne[:n_dims], arr.reshape(rows, row_bytes))
     if dtype not in _NP_DTYPE:
         raise ValueError(f"BadDtype {dtype}")
     n = ne0 * ne1 * ne2 * ne3

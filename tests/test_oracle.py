@@ -12,6 +12,8 @@
 """
 import math
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -37,6 +39,8 @@ def test_fixture_case_counts(oracle):
     assert len(_cases(oracle, "rope")) == 3
     assert len(_cases(oracle, "attention")) == 6
     assert len(_cases(oracle, "matmul_quant")) == 4
+    assert len(_cases(oracle, "router")) == 3  # kernels_c.zig:317
+    assert len(_cases(oracle, "expert_mlp")) == 3  # kernels_c.zig:400
 
 
 @pytest.mark.parametrize("i", range(4))
@@ -511,3 +515,186 @@ def test_add_rejections(oracle):
     assert call(a, b, a, 8) == oracle.SHAPE_MISMATCH
     assert call(a, a, b, 8) == oracle.SHAPE_MISMATCH
     assert call(b, b, b, 0) == oracle.OK
+
+
+# ---------------------------------------------------------------------------
+# MoE router and expert MLP (kernels_c.zig)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("i", range(3))
+def test_router_fixtures(oracle, i):
+    """kernels_c.zig:250-318: expert ids 100% exact, gate weights within the case tolerance."""
+    c = _cases(oracle, "router")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w = _t(oracle, c, "input"), _t(oracle, c, "weight")
+    want_ids, want_w = _t(oracle, c, "expert_ids"), _t(oracle, c, "gate_weights")
+    assert want_ids.ne == (p["top_k"], p["n_tokens"]) and p["w_dtype"] == "f32"
+    ids, wts = oracle.router_topk(x.data, w.data, oracle.F32, p["n_tokens"], p["dim"], p["n_experts"], p["top_k"],
+                                  p["norm_topk_prob"])
+    assert np.array_equal(ids.astype(np.int32), want_ids.data.reshape(ids.shape))
+    r = oracle.compare(want_w.data.reshape(wts.shape), wts, tol["atol"], tol["rtol"])
+    assert r.passed, r
+
+
+def test_router_raw_probabilities(oracle):
+    """kernels_c.zig:403-439: norm_topk_prob = false keeps the softmax over all experts."""
+    x = np.array([[1, 0, 0, 0]], np.float32)
+    w = np.array([[2, 0, 0, 0], [0, 9, 9, 9], [1, 0, 0, 0], [-1, 0, 0, 0]], np.float32)
+    ids, wts = oracle.router_topk(x, w, oracle.F32, 1, 4, 4, 2, False)
+    assert ids.tolist() == [[0, 2]]
+    denom = sum(np.exp(np.float64(l) - 2.0) for l in (2, 0, 1, -1))
+    assert abs(wts[0, 0] - 1.0 / denom) <= 1e-6 and abs(wts[0, 1] - np.exp(-1.0) / denom) <= 1e-6
+    assert wts.sum() < 1.0
+
+
+def test_router_tie_break_lower_id(oracle):
+    """kernels_c.zig:441-477: equal probabilities pick the lower expert id."""
+    x = np.array([[1, 0, 0, 0]], np.float32)
+    w = np.array([[1, 0, 0, 0], [3, 0, 0, 0], [3, 0, 0, 0], [0, 0, 0, 0]], np.float32)
+    ids, wts = oracle.router_topk(x, w, oracle.F32, 1, 4, 4, 3, True)
+    assert ids.tolist() == [[1, 2, 0]] and wts[0, 0] == wts[0, 1]
+    assert abs(wts.sum() - 1.0) <= 1e-6
+
+
+def test_router_f16_and_q8_0_agree_with_f32(oracle):
+    """kernels_c.zig:479-548: f16 and Q8_0 weights give the ids of their dequantised f32 rows
+    and weights within 1e-6 (scale * q exact in f16 here)."""
+    g = np.random.default_rng(7)
+    dim, E = 32, 4
+    q8 = np.zeros((E, 34), np.uint8)
+    wf = np.zeros((E, dim), np.float32)
+    for e in range(E):
+        sc = np.float16(0.01 + 0.02 * e)
+        q = g.integers(-127, 128, dim).astype(np.int8)
+        q8[e, :2] = np.array([sc], np.float16).view(np.uint8)
+        q8[e, 2:] = q.view(np.uint8)
+        wf[e] = np.float32(sc) * q.astype(np.float32)
+    x = g.standard_normal((1, dim)).astype(np.float32)
+    i32, w32 = oracle.router_topk(x, wf, oracle.F32, 1, dim, E, 2, True)
+    i8, w8 = oracle.router_topk(x, q8, oracle.Q8_0, 1, dim, E, 2, True)
+    i16, w16 = oracle.router_topk(x, wf.astype(np.float16).view(np.uint16), oracle.F16, 1, dim, E, 2, True)
+    assert np.array_equal(i32, i8) and np.array_equal(i32, i16)
+    assert np.all(np.abs(w32 - w8) <= 1e-6) and np.all(np.abs(w32 - w16) <= 1e-6)
+
+
+def test_router_matches_float64(oracle):
+    """Seeded routers against a float64 softmax / top-k of the same logits (ids exact where
+    the float64 ranking has no near-ties; weights within 1e-5)."""
+    g = np.random.default_rng(3)
+    T, dim, E, K = 9, 64, 16, 4
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    w = g.standard_normal((E, dim)).astype(np.float32)
+    for norm in (True, False):
+        ids, wts = oracle.router_topk(x, w, oracle.F32, T, dim, E, K, norm)
+        lg = x.astype(np.float64) @ w.astype(np.float64).T
+        pr = np.exp(lg - lg.max(1, keepdims=True))
+        pr /= pr.sum(1, keepdims=True)
+        order = np.argsort(-pr, axis=1, kind="stable")[:, :K]
+        assert np.array_equal(ids, order)
+        top = np.take_along_axis(pr, order, 1)
+        if norm:
+            top = top / top.sum(1, keepdims=True)
+        assert np.all(np.abs(wts - top) <= 1e-5)
+
+
+def test_router_rejections(oracle):
+    """kernels_c.zig:81-95 and :625-655: dtype, then top_k, dim, the two output lengths, x, w."""
+    x, w = np.zeros((1, 32), np.float32), np.zeros((2, 32), np.float32)
+    ids, wts = np.zeros(1, np.uint16), np.zeros(1, np.float32)
+
+    def call(dt=oracle.F32, T=1, dim=32, E=2, K=1, xa=x, wa=w, nid=1, nw=1):
+        return oracle.lib().ds5o_router_topk(oracle.RouterArgs(
+            oracle.buf(xa), oracle.buf(wa), dt, T, dim, E, K, 1, ids.ctypes.data_as(C.POINTER(C.c_uint16)), nid,
+            wts.ctypes.data_as(C.POINTER(C.c_float)), nw))
+    assert call() == oracle.OK
+    assert call(dt=12) == oracle.UNSUPPORTED_DTYPE  # q4_k
+    assert call(K=0) == oracle.SHAPE_MISMATCH
+    assert call(K=3) == oracle.SHAPE_MISMATCH
+    assert call(dt=oracle.Q8_0, dim=16) == oracle.SHAPE_MISMATCH
+    assert call(nid=2) == oracle.SHAPE_MISMATCH
+    assert call(nw=0) == oracle.SHAPE_MISMATCH
+    assert call(xa=np.zeros(31, np.float32)) == oracle.SHAPE_MISMATCH
+    assert call(wa=np.zeros(63, np.float32)) == oracle.SHAPE_MISMATCH
+
+
+@pytest.mark.parametrize("i", range(3))
+def test_expert_mlp_fixtures(oracle, i):
+    """kernels_c.zig:320-401: Q8_0 banks, token-major pairs from the fixture's ids and
+    weights, output within the case tolerance."""
+    c = _cases(oracle, "expert_mlp")[i]
+    p, tol = c["params"], c["tolerance"]
+    x = _t(oracle, c, "input")
+    gate, up, down = (_t(oracle, c, n) for n in ("gate", "up", "down"))
+    assert gate.ne == (p["dim"], p["ffn_dim"], p["n_experts"]) and down.ne == (p["ffn_dim"], p["dim"], p["n_experts"])
+    ids = _t(oracle, c, "expert_ids").data.reshape(p["n_tokens"], p["top_k"])
+    gw = _t(oracle, c, "gate_weights").data.reshape(p["n_tokens"], p["top_k"])
+    pairs = oracle.pairs_from_router(ids, gw)
+    got = oracle.expert_mlp_swiglu(x.data, gate.data, up.data, down.data, oracle.Q8_0, pairs, p["n_tokens"], p["dim"],
+                                   p["ffn_dim"], p["n_experts"])
+    r = oracle.compare(_t(oracle, c, "output").data.reshape(got.shape), got, tol["atol"], tol["rtol"])
+    assert r.passed, r
+
+
+def test_expert_mlp_empty_pairs(oracle):
+    """kernels_c.zig:550-572: no pairs leave the output untouched."""
+    bank = np.zeros((32, 34), np.uint8)
+    out = oracle.expert_mlp_swiglu(np.zeros((2, 32), np.float32), bank, bank, bank, oracle.Q8_0,
+                                   np.zeros(0, oracle.PAIR_DTYPE), 2, 32, 32, 1)
+    assert np.all(out == 0)
+
+
+def test_expert_mlp_f32_hand_case(oracle):
+    """kernels_c.zig:574-623: two pairs accumulate (identity and swapped down projections)."""
+    silu = lambda v: np.float32(v) / (np.float32(1) + np.exp(np.float32(-v)))
+    x = np.array([[1.0, -2.0]], np.float32)
+    gate = np.array([1, 0, 0, 1, 0, 1, 1, 0], np.float32)
+    up = np.array([2, 0, 0, 2, 2, 0, 0, 2], np.float32)
+    down = np.array([1, 0, 0, 1, 0, 1, 1, 0], np.float32)
+    pairs = np.array([(0, 0, 0.5), (0, 1, 2.0)], oracle.PAIR_DTYPE)
+    got = oracle.expert_mlp_swiglu(x, gate, up, down, oracle.F32, pairs, 1, 2, 2, 2)
+    s1, s2 = silu(1.0), silu(-2.0)
+    want = [0.5 * s1 * 2 + 2.0 * s1 * -4, 0.5 * s2 * -4 + 2.0 * s2 * 2]
+    assert np.all(np.abs(got[0] - np.array(want, np.float32)) <= 1e-6)
+
+
+def test_expert_mlp_matches_float64(oracle):
+    """Seeded Q8_0 banks: the oracle against a float64 evaluation of the dequantised weights."""
+    g = np.random.default_rng(9)
+    T, dim, ffn, E = 3, 64, 96, 4
+    bank = lambda rows, k: oracle.q8_0_quantize(g.standard_normal((rows, k)).astype(np.float32) * 0.1)
+    gate, up, down = bank(E * ffn, dim), bank(E * ffn, dim), bank(E * dim, ffn)
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    pairs = np.array([(0, 1, 0.6), (0, 3, 0.4), (2, 0, 1.0), (1, 2, 0.25), (2, 2, 0.5)], oracle.PAIR_DTYPE)
+    got = oracle.expert_mlp_swiglu(x, gate, up, down, oracle.Q8_0, pairs, T, dim, ffn, E)
+    G, U = oracle.q8_0_dequantize(gate, dim).astype(np.float64), oracle.q8_0_dequantize(up, dim).astype(np.float64)
+    D = oracle.q8_0_dequantize(down, ffn).astype(np.float64)
+    want = np.zeros((T, dim))
+    for t, e, wt in pairs.tolist():
+        gv = G[e * ffn:(e + 1) * ffn] @ x[t]
+        h = gv / (1 + np.exp(-gv)) * (U[e * ffn:(e + 1) * ffn] @ x[t])
+        want[t] += wt * (D[e * dim:(e + 1) * dim] @ h)
+    assert np.all(np.abs(got - want) <= 1e-4 * (1 + np.abs(want)))
+
+
+def test_expert_mlp_rejections(oracle):
+    """kernels_c.zig:157-183, :625-655: dtype; zero or unblocked dims; x, out, gate, up, down
+    sizes; a pair out of range (reached after the pairs before it were added)."""
+    bank = np.zeros((32, 34), np.uint8)
+    x, out = np.zeros((1, 32), np.float32), np.zeros((1, 32), np.float32)
+
+    def call(dt=oracle.Q8_0, dim=32, ffn=32, E=1, xa=x, oa=out, ga=bank, ua=bank, da=bank, pairs=None):
+        pr = np.zeros(0, oracle.PAIR_DTYPE) if pairs is None else pairs
+        return oracle.lib().ds5o_expert_mlp_swiglu(oracle.ExpertMlpArgs(
+            oracle.buf(xa), oracle.buf(ga), oracle.buf(ua), oracle.buf(da), dt, pr.ctypes.data if pr.size else None,
+            pr.size, oracle.buf(oa), 1, dim, ffn, E))
+    assert call() == oracle.OK
+    assert call(dt=oracle.F16) == oracle.UNSUPPORTED_DTYPE
+    assert call(ffn=0) == oracle.SHAPE_MISMATCH
+    assert call(dim=16) == oracle.SHAPE_MISMATCH
+    assert call(xa=np.zeros(31, np.float32)) == oracle.SHAPE_MISMATCH
+    assert call(oa=np.zeros(31, np.float32)) == oracle.SHAPE_MISMATCH
+    assert call(ga=bank[:31]) == oracle.SHAPE_MISMATCH
+    assert call(ua=bank[:31]) == oracle.SHAPE_MISMATCH
+    assert call(da=bank[:31]) == oracle.SHAPE_MISMATCH
+    assert call(pairs=np.array([(0, 1, 1.0)], oracle.PAIR_DTYPE)) == oracle.SHAPE_MISMATCH
+    assert call(pairs=np.array([(1, 0, 1.0)], oracle.PAIR_DTYPE)) == oracle.SHAPE_MISMATCH
