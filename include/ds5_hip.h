@@ -228,9 +228,98 @@ typedef struct ds5_add_args {
 } ds5_add_args;
 int ds5_hip_add(ds5_hip_ctx* ctx, const ds5_add_args* args);
 
+/* contracts.zig:293-304 RouterArgs; replaces kernels_c.zig:80-155 routerTopK.
+ * logits = x . W^T, softmax over all n_experts, the top_k largest descending
+ * (ties: the lower id), divided by their sum iff norm_topk_prob. The outputs
+ * are HOST arrays, as in the reference: the call waits for the device and
+ * copies them back. Checks in the reference's order: w_dtype (f32, f16, q8_0)
+ * else UnsupportedDtype; top_k in 1..n_experts; dim a positive multiple of the
+ * dtype's block; both output lengths == n_tokens * top_k; x; w -- each else
+ * ShapeMismatch. dim + n_experts above 16384 is ShapeMismatch here (the token
+ * and its logits are held in 64 KiB of LDS). Logits are the reference's serial
+ * dot, bit for bit; exp is the device's, so weights agree within an ulp or so
+ * and ids agree unless two probabilities do as well. */
+typedef struct ds5_router_args {
+    ds5_buf x;                 /* f32 [n_tokens, dim] */
+    ds5_buf w;                 /* w_dtype: n_experts rows of dim */
+    uint32_t w_dtype;
+    uint32_t n_tokens;
+    uint32_t dim;
+    uint32_t n_experts;
+    uint32_t top_k;
+    uint32_t norm_topk_prob;   /* bool */
+    uint16_t* out_ids;         /* host [n_tokens * top_k] */
+    uint64_t out_ids_len;
+    float* out_weights;        /* host [n_tokens * top_k] */
+    uint64_t out_weights_len;
+} ds5_router_args;
+int ds5_hip_router_topk(ds5_hip_ctx* ctx, const ds5_router_args* args);
+
+/* contracts.zig:308-312 PairDispatch (extern struct): one (token, expert) to run. */
+typedef struct ds5_pair {
+    uint32_t token;
+    uint32_t expert;
+    float weight;
+} ds5_pair;
+
+/* contracts.zig:319-331 ExpertMlpArgs; replaces kernels_c.zig:157-214
+ * expertMlpSwiglu: per pair, out[token] += weight * down(silu(gate . x) *
+ * (up . x)), in list order per token; out is accumulated into (the caller
+ * zeroes it). Banks are GGUF 3-D tensors: expert e of gate/up at
+ * e * ffn_dim * rowBytes(dim), of down at e * dim * rowBytes(ffn_dim). pairs is
+ * a HOST array (uploaded by the call). Checks in the reference's order: w_dtype
+ * (f32, q8_0); dim and ffn_dim positive multiples of the block; x, out, gate,
+ * up, down sizes; then every pair's token and expert in range -- all before
+ * anything runs (the reference adds the pairs before a bad one; here out is left
+ * untouched). Dots agree with the reference's serial ones to rounding (the
+ * serial kernels, for views the wavefront kernels cannot read, are exact). */
+typedef struct ds5_expert_mlp_args {
+    ds5_buf x;               /* f32 [n_tokens, dim] */
+    ds5_buf gate;            /* w_dtype [n_experts, ffn_dim, dim] */
+    ds5_buf up;              /* w_dtype [n_experts, ffn_dim, dim] */
+    ds5_buf down;            /* w_dtype [n_experts, dim, ffn_dim] */
+    uint32_t w_dtype;
+    const ds5_pair* pairs;   /* host */
+    uint64_t n_pairs;
+    ds5_buf out;             /* f32 [n_tokens, dim] */
+    uint32_t n_tokens;
+    uint32_t dim;
+    uint32_t ffn_dim;
+    uint32_t n_experts;
+} ds5_expert_mlp_args;
+int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* args);
+
 /* ========================================================================
  * 3. Fused extensions (optional decls; the engine uses them via @hasDecl)
  * ======================================================================== */
+
+/* The MoE block of one layer without a host round trip (no reference
+ * counterpart; the reference routes on the host and builds the pairs there):
+ * routerTopK on the device, its token-major pairs (token t's experts in pick
+ * order) kept in device memory, and expertMlpSwiglu over them, accumulating
+ * into out. Equal to ds5_hip_router_topk then ds5_hip_expert_mlp_swiglu on
+ * those pairs. Checked as the two calls are (router first); ids / weights,
+ * when given (len >= 2 * and 4 * n_tokens * top_k), receive the router's
+ * outputs on the device. */
+typedef struct ds5_moe_args {
+    ds5_buf x;                 /* f32 [n_tokens, dim] */
+    ds5_buf router_w;          /* router_dtype: n_experts rows of dim */
+    uint32_t router_dtype;     /* f32, f16 or q8_0 */
+    ds5_buf gate;
+    ds5_buf up;
+    ds5_buf down;
+    uint32_t w_dtype;          /* f32 or q8_0 */
+    ds5_buf out;               /* f32 [n_tokens, dim], accumulated into */
+    ds5_buf ids;               /* optional u16 [n_tokens, top_k] */
+    ds5_buf weights;           /* optional f32 [n_tokens, top_k] */
+    uint32_t n_tokens;
+    uint32_t dim;
+    uint32_t ffn_dim;
+    uint32_t n_experts;
+    uint32_t top_k;
+    uint32_t norm_topk_prob;
+} ds5_moe_args;
+int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* args);
 
 /* The output projection and residual of forward.zig:416-418 as one call:
  * out = residual + x . W^T, bit-identical to ds5_hip_matmul(x, w -> proj)

@@ -121,6 +121,41 @@ int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const Matm
 // Residual add out = x + y over n f32 elements (any views; out may be x or y).
 int launch_add(ds5_hip_ctx* ctx, const void* x, const void* y, void* out, uint64_t n);
 
+// MoE router (k_moe.hip): per token, ids / weights (device) and optionally the
+// token-major dispatch pairs.
+struct RouterLaunch {
+    const float* x;
+    const uint8_t* w;
+    uint32_t w_dtype;
+    uint64_t row_bytes;
+    uint32_t n_tokens, dim, n_experts, top_k;
+    bool norm;
+    uint16_t* ids;
+    float* weights;
+    ds5_pair* pairs;  // may be null
+};
+int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a);
+
+// SwiGLU experts over device dispatch pairs; out accumulates. Token t's pairs
+// are order[offsets[t] .. offsets[t + 1]) in list order, or t*top_k .. when
+// offsets is null. h [n_pairs, ffn] and y [n_pairs, dim] are scratch.
+struct ExpertLaunch {
+    const float* x;
+    const uint8_t *gate, *up, *down;
+    bool q8;
+    bool fast;  // the wavefront GEMVs (else the serial kernels)
+    const ds5_pair* pairs;
+    const uint32_t* order;
+    const uint32_t* offsets;
+    uint32_t top_k;
+    float* out;
+    float* h;
+    float* y;
+    uint32_t n_tokens, n_pairs, dim, ffn;
+    uint64_t row_h, row_f, stride_gu, stride_d;
+};
+int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a);
+
 struct RmsNormLaunch {
     const float* x;
     const float* w;
@@ -281,6 +316,45 @@ struct OpMax {
 };
 
 DS5_DEVICE_INLINE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Q8_0 (GGUF): 34-byte blocks of an f16 scale and 32 int8; value = f32(scale) * q.
+constexpr int kQ8Bytes = 34;
+
+DS5_DEVICE_INLINE float f16_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// The 32 int8 of a Q8_0 block as 8 dwords plus its f32 scale, from the nine
+// dwords d[0..8] read at (block offset & ~3); sh = block offset & 3 (0 or 2).
+// Both cases run the same instructions: a per-lane byte-permute selector picks
+// bytes 2..5 (sh = 0) or 4..7 (sh = 2) of each dword pair.
+struct Q8Block {
+    uint32_t q[8];
+    float scale;
+};
+
+DS5_DEVICE_INLINE Q8Block q8_unpack(const uint32_t (&d)[9], uint32_t sh) {
+    Q8Block r;
+    r.scale = f16_bits_to_f32((d[0] >> (8 * sh)) & 0xffffu);
+    const uint32_t sel = sh ? 0x07060504u : 0x05040302u;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_perm(d[i + 1], d[i], sel);
+    return r;
+}
+
+// sum_i q_i * x_i over one block (four interleaved partial sums)
+DS5_DEVICE_INLINE float q8_dot(const uint32_t (&q)[8], const float (&x)[32]) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int v = (int)(int8_t)(q[i] >> (8 * e));  // sign-extended byte e
+            s[e] = __builtin_fmaf((float)v, x[4 * i + e], s[e]);
+        }
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
 
 // Correctly rounded f32 square root. The compiler lowers __fsqrt_rn and
 // sqrtf to v_sqrt_f32, which is only 1-ulp accurate, while the reference's

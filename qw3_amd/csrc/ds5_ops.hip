@@ -182,6 +182,220 @@ int ds5_hip_matmul_add(ds5_hip_ctx* ctx, const ds5_matmul_add_args* a) {
     return launch_matmul(ctx, l, matmul_path(l, a->w.len));
 }
 
+// ---------------------------------------------------------------------------
+// MoE: router top-k and SwiGLU experts (kernels_c.zig)
+// ---------------------------------------------------------------------------
+
+static uint64_t row_bytes_of(uint32_t dtype, uint64_t k) {
+    return dtype == DS5_DTYPE_Q8_0 ? k / 32 * 34 : k * (dtype == DS5_DTYPE_F16 ? 2 : 4);
+}
+
+// kernels_c.zig:81-95, without the output slices (checked by the caller).
+static int check_router(ds5_hip_ctx* ctx, const char* op, ds5_buf x, ds5_buf w, uint32_t dt, uint64_t T,
+                        uint64_t dim, uint64_t E, uint64_t K, bool outputs_ok) {
+    if (dt != DS5_DTYPE_F32 && dt != DS5_DTYPE_F16 && dt != DS5_DTYPE_Q8_0)
+        return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "%s: router w_dtype %u (f32, f16 and q8_0 are supported)", op, dt);
+    if (K == 0 || K > E) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: top_k %llu of %llu experts", op,
+                                         (unsigned long long)K, (unsigned long long)E);
+    if (dim == 0 || dim % (dt == DS5_DTYPE_Q8_0 ? 32 : 1) != 0)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dim %llu is not a positive multiple of the block", op,
+                        (unsigned long long)dim);
+    if (!outputs_ok) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: output lengths are not n_tokens * top_k", op);
+    if (!covers(x, T * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: x too small", op);
+    if (!covers(w, E * row_bytes_of(dt, dim))) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: router w too small", op);
+    if (dim + E > 16384)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dim + n_experts = %llu exceeds 16384 (LDS)", op,
+                        (unsigned long long)(dim + E));
+    return DS5_OK;
+}
+
+// kernels_c.zig:157-183 (sizes; the pairs are checked by the caller).
+static int check_experts(ds5_hip_ctx* ctx, const char* op, ds5_buf x, ds5_buf gate, ds5_buf up, ds5_buf down,
+                         uint32_t dt, ds5_buf out, uint64_t T, uint64_t dim, uint64_t ffn, uint64_t E) {
+    if (dt != DS5_DTYPE_F32 && dt != DS5_DTYPE_Q8_0)
+        return ds5_fail(ctx, DS5_UNSUPPORTED_DTYPE, "%s: expert w_dtype %u (f32 and q8_0 are supported)", op, dt);
+    const uint64_t block = dt == DS5_DTYPE_Q8_0 ? 32 : 1;
+    if (dim == 0 || ffn == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dim or ffn_dim is 0", op);
+    if (dim % block || ffn % block) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dims not block multiples", op);
+    if (!covers(x, T * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: x too small", op);
+    if (!covers(out, T * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: out too small", op);
+    const uint64_t gstride = row_bytes_of(dt, dim) * ffn, dstride = row_bytes_of(dt, ffn) * dim;
+    if (!covers(gate, E * gstride)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: gate too small", op);
+    if (!covers(up, E * gstride)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: up too small", op);
+    if (!covers(down, E * dstride)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: down too small", op);
+    return DS5_OK;
+}
+
+// The wavefront GEMVs work in 32-element blocks (dim and ffn multiples of 32,
+// as Q8_0 always is), read x / h as float4 and each Q8_0 block as the nine
+// dwords from its dword floor (2 bytes past the last block unless the bank
+// ends on a dword boundary or its view has 2 more bytes); f32 rows as floats.
+static bool experts_fast(ds5_buf x, ds5_buf gate, ds5_buf up, ds5_buf down, uint32_t dt, uint64_t dim, uint64_t ffn,
+                         uint64_t E) {
+    if (dim % 32 || ffn % 32 || ((uintptr_t)ds5_ptr(x) & 15u)) return false;
+    const uint64_t ends[3] = {row_bytes_of(dt, dim) * ffn * E, row_bytes_of(dt, dim) * ffn * E,
+                              row_bytes_of(dt, ffn) * dim * E};
+    const ds5_buf banks[3] = {gate, up, down};
+    for (int i = 0; i < 3; i++) {
+        const uintptr_t a = (uintptr_t)ds5_ptr(banks[i]);
+        if (a & 3u) return false;
+        if (dt == DS5_DTYPE_Q8_0 && (a + ends[i]) % 4 != 0 && banks[i].len < ends[i] + 2) return false;
+    }
+    return true;
+}
+
+struct MoeScratch {
+    ds5_pair* pairs;
+    uint32_t* order;
+    uint32_t* offsets;
+    float* h;
+    float* y;
+    uint16_t* ids;
+    float* weights;
+};
+
+static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int moe_scratch(ds5_hip_ctx* ctx, uint64_t T, uint64_t P, uint64_t dim, uint64_t ffn, MoeScratch* s) {
+    const size_t sz[7] = {up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4), up256(P * ffn * 4),
+                          up256(P * dim * 4), up256(P * 2), up256(P * 4)};
+    size_t total = 0;
+    for (size_t v : sz) total += v;
+    void* ws = nullptr;
+    if (int rc = ds5_workspace(ctx, total, &ws)) return rc;
+    char* p = (char*)ws;
+    s->pairs = (ds5_pair*)p;
+    p += sz[0];
+    s->order = (uint32_t*)p;
+    p += sz[1];
+    s->offsets = (uint32_t*)p;
+    p += sz[2];
+    s->h = (float*)p;
+    p += sz[3];
+    s->y = (float*)p;
+    p += sz[4];
+    s->ids = (uint16_t*)p;
+    p += sz[5];
+    s->weights = (float*)p;
+    return DS5_OK;
+}
+
+static ExpertLaunch expert_launch(const ds5_buf& x, const ds5_buf& gate, const ds5_buf& up, const ds5_buf& down,
+                                  uint32_t dt, const ds5_buf& out, uint32_t T, uint32_t P, uint32_t dim, uint32_t ffn,
+                                  uint32_t E, const MoeScratch& s) {
+    ExpertLaunch l{};
+    l.x = (const float*)ds5_ptr(x);
+    l.gate = (const uint8_t*)ds5_ptr(gate);
+    l.up = (const uint8_t*)ds5_ptr(up);
+    l.down = (const uint8_t*)ds5_ptr(down);
+    l.q8 = dt == DS5_DTYPE_Q8_0;
+    l.fast = experts_fast(x, gate, up, down, dt, dim, ffn, E);
+    l.pairs = s.pairs;
+    l.out = (float*)ds5_ptr(out);
+    l.h = s.h;
+    l.y = s.y;
+    l.n_tokens = T;
+    l.n_pairs = P;
+    l.dim = dim;
+    l.ffn = ffn;
+    l.row_h = row_bytes_of(dt, dim);
+    l.row_f = row_bytes_of(dt, ffn);
+    l.stride_gu = l.row_h * ffn;
+    l.stride_d = l.row_f * dim;
+    return l;
+}
+
+int ds5_hip_router_topk(ds5_hip_ctx* ctx, const ds5_router_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t TK = (uint64_t)a->n_tokens * a->top_k;
+    if (int rc = check_router(ctx, "router_topk", a->x, a->w, a->w_dtype, a->n_tokens, a->dim, a->n_experts, a->top_k,
+                              a->out_ids_len == TK && a->out_weights_len == TK))
+        return rc;
+    if ((TK && (!a->out_ids || !a->out_weights))) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "router_topk: null output");
+    if (a->n_tokens == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    MoeScratch s{};
+    if (int rc = moe_scratch(ctx, a->n_tokens, TK, 0, 0, &s)) return rc;
+    RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), a->w_dtype,
+                   row_bytes_of(a->w_dtype, a->dim), a->n_tokens, a->dim, a->n_experts, a->top_k,
+                   a->norm_topk_prob != 0, s.ids, s.weights, nullptr};
+    if (int rc = launch_router(ctx, r)) return rc;
+    // host outputs (the reference's contract): wait, then copy back
+    int rc = ds5_hip_status(ctx, hipMemcpyAsync(a->out_ids, s.ids, TK * 2, hipMemcpyDeviceToHost, ctx->stream), "ids");
+    if (!rc) rc = ds5_hip_status(ctx, hipMemcpyAsync(a->out_weights, s.weights, TK * 4, hipMemcpyDeviceToHost,
+                                                     ctx->stream), "weights");
+    if (!rc) rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "router sync");
+    return rc;
+}
+
+int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (int rc = check_experts(ctx, "expert_mlp", a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens,
+                               a->dim, a->ffn_dim, a->n_experts))
+        return rc;
+    const uint64_t P = a->n_pairs;
+    if (P && !a->pairs) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "expert_mlp: null pairs");
+    for (uint64_t p = 0; p < P; p++)
+        if (a->pairs[p].token >= a->n_tokens || a->pairs[p].expert >= a->n_experts)
+            return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "expert_mlp: pair %llu (token %u, expert %u) out of range",
+                            (unsigned long long)p, a->pairs[p].token, a->pairs[p].expert);
+    if (P == 0 || a->n_tokens == 0) return DS5_OK;
+    if (P > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "expert_mlp: too many pairs");
+    if (int rc = set_device(ctx)) return rc;
+    // token-ordered view of the list, each token's pairs in list order
+    std::vector<uint32_t> offsets(a->n_tokens + 1, 0), order(P);
+    for (uint64_t p = 0; p < P; p++) offsets[a->pairs[p].token + 1]++;
+    for (uint32_t t = 0; t < a->n_tokens; t++) offsets[t + 1] += offsets[t];
+    {
+        std::vector<uint32_t> fill(offsets.begin(), offsets.end() - 1);
+        for (uint64_t p = 0; p < P; p++) order[fill[a->pairs[p].token]++] = (uint32_t)p;
+    }
+    MoeScratch s{};
+    if (int rc = moe_scratch(ctx, a->n_tokens, P, a->dim, a->ffn_dim, &s)) return rc;
+    int rc = ds5_hip_status(ctx, hipMemcpyAsync(s.pairs, a->pairs, P * sizeof(ds5_pair), hipMemcpyHostToDevice,
+                                                ctx->stream), "pairs");
+    if (!rc) rc = ds5_hip_status(ctx, hipMemcpyAsync(s.order, order.data(), P * 4, hipMemcpyHostToDevice, ctx->stream),
+                                 "pair order");
+    if (!rc) rc = ds5_hip_status(ctx, hipMemcpyAsync(s.offsets, offsets.data(), offsets.size() * 4,
+                                                     hipMemcpyHostToDevice, ctx->stream), "pair offsets");
+    // the host arrays must outlive the copies
+    if (!rc) rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "pairs sync");
+    if (rc) return rc;
+    ExpertLaunch l = expert_launch(a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)P, a->dim,
+                                   a->ffn_dim, a->n_experts, s);
+    l.order = s.order;
+    l.offsets = s.offsets;
+    return launch_experts(ctx, l);
+}
+
+int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const uint64_t TK = (uint64_t)a->n_tokens * a->top_k;
+    if (int rc = check_router(ctx, "moe", a->x, a->router_w, a->router_dtype, a->n_tokens, a->dim, a->n_experts,
+                              a->top_k, true))
+        return rc;
+    if (int rc = check_experts(ctx, "moe", a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, a->dim,
+                               a->ffn_dim, a->n_experts))
+        return rc;
+    if ((a->ids.len && !covers(a->ids, TK * 2)) || (a->weights.len && !covers(a->weights, TK * 4)))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: ids / weights outputs too small");
+    if (a->n_tokens == 0) return DS5_OK;
+    if (TK > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: too many pairs");
+    if (int rc = set_device(ctx)) return rc;
+    MoeScratch s{};
+    if (int rc = moe_scratch(ctx, a->n_tokens, TK, a->dim, a->ffn_dim, &s)) return rc;
+    RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->router_w), a->router_dtype,
+                   row_bytes_of(a->router_dtype, a->dim), a->n_tokens, a->dim, a->n_experts, a->top_k,
+                   a->norm_topk_prob != 0,
+                   a->ids.len ? (uint16_t*)ds5_ptr(a->ids) : s.ids,
+                   a->weights.len ? (float*)ds5_ptr(a->weights) : s.weights, s.pairs};
+    if (int rc = launch_router(ctx, r)) return rc;
+    ExpertLaunch l = expert_launch(a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)TK,
+                                   a->dim, a->ffn_dim, a->n_experts, s);
+    l.top_k = a->top_k;  // token t's pairs are t * top_k .. (t + 1) * top_k - 1
+    return launch_experts(ctx, l);
+}
+
 int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
     if (a->count == 0 || a->count > DS5_MATMUL_GROUP_MAX)

@@ -21,42 +21,7 @@
 namespace {
 
 constexpr int kMmThreads = 512;  // 8 wavefronts, one weight row each
-constexpr int kQ8Bytes = 34;     // Q8_0 block: f16 scale + 32 x int8
 
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-}
-
-// The 32 int8 of a Q8_0 block as 8 dwords plus its f32 scale, from the nine
-// dwords d[0..8] read at (block offset & ~3); sh = block offset & 3 (0 or 2).
-// Both cases run the same instructions: a per-lane byte-permute selector picks
-// bytes 2..5 (sh = 0) or 4..7 (sh = 2) of each dword pair.
-struct Q8Block {
-    uint32_t q[8];
-    float scale;
-};
-
-__device__ __forceinline__ Q8Block q8_unpack(const uint32_t (&d)[9], uint32_t sh) {
-    Q8Block r;
-    r.scale = f16_bits_to_f32((d[0] >> (8 * sh)) & 0xffffu);
-    const uint32_t sel = sh ? 0x07060504u : 0x05040302u;
-#pragma unroll
-    for (int i = 0; i < 8; i++) r.q[i] = __builtin_amdgcn_perm(d[i + 1], d[i], sel);
-    return r;
-}
-
-// sum_i q_i * x_i over one block (four interleaved partial sums)
-__device__ __forceinline__ float q8_dot(const uint32_t (&q)[8], const float (&x)[32]) {
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int v = (int)(int8_t)(q[i] >> (8 * e));  // sign-extended byte e
-            s[e] = __builtin_fmaf((float)v, x[4 * i + e], s[e]);
-        }
-    return (s[0] + s[1]) + (s[2] + s[3]);
-}
 
 // Up to kMatmulGroupMax weight matrices sharing x, in one launch: entry e owns
 // the workgroups (row kernel) or column tiles (GEMM) [wg0[e], wg0[e + 1]).

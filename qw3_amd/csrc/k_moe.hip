@@ -1,0 +1,348 @@
+// k_moe.hip -- the MoE step after the attention block: router top-k and the
+// SwiGLU expert MLP (kernels_c.zig:80-155 routerTopK, :157-214 expertMlpSwiglu).
+//
+// Router: one workgroup per token. Each expert's logit is the reference's
+// serial f32 dot (dotRow, kernels_c.zig:40-68: products and sums rounded one by
+// one, in storage order), so logits are bit-identical to the reference. The
+// softmax keeps its order too: max, exp(l - max) per expert, the sum in expert
+// order, then the reciprocal; the top-k rounds pick the largest probability
+// with ties to the lower id (a wavefront argmax under that total order equals
+// the reference's ascending scan with a strict >); the k weights are summed in
+// pick order and optionally divided by that sum. exp is the device's expf, so
+// probabilities may differ from the reference's in the last bit; ids can then
+// differ only where two probabilities are that close.
+//
+// Experts, per dispatch pair p = (token t, expert e, weight w):
+//   h[p][j] = silu(gate_e[j] . x_t) * (up_e[j] . x_t)     (moe_gate_up_kernel)
+//   y[p][i] = down_e[i] . h[p]                            (moe_down_kernel)
+//   out[t][i] += w * y[p][i] over t's pairs in list order (moe_combine_kernel)
+// The GEMVs are weight-bandwidth bound: one wavefront per weight row, lane L
+// owning the 32-element blocks L + 64 j, a fixed-order wavefront reduction (so
+// they agree with the reference's serial dots to rounding). The combine adds
+// each product in the reference's order, rounding as it does.
+#include "ds5_common.hpp"
+
+namespace {
+
+constexpr int kRouterThreads = 256;
+constexpr int kMoeWaves = 8;  // wavefronts (weight rows) per GEMV workgroup
+
+// ---------------------------------------------------------------------------
+// router
+// ---------------------------------------------------------------------------
+
+// Weight element i of a router row, as the reference widens it (AL: the row
+// is aligned to its element size; else it is read bytewise).
+template <uint32_t DT, bool AL>
+__device__ __forceinline__ float router_w(const uint8_t* row, uint32_t i) {
+    if constexpr (DT == DS5_DTYPE_F32) {
+        if constexpr (AL) return ((const float*)row)[i];
+        float v;
+        __builtin_memcpy(&v, row + 4 * i, 4);
+        return v;
+    } else {
+        if constexpr (AL) return f16_bits_to_f32(((const uint16_t*)row)[i]);
+        uint16_t b;
+        __builtin_memcpy(&b, row + 2 * i, 2);
+        return f16_bits_to_f32(b);
+    }
+}
+
+// dotRow (kernels_c.zig:40-68) in its order: acc += w * x for f32 / f16; for
+// Q8_0, acc += (scale * q) * x per element.
+template <uint32_t DT, bool AL>
+__device__ float serial_dot(const float* x, const uint8_t* row, uint32_t dim) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+    if constexpr (DT == DS5_DTYPE_Q8_0) {
+        for (uint32_t b = 0; b < dim / 32; b++) {
+            const uint8_t* blk = row + (uint64_t)b * kQ8Bytes;
+            const float scale = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            for (int i = 0; i < 32; i++) acc += (scale * (float)(int8_t)blk[2 + i]) * x[32 * b + i];
+        }
+    } else {
+        for (uint32_t i = 0; i < dim; i++) acc += router_w<DT, AL>(row, i) * x[i];
+    }
+    return acc;
+}
+
+// Dynamic LDS: x of the token (dim floats), then the n_experts probabilities.
+template <uint32_t DT, bool AL>
+__global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __restrict__ x,
+                                                                const uint8_t* __restrict__ w, uint64_t row_bytes,
+                                                                uint32_t dim, uint32_t n_experts, uint32_t top_k,
+                                                                uint32_t norm, uint16_t* __restrict__ out_ids,
+                                                                float* __restrict__ out_w,
+                                                                ds5_pair* __restrict__ pairs) {
+#pragma clang fp contract(off)
+    extern __shared__ float router_smem[];
+    float* xs = router_smem;
+    float* probs = router_smem + dim;
+    __shared__ float s_inv_sum;
+    const uint32_t t = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < dim; i += kRouterThreads) xs[i] = x[(uint64_t)t * dim + i];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < n_experts; e += kRouterThreads)
+        probs[e] = serial_dot<DT, AL>(xs, w + (uint64_t)e * row_bytes, dim);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float mx = -__builtin_inff();
+        for (uint32_t e = 0; e < n_experts; e++) mx = fmaxf(mx, probs[e]);
+        float sum = 0.0f;
+        for (uint32_t e = 0; e < n_experts; e++) {
+            const float p = expf(probs[e] - mx);
+            probs[e] = p;
+            sum += p;
+        }
+        s_inv_sum = 1.0f / sum;
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < n_experts; e += kRouterThreads) probs[e] *= s_inv_sum;
+    __syncthreads();
+    if (threadIdx.x >= 64) return;  // wavefront 0 picks; no barrier follows
+
+    // top-k: round j takes the largest untaken probability, the lower id on ties
+    // (lanes scan their experts in ascending order with a strict >, as the
+    // reference does; the cross-lane merge keeps that order). A probability
+    // picked is overwritten with -1 (below every probability and the -1 start).
+    const int lane = threadIdx.x;
+    float picked = 0.0f;
+    for (uint32_t j = 0; j < top_k; j++) {
+        uint32_t best = 0;
+        float best_p = -1.0f;
+        for (uint32_t e = lane; e < n_experts; e += 64)
+            if (probs[e] > best_p) {
+                best = e;
+                best_p = probs[e];
+            }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float op = __shfl_xor(best_p, off, 64);
+            const uint32_t oe = (uint32_t)__shfl_xor((int)best, off, 64);
+            if (op > best_p || (op == best_p && oe < best)) {
+                best_p = op;
+                best = oe;
+            }
+        }
+        if (lane == 0) {
+            probs[best] = -1.0f;  // taken
+            out_ids[(uint64_t)t * top_k + j] = (uint16_t)best;
+            out_w[(uint64_t)t * top_k + j] = best_p;
+            picked += best_p;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0) {
+        const float inv = norm ? 1.0f / picked : 1.0f;
+        for (uint32_t j = 0; j < top_k; j++) {
+            const uint64_t o = (uint64_t)t * top_k + j;
+            if (norm) out_w[o] *= inv;
+            if (pairs) pairs[o] = ds5_pair{t, out_ids[o], out_w[o]};
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// expert GEMVs
+// ---------------------------------------------------------------------------
+
+// This lane's share of x . row over blocks L, L + 64, ... (f32 or Q8_0 rows;
+// Q8_0 rows read as nine dwords from the dword floor of each block).
+template <bool Q8>
+__device__ __forceinline__ float lane_dot(const float* __restrict__ x, const uint8_t* __restrict__ row,
+                                          const uint8_t* __restrict__ base, uint32_t k, int lane) {
+    const uint32_t nb = k / 32;
+    float acc = 0.0f;
+    for (uint32_t b = lane; b < nb; b += 64) {
+        float xr[32];
+        const float4* xs = (const float4*)(x + 32 * b);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = xs[i];
+            xr[4 * i] = v.x;
+            xr[4 * i + 1] = v.y;
+            xr[4 * i + 2] = v.z;
+            xr[4 * i + 3] = v.w;
+        }
+        if constexpr (Q8) {
+            const uint64_t off = (uint64_t)(row - base) + (uint64_t)b * kQ8Bytes;
+            const uint32_t sh = (uint32_t)off & 3u;  // base is 4-byte aligned
+            const uint32_t* p = (const uint32_t*)(base + (off - sh));
+            uint32_t d[9];
+#pragma unroll
+            for (int i = 0; i < 9; i++) d[i] = p[i];
+            const Q8Block blk = q8_unpack(d, sh);
+            acc = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), acc);
+        } else {
+            const float* wr = (const float*)row + 32 * b;
+            float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 32; i++) s[i & 3] = __builtin_fmaf(wr[i], xr[i], s[i & 3]);
+            acc += (s[0] + s[1]) + (s[2] + s[3]);
+        }
+    }
+    return acc;
+}
+
+// One wavefront per (pair, ffn row j); x rows 16-byte aligned (dim % 32 == 0).
+template <bool Q8>
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(const float* __restrict__ x,
+                                                                     const uint8_t* __restrict__ gate,
+                                                                     const uint8_t* __restrict__ up,
+                                                                     const ds5_pair* __restrict__ pairs,
+                                                                     float* __restrict__ h, uint32_t n_pairs,
+                                                                     uint32_t dim, uint32_t ffn, uint64_t row_h,
+                                                                     uint64_t stride) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t r = (uint64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
+    if (r >= (uint64_t)n_pairs * ffn) return;  // wave-uniform
+    const uint32_t p = (uint32_t)(r / ffn), j = (uint32_t)(r % ffn);
+    const ds5_pair pr = pairs[p];
+    const float* xr = x + (uint64_t)pr.token * dim;
+    const uint64_t row = (uint64_t)pr.expert * stride + (uint64_t)j * row_h;
+    const float g = wave_allreduce(lane_dot<Q8>(xr, gate + row, gate, dim, lane), OpAdd{});
+    const float u = wave_allreduce(lane_dot<Q8>(xr, up + row, up, dim, lane), OpAdd{});
+    if (lane == 0) h[r] = g / (1.0f + expf(-g)) * u;  // silu(g) * u, kernels_c.zig:70-72
+}
+
+// One wavefront per (pair, output row i); h rows 16-byte aligned (ffn % 32 == 0).
+template <bool Q8>
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* __restrict__ h,
+                                                                  const uint8_t* __restrict__ down,
+                                                                  const ds5_pair* __restrict__ pairs,
+                                                                  float* __restrict__ y, uint32_t n_pairs, uint32_t dim,
+                                                                  uint32_t ffn, uint64_t row_f, uint64_t stride) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t r = (uint64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
+    if (r >= (uint64_t)n_pairs * dim) return;  // wave-uniform
+    const uint32_t p = (uint32_t)(r / dim), i = (uint32_t)(r % dim);
+    const uint64_t row = (uint64_t)pairs[p].expert * stride + (uint64_t)i * row_f;
+    const float v = wave_allreduce(lane_dot<Q8>(h + (uint64_t)p * ffn, down + row, down, ffn, lane), OpAdd{});
+    if (lane == 0) y[r] = v;
+}
+
+// out[t][i] += w_p * y[p][i] over token t's pairs in list order: pair q of the
+// token is order[offsets[t] + q] (or t * top_k + q when offsets is null).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
+                                                          const ds5_pair* __restrict__ pairs,
+                                                          const uint32_t* __restrict__ order,
+                                                          const uint32_t* __restrict__ offsets, uint32_t top_k,
+                                                          float* __restrict__ out, uint32_t n_tokens, uint32_t dim) {
+#pragma clang fp contract(off)
+    const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (uint64_t)n_tokens * dim) return;
+    const uint32_t t = (uint32_t)(id / dim), i = (uint32_t)(id % dim);
+    const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
+    float acc = out[id];
+    for (uint32_t q = q0; q < q1; q++) {
+        const uint32_t p = order ? order[q] : q;
+        acc += pairs[p].weight * y[(uint64_t)p * dim + i];
+    }
+    out[id] = acc;
+}
+
+// Serial fallback for banks the GEMV kernels cannot read (a Q8_0 view that is
+// not 4-byte aligned, or that ends 2 bytes short of the dword past its last
+// block): one thread per (pair, row), dotRow's order.
+__device__ float serial_row_dot(const float* x, const uint8_t* row, bool q8, uint32_t k) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+    if (q8) {
+        for (uint32_t b = 0; b < k / 32; b++) {
+            const uint8_t* blk = row + (uint64_t)b * kQ8Bytes;
+            const float scale = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            for (int i = 0; i < 32; i++) acc += (scale * (float)(int8_t)blk[2 + i]) * x[32 * b + i];
+        }
+    } else {
+        for (uint32_t i = 0; i < k; i++) {
+            float wv;
+            __builtin_memcpy(&wv, row + 4 * (uint64_t)i, 4);
+            acc += wv * x[i];
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void moe_gate_up_serial_kernel(const float* x, const uint8_t* gate,
+                                                                 const uint8_t* up, const ds5_pair* pairs, float* h,
+                                                                 uint32_t n_pairs, uint32_t dim, uint32_t ffn,
+                                                                 uint32_t q8, uint64_t row_h, uint64_t stride) {
+#pragma clang fp contract(off)
+    const uint64_t r = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= (uint64_t)n_pairs * ffn) return;
+    const uint32_t p = (uint32_t)(r / ffn), j = (uint32_t)(r % ffn);
+    const ds5_pair pr = pairs[p];
+    const float* xr = x + (uint64_t)pr.token * dim;
+    const uint64_t row = (uint64_t)pr.expert * stride + (uint64_t)j * row_h;
+    const float g = serial_row_dot(xr, gate + row, q8, dim), u = serial_row_dot(xr, up + row, q8, dim);
+    h[r] = g / (1.0f + expf(-g)) * u;
+}
+
+__global__ __launch_bounds__(256) void moe_down_serial_kernel(const float* h, const uint8_t* down,
+                                                              const ds5_pair* pairs, float* y, uint32_t n_pairs,
+                                                              uint32_t dim, uint32_t ffn, uint32_t q8, uint64_t row_f,
+                                                              uint64_t stride) {
+    const uint64_t r = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= (uint64_t)n_pairs * dim) return;
+    const uint32_t p = (uint32_t)(r / dim), i = (uint32_t)(r % dim);
+    const uint64_t row = (uint64_t)pairs[p].expert * stride + (uint64_t)i * row_f;
+    y[r] = serial_row_dot(h + (uint64_t)p * ffn, down + row, q8, ffn);
+}
+
+}  // namespace
+
+template <uint32_t DT, bool AL>
+static void launch_router_t(ds5_hip_ctx* ctx, const RouterLaunch& a, size_t smem) {
+    DS5_TIMED_LAUNCH(ctx, "router_kernel", (router_kernel<DT, AL>), dim3(a.n_tokens), dim3(kRouterThreads), smem,
+                     ctx->stream, a.x, a.w, a.row_bytes, a.dim, a.n_experts, a.top_k, (uint32_t)a.norm, a.ids,
+                     a.weights, a.pairs);
+}
+
+int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
+    if (a.n_tokens == 0) return DS5_OK;
+    const size_t smem = ((size_t)a.dim + a.n_experts) * sizeof(float);
+    const uintptr_t w = (uintptr_t)a.w;
+    if (a.w_dtype == DS5_DTYPE_F32)
+        (w & 3u) ? launch_router_t<DS5_DTYPE_F32, false>(ctx, a, smem) : launch_router_t<DS5_DTYPE_F32, true>(ctx, a, smem);
+    else if (a.w_dtype == DS5_DTYPE_F16)
+        (w & 1u) ? launch_router_t<DS5_DTYPE_F16, false>(ctx, a, smem) : launch_router_t<DS5_DTYPE_F16, true>(ctx, a, smem);
+    else
+        launch_router_t<DS5_DTYPE_Q8_0, true>(ctx, a, smem);
+    return ds5_after_launch(ctx, "router_kernel");
+}
+
+int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
+    if (a.n_pairs == 0 || a.n_tokens == 0) return DS5_OK;
+    const uint64_t gu_rows = (uint64_t)a.n_pairs * a.ffn, dn_rows = (uint64_t)a.n_pairs * a.dim;
+    if (a.fast) {
+        const dim3 blk(kMoeWaves * 64);
+        const dim3 g1((unsigned)((gu_rows + kMoeWaves - 1) / kMoeWaves)), g2((unsigned)((dn_rows + kMoeWaves - 1) / kMoeWaves));
+        if (a.q8) {
+            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, 0, ctx->stream, a.x, a.gate,
+                             a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
+            if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
+            DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<true>, g2, blk, 0, ctx->stream, a.h, a.down,
+                             a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+        } else {
+            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, 0, ctx->stream, a.x, a.gate,
+                             a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
+            if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
+            DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<false>, g2, blk, 0, ctx->stream, a.h, a.down,
+                             a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+        }
+        if (int rc = ds5_after_launch(ctx, "moe_down_kernel")) return rc;
+    } else {
+        DS5_TIMED_LAUNCH(ctx, "moe_gate_up_serial_kernel", moe_gate_up_serial_kernel,
+                         dim3((unsigned)((gu_rows + 255) / 256)), dim3(256), 0, ctx->stream, a.x, a.gate, a.up, a.pairs,
+                         a.h, a.n_pairs, a.dim, a.ffn, (uint32_t)a.q8, a.row_h, a.stride_gu);
+        if (int rc = ds5_after_launch(ctx, "moe_gate_up_serial_kernel")) return rc;
+        DS5_TIMED_LAUNCH(ctx, "moe_down_serial_kernel", moe_down_serial_kernel, dim3((unsigned)((dn_rows + 255) / 256)),
+                         dim3(256), 0, ctx->stream, a.h, a.down, a.pairs, a.y, a.n_pairs, a.dim, a.ffn, (uint32_t)a.q8,
+                         a.row_f, a.stride_d);
+        if (int rc = ds5_after_launch(ctx, "moe_down_serial_kernel")) return rc;
+    }
+    const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
+    DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
+                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.n_tokens, a.dim);
+    return ds5_after_launch(ctx, "moe_combine_kernel");
+}

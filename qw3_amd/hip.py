@@ -105,6 +105,33 @@ class MatmulAddArgs(C.Structure):
                 ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32)]
 
 
+class RouterArgs(C.Structure):
+    _fields_ = [("x", Buf), ("w", Buf), ("w_dtype", C.c_uint32), ("n_tokens", C.c_uint32), ("dim", C.c_uint32),
+                ("n_experts", C.c_uint32), ("top_k", C.c_uint32), ("norm_topk_prob", C.c_uint32),
+                ("out_ids", C.POINTER(C.c_uint16)), ("out_ids_len", C.c_uint64),
+                ("out_weights", C.POINTER(C.c_float)), ("out_weights_len", C.c_uint64)]
+
+
+class Pair(C.Structure):  # contracts.zig:308-312 PairDispatch
+    _fields_ = [("token", C.c_uint32), ("expert", C.c_uint32), ("weight", C.c_float)]
+
+
+PAIR_DTYPE = np.dtype([("token", np.uint32), ("expert", np.uint32), ("weight", np.float32)])
+
+
+class ExpertMlpArgs(C.Structure):
+    _fields_ = [("x", Buf), ("gate", Buf), ("up", Buf), ("down", Buf), ("w_dtype", C.c_uint32),
+                ("pairs", C.c_void_p), ("n_pairs", C.c_uint64), ("out", Buf), ("n_tokens", C.c_uint32),
+                ("dim", C.c_uint32), ("ffn_dim", C.c_uint32), ("n_experts", C.c_uint32)]
+
+
+class MoeArgs(C.Structure):
+    _fields_ = [("x", Buf), ("router_w", Buf), ("router_dtype", C.c_uint32), ("gate", Buf), ("up", Buf),
+                ("down", Buf), ("w_dtype", C.c_uint32), ("out", Buf), ("ids", Buf), ("weights", Buf),
+                ("n_tokens", C.c_uint32), ("dim", C.c_uint32), ("ffn_dim", C.c_uint32), ("n_experts", C.c_uint32),
+                ("top_k", C.c_uint32), ("norm_topk_prob", C.c_uint32)]
+
+
 MATMUL_GROUP_MAX = 4
 
 
@@ -171,6 +198,9 @@ SIGNATURES = {
     "ds5_hip_matmul_group": ([_P, C.POINTER(MatmulGroupArgs)], C.c_int),
     "ds5_hip_add": ([_P, C.POINTER(AddArgs)], C.c_int),
     "ds5_hip_matmul_add": ([_P, C.POINTER(MatmulAddArgs)], C.c_int),
+    "ds5_hip_router_topk": ([_P, C.POINTER(RouterArgs)], C.c_int),
+    "ds5_hip_expert_mlp_swiglu": ([_P, C.POINTER(ExpertMlpArgs)], C.c_int),
+    "ds5_hip_moe": ([_P, C.POINTER(MoeArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
@@ -357,6 +387,33 @@ def add(ctx: Ctx, args: AddArgs) -> None:
 def matmulAdd(ctx: Ctx, args: MatmulAddArgs) -> None:
     """out = residual + x . W^T (forward.zig:416-418's matmul then add, one launch)."""
     ctx.check(LIB.ds5_hip_matmul_add(ctx.handle, C.byref(args)))
+
+
+def routerTopK(ctx: Ctx, x: Buf, w: Buf, w_dtype: int, n_tokens: int, dim: int, n_experts: int, top_k: int,
+               norm_topk_prob: bool):
+    """(ids uint16 [n_tokens, top_k], weights f32 [n_tokens, top_k]) on the host
+    (kernels_c.zig:80-155; waits for the device)."""
+    ids = np.zeros((n_tokens, top_k), np.uint16)
+    wts = np.zeros((n_tokens, top_k), np.float32)
+    ctx.check(LIB.ds5_hip_router_topk(ctx.handle, C.byref(RouterArgs(
+        x, w, w_dtype, n_tokens, dim, n_experts, top_k, int(norm_topk_prob),
+        ids.ctypes.data_as(C.POINTER(C.c_uint16)), ids.size, wts.ctypes.data_as(C.POINTER(C.c_float)), wts.size))))
+    return ids, wts
+
+
+def expertMlpSwiglu(ctx: Ctx, x: Buf, gate: Buf, up: Buf, down: Buf, w_dtype: int, pairs: np.ndarray, out: Buf,
+                    n_tokens: int, dim: int, ffn_dim: int, n_experts: int) -> None:
+    """out[token] += weight * down(silu(gate(x)) * up(x)) per (token, expert, weight)
+    pair of the host array `pairs` (PAIR_DTYPE) (kernels_c.zig:157-214)."""
+    pairs = np.ascontiguousarray(pairs, dtype=PAIR_DTYPE)
+    ctx.check(LIB.ds5_hip_expert_mlp_swiglu(ctx.handle, C.byref(ExpertMlpArgs(
+        x, gate, up, down, w_dtype, pairs.ctypes.data if pairs.size else None, pairs.size, out, n_tokens, dim,
+        ffn_dim, n_experts))))
+
+
+def moe(ctx: Ctx, args: MoeArgs) -> None:
+    """Router and experts on the device, no host round trip (ds5_hip_moe)."""
+    ctx.check(LIB.ds5_hip_moe(ctx.handle, C.byref(args)))
 
 
 def matmulGroup(ctx: Ctx, args: MatmulGroupArgs) -> None:

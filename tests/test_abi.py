@@ -37,7 +37,8 @@ STRUCTS = {
     "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
     "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
     "ds5_matmul_args": "MatmulArgs", "ds5_matmul_group_args": "MatmulGroupArgs", "ds5_add_args": "AddArgs",
-    "ds5_matmul_add_args": "MatmulAddArgs",
+    "ds5_matmul_add_args": "MatmulAddArgs", "ds5_router_args": "RouterArgs", "ds5_pair": "Pair",
+    "ds5_expert_mlp_args": "ExpertMlpArgs", "ds5_moe_args": "MoeArgs",
 }
 
 
@@ -137,6 +138,58 @@ def test_matmul_add_preconditions(hip):
     assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, 8, 8, 1, 2, 48)) == 1
     assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, 4, 8, 1, 2, 64)) == 1  # residual
     assert rc_of(hip, "ds5_hip_matmul_add", M(4 * 64, 2 * 68, q8, hip.Buf(FAKE, 2, 8), 8, 1, 2, 64)) == 1  # unaligned
+
+
+def test_router_preconditions(hip):
+    """kernels_c.zig:81-95: dtype, top_k, dim, output lengths, x, w (no device touched)."""
+    ids, wts = np.zeros(4, np.uint16), np.zeros(4, np.float32)
+
+    def R(x=4 * 2 * 32, w=4 * 8 * 32, dt=hip.DTYPE_F32, T=2, dim=32, E=8, K=2, nid=4, nw=4):
+        return hip.RouterArgs(B(x), B(w), dt, T, dim, E, K, 1, ids.ctypes.data_as(C.POINTER(C.c_uint16)), nid,
+                              wts.ctypes.data_as(C.POINTER(C.c_float)), nw)
+    assert rc_of(hip, "ds5_hip_router_topk", R()) == 3
+    assert rc_of(hip, "ds5_hip_router_topk", R(dt=12)) == 2
+    assert rc_of(hip, "ds5_hip_router_topk", R(dt=hip.DTYPE_F16, w=2 * 8 * 32)) == 3
+    for bad in (R(K=0), R(K=9), R(dt=hip.DTYPE_Q8_0, dim=16, w=8 * 34), R(nid=3), R(nw=5), R(x=4 * 2 * 32 - 4),
+                R(w=4 * 8 * 32 - 1), R(dim=16384, x=4 * 2 * 16384, w=4 * 8 * 16384)):
+        assert rc_of(hip, "ds5_hip_router_topk", bad) == 1
+
+
+def test_expert_mlp_preconditions(hip):
+    """kernels_c.zig:157-183 and every pair in range, before anything runs."""
+    q8 = hip.DTYPE_Q8_0
+    bank = 2 * 32 * 34  # 2 experts, ffn = dim = 32
+
+    def E(pairs=(), dt=q8, x=4 * 32, out=4 * 32, g=bank, u=bank, d=bank, dim=32, ffn=32):
+        pr = np.array(list(pairs), hip.PAIR_DTYPE)
+        return hip.ExpertMlpArgs(B(x), B(g), B(u), B(d), dt, pr.ctypes.data if pr.size else None, pr.size, B(out),
+                                 1, dim, ffn, 2), pr
+    ok, _keep = E([(0, 1, 0.5)])
+    assert rc_of(hip, "ds5_hip_expert_mlp_swiglu", ok) == 3
+    empty, _keep2 = E()
+    assert rc_of(hip, "ds5_hip_expert_mlp_swiglu", empty) == 0  # nothing to do
+    bad_dt, _k = E(dt=hip.DTYPE_F16)
+    assert rc_of(hip, "ds5_hip_expert_mlp_swiglu", bad_dt) == 2
+    for kw in (dict(ffn=0), dict(dim=16), dict(x=4 * 31), dict(out=4 * 31), dict(g=bank - 1), dict(u=bank - 1),
+               dict(d=bank - 1), dict(pairs=[(0, 2, 1.0)]), dict(pairs=[(0, 0, 1.0), (1, 0, 1.0)])):
+        args, _k = E(**kw)
+        assert rc_of(hip, "ds5_hip_expert_mlp_swiglu", args) == 1, kw
+
+
+def test_moe_preconditions(hip):
+    """The router's checks, then the experts', then the optional outputs' sizes."""
+    q8 = hip.DTYPE_Q8_0
+    bank = 8 * 32 * 34
+
+    def M(rdt=hip.DTYPE_F32, dt=q8, K=2, ids=0, wts=0, g=bank):
+        return hip.MoeArgs(B(4 * 32), B(4 * 8 * 32), rdt, B(g), B(bank), B(bank), dt, B(4 * 32), B(ids), B(wts),
+                           1, 32, 32, 8, K, 1)
+    assert rc_of(hip, "ds5_hip_moe", M()) == 3
+    assert rc_of(hip, "ds5_hip_moe", M(ids=4, wts=8)) == 3
+    assert rc_of(hip, "ds5_hip_moe", M(rdt=12)) == 2
+    assert rc_of(hip, "ds5_hip_moe", M(dt=hip.DTYPE_F16)) == 2
+    for bad in (M(K=0), M(g=bank - 1), M(ids=2), M(wts=4)):
+        assert rc_of(hip, "ds5_hip_moe", bad) == 1
 
 
 def test_rope_preconditions(hip):

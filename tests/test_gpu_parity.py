@@ -748,6 +748,198 @@ def test_matmul_add_equals_matmul_then_add(ctx, hip, oracle, m, n, k, w_off):
     assert np.all(np.abs(fused - want) <= _dot_bound(x, oracle.q8_0_dequantize(rows, k)) + 1e-6 * np.abs(r))
 
 
+# ---------------------------------------------------------------------------
+# MoE router and experts (kernels_c.zig)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("i", range(3))
+def test_router_fixtures(ctx, hip, oracle, i):
+    """kernels_c.zig:250-318 through the GPU: ids exact, weights within the case tolerance,
+    and ids equal to the oracle's, weights within 1e-6 of it (the device's expf against
+    the C library's, through the softmax sum and the renormalisation)."""
+    c = _cases(oracle, "router")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w = _t(oracle, c, "input"), _t(oracle, c, "weight")
+    T, K = p["n_tokens"], p["top_k"]
+    ids, wts = hip.routerTopK(ctx, ctx.from_numpy(x), ctx.from_numpy(w), hip.DTYPE_F32, T, p["dim"], p["n_experts"],
+                              K, p["norm_topk_prob"])
+    assert np.array_equal(ids.astype(np.int32), _t(oracle, c, "expert_ids").reshape(T, K))
+    assert oracle.compare(_t(oracle, c, "gate_weights").reshape(T, K), wts, tol["atol"], tol["rtol"]).passed
+    oi, ow = oracle.router_topk(x, w, oracle.F32, T, p["dim"], p["n_experts"], K, p["norm_topk_prob"])
+    rel = np.abs(wts - ow) / np.abs(ow)
+    print(f"  weights vs oracle: max rel {rel.max():.2e} ({(np.abs(wts - ow) / np.spacing(np.abs(ow))).max():.0f} ulp)")
+    assert np.array_equal(ids, oi) and np.all(rel <= 1e-6)
+
+
+def test_router_hand_cases(ctx, hip):
+    """kernels_c.zig:403-477: raw probabilities without renormalisation; exact ties go to
+    the lower id."""
+    x = ctx.from_numpy(np.array([[1, 0, 0, 0]], np.float32))
+    w = ctx.from_numpy(np.array([[2, 0, 0, 0], [0, 9, 9, 9], [1, 0, 0, 0], [-1, 0, 0, 0]], np.float32))
+    ids, wts = hip.routerTopK(ctx, x, w, hip.DTYPE_F32, 1, 4, 4, 2, False)
+    denom = sum(np.exp(np.float64(l) - 2.0) for l in (2, 0, 1, -1))
+    assert ids.tolist() == [[0, 2]] and abs(wts[0, 0] - 1 / denom) <= 1e-6 and abs(wts[0, 1] - np.exp(-1) / denom) <= 1e-6
+    w = ctx.from_numpy(np.array([[1, 0, 0, 0], [3, 0, 0, 0], [3, 0, 0, 0], [0, 0, 0, 0]], np.float32))
+    ids, wts = hip.routerTopK(ctx, x, w, hip.DTYPE_F32, 1, 4, 4, 3, True)
+    assert ids.tolist() == [[1, 2, 0]] and wts[0, 0] == wts[0, 1] and abs(wts.sum() - 1) <= 1e-6
+
+
+@pytest.mark.parametrize("dt,off", [("f32", 0), ("f16", 0), ("q8", 0), ("f32", 2), ("f16", 1)])
+def test_router_vs_oracle(ctx, hip, oracle, dt, off):
+    """Qwen3-30B-A3B's router shape (dim 2048, 128 experts, top 8) on 5 tokens, every weight
+    dtype, and views at odd offsets (bytewise reads): ids equal to the oracle's, weights
+    within 1e-6; logits are the reference's serial dot, so only exp may differ."""
+    g = np.random.default_rng(len(dt) * 7 + off)
+    T, dim, E, K = 5, 2048, 128, 8
+    wf = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
+    if dt == "q8":
+        wv, odt, hdt = oracle.q8_0_quantize(wf), oracle.Q8_0, hip.DTYPE_Q8_0
+    elif dt == "f16":
+        wv, odt, hdt = wf.astype(np.float16).view(np.uint16), oracle.F16, hip.DTYPE_F16
+    else:
+        wv, odt, hdt = wf, oracle.F32, hip.DTYPE_F32
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    wb = ctx.createBuffer(wv.nbytes + off)
+    ctx.upload(wb, off, np.ascontiguousarray(wv))
+    ids, wts = hip.routerTopK(ctx, ctx.from_numpy(x), hip.Buf(wb.handle, wb.offset + off, wv.nbytes), hdt, T, dim, E,
+                              K, True)
+    oi, ow = oracle.router_topk(x, wv, odt, T, dim, E, K, True)
+    assert np.array_equal(ids, oi)
+    rel = np.abs(wts - ow) / np.abs(ow)
+    print(f"  weights vs oracle: max rel {rel.max():.2e}", flush=True)
+    assert np.all(rel <= 1e-6)
+
+
+@pytest.mark.parametrize("i", range(3))
+def test_expert_mlp_fixtures(ctx, hip, oracle, i):
+    """kernels_c.zig:320-401 through the GPU: Q8_0 banks, token-major pairs, the case tolerance."""
+    c = _cases(oracle, "expert_mlp")[i]
+    p, tol = c["params"], c["tolerance"]
+    T, dim, ffn, E, K = p["n_tokens"], p["dim"], p["ffn_dim"], p["n_experts"], p["top_k"]
+    x = _t(oracle, c, "input")
+    banks = [ctx.from_numpy(_t(oracle, c, n)) for n in ("gate", "up", "down")]
+    pairs = oracle.pairs_from_router(_t(oracle, c, "expert_ids").reshape(T, K), _t(oracle, c, "gate_weights").reshape(T, K))
+    out = ctx.from_numpy(np.zeros((T, dim), np.float32))
+    hip.expertMlpSwiglu(ctx, ctx.from_numpy(x), *banks, hip.DTYPE_Q8_0, pairs, out, T, dim, ffn, E)
+    got = ctx.to_numpy(out, np.float32, (T, dim))
+    assert oracle.compare(_t(oracle, c, "output").reshape(T, dim), got, tol["atol"], tol["rtol"]).passed
+
+
+def test_expert_mlp_hand_cases(ctx, hip, oracle):
+    """kernels_c.zig:550-623: no pairs leave out untouched; two f32 pairs accumulate."""
+    bank = ctx.from_numpy(np.zeros((32, 34), np.uint8))
+    out = ctx.from_numpy(np.full((2, 32), 7.0, np.float32))
+    hip.expertMlpSwiglu(ctx, ctx.from_numpy(np.zeros((2, 32), np.float32)), bank, bank, bank, hip.DTYPE_Q8_0,
+                        np.zeros(0, hip.PAIR_DTYPE), out, 2, 32, 32, 1)
+    assert np.all(ctx.to_numpy(out, np.float32, (2, 32)) == 7.0)
+    x = np.array([[1.0, -2.0]], np.float32)
+    gate, up, down = (np.array(v, np.float32) for v in ([1, 0, 0, 1, 0, 1, 1, 0], [2, 0, 0, 2, 2, 0, 0, 2],
+                                                        [1, 0, 0, 1, 0, 1, 1, 0]))
+    pairs = np.array([(0, 0, 0.5), (0, 1, 2.0)], hip.PAIR_DTYPE)
+    out = ctx.from_numpy(np.zeros((1, 2), np.float32))
+    hip.expertMlpSwiglu(ctx, ctx.from_numpy(x), ctx.from_numpy(gate), ctx.from_numpy(up), ctx.from_numpy(down),
+                        hip.DTYPE_F32, pairs, out, 1, 2, 2, 2)
+    want = oracle.expert_mlp_swiglu(x, gate, up, down, oracle.F32, pairs.astype(oracle.PAIR_DTYPE), 1, 2, 2, 2)
+    assert np.all(np.abs(ctx.to_numpy(out, np.float32, (1, 2)) - want) <= 1e-6)
+
+
+def _expert_bound(x, G, U, D, pairs, T, dim, ffn):
+    """Elementwise bound for two f32 evaluations of the expert MLP in different orders:
+    1e-5 of the magnitudes the sums run over, through silu and the down projection."""
+    ax = np.abs(x).astype(np.float64)
+    b = np.zeros((T, dim))
+    for t, e, wt in pairs.tolist():
+        gm = np.abs(G[e * ffn:(e + 1) * ffn]) @ ax[t]
+        um = np.abs(U[e * ffn:(e + 1) * ffn]) @ ax[t]
+        hm = (gm + 1e-30) * (um + 1e-30) * 1.5
+        b[t] += abs(wt) * (np.abs(D[e * dim:(e + 1) * dim]) @ hm)
+    return 1e-5 * b + 1e-30
+
+
+@pytest.mark.parametrize("case", ["decode_q8", "prefill_q8_interleaved", "f32", "serial_unaligned"])
+def test_expert_mlp_vs_oracle(ctx, hip, oracle, case):
+    """Qwen3-30B-A3B-shaped experts (dim 2048, ffn 768; fewer experts) against the oracle
+    within a reordering bound: a decode token's 8 pairs; 6 tokens with their pairs
+    interleaved (each token's contributions still added in list order); f32 banks; a bank
+    view at a 2-byte offset (serial kernels)."""
+    g = np.random.default_rng(len(case))
+    E = 16
+    T, dim, ffn = {"decode_q8": (1, 2048, 768), "prefill_q8_interleaved": (6, 2048, 768), "f32": (3, 256, 96),
+                   "serial_unaligned": (2, 256, 96)}[case]
+    q8 = case != "f32"
+    mk = lambda rows, k: (g.standard_normal((rows, k)) * 0.05).astype(np.float32)
+    Gf, Uf, Df = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    if q8:
+        G, U, D = (oracle.q8_0_quantize(v) for v in (Gf, Uf, Df))
+        Gf, Uf, Df = oracle.q8_0_dequantize(G, dim), oracle.q8_0_dequantize(U, dim), oracle.q8_0_dequantize(D, ffn)
+    else:
+        G, U, D = Gf, Uf, Df
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    K = 8 if case == "decode_q8" else 3
+    pairs = np.zeros(T * K, hip.PAIR_DTYPE)
+    pairs["token"] = np.tile(np.arange(T), K) if case == "prefill_q8_interleaved" else np.repeat(np.arange(T), K)
+    pairs["expert"] = g.integers(0, E, T * K)
+    pairs["weight"] = g.random(T * K).astype(np.float32)
+    off = 2 if case == "serial_unaligned" else 0
+    bufs = []
+    for arr in (G, U, D):
+        b = ctx.createBuffer(arr.nbytes + off + 4)
+        ctx.upload(b, off, np.ascontiguousarray(arr))
+        bufs.append(hip.Buf(b.handle, b.offset + off, arr.nbytes))
+    r = g.standard_normal((T, dim)).astype(np.float32)
+    out = ctx.from_numpy(r)
+    ctx.set_kernel_timing(True)
+    try:
+        hip.expertMlpSwiglu(ctx, ctx.from_numpy(x), *bufs, hip.DTYPE_Q8_0 if q8 else hip.DTYPE_F32, pairs, out, T, dim,
+                            ffn, E)
+        ctx.submit()
+        serial = ctx.kernel_time("moe_gate_up_serial_kernel")[0]
+    finally:
+        ctx.set_kernel_timing(False)
+    assert serial == (1 if case == "serial_unaligned" else 0)
+    got = ctx.to_numpy(out, np.float32, (T, dim))
+    want = oracle.expert_mlp_swiglu(x, G, U, D, oracle.Q8_0 if q8 else oracle.F32, pairs.astype(oracle.PAIR_DTYPE), T,
+                                    dim, ffn, E, out=r)
+    bound = _expert_bound(x, Gf.astype(np.float64), Uf.astype(np.float64), Df.astype(np.float64), pairs, T, dim, ffn)
+    assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
+
+
+def test_expert_mlp_bad_pair_leaves_out(ctx, hip):
+    """A pair out of range is ShapeMismatch before anything runs (out unchanged)."""
+    bank = ctx.from_numpy(np.zeros((2 * 32, 34), np.uint8))
+    out = ctx.from_numpy(np.full((1, 32), 3.0, np.float32))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.expertMlpSwiglu(ctx, ctx.from_numpy(np.ones((1, 32), np.float32)), bank, bank, bank, hip.DTYPE_Q8_0,
+                            np.array([(0, 1, 1.0), (0, 2, 1.0)], hip.PAIR_DTYPE), out, 1, 32, 32, 2)
+    assert np.all(ctx.to_numpy(out, np.float32, (1, 32)) == 3.0)
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T):
+    """ds5_hip_moe (router and experts on the device, pairs never leave it) equals
+    ds5_hip_router_topk then ds5_hip_expert_mlp_swiglu on the router's pairs, bit for bit;
+    the device ids / weights equal the host ones."""
+    g = np.random.default_rng(T)
+    dim, ffn, E, K = 2048, 768, 32, 8
+    rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    xb, rwb = ctx.from_numpy(x), ctx.from_numpy(rw)
+    banks = [ctx.from_numpy(v) for v in (G, U, D)]
+    r = g.standard_normal((T, dim)).astype(np.float32)
+    out1, ids_b, w_b = ctx.from_numpy(r), ctx.createBuffer(T * K * 2), ctx.createBuffer(T * K * 4)
+    hip.moe(ctx, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, out1, ids_b, w_b, T, dim, ffn, E, K, 1))
+    ids, wts = hip.routerTopK(ctx, xb, rwb, hip.DTYPE_F32, T, dim, E, K, True)
+    out2 = ctx.from_numpy(r)
+    hip.expertMlpSwiglu(ctx, xb, *banks, hip.DTYPE_Q8_0, oracle.pairs_from_router(ids, wts).astype(hip.PAIR_DTYPE),
+                        out2, T, dim, ffn, E)
+    assert np.array_equal(ctx.to_numpy(ids_b, np.uint16, (T, K)), ids)
+    assert np.array_equal(ctx.to_numpy(w_b, np.float32, (T, K)).view(np.uint32), wts.view(np.uint32))
+    a, b = ctx.to_numpy(out1, np.float32, (T, dim)), ctx.to_numpy(out2, np.float32, (T, dim))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):
