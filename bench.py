@@ -162,6 +162,38 @@ class WoSweep:
                 self.H.add(self.ctx, a[1])
 
 
+class MoeSweep:
+    """The MoE block of a decode step (forward.zig after the attention block): n_layers of
+    router top-8 of 128 experts (f32 router weights [128 x 2048]) and the SwiGLU experts
+    (Q8_0 banks: gate/up [128, 768, 2048], down [128, 2048, 768]) for one token, on the
+    device (ds5_hip_moe: no host round trip). Every layer has its own banks (642 MB) and
+    its own x, so its 8 experts differ; the 16 layers' 640 MB of touched experts exceed the
+    256 MB MALL. Bank bytes are random with small scales (one random template per shape)."""
+
+    def __init__(self, H, ctx, layers=16, dim=2048, ffn=768, E=128, K=8, seed=13):
+        self.H, self.ctx, self.layers = H, ctx, layers
+        g = np.random.default_rng(seed)
+
+        def template(rows, k):
+            w = g.integers(0, 256, (rows, k // 32, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.002], np.float16).view(np.uint8)
+            return w.reshape(rows, k // 32 * 34)
+        gu, dn = template(E * ffn, dim), template(E * dim, ffn)
+        empty = H.Buf(None, 0, 0)
+        self.args = []
+        for _ in range(layers):
+            x = ctx.from_numpy(g.standard_normal((1, dim)).astype(np.float32))
+            rw = ctx.from_numpy((g.standard_normal((E, dim)) * 0.03).astype(np.float32))
+            self.args.append(H.MoeArgs(x, rw, H.DTYPE_F32, ctx.from_numpy(gu), ctx.from_numpy(gu), ctx.from_numpy(dn),
+                                       H.DTYPE_Q8_0, ctx.createBuffer(dim * 4), empty, empty, 1, dim, ffn, E, K, 1))
+        # bytes one token moves: router weights, its 8 experts' three matrices, x, out (read and written)
+        self.bytes_per_layer = E * dim * 4 + K * 3 * ffn * (dim // 32) * 34 + 3 * dim * 4
+
+    def sweep(self):
+        for a in self.args:
+            self.H.moe(self.ctx, a)
+
+
 class ProjPrefill:
     """The q/k/v projections of a 2048-token prefill (forward.zig:337-339 at m = T):
     x [T, hidden] f32 . W^T for wq [n_q_heads*d, hidden], wk and wv [n_kv_heads*d,
@@ -317,9 +349,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,WO,QKVP",
+    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,WO,MOE,QKVP",
                     help="comma list of configs to run (C1 is the headline; QKV / QKVP: the decode / prefill "
-                         "q/k/v projections; WO: the decode output projection and residual)")
+                         "q/k/v projections; WO: the decode output projection and residual; MOE: the decode MoE block)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -465,6 +497,24 @@ def main():
                   "us_per_layer_matmul_then_add)")
         log(f"[bench] WO fused {us:.3f} us/layer ({bpl / (us * 1e3):.1f} GB/s); kernel {ns_k / 1e3:.3f} us; "
             f"matmul then add {us_sep:.3f} us/layer")
+
+    if "MOE" in only:
+        log("[bench] MOE: decode MoE block (router top-8 of 128, SwiGLU experts 2048 x 768 Q8_0), 16 layers")
+        w = MoeSweep(H, ctx)
+        stepsm = max(5, args.steps // 4)
+        elapsed, _ = time_graph(ctx, w, stepsm, 2)
+        us = elapsed / (w.layers * stepsm) * 1e6
+        per = {kn: kernel_mean_ns(ctx, w, kn, 2)[0] / 1e3 for kn in
+               ("router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_kernel",
+                "moe_combine_kernel")}
+        extra["moe_block_decode"] = dict(
+            us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2), bytes_per_layer=w.bytes_per_layer,
+            kernel_us={k: round(v, 3) for k, v in per.items()},
+            shape="1 token, dim 2048, 128 experts top 8, ffn 768, Q8_0 banks, f32 router; router and experts on the "
+                  "device (ds5_hip_moe)")
+        log(f"[bench] MOE {us:.3f} us/layer ({w.bytes_per_layer / (us * 1e3):.1f} GB/s); kernels "
+            + ", ".join(f"{k} {v:.2f} us" for k, v in per.items()))
+        del w
 
     if "QKVP" in only:
         log("[bench] QKVP: prefill q/k/v projections, 2048 tokens, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048]")

@@ -235,8 +235,8 @@ int ds5_hip_add(ds5_hip_ctx* ctx, const ds5_add_args* args);
  * copies them back. Checks in the reference's order: w_dtype (f32, f16, q8_0)
  * else UnsupportedDtype; top_k in 1..n_experts; dim a positive multiple of the
  * dtype's block; both output lengths == n_tokens * top_k; x; w -- each else
- * ShapeMismatch. dim + n_experts above 16384 is ShapeMismatch here (the token
- * and its logits are held in 64 KiB of LDS). Logits are the reference's serial
+ * ShapeMismatch. Also ShapeMismatch here: a router row above 64 KiB, 4*dim plus a
+ * row above 128 KiB, or n_experts above 16384 (LDS). Logits are the reference's serial
  * dot, bit for bit; exp is the device's, so weights agree within an ulp or so
  * and ids agree unless two probabilities do as well. */
 typedef struct ds5_router_args {

@@ -133,6 +133,7 @@ struct RouterLaunch {
     uint16_t* ids;
     float* weights;
     ds5_pair* pairs;  // may be null
+    float* logits;    // scratch [n_tokens, n_experts]
 };
 int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a);
 

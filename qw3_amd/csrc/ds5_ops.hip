@@ -203,9 +203,10 @@ static int check_router(ds5_hip_ctx* ctx, const char* op, ds5_buf x, ds5_buf w, 
     if (!outputs_ok) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: output lengths are not n_tokens * top_k", op);
     if (!covers(x, T * dim * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: x too small", op);
     if (!covers(w, E * row_bytes_of(dt, dim))) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: router w too small", op);
-    if (dim + E > 16384)
-        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dim + n_experts = %llu exceeds 16384 (LDS)", op,
-                        (unsigned long long)(dim + E));
+    // LDS: a token's x and at least one router row (<= 128 KiB), the logits of a token (<= 64 KiB)
+    if (row_bytes_of(dt, dim) > 65536 || dim * 4 + row_bytes_of(dt, dim) > 131072 || E > 16384)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "%s: dim %llu / n_experts %llu exceed the router's LDS", op,
+                        (unsigned long long)dim, (unsigned long long)E);
     return DS5_OK;
 }
 
@@ -245,6 +246,7 @@ static bool experts_fast(ds5_buf x, ds5_buf gate, ds5_buf up, ds5_buf down, uint
 }
 
 struct MoeScratch {
+    float* logits;
     ds5_pair* pairs;
     uint32_t* order;
     uint32_t* offsets;
@@ -256,27 +258,21 @@ struct MoeScratch {
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static int moe_scratch(ds5_hip_ctx* ctx, uint64_t T, uint64_t P, uint64_t dim, uint64_t ffn, MoeScratch* s) {
-    const size_t sz[7] = {up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4), up256(P * ffn * 4),
-                          up256(P * dim * 4), up256(P * 2), up256(P * 4)};
+static int moe_scratch(ds5_hip_ctx* ctx, uint64_t T, uint64_t E, uint64_t P, uint64_t dim, uint64_t ffn,
+                       MoeScratch* s) {
+    const size_t sz[8] = {up256(T * E * 4), up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4),
+                          up256(P * ffn * 4), up256(P * dim * 4), up256(P * 2), up256(P * 4)};
     size_t total = 0;
     for (size_t v : sz) total += v;
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, total, &ws)) return rc;
     char* p = (char*)ws;
-    s->pairs = (ds5_pair*)p;
-    p += sz[0];
-    s->order = (uint32_t*)p;
-    p += sz[1];
-    s->offsets = (uint32_t*)p;
-    p += sz[2];
-    s->h = (float*)p;
-    p += sz[3];
-    s->y = (float*)p;
-    p += sz[4];
-    s->ids = (uint16_t*)p;
-    p += sz[5];
-    s->weights = (float*)p;
+    void** dst[8] = {(void**)&s->logits, (void**)&s->pairs, (void**)&s->order, (void**)&s->offsets,
+                     (void**)&s->h, (void**)&s->y, (void**)&s->ids, (void**)&s->weights};
+    for (int i = 0; i < 8; i++) {
+        *dst[i] = p;
+        p += sz[i];
+    }
     return DS5_OK;
 }
 
@@ -315,10 +311,10 @@ int ds5_hip_router_topk(ds5_hip_ctx* ctx, const ds5_router_args* a) {
     if (a->n_tokens == 0) return DS5_OK;
     if (int rc = set_device(ctx)) return rc;
     MoeScratch s{};
-    if (int rc = moe_scratch(ctx, a->n_tokens, TK, 0, 0, &s)) return rc;
+    if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, 0, 0, &s)) return rc;
     RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->w), a->w_dtype,
                    row_bytes_of(a->w_dtype, a->dim), a->n_tokens, a->dim, a->n_experts, a->top_k,
-                   a->norm_topk_prob != 0, s.ids, s.weights, nullptr};
+                   a->norm_topk_prob != 0, s.ids, s.weights, nullptr, s.logits};
     if (int rc = launch_router(ctx, r)) return rc;
     // host outputs (the reference's contract): wait, then copy back
     int rc = ds5_hip_status(ctx, hipMemcpyAsync(a->out_ids, s.ids, TK * 2, hipMemcpyDeviceToHost, ctx->stream), "ids");
@@ -351,7 +347,7 @@ int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* a) {
         for (uint64_t p = 0; p < P; p++) order[fill[a->pairs[p].token]++] = (uint32_t)p;
     }
     MoeScratch s{};
-    if (int rc = moe_scratch(ctx, a->n_tokens, P, a->dim, a->ffn_dim, &s)) return rc;
+    if (int rc = moe_scratch(ctx, a->n_tokens, 0, P, a->dim, a->ffn_dim, &s)) return rc;
     int rc = ds5_hip_status(ctx, hipMemcpyAsync(s.pairs, a->pairs, P * sizeof(ds5_pair), hipMemcpyHostToDevice,
                                                 ctx->stream), "pairs");
     if (!rc) rc = ds5_hip_status(ctx, hipMemcpyAsync(s.order, order.data(), P * 4, hipMemcpyHostToDevice, ctx->stream),
@@ -383,12 +379,12 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     if (TK > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: too many pairs");
     if (int rc = set_device(ctx)) return rc;
     MoeScratch s{};
-    if (int rc = moe_scratch(ctx, a->n_tokens, TK, a->dim, a->ffn_dim, &s)) return rc;
+    if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, a->dim, a->ffn_dim, &s)) return rc;
     RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->router_w), a->router_dtype,
                    row_bytes_of(a->router_dtype, a->dim), a->n_tokens, a->dim, a->n_experts, a->top_k,
                    a->norm_topk_prob != 0,
                    a->ids.len ? (uint16_t*)ds5_ptr(a->ids) : s.ids,
-                   a->weights.len ? (float*)ds5_ptr(a->weights) : s.weights, s.pairs};
+                   a->weights.len ? (float*)ds5_ptr(a->weights) : s.weights, s.pairs, s.logits};
     if (int rc = launch_router(ctx, r)) return rc;
     ExpertLaunch l = expert_launch(a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)TK,
                                    a->dim, a->ffn_dim, a->n_experts, s);

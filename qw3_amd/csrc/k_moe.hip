@@ -20,6 +20,8 @@
 // owning the 32-element blocks L + 64 j, a fixed-order wavefront reduction (so
 // they agree with the reference's serial dots to rounding). The combine adds
 // each product in the reference's order, rounding as it does.
+#include <type_traits>
+
 #include "ds5_common.hpp"
 
 namespace {
@@ -31,81 +33,132 @@ constexpr int kMoeWaves = 8;  // wavefronts (weight rows) per GEMV workgroup
 // router
 // ---------------------------------------------------------------------------
 
-// Weight element i of a router row, as the reference widens it (AL: the row
-// is aligned to its element size; else it is read bytewise).
+// Weight element i of a router row, widened exactly as the reference widens it
+// (f16 -> f32, and a Q8_0 element's f32(scale) * q, exact in f32). AL: the row
+// is aligned to its element size; else it is read bytewise.
 template <uint32_t DT, bool AL>
 __device__ __forceinline__ float router_w(const uint8_t* row, uint32_t i) {
-    if constexpr (DT == DS5_DTYPE_F32) {
+    if constexpr (DT == DS5_DTYPE_Q8_0) {
+        const uint8_t* blk = row + (uint64_t)(i / 32) * kQ8Bytes;
+        const float scale = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        return scale * (float)(int8_t)blk[2 + i % 32];
+    } else if constexpr (DT == DS5_DTYPE_F32) {
         if constexpr (AL) return ((const float*)row)[i];
         float v;
-        __builtin_memcpy(&v, row + 4 * i, 4);
+        __builtin_memcpy(&v, row + 4 * (uint64_t)i, 4);
         return v;
     } else {
         if constexpr (AL) return f16_bits_to_f32(((const uint16_t*)row)[i]);
         uint16_t b;
-        __builtin_memcpy(&b, row + 2 * i, 2);
+        __builtin_memcpy(&b, row + 2 * (uint64_t)i, 2);
         return f16_bits_to_f32(b);
     }
 }
 
-// dotRow (kernels_c.zig:40-68) in its order: acc += w * x for f32 / f16; for
-// Q8_0, acc += (scale * q) * x per element.
-template <uint32_t DT, bool AL>
-__device__ float serial_dot(const float* x, const uint8_t* row, uint32_t dim) {
-#pragma clang fp contract(off)
-    float acc = 0.0f;
-    if constexpr (DT == DS5_DTYPE_Q8_0) {
-        for (uint32_t b = 0; b < dim / 32; b++) {
-            const uint8_t* blk = row + (uint64_t)b * kQ8Bytes;
-            const float scale = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-            for (int i = 0; i < 32; i++) acc += (scale * (float)(int8_t)blk[2 + i]) * x[32 * b + i];
-        }
-    } else {
-        for (uint32_t i = 0; i < dim; i++) acc += router_w<DT, AL>(row, i) * x[i];
-    }
-    return acc;
+// Logits (router_logits_kernel): workgroup (token t, expert group g) holds the
+// token's x and the raw bytes of R consecutive expert rows in LDS, loaded with
+// every load in flight at once (the rows are contiguous); thread r < R then
+// sums its row in element order, exactly dotRow (kernels_c.zig:40-68). Many
+// workgroups per token spread the weight traffic over the CUs; the serial sum
+// (one add per element) bounds each.
+constexpr uint32_t kRouterRowBytes = 65536;  // LDS for one group's rows
+
+__host__ __device__ inline uint32_t router_rows_per_group(uint64_t row_bytes) {
+    const uint64_t r = kRouterRowBytes / row_bytes;
+    return (uint32_t)(r > 16 ? 16 : (r ? r : 1));
 }
 
-// Dynamic LDS: x of the token (dim floats), then the n_experts probabilities.
-template <uint32_t DT, bool AL>
-__global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __restrict__ x,
-                                                                const uint8_t* __restrict__ w, uint64_t row_bytes,
-                                                                uint32_t dim, uint32_t n_experts, uint32_t top_k,
-                                                                uint32_t norm, uint16_t* __restrict__ out_ids,
-                                                                float* __restrict__ out_w,
-                                                                ds5_pair* __restrict__ pairs) {
+// Dynamic LDS: x (dim floats), then R rows of raw weights. CP: the rows are
+// copied in 16-byte, 4-byte or 1-byte units (by the source's alignment), every
+// thread's loads issued before its stores.
+template <int CP>
+__device__ __forceinline__ void router_copy_rows(const uint8_t* src, uint8_t* dst, uint64_t nbytes) {
+    if constexpr (CP == 1) {
+        for (uint64_t i = threadIdx.x; i < nbytes; i += kRouterThreads) dst[i] = src[i];
+    } else {
+        typedef typename std::conditional<CP == 16, f32x4, uint32_t>::type U;
+        constexpr int kN = kRouterRowBytes / CP / kRouterThreads;
+        const U* s = (const U*)src;
+        U* d = (U*)dst;
+        const uint32_t n = (uint32_t)(nbytes / CP);
+        U v[kN];
+#pragma unroll
+        for (int k = 0; k < kN; k++) {
+            const uint32_t i = threadIdx.x + kRouterThreads * k;
+            if (i < n) v[k] = s[i];
+        }
+#pragma unroll
+        for (int k = 0; k < kN; k++) {
+            const uint32_t i = threadIdx.x + kRouterThreads * k;
+            if (i < n) d[i] = v[k];
+        }
+    }
+}
+
+template <uint32_t DT, int CP>
+__global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const float* __restrict__ x,
+                                                                       const uint8_t* __restrict__ w,
+                                                                       uint64_t row_bytes, uint32_t dim,
+                                                                       uint32_t n_experts, uint32_t rows,
+                                                                       float* __restrict__ logits) {
 #pragma clang fp contract(off)
-    extern __shared__ float router_smem[];
+    extern __shared__ __attribute__((aligned(16))) float router_smem[];
     float* xs = router_smem;
-    float* probs = router_smem + dim;
-    __shared__ float s_inv_sum;
-    const uint32_t t = blockIdx.x;
+    uint8_t* ws = (uint8_t*)(router_smem + ((dim + 3) & ~3u));
+    const uint32_t t = blockIdx.x, e0 = blockIdx.y * rows;
+    const uint32_t nr = min(rows, n_experts - e0);
+    router_copy_rows<CP>(w + (uint64_t)e0 * row_bytes, ws, (uint64_t)nr * row_bytes);
     for (uint32_t i = threadIdx.x; i < dim; i += kRouterThreads) xs[i] = x[(uint64_t)t * dim + i];
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < n_experts; e += kRouterThreads)
-        probs[e] = serial_dot<DT, AL>(xs, w + (uint64_t)e * row_bytes, dim);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float mx = -__builtin_inff();
-        for (uint32_t e = 0; e < n_experts; e++) mx = fmaxf(mx, probs[e]);
-        float sum = 0.0f;
-        for (uint32_t e = 0; e < n_experts; e++) {
-            const float p = expf(probs[e] - mx);
-            probs[e] = p;
-            sum += p;
+    if (threadIdx.x < nr) {
+        const uint8_t* row = ws + (uint64_t)threadIdx.x * row_bytes;
+        float acc = 0.0f;
+        uint32_t i = 0;
+        if constexpr (DT == DS5_DTYPE_F32) {
+            if (dim % 4 == 0) {  // rows and x 16-byte aligned in LDS: 16-byte reads, the sum element by element
+                const f32x4* w4 = (const f32x4*)row;
+                const f32x4* x4 = (const f32x4*)xs;
+                for (; i < dim; i += 4) {
+                    const f32x4 wv = w4[i / 4], xv = x4[i / 4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc += wv[c] * xv[c];
+                }
+            }
         }
+        for (; i < dim; i++) acc += router_w<DT, DT != DS5_DTYPE_Q8_0>(row, i) * xs[i];
+        logits[(uint64_t)t * n_experts + e0 + threadIdx.x] = acc;
+    }
+}
+
+// Softmax and top-k of one token's logits (router_select_kernel, one wavefront).
+__global__ __launch_bounds__(64) void router_select_kernel(const float* __restrict__ logits, uint32_t n_experts,
+                                                           uint32_t top_k, uint32_t norm, uint16_t* __restrict__ out_ids,
+                                                           float* __restrict__ out_w, ds5_pair* __restrict__ pairs) {
+#pragma clang fp contract(off)
+    extern __shared__ float probs[];
+    __shared__ float s_inv_sum;
+    const uint32_t t = blockIdx.x;
+    const int lane = threadIdx.x;
+    // max (order-free), exp of each logit (independent), then the sum in expert
+    // order by one lane, as the reference sums
+    float mx = -__builtin_inff();
+    for (uint32_t e = lane; e < n_experts; e += 64) mx = fmaxf(mx, logits[(uint64_t)t * n_experts + e]);
+    mx = wave_allreduce(mx, OpMax{});
+    for (uint32_t e = lane; e < n_experts; e += 64) probs[e] = expf(logits[(uint64_t)t * n_experts + e] - mx);
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (uint32_t e = 0; e < n_experts; e++) sum += probs[e];
         s_inv_sum = 1.0f / sum;
     }
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < n_experts; e += kRouterThreads) probs[e] *= s_inv_sum;
+    for (uint32_t e = lane; e < n_experts; e += 64) probs[e] *= s_inv_sum;
     __syncthreads();
-    if (threadIdx.x >= 64) return;  // wavefront 0 picks; no barrier follows
 
     // top-k: round j takes the largest untaken probability, the lower id on ties
     // (lanes scan their experts in ascending order with a strict >, as the
     // reference does; the cross-lane merge keeps that order). A probability
     // picked is overwritten with -1 (below every probability and the -1 start).
-    const int lane = threadIdx.x;
     float picked = 0.0f;
     for (uint32_t j = 0; j < top_k; j++) {
         uint32_t best = 0;
@@ -291,24 +344,44 @@ __global__ __launch_bounds__(256) void moe_down_serial_kernel(const float* h, co
 
 }  // namespace
 
-template <uint32_t DT, bool AL>
-static void launch_router_t(ds5_hip_ctx* ctx, const RouterLaunch& a, size_t smem) {
-    DS5_TIMED_LAUNCH(ctx, "router_kernel", (router_kernel<DT, AL>), dim3(a.n_tokens), dim3(kRouterThreads), smem,
-                     ctx->stream, a.x, a.w, a.row_bytes, a.dim, a.n_experts, a.top_k, (uint32_t)a.norm, a.ids,
-                     a.weights, a.pairs);
+template <uint32_t DT, int CP>
+static int launch_router_t(ds5_hip_ctx* ctx, const RouterLaunch& a) {
+    const uint32_t rows = router_rows_per_group(a.row_bytes);
+    const size_t smem = ((size_t)((a.dim + 3) & ~3u)) * sizeof(float) + (size_t)rows * a.row_bytes;
+    if (smem > 131072)  // nothing is enqueued yet: the router is the first launch of its calls
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "router: dim %u needs %zu bytes of LDS (131072 at most)", a.dim, smem);
+    static bool big_lds = false;  // allow the 64 KiB of rows plus x (up to 128 KiB) once per instantiation
+    if (!big_lds) {
+        if (int rc = ds5_hip_status(ctx, hipFuncSetAttribute((const void*)router_logits_kernel<DT, CP>,
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize, 131072),
+                                    "router lds"))
+            return rc;
+        big_lds = true;
+    }
+    const dim3 grid(a.n_tokens, (a.n_experts + rows - 1) / rows);
+    DS5_TIMED_LAUNCH(ctx, "router_logits_kernel", (router_logits_kernel<DT, CP>), grid, dim3(kRouterThreads), smem,
+                     ctx->stream, a.x, a.w, a.row_bytes, a.dim, a.n_experts, rows, a.logits);
+    return ds5_after_launch(ctx, "router_logits_kernel");
+}
+
+template <uint32_t DT>
+static int launch_router_dt(ds5_hip_ctx* ctx, const RouterLaunch& a) {
+    const uintptr_t w = (uintptr_t)a.w;
+    if ((w & 15u) == 0 && a.row_bytes % 16 == 0) return launch_router_t<DT, 16>(ctx, a);
+    if ((w & 3u) == 0 && a.row_bytes % 4 == 0) return launch_router_t<DT, 4>(ctx, a);
+    return launch_router_t<DT, 1>(ctx, a);
 }
 
 int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
-    const size_t smem = ((size_t)a.dim + a.n_experts) * sizeof(float);
-    const uintptr_t w = (uintptr_t)a.w;
-    if (a.w_dtype == DS5_DTYPE_F32)
-        (w & 3u) ? launch_router_t<DS5_DTYPE_F32, false>(ctx, a, smem) : launch_router_t<DS5_DTYPE_F32, true>(ctx, a, smem);
-    else if (a.w_dtype == DS5_DTYPE_F16)
-        (w & 1u) ? launch_router_t<DS5_DTYPE_F16, false>(ctx, a, smem) : launch_router_t<DS5_DTYPE_F16, true>(ctx, a, smem);
-    else
-        launch_router_t<DS5_DTYPE_Q8_0, true>(ctx, a, smem);
-    return ds5_after_launch(ctx, "router_kernel");
+    int rc = a.w_dtype == DS5_DTYPE_F32   ? launch_router_dt<DS5_DTYPE_F32>(ctx, a)
+             : a.w_dtype == DS5_DTYPE_F16 ? launch_router_dt<DS5_DTYPE_F16>(ctx, a)
+                                          : launch_router_dt<DS5_DTYPE_Q8_0>(ctx, a);
+    if (rc) return rc;
+    DS5_TIMED_LAUNCH(ctx, "router_select_kernel", router_select_kernel, dim3(a.n_tokens), dim3(64),
+                     (size_t)a.n_experts * sizeof(float), ctx->stream, a.logits, a.n_experts, a.top_k, (uint32_t)a.norm,
+                     a.ids, a.weights, a.pairs);
+    return ds5_after_launch(ctx, "router_select_kernel");
 }
 
 int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {

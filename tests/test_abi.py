@@ -150,8 +150,11 @@ def test_router_preconditions(hip):
     assert rc_of(hip, "ds5_hip_router_topk", R()) == 3
     assert rc_of(hip, "ds5_hip_router_topk", R(dt=12)) == 2
     assert rc_of(hip, "ds5_hip_router_topk", R(dt=hip.DTYPE_F16, w=2 * 8 * 32)) == 3
+    assert rc_of(hip, "ds5_hip_router_topk", R(E=16385, w=4 * 16385 * 32)) == 1  # n_experts > 16384 (LDS)
+    assert rc_of(hip, "ds5_hip_router_topk", R(dim=16416, x=4 * 2 * 16416, w=4 * 8 * 16416)) == 1  # row > 64 KiB
+    assert rc_of(hip, "ds5_hip_router_topk", R(dim=16384, x=4 * 2 * 16384, w=4 * 8 * 16384)) == 3
     for bad in (R(K=0), R(K=9), R(dt=hip.DTYPE_Q8_0, dim=16, w=8 * 34), R(nid=3), R(nw=5), R(x=4 * 2 * 32 - 4),
-                R(w=4 * 8 * 32 - 1), R(dim=16384, x=4 * 2 * 16384, w=4 * 8 * 16384)):
+                R(w=4 * 8 * 32 - 1)):
         assert rc_of(hip, "ds5_hip_router_topk", bad) == 1
 
 
