@@ -1,0 +1,111 @@
+"""The whole synthetic model through the device engine (qw3_amd/engine.py), every kernel on
+the MI355X: the reference's end-to-end gates (src/test_forward.zig:192-330,
+src/test_gpu_forward.zig:94-360) plus a live diff against the oracle engine.
+
+- per-layer trace diff: the residual stream after layers 0, 2 and 3 of p0's prefill
+  against `l{0,2,3}_block.output`, and after every layer against the oracle engine
+  (layer tolerance atol 2e-3, rtol 1e-2, as test_gpu_forward.zig:338-341);
+- the five prompts: logits within the manifest tolerance and, with an f32 cache, every
+  greedy pick exact (p3's first pick is a near-tie an f16 cache flips; see
+  test_engine_oracle.py);
+- the f16 cache within 0.02 of the f32 engine (test_forward.zig:131-190);
+- both modes: the eight provider ops one call each, and the fused decls
+  (matmulGroup, attentionStep, matmulAdd, moe).
+"""
+import numpy as np
+import pytest
+
+import synth_model as S
+
+pytestmark = pytest.mark.gpu
+
+LAYER_ATOL, LAYER_RTOL = 2e-3, 1e-2
+
+
+@pytest.fixture(scope="module")
+def model(oracle):
+    return S.load()
+
+
+@pytest.fixture(scope="module")
+def weights(ctx, model):
+    from qw3_amd import engine as E
+    cfg, w, _ = model
+    return E.Weights(ctx, w, cfg)
+
+
+def _engine(ctx, hip, weights, kv, fused, capacity=64):
+    from qw3_amd import engine as E
+    return E.Engine(ctx, weights, max_batch=capacity, context_capacity=capacity,
+                    kv_dtype=hip.DTYPE_F32 if kv == "f32" else hip.DTYPE_F16, fused=fused)
+
+
+MODES = [("f32", False), ("f16", False), ("f32", True), ("f16", True)]
+IDS = ["ops-f32", "ops-f16", "fused-f32", "fused-f16"]
+
+
+@pytest.mark.parametrize("kv,fused", MODES, ids=IDS)
+def test_block_trace(ctx, hip, oracle, model, weights, kv, fused):
+    from oracle import engine as OE
+    cfg, w, prompts = model
+    toks = prompts[0]["token_ids"]
+    print(f"[engine] block trace kv={kv} fused={fused} tokens={len(toks)}", flush=True)
+    eng = _engine(ctx, hip, weights, kv, fused)
+    got = {}
+    eng.trace = lambda layer, op, a: got.__setitem__((layer, op), a) if op in ("block", "embed") else None
+    eng.forward(toks)
+    want = {}
+    ref = OE.Engine(w, cfg, 64, oracle.F32 if kv == "f32" else oracle.F16)
+    ref.forward(toks, trace=lambda layer, op, a: want.__setitem__((layer, op), a.copy()))
+    assert np.array_equal(got[(-1, "embed")], want[(-1, "embed")].reshape(-1))
+    for layer, x_in, _, x_out, atol, rtol in S.block_cases():
+        r = oracle.compare(x_out.reshape(-1), got[(layer, "block")], atol, rtol)
+        assert r.passed, ("fixture", layer, r)
+    for layer in range(cfg["n_layers"]):
+        r = oracle.compare(want[(layer, "block")].reshape(-1), got[(layer, "block")], LAYER_ATOL, LAYER_RTOL)
+        assert r.passed, ("oracle", layer, r)
+
+
+@pytest.mark.parametrize("kv,fused", MODES, ids=IDS)
+def test_prompts(ctx, hip, oracle, model, weights, kv, fused):
+    from qw3_amd import engine as E
+    cfg, w, prompts = model
+    eng = _engine(ctx, hip, weights, kv, fused)
+    for p in prompts:
+        print(f"[engine] prompt {p['name']} kv={kv} fused={fused}", flush=True)
+        logits, picks = S.run_prompt(eng, p, E.argmax)
+        want = S.prompt_logits(p)
+        assert logits.shape == want.shape
+        if kv == "f32":
+            assert picks == list(p["greedy_tokens"]), (p["name"], picks)
+        r = oracle.compare(want.reshape(-1), logits.reshape(-1), p["tolerance"]["atol"], p["tolerance"]["rtol"])
+        assert r.passed, (p["name"], r)
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["ops", "fused"])
+def test_f16_cache_close_to_f32(ctx, hip, oracle, weights, fused):
+    from qw3_amd import engine as E
+    e32 = _engine(ctx, hip, weights, "f32", fused, capacity=3)
+    e16 = _engine(ctx, hip, weights, "f16", fused, capacity=3)
+    a, b = e32.forward([1, 2, 3]), e16.forward([1, 2, 3])
+    assert oracle.compare(a.reshape(-1), b.reshape(-1), 0.02, 0.02).passed
+    assert E.argmax(a[-1]) == E.argmax(b[-1])
+    e32.reset(), e16.reset()
+    e32.forward([1, 2]), e16.forward([1, 2])
+    a, b = e32.forward([3]), e16.forward([3])
+    assert oracle.compare(a.reshape(-1), b.reshape(-1), 0.02, 0.02).passed
+    assert E.argmax(a[-1]) == E.argmax(b[-1])
+    with pytest.raises(ValueError, match="ContextOverflow"):
+        e32.forward([4])
+
+
+def test_fused_matches_ops(ctx, hip, oracle, model, weights):
+    """The fused decls against the eight-op engine on p4 (33 tokens, then 4 decode steps)."""
+    cfg, w, prompts = model
+    p = prompts[4]
+    a_eng, b_eng = _engine(ctx, hip, weights, "f16", False), _engine(ctx, hip, weights, "f16", True)
+    a, b = a_eng.forward(p["token_ids"]), b_eng.forward(p["token_ids"])
+    assert oracle.compare(a.reshape(-1), b.reshape(-1), LAYER_ATOL, LAYER_RTOL).passed
+    for t in p["greedy_tokens"][:4]:
+        a, b = a_eng.forward([t]), b_eng.forward([t])
+        assert oracle.compare(a.reshape(-1), b.reshape(-1), LAYER_ATOL, LAYER_RTOL).passed
