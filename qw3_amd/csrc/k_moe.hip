@@ -95,6 +95,51 @@ __device__ __forceinline__ void router_copy_rows(const uint8_t* src, uint8_t* ds
     }
 }
 
+// The row's sum of products p4[0 .. 4·n4) in element order (dotRow's adds), reading
+// eight 16-byte chunks ahead of the adds in two register sets in turn, so the chain
+// of dependent adds never waits for LDS.
+__device__ __forceinline__ float router_chain(const f32x4* __restrict__ p4, uint32_t n4) {
+#pragma clang fp contract(off)
+    constexpr uint32_t B = 8;
+    float acc = 0.0f;
+    uint32_t j = 0;
+    auto read = [&](f32x4* v, uint32_t at) {
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) v[b] = p4[at + b];
+        __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds
+    };
+    auto sum = [&](const f32x4* v) {
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc += v[b][c];
+    };
+    if (n4 >= B) {
+        f32x4 va[B], vb[B];
+        read(va, 0);
+        for (j = B; j + 2 * B <= n4; j += 2 * B) {
+            read(vb, j);
+            sum(va);
+            read(va, j + B);
+            sum(vb);
+        }
+        if (j + B <= n4) {
+            read(vb, j);
+            sum(va);
+            sum(vb);
+            j += B;
+        } else {
+            sum(va);
+        }
+    }
+    for (; j < n4; j++) {
+        const f32x4 v = p4[j];
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc += v[c];
+    }
+    return acc;
+}
+
 template <uint32_t DT, int CP>
 __global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const float* __restrict__ x,
                                                                        const uint8_t* __restrict__ w,
@@ -107,25 +152,60 @@ __global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const flo
     uint8_t* ws = (uint8_t*)(router_smem + ((dim + 3) & ~3u));
     const uint32_t t = blockIdx.x, e0 = blockIdx.y * rows;
     const uint32_t nr = min(rows, n_experts - e0);
+    if constexpr (DT == DS5_DTYPE_F32 && CP == 16) {
+        if (dim % 4 == 0 && ((uintptr_t)x & 15) == 0) {
+            // rows and x read together (one memory latency), the products w[i]·x[i]
+            // (each rounded, as dotRow rounds them) stored to LDS, then each row's
+            // thread adds them in order
+            const uint32_t n4 = dim / 4, total = nr * n4;
+            const f32x4* g4 = (const f32x4*)(w + (uint64_t)e0 * row_bytes);
+            const f32x4* xg4 = (const f32x4*)(x + (uint64_t)t * dim);
+            f32x4* p4s = (f32x4*)ws;
+            constexpr int kN = kRouterRowBytes / 16 / kRouterThreads;
+            f32x4 wv[kN], xv[kN];
+#pragma unroll
+            for (int k = 0; k < kN; k++) {
+                const uint32_t u = threadIdx.x + kRouterThreads * k;
+                if (u < total) {
+                    wv[k] = g4[u];
+                    xv[k] = xg4[u % n4];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kN; k++) {
+                const uint32_t u = threadIdx.x + kRouterThreads * k;
+                if (u < total) p4s[u] = wv[k] * xv[k];
+            }
+            __syncthreads();
+            if (threadIdx.x < nr)
+                logits[(uint64_t)t * n_experts + e0 + threadIdx.x] = router_chain(p4s + (uint64_t)threadIdx.x * n4, n4);
+            return;
+        }
+    }
     router_copy_rows<CP>(w + (uint64_t)e0 * row_bytes, ws, (uint64_t)nr * row_bytes);
     for (uint32_t i = threadIdx.x; i < dim; i += kRouterThreads) xs[i] = x[(uint64_t)t * dim + i];
     __syncthreads();
+    if constexpr (DT == DS5_DTYPE_F32) {
+        if (dim % 4 == 0) {
+            // f32 rows of 4·dim bytes, 16-byte aligned in LDS. Every thread first
+            // turns the rows into their products w[i]·x[i] in place (each rounded to
+            // f32, as dotRow rounds them); the row's thread then only adds, in
+            // element order, reading eight 16-byte chunks ahead of its adds so the
+            // chain of dependent adds never waits for LDS.
+            const uint32_t n4 = dim / 4;
+            f32x4* w4 = (f32x4*)ws;
+            const f32x4* x4 = (const f32x4*)xs;
+            for (uint32_t u = threadIdx.x; u < nr * n4; u += kRouterThreads) w4[u] = w4[u] * x4[u % n4];
+            __syncthreads();
+            if (threadIdx.x < nr)
+                logits[(uint64_t)t * n_experts + e0 + threadIdx.x] = router_chain(w4 + (uint64_t)threadIdx.x * n4, n4);
+            return;
+        }
+    }
     if (threadIdx.x < nr) {
         const uint8_t* row = ws + (uint64_t)threadIdx.x * row_bytes;
         float acc = 0.0f;
-        uint32_t i = 0;
-        if constexpr (DT == DS5_DTYPE_F32) {
-            if (dim % 4 == 0) {  // rows and x 16-byte aligned in LDS: 16-byte reads, the sum element by element
-                const f32x4* w4 = (const f32x4*)row;
-                const f32x4* x4 = (const f32x4*)xs;
-                for (; i < dim; i += 4) {
-                    const f32x4 wv = w4[i / 4], xv = x4[i / 4];
-#pragma unroll
-                    for (int c = 0; c < 4; c++) acc += wv[c] * xv[c];
-                }
-            }
-        }
-        for (; i < dim; i++) acc += router_w<DT, DT != DS5_DTYPE_Q8_0>(row, i) * xs[i];
+        for (uint32_t i = 0; i < dim; i++) acc += router_w<DT, DT != DS5_DTYPE_Q8_0>(row, i) * xs[i];
         logits[(uint64_t)t * n_experts + e0 + threadIdx.x] = acc;
     }
 }
@@ -135,7 +215,7 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
                                                            uint32_t top_k, uint32_t norm, uint16_t* __restrict__ out_ids,
                                                            float* __restrict__ out_w, ds5_pair* __restrict__ pairs) {
 #pragma clang fp contract(off)
-    extern __shared__ float probs[];
+    extern __shared__ __attribute__((aligned(16))) float probs[];
     __shared__ float s_inv_sum;
     const uint32_t t = blockIdx.x;
     const int lane = threadIdx.x;
@@ -147,8 +227,23 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
     for (uint32_t e = lane; e < n_experts; e += 64) probs[e] = expf(logits[(uint64_t)t * n_experts + e] - mx);
     __syncthreads();
     if (lane == 0) {
+        // in expert order; 32 values read before their adds, so the adds do not
+        // wait for LDS one read at a time
         float sum = 0.0f;
-        for (uint32_t e = 0; e < n_experts; e++) sum += probs[e];
+        uint32_t e = 0;
+        if (n_experts % 4 == 0) {
+            const f32x4* p4 = (const f32x4*)probs;
+            for (; e + 32 <= n_experts; e += 32) {
+                f32x4 v[8];
+#pragma unroll
+                for (int b = 0; b < 8; b++) v[b] = p4[e / 4 + b];
+#pragma unroll
+                for (int b = 0; b < 8; b++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) sum += v[b][c];
+            }
+        }
+        for (; e < n_experts; e++) sum += probs[e];
         s_inv_sum = 1.0f / sum;
     }
     __syncthreads();
@@ -159,7 +254,12 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
     // (lanes scan their experts in ascending order with a strict >, as the
     // reference does; the cross-lane merge keeps that order). A probability
     // picked is overwritten with -1 (below every probability and the -1 start).
-    float picked = 0.0f;
+    // Every lane ends a round holding the same pick, so each keeps the running sum
+    // (in pick order) and lane j keeps pick j; with top_k <= 64 the outputs are then
+    // written by top_k lanes at once, with no global round trip.
+    const bool in_regs = top_k <= 64;
+    float picked = 0.0f, my_p = 0.0f;
+    uint32_t my_id = 0;
     for (uint32_t j = 0; j < top_k; j++) {
         uint32_t best = 0;
         float best_p = -1.0f;
@@ -177,16 +277,28 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
                 best = oe;
             }
         }
-        if (lane == 0) {
-            probs[best] = -1.0f;  // taken
+        if (lane == 0) probs[best] = -1.0f;  // taken
+        if (lane == (int)(j & 63)) {
+            my_id = best;
+            my_p = best_p;
+        }
+        picked += best_p;
+        if (!in_regs && lane == 0) {
             out_ids[(uint64_t)t * top_k + j] = (uint16_t)best;
             out_w[(uint64_t)t * top_k + j] = best_p;
-            picked += best_p;
         }
         __builtin_amdgcn_wave_barrier();
     }
-    if (lane == 0) {
-        const float inv = norm ? 1.0f / picked : 1.0f;
+    const float inv = norm ? 1.0f / picked : 1.0f;
+    if (in_regs) {
+        if ((uint32_t)lane < top_k) {
+            const uint64_t o = (uint64_t)t * top_k + lane;
+            const float wv = norm ? my_p * inv : my_p;
+            out_ids[o] = (uint16_t)my_id;
+            out_w[o] = wv;
+            if (pairs) pairs[o] = ds5_pair{t, my_id, wv};
+        }
+    } else if (lane == 0) {
         for (uint32_t j = 0; j < top_k; j++) {
             const uint64_t o = (uint64_t)t * top_k + j;
             if (norm) out_w[o] *= inv;
