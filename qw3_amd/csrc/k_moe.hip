@@ -29,6 +29,10 @@ namespace {
 constexpr int kRouterThreads = 256;
 constexpr int kMoeWaves = 8;  // wavefronts (weight rows) per GEMV workgroup
 
+struct OpMinF {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fminf(a, b); }
+};
+
 // ---------------------------------------------------------------------------
 // router
 // ---------------------------------------------------------------------------
@@ -258,26 +262,52 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
     // (in pick order) and lane j keeps pick j; with top_k <= 64 the outputs are then
     // written by top_k lanes at once, with no global round trip.
     const bool in_regs = top_k <= 64;
+    // With at most 256 experts each lane also keeps its probabilities (experts
+    // lane, lane + 64, ...) in registers, and a round is two DPP all-reduces: the
+    // largest probability, then the lowest id holding it.
+    constexpr uint32_t kSelRegs = 4;
+    const bool fast = in_regs && n_experts <= 64 * kSelRegs;
+    float pv[kSelRegs];
+#pragma unroll
+    for (uint32_t m = 0; m < kSelRegs; m++) {
+        const uint32_t e = lane + 64 * m;
+        pv[m] = (fast && e < n_experts) ? probs[e] : -2.0f;  // -2: no expert (never beats the -1 start)
+    }
     float picked = 0.0f, my_p = 0.0f;
     uint32_t my_id = 0;
     for (uint32_t j = 0; j < top_k; j++) {
         uint32_t best = 0;
         float best_p = -1.0f;
-        for (uint32_t e = lane; e < n_experts; e += 64)
-            if (probs[e] > best_p) {
-                best = e;
-                best_p = probs[e];
-            }
+        if (fast) {
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float op = __shfl_xor(best_p, off, 64);
-            const uint32_t oe = (uint32_t)__shfl_xor((int)best, off, 64);
-            if (op > best_p || (op == best_p && oe < best)) {
-                best_p = op;
-                best = oe;
+            for (uint32_t m = 0; m < kSelRegs; m++)
+                if (pv[m] > best_p) {
+                    best = lane + 64 * m;
+                    best_p = pv[m];
+                }
+            const float mx = wave_allreduce(best_p, OpMax{});
+            best = (uint32_t)wave_allreduce(best_p == mx ? (float)best : 3.0e38f, OpMinF{});
+            best_p = mx;
+#pragma unroll
+            for (uint32_t m = 0; m < kSelRegs; m++)
+                if (lane + 64 * m == best) pv[m] = -1.0f;  // taken
+        } else {
+            for (uint32_t e = lane; e < n_experts; e += 64)
+                if (probs[e] > best_p) {
+                    best = e;
+                    best_p = probs[e];
+                }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float op = __shfl_xor(best_p, off, 64);
+                const uint32_t oe = (uint32_t)__shfl_xor((int)best, off, 64);
+                if (op > best_p || (op == best_p && oe < best)) {
+                    best_p = op;
+                    best = oe;
+                }
             }
+            if (lane == 0) probs[best] = -1.0f;  // taken
         }
-        if (lane == 0) probs[best] = -1.0f;  // taken
         if (lane == (int)(j & 63)) {
             my_id = best;
             my_p = best_p;
