@@ -505,8 +505,7 @@ def main():
         elapsed, _ = time_graph(ctx, w, stepsm, 2)
         us = elapsed / (w.layers * stepsm) * 1e6
         per = {kn: kernel_mean_ns(ctx, w, kn, 2)[0] / 1e3 for kn in
-               ("router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_kernel",
-                "moe_combine_kernel")}
+               ("router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel")}
         extra["moe_block_decode"] = dict(
             us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2), bytes_per_layer=w.bytes_per_layer,
             kernel_us={k: round(v, 3) for k, v in per.items()},

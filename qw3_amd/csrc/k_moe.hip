@@ -1,14 +1,14 @@
 // k_moe.hip -- the MoE step after the attention block: router top-k and the
 // SwiGLU expert MLP (kernels_c.zig:80-155 routerTopK, :157-214 expertMlpSwiglu).
 //
-// Router: one workgroup per token. Each expert's logit is the reference's
+// Router: workgroups of (token, group of experts). Each expert's logit is the reference's
 // serial f32 dot (dotRow, kernels_c.zig:40-68: products and sums rounded one by
 // one, in storage order), so logits are bit-identical to the reference. The
 // softmax keeps its order too: max, exp(l - max) per expert, the sum in expert
 // order, then the reciprocal; the top-k rounds pick the largest probability
 // with ties to the lower id (a wavefront argmax under that total order equals
 // the reference's ascending scan with a strict >); the k weights are summed in
-// pick order and optionally divided by that sum. exp is the device's expf, so
+// pick order and optionally scaled by its reciprocal. exp is the device's expf, so
 // probabilities may differ from the reference's in the last bit; ids can then
 // differ only where two probabilities are that close.
 //
@@ -16,6 +16,8 @@
 //   h[p][j] = silu(gate_e[j] . x_t) * (up_e[j] . x_t)     (moe_gate_up_kernel)
 //   y[p][i] = down_e[i] . h[p]                            (moe_down_kernel)
 //   out[t][i] += w * y[p][i] over t's pairs in list order (moe_combine_kernel)
+// (the last two in one launch, moe_down_combine_kernel, where the outputs fit
+// one grid)
 // The GEMVs are weight-bandwidth bound: one wavefront per weight row, lane L
 // owning the 32-element blocks L + 64 j, a fixed-order wavefront reduction (so
 // they agree with the reference's serial dots to rounding). The combine adds
@@ -416,6 +418,47 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* _
     if (lane == 0) y[r] = v;
 }
 
+// The down GEMV and the combine in one launch: workgroup (token t, output row i),
+// wavefront w computing y[p][i] for the token's pair q0 + w (+ 8, ...) exactly as
+// moe_down_kernel does, then one thread adding w_p * y[p][i] into out[t][i] in
+// list order, as moe_combine_kernel does: bit-identical to the two launches,
+// without the y round trip through memory.
+template <bool Q8>
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
+    const float* __restrict__ h, const uint8_t* __restrict__ down, const ds5_pair* __restrict__ pairs,
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offsets, uint32_t top_k, float* __restrict__ out,
+    uint32_t dim, uint32_t ffn, uint64_t row_f, uint64_t stride) {
+#pragma clang fp contract(off)
+    __shared__ float ys[kMoeWaves], wts[kMoeWaves];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint64_t id = blockIdx.x;
+    const uint32_t t = (uint32_t)(id / dim), i = (uint32_t)(id % dim);
+    const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
+    if (q0 == q1) return;  // no pairs: out stays as it is (workgroup-uniform)
+    float acc = 0.0f;
+    if (threadIdx.x == 0) acc = out[id];
+    for (uint32_t qb = q0; qb < q1; qb += kMoeWaves) {
+        const uint32_t q = qb + wv;
+        if (q < q1) {  // wave-uniform
+            const uint32_t p = order ? order[q] : q;
+            const ds5_pair pr = pairs[p];
+            const uint64_t row = (uint64_t)pr.expert * stride + (uint64_t)i * row_f;
+            const float v = wave_allreduce(lane_dot<Q8>(h + (uint64_t)p * ffn, down + row, down, ffn, lane), OpAdd{});
+            if (lane == 0) {
+                ys[wv] = v;
+                wts[wv] = pr.weight;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t n = min((uint32_t)kMoeWaves, q1 - qb);
+            for (uint32_t w = 0; w < n; w++) acc += wts[w] * ys[w];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[id] = acc;
+}
+
 // out[t][i] += w_p * y[p][i] over token t's pairs in list order: pair q of the
 // token is order[offsets[t] + q] (or t * top_k + q when offsets is null).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
@@ -532,20 +575,44 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     if (a.fast) {
         const dim3 blk(kMoeWaves * 64);
         const dim3 g1((unsigned)((gu_rows + kMoeWaves - 1) / kMoeWaves)), g2((unsigned)((dn_rows + kMoeWaves - 1) / kMoeWaves));
+        const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
+        if (outs > 0x7fffffffu) {  // more outputs than one grid holds workgroups: down, then the combine
+            if (a.q8) {
+                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, 0, ctx->stream, a.x,
+                                 a.gate, a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
+                if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
+                DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<true>, g2, blk, 0, ctx->stream, a.h, a.down,
+                                 a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+            } else {
+                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, 0, ctx->stream, a.x,
+                                 a.gate, a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
+                if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
+                DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<false>, g2, blk, 0, ctx->stream, a.h, a.down,
+                                 a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+            }
+            if (int rc = ds5_after_launch(ctx, "moe_down_kernel")) return rc;
+            DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)),
+                             dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.n_tokens,
+                             a.dim);
+            return ds5_after_launch(ctx, "moe_combine_kernel");
+        }
+        const dim3 g3((unsigned)outs);
         if (a.q8) {
             DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, 0, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
-            DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<true>, g2, blk, 0, ctx->stream, a.h, a.down,
-                             a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+            DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<true>, g3, blk, 0, ctx->stream,
+                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.dim, a.ffn, a.row_f,
+                             a.stride_d);
         } else {
             DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, 0, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
-            DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<false>, g2, blk, 0, ctx->stream, a.h, a.down,
-                             a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
+            DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<false>, g3, blk, 0, ctx->stream,
+                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.dim, a.ffn, a.row_f,
+                             a.stride_d);
         }
-        if (int rc = ds5_after_launch(ctx, "moe_down_kernel")) return rc;
+        return ds5_after_launch(ctx, "moe_down_combine_kernel");
     } else {
         DS5_TIMED_LAUNCH(ctx, "moe_gate_up_serial_kernel", moe_gate_up_serial_kernel,
                          dim3((unsigned)((gu_rows + 255) / 256)), dim3(256), 0, ctx->stream, a.x, a.gate, a.up, a.pairs,
