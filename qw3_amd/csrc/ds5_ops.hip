@@ -233,7 +233,7 @@ static int check_experts(ds5_hip_ctx* ctx, const char* op, ds5_buf x, ds5_buf ga
 // ends on a dword boundary or its view has 2 more bytes); f32 rows as floats.
 static bool experts_fast(ds5_buf x, ds5_buf gate, ds5_buf up, ds5_buf down, uint32_t dt, uint64_t dim, uint64_t ffn,
                          uint64_t E) {
-    if (dim % 32 || ffn % 32 || ((uintptr_t)ds5_ptr(x) & 15u)) return false;
+    if (dim % 32 || ffn % 32 || dim > 16384 || ((uintptr_t)ds5_ptr(x) & 15u)) return false;  // x staged in LDS
     const uint64_t ends[3] = {row_bytes_of(dt, dim) * ffn * E, row_bytes_of(dt, dim) * ffn * E,
                               row_bytes_of(dt, ffn) * dim * E};
     const ds5_buf banks[3] = {gate, up, down};

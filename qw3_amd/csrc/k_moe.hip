@@ -343,45 +343,52 @@ __global__ __launch_bounds__(64) void router_select_kernel(const float* __restri
 // expert GEMVs
 // ---------------------------------------------------------------------------
 
-// This lane's share of x . row over blocks L, L + 64, ... (f32 or Q8_0 rows;
-// Q8_0 rows read as nine dwords from the dword floor of each block).
+// Block b of x . row added into acc (f32 or Q8_0 rows; a Q8_0 block read as
+// nine dwords from its dword floor).
+template <bool Q8>
+__device__ __forceinline__ float lane_block(float acc, const float* __restrict__ x, const uint8_t* __restrict__ row,
+                                            const uint8_t* __restrict__ base, uint32_t b) {
+    float xr[32];
+    const float4* xs = (const float4*)(x + 32 * b);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = xs[i];
+        xr[4 * i] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    if constexpr (Q8) {
+        const uint64_t off = (uint64_t)(row - base) + (uint64_t)b * kQ8Bytes;
+        const uint32_t sh = (uint32_t)off & 3u;  // base is 4-byte aligned
+        const uint32_t* p = (const uint32_t*)(base + (off - sh));
+        uint32_t d[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) d[i] = p[i];
+        const Q8Block blk = q8_unpack(d, sh);
+        return __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), acc);
+    } else {
+        const float* wr = (const float*)row + 32 * b;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 32; i++) s[i & 3] = __builtin_fmaf(wr[i], xr[i], s[i & 3]);
+        return acc + ((s[0] + s[1]) + (s[2] + s[3]));
+    }
+}
+
+// This lane's share of x . row over blocks L, L + 64, ...
 template <bool Q8>
 __device__ __forceinline__ float lane_dot(const float* __restrict__ x, const uint8_t* __restrict__ row,
                                           const uint8_t* __restrict__ base, uint32_t k, int lane) {
-    const uint32_t nb = k / 32;
     float acc = 0.0f;
-    for (uint32_t b = lane; b < nb; b += 64) {
-        float xr[32];
-        const float4* xs = (const float4*)(x + 32 * b);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = xs[i];
-            xr[4 * i] = v.x;
-            xr[4 * i + 1] = v.y;
-            xr[4 * i + 2] = v.z;
-            xr[4 * i + 3] = v.w;
-        }
-        if constexpr (Q8) {
-            const uint64_t off = (uint64_t)(row - base) + (uint64_t)b * kQ8Bytes;
-            const uint32_t sh = (uint32_t)off & 3u;  // base is 4-byte aligned
-            const uint32_t* p = (const uint32_t*)(base + (off - sh));
-            uint32_t d[9];
-#pragma unroll
-            for (int i = 0; i < 9; i++) d[i] = p[i];
-            const Q8Block blk = q8_unpack(d, sh);
-            acc = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), acc);
-        } else {
-            const float* wr = (const float*)row + 32 * b;
-            float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int i = 0; i < 32; i++) s[i & 3] = __builtin_fmaf(wr[i], xr[i], s[i & 3]);
-            acc += (s[0] + s[1]) + (s[2] + s[3]);
-        }
-    }
+    for (uint32_t b = lane; b < k / 32; b += 64) acc = lane_block<Q8>(acc, x, row, base, b);
     return acc;
 }
 
 // One wavefront per (pair, ffn row j); x rows 16-byte aligned (dim % 32 == 0).
+// ffn % 32 == 0, so the 8 rows of a workgroup belong to one pair: the token's x
+// is staged in LDS once per workgroup, after each lane has asked for its first
+// Q8_0 blocks (one memory latency covers both).
 template <bool Q8>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(const float* __restrict__ x,
                                                                      const uint8_t* __restrict__ gate,
@@ -390,15 +397,62 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(const float
                                                                      float* __restrict__ h, uint32_t n_pairs,
                                                                      uint32_t dim, uint32_t ffn, uint64_t row_h,
                                                                      uint64_t stride) {
+    extern __shared__ __attribute__((aligned(16))) float moe_xs[];
     const int lane = threadIdx.x & 63;
-    const uint64_t r = (uint64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
-    if (r >= (uint64_t)n_pairs * ffn) return;  // wave-uniform
-    const uint32_t p = (uint32_t)(r / ffn), j = (uint32_t)(r % ffn);
+    const uint64_t r0 = (uint64_t)blockIdx.x * kMoeWaves, r = r0 + (threadIdx.x >> 6);
+    const uint32_t p = (uint32_t)(r0 / ffn), j = (uint32_t)(r % ffn);
+    const bool live = r < (uint64_t)n_pairs * ffn;  // wave-uniform
     const ds5_pair pr = pairs[p];
-    const float* xr = x + (uint64_t)pr.token * dim;
     const uint64_t row = (uint64_t)pr.expert * stride + (uint64_t)j * row_h;
-    const float g = wave_allreduce(lane_dot<Q8>(xr, gate + row, gate, dim, lane), OpAdd{});
-    const float u = wave_allreduce(lane_dot<Q8>(xr, up + row, up, dim, lane), OpAdd{});
+    const uint32_t nb = dim / 32;
+    uint32_t dg[9] = {}, du[9] = {};
+    uint32_t shg = 0, shu = 0;
+    if constexpr (Q8) {
+        if (live && (uint32_t)lane < nb) {
+            const uint64_t og = row + (uint64_t)lane * kQ8Bytes;  // gate and up share the row offset
+            shg = (uint32_t)og & 3u;
+            shu = shg;
+            const uint32_t* pg = (const uint32_t*)(gate + (og - shg));
+            const uint32_t* pu = (const uint32_t*)(up + (og - shu));
+#pragma unroll
+            for (int i = 0; i < 9; i++) dg[i] = pg[i];
+#pragma unroll
+            for (int i = 0; i < 9; i++) du[i] = pu[i];
+        }
+    }
+    const f32x4* xg = (const f32x4*)(x + (uint64_t)pr.token * dim);
+    f32x4* xs4 = (f32x4*)moe_xs;
+    for (uint32_t u = threadIdx.x; u < dim / 4; u += kMoeWaves * 64) xs4[u] = xg[u];
+    __syncthreads();
+    if (!live) return;
+    float g = 0.0f, uacc = 0.0f;
+    uint32_t b0 = lane;
+    if constexpr (Q8) {
+        if ((uint32_t)lane < nb) {
+            float xr[32];
+            const f32x4* xb = xs4 + 8 * lane;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const f32x4 v = xb[i];
+                xr[4 * i] = v[0];
+                xr[4 * i + 1] = v[1];
+                xr[4 * i + 2] = v[2];
+                xr[4 * i + 3] = v[3];
+            }
+            const Q8Block bg = q8_unpack(dg, shg);
+            g = __builtin_fmaf(bg.scale, q8_dot(bg.q, xr), g);
+            const Q8Block bu = q8_unpack(du, shu);
+            uacc = __builtin_fmaf(bu.scale, q8_dot(bu.q, xr), uacc);
+        }
+        b0 = lane + 64;
+    }
+    // the remaining blocks (all of them for f32 rows), in lane_dot's order
+    for (uint32_t b = b0; b < nb; b += 64) {
+        g = lane_block<Q8>(g, moe_xs, gate + row, gate, b);
+        uacc = lane_block<Q8>(uacc, moe_xs, up + row, up, b);
+    }
+    g = wave_allreduce(g, OpAdd{});
+    const float u = wave_allreduce(uacc, OpAdd{});
     if (lane == 0) h[r] = g / (1.0f + expf(-g)) * u;  // silu(g) * u, kernels_c.zig:70-72
 }
 
@@ -574,17 +628,18 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     const uint64_t gu_rows = (uint64_t)a.n_pairs * a.ffn, dn_rows = (uint64_t)a.n_pairs * a.dim;
     if (a.fast) {
         const dim3 blk(kMoeWaves * 64);
+        const size_t xs_bytes = (size_t)a.dim * sizeof(float);  // the token's x, staged per gate/up workgroup
         const dim3 g1((unsigned)((gu_rows + kMoeWaves - 1) / kMoeWaves)), g2((unsigned)((dn_rows + kMoeWaves - 1) / kMoeWaves));
         const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
         if (outs > 0x7fffffffu) {  // more outputs than one grid holds workgroups: down, then the combine
             if (a.q8) {
-                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, 0, ctx->stream, a.x,
+                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, xs_bytes, ctx->stream, a.x,
                                  a.gate, a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
                 if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
                 DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<true>, g2, blk, 0, ctx->stream, a.h, a.down,
                                  a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
             } else {
-                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, 0, ctx->stream, a.x,
+                DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, xs_bytes, ctx->stream, a.x,
                                  a.gate, a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
                 if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
                 DS5_TIMED_LAUNCH(ctx, "moe_down_kernel", moe_down_kernel<false>, g2, blk, 0, ctx->stream, a.h, a.down,
@@ -598,14 +653,14 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
         }
         const dim3 g3((unsigned)outs);
         if (a.q8) {
-            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, 0, ctx->stream, a.x, a.gate,
+            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, xs_bytes, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
             DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<true>, g3, blk, 0, ctx->stream,
                              a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.dim, a.ffn, a.row_f,
                              a.stride_d);
         } else {
-            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, 0, ctx->stream, a.x, a.gate,
+            DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, xs_bytes, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
             DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<false>, g3, blk, 0, ctx->stream,
