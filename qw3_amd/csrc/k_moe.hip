@@ -472,45 +472,91 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* _
     if (lane == 0) y[r] = v;
 }
 
-// The down GEMV and the combine in one launch: workgroup (token t, output row i),
-// wavefront w computing y[p][i] for the token's pair q0 + w (+ 8, ...) exactly as
-// moe_down_kernel does, then one thread adding w_p * y[p][i] into out[t][i] in
-// list order, as moe_combine_kernel does: bit-identical to the two launches,
-// without the y round trip through memory.
+// The down GEMV and the combine in one launch: workgroup (token t, output rows
+// i0 .. i0 + 7), wavefront w computing y[p][i] of those 8 rows for the token's
+// pair q0 + w (+ 8, ...) with moe_down_kernel's lane layout and order (its h
+// block read once for the 8 rows), then thread r adding w_p * y[p][i0 + r] into
+// out[t][i0 + r] in list order, as moe_combine_kernel does: bit-identical to the
+// two launches, without the y round trip through memory. dim % 8 == 0.
+constexpr uint32_t kDownRows = 8;
 template <bool Q8>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
     const float* __restrict__ h, const uint8_t* __restrict__ down, const ds5_pair* __restrict__ pairs,
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offsets, uint32_t top_k, float* __restrict__ out,
     uint32_t dim, uint32_t ffn, uint64_t row_f, uint64_t stride) {
 #pragma clang fp contract(off)
-    __shared__ float ys[kMoeWaves], wts[kMoeWaves];
+    __shared__ float ys[kMoeWaves][kDownRows], wts[kMoeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint64_t id = blockIdx.x;
-    const uint32_t t = (uint32_t)(id / dim), i = (uint32_t)(id % dim);
+    const uint32_t groups = dim / kDownRows;
+    const uint32_t t = blockIdx.x / groups, i0 = (blockIdx.x % groups) * kDownRows;
     const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
     if (q0 == q1) return;  // no pairs: out stays as it is (workgroup-uniform)
+    const uint32_t nb = ffn / 32;
     float acc = 0.0f;
-    if (threadIdx.x == 0) acc = out[id];
+    if (threadIdx.x < kDownRows) acc = out[(uint64_t)t * dim + i0 + threadIdx.x];
     for (uint32_t qb = q0; qb < q1; qb += kMoeWaves) {
         const uint32_t q = qb + wv;
         if (q < q1) {  // wave-uniform
             const uint32_t p = order ? order[q] : q;
             const ds5_pair pr = pairs[p];
-            const uint64_t row = (uint64_t)pr.expert * stride + (uint64_t)i * row_f;
-            const float v = wave_allreduce(lane_dot<Q8>(h + (uint64_t)p * ffn, down + row, down, ffn, lane), OpAdd{});
-            if (lane == 0) {
-                ys[wv] = v;
-                wts[wv] = pr.weight;
+            const uint8_t* rows = down + (uint64_t)pr.expert * stride + (uint64_t)i0 * row_f;
+            const float* hp = h + (uint64_t)p * ffn;
+            float a[kDownRows];
+#pragma unroll
+            for (uint32_t r = 0; r < kDownRows; r++) a[r] = 0.0f;
+            for (uint32_t b = lane; b < nb; b += 64) {
+                float xr[32];
+                const float4* xs = (const float4*)(hp + 32 * b);
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 v = xs[k];
+                    xr[4 * k] = v.x;
+                    xr[4 * k + 1] = v.y;
+                    xr[4 * k + 2] = v.z;
+                    xr[4 * k + 3] = v.w;
+                }
+                if constexpr (Q8) {
+                    uint32_t d[kDownRows][9];
+                    uint32_t sh[kDownRows];
+#pragma unroll
+                    for (uint32_t r = 0; r < kDownRows; r++) {
+                        const uint64_t off = (uint64_t)(rows - down) + r * row_f + (uint64_t)b * kQ8Bytes;
+                        sh[r] = (uint32_t)off & 3u;
+                        const uint32_t* pw = (const uint32_t*)(down + (off - sh[r]));
+#pragma unroll
+                        for (int k = 0; k < 9; k++) d[r][k] = pw[k];
+                    }
+#pragma unroll
+                    for (uint32_t r = 0; r < kDownRows; r++) {
+                        const Q8Block blk = q8_unpack(d[r], sh[r]);
+                        a[r] = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), a[r]);
+                    }
+                } else {
+#pragma unroll
+                    for (uint32_t r = 0; r < kDownRows; r++) {
+                        const float* wr = (const float*)(rows + r * row_f) + 32 * b;
+                        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int k = 0; k < 32; k++) s4[k & 3] = __builtin_fmaf(wr[k], xr[k], s4[k & 3]);
+                        a[r] = a[r] + ((s4[0] + s4[1]) + (s4[2] + s4[3]));
+                    }
+                }
             }
+#pragma unroll
+            for (uint32_t r = 0; r < kDownRows; r++) {
+                const float v = wave_allreduce(a[r], OpAdd{});
+                if (lane == 0) ys[wv][r] = v;
+            }
+            if (lane == 0) wts[wv] = pr.weight;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
+        if (threadIdx.x < kDownRows) {
             const uint32_t n = min((uint32_t)kMoeWaves, q1 - qb);
-            for (uint32_t w = 0; w < n; w++) acc += wts[w] * ys[w];
+            for (uint32_t w = 0; w < n; w++) acc += wts[w] * ys[w][threadIdx.x];
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) out[id] = acc;
+    if (threadIdx.x < kDownRows) out[(uint64_t)t * dim + i0 + threadIdx.x] = acc;
 }
 
 // out[t][i] += w_p * y[p][i] over token t's pairs in list order: pair q of the
@@ -651,7 +697,7 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
                              a.dim);
             return ds5_after_launch(ctx, "moe_combine_kernel");
         }
-        const dim3 g3((unsigned)outs);
+        const dim3 g3((unsigned)(outs / kDownRows));  // dim % 32 == 0 on this path
         if (a.q8) {
             DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, xs_bytes, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
