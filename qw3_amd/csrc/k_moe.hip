@@ -69,8 +69,9 @@ __device__ __forceinline__ float router_w(const uint8_t* row, uint32_t i) {
 // (one add per element) bounds each.
 constexpr uint32_t kRouterRowBytes = 65536;  // LDS for one group's rows
 
+constexpr uint32_t kRouterGroupBytes = 16384;  // rows per group: about this many bytes (more workgroups load faster)
 __host__ __device__ inline uint32_t router_rows_per_group(uint64_t row_bytes) {
-    const uint64_t r = kRouterRowBytes / row_bytes;
+    const uint64_t r = kRouterGroupBytes / row_bytes;
     return (uint32_t)(r > 16 ? 16 : (r ? r : 1));
 }
 
