@@ -109,3 +109,24 @@ def test_fused_matches_ops(ctx, hip, oracle, model, weights):
     for t in p["greedy_tokens"][:4]:
         a, b = a_eng.forward([t]), b_eng.forward([t])
         assert oracle.compare(a.reshape(-1), b.reshape(-1), LAYER_ATOL, LAYER_RTOL).passed
+
+
+def test_engine_rejections(ctx, hip, weights):
+    """forward.zig's engine errors: capacity above the model's max_ctx (BadShape,
+    test_forward.zig:116-129), an empty or oversized batch, a token id past the
+    vocabulary, and a context overflow that leaves pos unchanged (:100-113)."""
+    from qw3_amd import engine as E
+    with pytest.raises(ValueError, match="BadShape"):
+        E.Engine(ctx, weights, max_batch=1, context_capacity=weights.cfg["max_ctx"] + 1)
+    eng = _engine(ctx, hip, weights, "f32", False, capacity=2)
+    with pytest.raises(ValueError, match="BatchTooLarge"):
+        eng.forward([])
+    with pytest.raises(ValueError, match="BatchTooLarge"):
+        eng.forward([1, 2, 3])
+    with pytest.raises(ValueError, match="TokenOutOfRange"):
+        eng.forward([weights.cfg["vocab_size"]])
+    eng.forward([1, 2])
+    assert eng.pos == 2
+    with pytest.raises(ValueError, match="ContextOverflow"):
+        eng.forward([3])
+    assert eng.pos == 2
