@@ -914,13 +914,14 @@ def test_expert_mlp_bad_pair_leaves_out(ctx, hip):
     assert np.all(ctx.to_numpy(out, np.float32, (1, 32)) == 3.0)
 
 
-@pytest.mark.parametrize("T", [1, 5])
-def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T):
+@pytest.mark.parametrize("T,E", [(1, 32), (5, 32), (1, 128), (3, 200)])
+def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T, E):
     """ds5_hip_moe (router and experts on the device, pairs never leave it) equals
     ds5_hip_router_topk then ds5_hip_expert_mlp_swiglu on the router's pairs, bit for bit;
-    the device ids / weights equal the host ones."""
+    the device ids / weights equal the host ones. 128 and 200 experts: two and four
+    register slots per lane in the selection, the last one partly filled at 200."""
     g = np.random.default_rng(T)
-    dim, ffn, E, K = 2048, 768, 32, 8
+    dim, ffn, K = 2048, 768, 8
     rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
     mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
     G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
