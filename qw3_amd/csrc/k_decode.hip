@@ -19,11 +19,14 @@
 // so the O accumulators are rescaled rarely.
 //
 // Latency structure (a decode layer is ~2 us of HBM time, so the critical path
-// matters more than instruction counts): every wavefront issues its first
-// tile's K/V loads before anything else, the q prologue (load, norm, rope,
-// hi/lo split) runs while they are in flight, and later tiles are prefetched
-// one tile ahead. Workgroup barriers before the main loop are LDS-only, so
-// they never wait for the outstanding K/V loads.
+// matters): every wavefront issues its first tile's K/V loads before anything
+// else, the q prologue (load, norm, rope, scale, hi/lo split) runs while they
+// are in flight, and later tiles are prefetched one tile ahead. Workgroup
+// barriers before the main loop are LDS-only, so they never wait for the
+// outstanding K/V loads. With one wavefront per SIMD every instruction a
+// wavefront issues is on the critical path, so the q operands are built once
+// per workgroup (not per wavefront) and the wavefront partials are combined
+// through LDS.
 //
 // Splits combine through a workspace: each workgroup writes its unnormalised
 // O, its reference max and its sum; decode_merge_kernel combines the splits of
@@ -41,7 +44,7 @@
 namespace {
 
 constexpr int kTile = 32;   // positions per wavefront tile
-constexpr int kWaves = 4;   // wavefronts per workgroup
+constexpr int kWaves = 4;   // wavefronts per workgroup (one per SIMD)
 constexpr int kThreads = kWaves * 64;
 constexpr int kHeads = 16;  // q heads per workgroup (the MFMA N dimension)
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (p <= 2^8 between rescales)
@@ -90,7 +93,15 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ __forceinline__ u32x4 ld16(const f16* ptr) { return *(const u32x4*)ptr; }
+// K/V rows are read once per step. A contiguous cache is read with
+// non-temporal loads (streaming hint to the caches), measured faster than plain
+// loads on gfx950; scattered pages are read with plain loads, which measured
+// faster for them.
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const f16* ptr) {
+    if constexpr (NT) return __builtin_nontemporal_load((const u32x4*)ptr);
+    else return *(const u32x4*)ptr;
+}
 
 // gfx950 LDS transpose read (ds_read_b64_tr_b16) of 4 halves; see its use below.
 __device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_byte_ptr) {
@@ -133,7 +144,7 @@ __device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p
         else
             row = min((uint32_t)(p0 + 16 * st + c16), end - 1);
 #pragma unroll
-        for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = ld16(kbase + row * D + kk * 32 + 8 * g);
+        for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = ld16<!PAGED>(kbase + row * D + kk * 32 + 8 * g);
     }
 #pragma unroll
     for (int r = 0; r < G::VC; r++) {
@@ -144,7 +155,7 @@ __device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p
             row = (r < G::VC / 2 ? rowA : rowB) + (tr & 15);
         else
             row = min((uint32_t)(p0 + tr), end - 1);
-        T.v[r] = ld16(vbase + row * D + (c % G::RC) * 8);
+        T.v[r] = ld16<!PAGED>(vbase + row * D + (c % G::RC) * 8);
     }
 }
 
@@ -159,18 +170,21 @@ __device__ __forceinline__ int vswz(int r) {
     else return 2 * ((r >> 1) & 3);
 }
 
-// Splits x into f16 hi + lo with x ~= hi + lo to ~22 significant bits.
-__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
-    hi = (_Float16)x;
-    lo = (_Float16)(x - (float)hi);
+// Splits two values into f16 hi + lo pairs (x ~= hi + lo to ~22 significant
+// bits): hi rounds to nearest, the residual x - hi is exact in f32 and is
+// rounded again. Packed conversions: three instructions per value.
+__device__ __forceinline__ void split2_f16(float x0, float x1, f16x2& hi, f16x2& lo) {
+    hi = f16x2{(f16)x0, (f16)x1};
+    lo = f16x2{(f16)(x0 - (float)hi[0]), (f16)(x1 - (float)hi[1])};
 }
 
+// One 32-position tile of a wavefront: scores, softmax update, P.V.
+// q operands are pre-scaled by softmax scale * log2(e), so S is in log2 units.
 template <int D, bool FUSED, bool PACK>
 __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32_t end, int g, int c16, int lane,
                                              const f16x8 (&qh)[Geo<D>::KK], const f16x8 (&ql)[Geo<D>::KK],
                                              f32x4 (&O)[Geo<D>::DT], float& m_ref, float& l_sum, char* vlds,
-                                             int new_row, const f16* s_knew, const f16* s_vnew, float scale_log2,
-                                             bool first) {
+                                             int new_row, const f16* s_knew, const f16* s_vnew, bool first) {
     using G = Geo<D>;
     // Fused: the tile holding the new position takes the freshly appended row from LDS.
     if (FUSED && new_row >= 0) {
@@ -209,15 +223,13 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
     // this lane: head c16, positions p0 + 16*st + 4g + i (score j = 4*st + i)
     float s[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) s[j] = S[j / 4][j % 4] * scale_log2;
+    for (int j = 0; j < 8; j++) s[j] = S[j / 4][j % 4];
     if (partial) {
 #pragma unroll
         for (int j = 0; j < 8; j++)
             if (p0 + 16 * (j / 4) + 4 * g + (j % 4) >= end) s[j] = -INFINITY;
     }
-    float mx = s[0];
-#pragma unroll
-    for (int j = 1; j < 8; j++) mx = fmaxf(mx, s[j]);
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     mx = swap32_op(swap16_op(mx, OpMax{}), OpMax{});
     // Lazy rescale: move the reference only when the tile max exceeds it by > 2^8.
     if (first) {
@@ -231,22 +243,27 @@ __device__ __forceinline__ void compute_tile(TileRegs<D>& T, uint32_t p0, uint32
         for (int dt = 0; dt < G::DT; dt++) O[dt] *= alpha;
         m_ref = m_new;
     }
-    f16x8 ph, pl;  // packed: ph alone, hi halves in columns 0-7 and lo halves in 8-15
-    float psum = 0.0f;
+    float pj[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const float pj = fast_exp2(s[j] - m_ref);
-        psum += pj;
-        _Float16 hi, lo;
-        split_f16(pj, hi, lo);
+    for (int j = 0; j < 8; j++) pj[j] = fast_exp2(s[j] - m_ref);
+    l_sum += ((pj[0] + pj[1]) + (pj[2] + pj[3])) + ((pj[4] + pj[5]) + (pj[6] + pj[7]));
+    // p as f16 hi + lo; packed: hi in columns 0-7, lo in columns 8-15
+    f16x8 ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        f16x2 hi, lo;
+        split2_f16(pj[j], pj[j + 1], hi, lo);
         if constexpr (PACK) {
-            ph[j] = c16 >= 8 ? lo : hi;
+            const f16x2 sel = c16 >= 8 ? lo : hi;
+            ph[j] = sel[0];
+            ph[j + 1] = sel[1];
         } else {
-            ph[j] = hi;
-            pl[j] = lo;
+            ph[j] = hi[0];
+            ph[j + 1] = hi[1];
+            pl[j] = lo[0];
+            pl[j + 1] = lo[1];
         }
     }
-    l_sum += psum;
 
     // V tile -> wavefront LDS area (rows past the split end zeroed: p is 0 there, V may be garbage)
 #pragma unroll
@@ -319,29 +336,57 @@ __device__ __forceinline__ float rope_angle(float pos, float freq_scale, float i
     return pos * freq_scale * inv;
 }
 
+// Sum over the n consecutive lanes of a group (n = 8 or 16, aligned), result
+// on every lane of the group: quad xor 1 and 2, then the 8-lane halves
+// (row_half_mirror) and, for 16, the rows (row_mirror).
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    if constexpr (N == 16) v += dpp_mov<0x140>(v);
+    return v;
+}
+
 // ONE: every wavefront has at most one tile (chunk <= kWaves * kTile). That case
 // gets a kernel of its own without the prefetch loop: the loop's four tile
 // bodies double the code, and a decode launch is short enough for instruction
 // fetch to show in its duration.
+//
+// The workgroup runs one wavefront per SIMD, so every instruction a wavefront
+// issues sits on the critical path: the q operands (norm, rope, scale, hi/lo
+// split) are built once per workgroup -- each thread takes 4 rope pairs of one
+// head -- and read from LDS, and the wavefront partials are combined through
+// LDS without lane shuffles.
 template <int D, bool FUSED, bool PAGED, bool PACK, bool ONE>
 __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, RopeTable table) {
     using G = Geo<D>;
+    constexpr int W = kWaves;
     constexpr int KK = G::KK, DT = G::DT;
+    constexpr int TPH = D / 8;   // prologue threads per q head; thread j owns pairs (4j + k, D/2 + 4j + k), k < 4
+    constexpr int QROW = D + 8;  // halves per LDS q-operand row (16-byte pad)
     // One area per wavefront: its V staging tile, later its O for the cross-wavefront
     // combine (a wavefront overwrites only its own staging, so no barrier is needed
     // between its last transpose read and its O writes).
     constexpr int V_BYTES = kTile * G::VROW;
     constexpr int O_BYTES = kHeads * G::OROW * 4;
     constexpr int AREA = V_BYTES > O_BYTES ? V_BYTES : O_BYTES;
-    __shared__ __attribute__((aligned(16))) char s_big[kWaves * AREA];
-    __shared__ __attribute__((aligned(16))) float s_q[kHeads][G::OROW];
+    __shared__ __attribute__((aligned(16))) char s_big[W * AREA];
+    // q operand rows (f16, pre-scaled): packed, rows 0-7 hold the hi halves of heads
+    // 0-7 and rows 8-15 their lo halves; otherwise s_qa holds hi and s_qb lo per head.
+    __shared__ __attribute__((aligned(16))) f16 s_qa[kHeads * QROW];
+    __shared__ __attribute__((aligned(16))) f16 s_qb[PACK ? 8 : kHeads * QROW];
     __shared__ __attribute__((aligned(16))) float s_krow[FUSED ? D : 4];
     __shared__ __attribute__((aligned(16))) float s_ksq[FUSED ? D : 4];  // squares of the new k row
-    __shared__ float s_qn[FUSED ? D : 1], s_kn[FUSED ? D : 1], s_cos[FUSED ? D / 2 : 1], s_sin[FUSED ? D / 2 : 1];
+    __shared__ __attribute__((aligned(16))) float s_qn[FUSED ? D : 4];
+    __shared__ float s_kn[FUSED ? D : 1];
+    __shared__ __attribute__((aligned(16))) float s_cos[FUSED ? D / 2 : 4];
+    __shared__ __attribute__((aligned(16))) float s_sin[FUSED ? D / 2 : 4];
     __shared__ __attribute__((aligned(16))) f16 s_knew[FUSED ? D : 8];
     __shared__ __attribute__((aligned(16))) f16 s_vnew[FUSED ? D : 8];
-    __shared__ float s_m[kWaves][kHeads], s_l[kWaves][kHeads];
-    __shared__ int s_badw[kWaves];
+    __shared__ float s_m[W][kHeads], s_l[W][kHeads];
+    __shared__ int s_badw[W];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -379,18 +424,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
 
     // ---- 1. small loads first: vmcnt retires loads in issue order, so a load
     //         issued after the K/V tile could only be used once the whole tile
-    //         has arrived. q rows, norm weights, position and the new k/v row.
-    constexpr int QV = (kHeads * D / 4 + kThreads - 1) / kThreads;  // q-row float4s per thread
-    // Every load here is unconditional with a clamped (valid) address: loads
-    // under divergent branches make the compiler wait for all outstanding
-    // loads at the join, which would include the K/V tile.
-    static_assert(QV == 1 || QV == 2, "q staging assumes at most two float4 per thread");
-    auto q_at = [&](int k) -> const float4* {
-        const int i = tid + k * kThreads, n = min(i / (D / 4), NS - 1);
-        return (const float4*)(p.q + (qrow0 + n) * D + (i % (D / 4)) * 4);
-    };
-    const float4 qv0 = *q_at(0);
-    const float4 qv1 = QV > 1 ? *q_at(QV - 1) : qv0;
+    //         has arrived. Every load here is unconditional with a clamped
+    //         (valid) address: loads under divergent branches make the compiler
+    //         wait for all outstanding loads at the join, which would include the
+    //         K/V tile.
+    const int qn = tid / TPH, qj = tid % TPH;  // prologue: head qn, pair block qj
+    const float* qsrc = p.q + (qrow0 + min(qn, NS - 1)) * D + 4 * qj;
+    const float4 xa = *(const float4*)qsrc;
+    const float4 xb = *(const float4*)(qsrc + D / 2);
     const uint64_t kv_off = ((uint64_t)b * p.n_kv_heads + kvh) * D;
     float wq = 0.f, wk = 0.f, kr = 0.f, vr = 0.f, inv_freq = 0.f;
     int32_t pos_raw = 0;
@@ -416,19 +457,11 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 3. q operands (hi/lo f16) from the LDS copy, built while the tile is in flight
-#pragma unroll
-    for (int k = 0; k < QV; k++) {
-        const int i = tid + k * kThreads, n = i / (D / 4);
-        if (n < NS) *(float4*)&s_q[n][(i % (D / 4)) * 4] = k == 0 ? qv0 : qv1;
-    }
-    f16x8 qh[KK], ql[KK];
-    const int hcol = PACK ? (c16 & 7) : c16;  // head of this lane's MFMA column
-    const int qn_row = hcol < NS ? hcol : 0;
+    // ---- 3. q operands, built once per workgroup while the tile is in flight
     // Fused: the wavefront that owns the tile holding the new position
-    // normalises, rotates and appends the new k row itself (no extra barrier).
-    const int new_wave = has_new ? (int)(((newpos - start) / kTile) % kWaves) : -1;
-    float x[KK][8];
+    // normalises, rotates and appends the new k row itself.
+    const int new_wave = has_new ? (int)(((newpos - start) / kTile) % W) : -1;
+    float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
     if constexpr (FUSED) {
         const float qpos = PAGED ? (float)newpos : (float)pos_raw;
         if (tid < D) {
@@ -452,7 +485,47 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
             s_vnew[tid] = hv;
             if (!pbad) vbase[vslot * D + tid] = hv;
         }
-        lds_barrier();  // the prologue's only workgroup barrier
+        lds_barrier();
+        // q RMSNorm: the head's sum of squares over its TPH threads (q only feeds
+        // attention, so the summation order is free), then (v * inv) * w and the rotation.
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss += x[j] * x[j];
+        const float inv = rms_inv(group_sum<TPH>(ss), (float)D, p.eps);
+        const float4 wa = *(const float4*)&s_qn[4 * qj], wb = *(const float4*)&s_qn[D / 2 + 4 * qj];
+        const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = norm_mul(x[j], inv, w8[j]);
+        const float4 cs = *(const float4*)&s_cos[4 * qj], sn = *(const float4*)&s_sin[4 * qj];
+        const float c4[4] = {cs.x, cs.y, cs.z, cs.w}, s4[4] = {sn.x, sn.y, sn.z, sn.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) rotate(x[k], x[4 + k], c4[k], s4[k], x[k], x[4 + k]);
+    }
+    // scale into log2 units, split into f16 hi + lo, write the operand rows
+    // (heads past NS get zero rows)
+    if (qn < (PACK ? kHeads / 2 : kHeads)) {
+        f16x2 hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float v0 = qn < NS ? x[2 * k] * p.scale_log2 : 0.0f;
+            const float v1 = qn < NS ? x[2 * k + 1] * p.scale_log2 : 0.0f;
+            split2_f16(v0, v1, hi[k], lo[k]);
+        }
+        f16* const rh = s_qa + qn * QROW + 4 * qj;
+        f16* const rl = (PACK ? s_qa + (qn + kHeads / 2) * QROW : s_qb + qn * QROW) + 4 * qj;
+        *(f16x4*)rh = f16x4{hi[0][0], hi[0][1], hi[1][0], hi[1][1]};
+        *(f16x4*)(rh + D / 2) = f16x4{hi[2][0], hi[2][1], hi[3][0], hi[3][1]};
+        *(f16x4*)rl = f16x4{lo[0][0], lo[0][1], lo[1][0], lo[1][1]};
+        *(f16x4*)(rl + D / 2) = f16x4{lo[2][0], lo[2][1], lo[3][0], lo[3][1]};
+    }
+    lds_barrier();
+    f16x8 qh[KK], ql[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        qh[kk] = *(const f16x8*)(s_qa + c16 * QROW + kk * 32 + 8 * g);
+        if constexpr (!PACK) ql[kk] = *(const f16x8*)(s_qb + c16 * QROW + kk * 32 + 8 * g);
+    }
+    if constexpr (FUSED) {
         if (wave == new_wave) {
             // k row: serial-order sum of squares (kernels_a.zig:85-86) in one lane,
             // then norm + rope of pair (lane, lane + D/2) and the f16 append.
@@ -474,61 +547,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
                 }
             }
         }
-        // q: this lane holds dims kk*32 + 8g + j of head c16; the head's sum of
-        // squares is the lane's partial sum reduced over the 4 lanes of the head
-        // (q only feeds attention, so the summation order is free).
-        float ss = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const float4 a4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g];
-            const float4 c4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g + 4];
-            const float r[8] = {a4.x, a4.y, a4.z, a4.w, c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                x[kk][j] = r[j];
-                ss += r[j] * r[j];
-            }
-        }
-        ss = swap32_op(swap16_op(ss, OpAdd{}), OpAdd{});
-        const float inv = rms_inv(ss, (float)D, p.eps);
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) x[kk][j] = norm_mul(x[kk][j], inv, s_qn[kk * 32 + 8 * g + j]);
-#pragma unroll
-        for (int kk = 0; kk < KK / 2; kk++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int d = kk * 32 + 8 * g + j;
-                float y0, y1;
-                rotate(x[kk][j], x[kk + KK / 2][j], s_cos[d], s_sin[d], y0, y1);
-                x[kk][j] = y0;
-                x[kk + KK / 2][j] = y1;
-            }
-    } else {
-        lds_barrier();
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            const float4 a4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g];
-            const float4 c4 = *(const float4*)&s_q[qn_row][kk * 32 + 8 * g + 4];
-            const float r[8] = {a4.x, a4.y, a4.z, a4.w, c4.x, c4.y, c4.z, c4.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) x[kk][j] = r[j];
-        }
     }
-#pragma unroll
-    for (int kk = 0; kk < KK; kk++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            _Float16 hi, lo;
-            split_f16(hcol < NS ? x[kk][j] : 0.0f, hi, lo);
-            if constexpr (PACK) {
-                qh[kk][j] = c16 >= 8 ? lo : hi;
-            } else {
-                qh[kk][j] = hi;
-                ql[kk][j] = lo;
-            }
-        }
 
     // ---- 4. main loop: prefetch one tile ahead, two register sets
     f32x4 O[DT];
@@ -546,86 +565,76 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
         if (it < n_tiles) {
             const uint32_t p0 = start + it * kTile;
             compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
-                                         s_vnew, p.scale_log2, true);
+                                         s_vnew, true);
         }
     } else if (it < n_tiles) {
         bool first = true;
         for (;;) {
-            uint32_t nx = it + kWaves;
+            uint32_t nx = it + W;
             uint32_t p0 = start + it * kTile;
             if (nx >= n_tiles) {
-                compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
-                                       s_vnew, p.scale_log2, first);
+                compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0),
+                                             s_knew, s_vnew, first);
                 break;
             }
             issue_tile<D, PAGED>(TB, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
             compute_tile<D, FUSED, PACK>(TA, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
-                                   s_vnew, p.scale_log2, first);
+                                         s_vnew, first);
             first = false;
             it = nx;
-            nx = it + kWaves;
+            nx = it + W;
             p0 = start + it * kTile;
             if (nx >= n_tiles) {
-                compute_tile<D, FUSED, PACK>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
-                                       s_vnew, p.scale_log2, false);
+                compute_tile<D, FUSED, PACK>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0),
+                                             s_knew, s_vnew, false);
                 break;
             }
             issue_tile<D, PAGED>(TA, p, kbase, vbase, b, start + nx * kTile, end, g, c16, lane, bad);
             compute_tile<D, FUSED, PACK>(TB, p0, end, g, c16, lane, qh, ql, O, m_ref, l_sum, vlds, new_row_of(p0), s_knew,
-                                   s_vnew, p.scale_log2, false);
+                                         s_vnew, false);
             it = nx;
         }
     }
 
-    // packed: columns c16 and c16 ^ 8 hold the hi and lo parts of one head
-    if constexpr (PACK) {
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) O[dt][i] += dpp_mov<0x128>(O[dt][i]);
-    }
-
-    // ---- 5. combine the wavefronts, then write the partial (or the output)
+    // ---- 5. combine the wavefronts through LDS, then write the partial (or the output)
+    // Wavefront w's O^T column c16 goes to row c16 of its area; packed, rows n and
+    // n + 8 hold the hi and lo parts of head n and are added here.
     const float l_w = swap32_op(swap16_op(l_sum, OpAdd{}), OpAdd{});
-    float* s_o = (float*)s_big;  // wavefront w's O: [w * AREA / 4 + head * OROW + dim]
+    float* s_o = (float*)s_big;  // wavefront w's O: [w * AREA / 4 + column * OROW + dim]
     if (g == 0) {
         s_m[wave][c16] = m_ref;
         s_l[wave][c16] = l_w;
     }
     if (lane == 0) s_badw[wave] = bad ? 1 : 0;  // page lookups are wave-uniform
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) s_o[wave * (AREA / 4) + c16 * G::OROW + dt * 16 + 4 * g + i] = O[dt][i];
+    for (int dt = 0; dt < DT; dt++) *(f32x4*)&s_o[wave * (AREA / 4) + c16 * G::OROW + dt * 16 + 4 * g] = O[dt];
     __syncthreads();
 
     bool poison = false;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) poison |= s_badw[w] != 0;
+    for (int w = 0; w < W; w++) poison |= s_badw[w] != 0;
     const bool single = p.n_splits == 1;
     for (int q4 = tid; q4 < NS * (D / 4); q4 += kThreads) {
         const int n = q4 / (D / 4), d0 = (q4 % (D / 4)) * 4;
         float M = s_m[0][n];
 #pragma unroll
-        for (int w = 1; w < kWaves; w++) M = fmaxf(M, s_m[w][n]);
-        float4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 1; w < W; w++) M = fmaxf(M, s_m[w][n]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         float lt = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) {
+        for (int w = 0; w < W; w++) {
             const float f = fast_exp2(s_m[w][n] - M);  // 0 for a wavefront without tiles
-            const float4 o = *(const float4*)&s_o[w * (AREA / 4) + n * G::OROW + d0];
-            acc.x += o.x * f;
-            acc.y += o.y * f;
-            acc.z += o.z * f;
-            acc.w += o.w * f;
+            f32x4 o = *(const f32x4*)&s_o[w * (AREA / 4) + n * G::OROW + d0];
+            if constexpr (PACK) o += *(const f32x4*)&s_o[w * (AREA / 4) + (n + kHeads / 2) * G::OROW + d0];
+            acc += o * f;
             lt += s_l[w][n] * f;
         }
-        if (poison) acc.x = acc.y = acc.z = acc.w = __builtin_nanf("");
+        if (poison) acc = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
         const uint64_t qi = qrow0 + n;
         if (single) {
-            *(float4*)(p.out + qi * D + d0) = float4{acc.x / lt, acc.y / lt, acc.z / lt, acc.w / lt};
+            *(f32x4*)(p.out + qi * D + d0) = acc / lt;
         } else {
-            *(float4*)(p.part_o + (qi * p.n_splits + split) * D + d0) = acc;
+            *(f32x4*)(p.part_o + (qi * p.n_splits + split) * D + d0) = acc;
             if (d0 == 0) *(float2*)(p.part_ml + (qi * p.n_splits + split) * 2) = float2{M, lt};
         }
     }
