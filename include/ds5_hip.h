@@ -395,6 +395,21 @@ typedef struct ds5_attention_step_args {
 } ds5_attention_step_args;
 int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* args);
 
+/* No reference counterpart. For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): ds5_hip_attention_step with the same kernels, arguments,
+ * preconditions and results, but the split-K partials (decode) or the f16 q
+ * operand (prefill) live in the library's static device scratch array of
+ * DS5_NOALLOC_SCRATCH_BYTES per GPU instead of the context's workspace, and
+ * the call allocates nothing. A call that would need more scratch than that
+ * (e.g. a long prefill) fails with ShapeMismatch before any device work.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other contexts or streams) race. Nothing in the array needs to start
+ * at zero; each call writes what it reads. Per-kernel timing is off during
+ * the call. */
+#define DS5_NOALLOC_SCRATCH_BYTES (4u << 20)
+int ds5_hip_attention_step_noalloc(ds5_hip_ctx* ctx, const ds5_attention_step_args* args);
+
 /* ========================================================================
  * 4. Paged KV decode (no reference counterpart: the reference has no paged
  *    cache; its spec names a "KV page table", docs/specs/DS5_Project_Spec_v0.3.md:65)

@@ -52,6 +52,13 @@ struct ds5_hip_ctx {
     // Split-K partial results: grown on demand, owned by the context.
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    // The library's static device scratch array on this context's device (its
+    // address from hipGetSymbolAddress, taken once per device at init). While
+    // use_scratch is set -- the allocation-free entry point -- the workspace
+    // comes from there and nothing is allocated.
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    bool use_scratch = false;
     // Decode tuning: positions per split-K workgroup (0 = heuristic).
     uint32_t decode_chunk = 0;
     // Optional per-kernel timing: events recorded around every launch on the
@@ -76,6 +83,9 @@ int ds5_fail(ds5_hip_ctx* ctx, int code, const char* fmt, ...) __attribute__((fo
 int ds5_hip_status(ds5_hip_ctx* ctx, hipError_t err, const char* what);
 int ds5_after_launch(ds5_hip_ctx* ctx, const char* what);
 int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out);
+// Looks up (once per device) the address of the static scratch array on the
+// context's device, which must be current, and records it in the context.
+int ds5_scratch_init(ds5_hip_ctx* ctx);
 void ds5_rope_table(float theta, uint32_t head_dim, RopeTable* t);
 
 #define DS5_TIMED_LAUNCH(ctx, name, ...)        \
@@ -245,6 +255,13 @@ struct DecodeLaunch {
     const RopeTable* table;
 };
 int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a);
+// Split-K geometry of a decode launch and the workspace bytes it needs (0 when
+// one split covers every sequence).
+struct DecodeGeometry {
+    uint32_t chunk, n_splits;
+};
+size_t decode_workspace_bytes(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_q_heads, uint32_t n_kv_heads,
+                              uint32_t head_dim, uint32_t max_len);
 
 // Causal flash-attention prefill on f16 MFMA (head_dim 128 or 64).
 struct PrefillLaunch {

@@ -37,6 +37,14 @@ int ds5_after_launch(ds5_hip_ctx* ctx, const char* what) {
 }
 
 int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
+    if (ctx->use_scratch) {
+        // allocation-free call: the static scratch array, never an allocation
+        if (bytes > ctx->scratch_bytes)
+            return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "needs %zu bytes of scratch; the allocation-free entry point "
+                            "holds at most %zu", bytes, ctx->scratch_bytes);
+        *out = ctx->scratch;
+        return DS5_OK;
+    }
     if (bytes > ctx->workspace_bytes) {
         // A larger workspace is a new allocation; the old one stays owned by the
         // context until deinit, because enqueued kernels and captured graphs may
@@ -122,6 +130,7 @@ int ds5_hip_init(int device_index, ds5_hip_ctx** out) {
     if (!rc) rc = ds5_hip_status(ctx, hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = ds5_hip_status(ctx, hipEventCreate(&ctx->ev_begin), "hipEventCreate");
     if (!rc) rc = ds5_hip_status(ctx, hipEventCreate(&ctx->ev_end), "hipEventCreate");
+    if (!rc) rc = ds5_scratch_init(ctx);
     if (rc) {
         ds5_hip_deinit(ctx);
         return rc;

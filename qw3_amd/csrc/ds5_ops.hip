@@ -11,7 +11,39 @@
 //                                          or the generic kernel
 #include <math.h>
 
+#include <mutex>
+
 #include "ds5_common.hpp"
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (ds5_hip_attention_step_noalloc):
+// a static device array, one copy per GPU, held until the process ends. Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in symbol): ds5_scratch_init looks up this device's address with
+// hipGetSymbolAddress once per device, and the workspace calls hand out that
+// address.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[DS5_NOALLOC_SCRATCH_BYTES];
+
+int ds5_scratch_init(ds5_hip_ctx* ctx) {
+    static std::mutex mu;
+    static std::map<int, void*> per_device;  // device index -> address of `scratch` there
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = per_device.find(ctx->device);
+    if (it == per_device.end()) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr) {
+            (void)hipGetLastError();  // do not leave the error for a later launch check
+            return ds5_fail(ctx, DS5_DEVICE_FAILURE, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                            hipGetErrorString(err));
+        }
+        it = per_device.emplace(ctx->device, ptr).first;
+    }
+    ctx->scratch = it->second;
+    ctx->scratch_bytes = DS5_NOALLOC_SCRATCH_BYTES;
+    return DS5_OK;
+}
 
 // ---------------------------------------------------------------------------
 // Rope inverse frequencies, evaluated as the reference evaluates
@@ -622,6 +654,48 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
                                                        a->n_kv_heads, a->head_dim, a->max_ctx});
     if (!rc) rc = ds5_hip_gqa_attention(ctx, &at);
     return rc;
+}
+
+// Workspace bytes ds5_hip_attention_step takes for these arguments: the same
+// kernel choices as its dispatch (the fused MFMA decode or prefill, else the
+// separate ops followed by ds5_hip_gqa_attention's own choice).
+static size_t step_workspace_bytes(const ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
+    const uint64_t T = a->n_tokens, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
+    if (T == 0 || hkv == 0 || hd == 0) return 0;
+    const bool fused = mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k, a->v, a->k_cache, a->v_cache, a->out});
+    if (fused && (T == 1 || prefill_prep_supported(a->n_kv_heads, a->head_dim)))
+        return T == 1 ? decode_workspace_bytes(ctx, 1, a->n_q_heads, a->n_kv_heads, a->head_dim, a->pos + 1)
+                      : (size_t)(T * hq * hd * sizeof(uint16_t));
+    if (mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k_cache, a->v_cache, a->out}))
+        return T == 1 ? decode_workspace_bytes(ctx, 1, a->n_q_heads, a->n_kv_heads, a->head_dim, a->pos + 1)
+                      : (size_t)(T * hq * hd * sizeof(uint16_t));
+    return 0;
+}
+
+int ds5_hip_attention_step_noalloc(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (!ctx) return ds5_hip_attention_step(ctx, a);  // preconditions, then DeviceFailure
+    if (!ctx->scratch) return ds5_fail(ctx, DS5_DEVICE_FAILURE, "attention_step_noalloc: no scratch on this device");
+    const size_t need = step_workspace_bytes(ctx, a);
+    if (need > ctx->scratch_bytes)
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH,
+                        "attention_step_noalloc: this call needs %zu bytes of scratch; the allocation-free entry "
+                        "point holds at most %zu (use ds5_hip_attention_step)", need, ctx->scratch_bytes);
+    // For the duration of the call: workspace from the static scratch array, and
+    // no per-kernel timing (its event pool grows by allocation).
+    struct Scope {
+        ds5_hip_ctx* c;
+        bool timing;
+        explicit Scope(ds5_hip_ctx* c_) : c(c_), timing(c_->kernel_timing) {
+            c->use_scratch = true;
+            c->kernel_timing = false;
+        }
+        ~Scope() {
+            c->use_scratch = false;
+            c->kernel_timing = timing;
+        }
+    } scope(ctx);
+    return ds5_hip_attention_step(ctx, a);
 }
 
 int ds5_hip_paged_decode(ds5_hip_ctx* ctx, const ds5_paged_decode_args* a) {

@@ -721,26 +721,41 @@ int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams&
 
 }  // namespace
 
-int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
-    const uint32_t group = a.n_q_heads / a.n_kv_heads;
-    const uint32_t n_sub = (group + kHeads - 1) / kHeads;
-    const uint32_t max_len = a.max_len;
-    if (a.n_seqs == 0 || max_len == 0) return DS5_OK;
-
-    // Positions per split: about four workgroups per CU over the longest
-    // sequence, whole 128-position steps (one 32-position tile per wavefront),
-    // at most 64 splits (the merge kernel's lane count).
+// Positions per split: about four workgroups per CU over the longest sequence,
+// whole 128-position steps (one 32-position tile per wavefront), at most 64
+// splits (the merge kernel's lane count).
+static DecodeGeometry decode_geometry_of(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_kv_heads, uint32_t n_sub,
+                                         uint32_t max_len) {
     constexpr uint32_t kStep = kWaves * kTile;
     uint32_t chunk = ctx->decode_chunk;
     if (chunk == 0) {
-        const uint64_t units = (uint64_t)a.n_seqs * a.n_kv_heads * n_sub;
+        const uint64_t units = (uint64_t)n_seqs * n_kv_heads * n_sub;
         const uint64_t target = 4ull * (ctx->cu_count > 0 ? ctx->cu_count : 256);
         chunk = (uint32_t)std::min<uint64_t>((max_len * units + target - 1) / target, max_len);
     }
     chunk = std::max<uint32_t>((chunk + kStep - 1) / kStep * kStep, kStep);
     chunk = std::max<uint32_t>(chunk, (max_len + 63) / 64);
     chunk = (chunk + kStep - 1) / kStep * kStep;
-    const uint32_t n_splits = (max_len + chunk - 1) / chunk;
+    return DecodeGeometry{chunk, (max_len + chunk - 1) / chunk};
+}
+
+size_t decode_workspace_bytes(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_q_heads, uint32_t n_kv_heads,
+                              uint32_t head_dim, uint32_t max_len) {
+    if (n_seqs == 0 || max_len == 0 || n_kv_heads == 0) return 0;
+    const uint32_t group = n_q_heads / n_kv_heads;
+    const uint32_t n_sub = (group + kHeads - 1) / kHeads;
+    const DecodeGeometry geo = decode_geometry_of(ctx, n_seqs, n_kv_heads, n_sub, max_len);
+    if (geo.n_splits <= 1) return 0;
+    return (size_t)n_seqs * n_q_heads * geo.n_splits * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
+    const uint32_t group = a.n_q_heads / a.n_kv_heads;
+    const uint32_t n_sub = (group + kHeads - 1) / kHeads;
+    const uint32_t max_len = a.max_len;
+    if (a.n_seqs == 0 || max_len == 0) return DS5_OK;
+    const DecodeGeometry geo = decode_geometry_of(ctx, a.n_seqs, a.n_kv_heads, n_sub, max_len);
+    const uint32_t chunk = geo.chunk, n_splits = geo.n_splits;
 
     DecodeParams prm{};
     prm.q = a.q;

@@ -202,6 +202,7 @@ SIGNATURES = {
     "ds5_hip_expert_mlp_swiglu": ([_P, C.POINTER(ExpertMlpArgs)], C.c_int),
     "ds5_hip_moe": ([_P, C.POINTER(MoeArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
+    "ds5_hip_attention_step_noalloc": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
     "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
@@ -425,6 +426,17 @@ def matmulGroup(ctx: Ctx, args: MatmulGroupArgs) -> None:
 def attentionStep(ctx: Ctx, args: AttentionStepArgs) -> None:
     """Fused q/k norm + rope + kvAppend + gqaAttention (one engine layer's attention block)."""
     ctx.check(LIB.ds5_hip_attention_step(ctx.handle, C.byref(args)))
+
+
+# DS5_NOALLOC_SCRATCH_BYTES (include/ds5_hip.h): the static scratch of the allocation-free entry point
+NOALLOC_SCRATCH_BYTES = 4 << 20
+
+
+def attentionStepNoAlloc(ctx: Ctx, args: AttentionStepArgs) -> None:
+    """attentionStep without any device allocation: its split-K partials or f16 q
+    operand live in the library's static per-GPU scratch (NOALLOC_SCRATCH_BYTES);
+    calls needing more fail with ShapeMismatch. No reference counterpart."""
+    ctx.check(LIB.ds5_hip_attention_step_noalloc(ctx.handle, C.byref(args)))
 
 
 def rope_table(theta: float, head_dim: int) -> np.ndarray:
