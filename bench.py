@@ -13,19 +13,30 @@ W untimed warmup sweeps precede EXACTLY K timed sweeps, bracketed by stream
 synchronisation on both sides and timed with HIP events on the context
 stream. Inputs are synthetic and already resident in HBM.
 
+Order of a run: every selected workload is built on the device; then the CPU
+legs run (the oracle -- a line-by-line single-threaded C restatement of the
+reference's CPU path -- on bounded samples of each configuration, timed on
+one core); then the GPU legs, each followed by the comparison of its sampled
+layers' GPU outputs with the oracle's (the parity figures of the record).
+
 value  = C1 algorithmic HBM bytes of the K sweeps / elapsed (GB/s)
 roofline.achieved = algorithmic bytes of one decode_split_kernel launch (one
-         layer) / that kernel's mean device duration from HIP events around
-         each launch on the context stream (a separate, eager pass)
-cpu_baseline = the CPU oracle (a line-by-line C restatement of the reference's
-         single-threaded CPU path) on a bounded sample of C1 layers, 1 core.
+         layer) / that kernel's mean duration, from start/stop events attached
+         to each launch (hipExtLaunchKernelGGL) on the context stream in an
+         eager pass of the same sweep; rocprof_* fields repeat the fraction
+         with the committed rocprofv3 kernel-trace average of that kernel
+cpu_baseline = the oracle on C1 layers, 1 core (per-config CPU figures are in
+         configs.C*.cpu)
 
-Secondary figures (prefill C2 TFLOP/s, C3 decode, C4 paged decode) are
-reported under "extra"; they are not the headline value.
+configs.C0..C4 hold each BASELINE configuration's GPU figures, CPU figures
+and parity; floors holds the measured cost of one dependent launch and of a
+bare once-read of a C1 layer's K/V; extra holds the projection / MoE legs
+(the rows after the attention path).
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import sys
@@ -40,6 +51,8 @@ HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2516.6
 BF16_MFMA_PEAK_TFLOPS = 2516.6  # dense bf16 matrix-core peak (same as f16)
 QKV_BYTES = 5120 * 64 * 34 + 2048 * 4 + 5120 * 4  # Qwen3-30B-A3B q/k/v weights + x + out per layer
+ROCPROF_JSON = os.path.join(ROOT, "profiles", "rocprof_kernel_us.json")
+OUT_ATOL, OUT_COS = 2e-3, 0.99999  # BASELINE attention-output gates
 LOG = sys.stderr
 
 
@@ -60,36 +73,174 @@ def prefill_flops(hq, d, S):
 
 
 # ---------------------------------------------------------------------------
-# Workloads
+# Workloads (device side)
 # ---------------------------------------------------------------------------
 
 class DecodeSweep:
-    """n_layers independent layers of single-token decode on a contiguous cache."""
+    """n_layers independent layers of single-token decode on a contiguous cache.
+    Each layer has its own cache (filled on the device), inputs and output."""
 
-    def __init__(self, H, synth, ctx, config, verbose=True):
+    def __init__(self, H, synth, ctx, config, repeat=1):
         cfg = synth.CONFIGS[config]
-        self.H, self.ctx, self.config = H, ctx, config
+        self.H, self.ctx, self.config, self.repeat = H, ctx, config, repeat
         s = self.s = cfg["shape"]
         self.cap, self.pos, self.layers = cfg["cap"], cfg["pos"], cfg["layers"]
         hkv, d = s.n_kv_heads, s.head_dim
         n = hkv * self.cap * d
-        self.args = []
-        pos_buf = ctx.from_numpy(np.array([self.pos], np.int32))
+        self.args, self.host, self.caches, self.outs = [], [], [], []
+        self.pos_buf = ctx.from_numpy(np.array([self.pos], np.int32))
         for layer in range(self.layers):
             kc, vc = ctx.createBuffer(2 * n), ctx.createBuffer(2 * n)
             ctx.fill_normal_f16(kc, n, seed=(config << 20) + 2 * layer + 1)
             ctx.fill_normal_f16(vc, n, seed=(config << 20) + 2 * layer + 2)
             q, k, v, qn, kn = synth.step_inputs(config, layer, 1, s)
             out = ctx.createBuffer(s.n_q_heads * d * 4)
+            self.host.append((q, k, v, qn, kn))
+            self.caches.append((kc, vc))
+            self.outs.append(out)
             self.args.append(H.AttentionStepArgs(ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v),
-                                                 ctx.from_numpy(qn), ctx.from_numpy(kn), pos_buf, kc, vc, out,
+                                                 ctx.from_numpy(qn), ctx.from_numpy(kn), self.pos_buf, kc, vc, out,
                                                  H.DTYPE_F16, self.pos, 1, s.n_q_heads, hkv, d, self.cap, s.eps,
                                                  s.theta, 1.0, s.scale))
         self.bytes_per_layer = decode_bytes(s.n_q_heads, hkv, d, self.pos + 1)
 
+    def cache_host(self, layer):
+        """The layer's K/V cache as f16 bits [Hkv, cap, d] (rows < pos are never written by a step)."""
+        shape = (self.s.n_kv_heads, self.cap, self.s.head_dim)
+        kc, vc = self.caches[layer]
+        return self.ctx.to_numpy(kc, np.uint16, shape), self.ctx.to_numpy(vc, np.uint16, shape)
+
+    def sweep(self):
+        for _ in range(self.repeat):
+            for a in self.args:
+                self.H.attentionStep(self.ctx, a)
+
+
+class SixOpSweep:
+    """C1's layers through the engine's six separate ops (forward.zig:345-412) on
+    their own q/k/out buffers: part "prep" = rmsNorm q, rmsNorm k, rope q, rope k,
+    kvAppend (five launches); part "attn" = gqaAttention; "all" = the six."""
+
+    def __init__(self, H, ctx, dec: DecodeSweep, part: str):
+        self.H, self.ctx, self.part, self.layers = H, ctx, part, dec.layers
+        s, pos, cap = dec.s, dec.pos, dec.cap
+        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
+        self.calls = []
+        for layer in range(dec.layers):
+            q, k, v, qn, kn = dec.host[layer]
+            qb, kb, vb, qnb, knb = (ctx.from_numpy(a) for a in (q, k, v, qn, kn))
+            kc, vc = dec.caches[layer]
+            out = ctx.createBuffer(hq * d * 4)
+            prep = [(H.rmsNorm, H.RmsNormArgs(qb, qnb, qb, hq, d, s.eps)),
+                    (H.rmsNorm, H.RmsNormArgs(kb, knb, kb, hkv, d, s.eps)),
+                    (H.rope, H.RopeArgs(qb, dec.pos_buf, 1, hq, d, s.theta)),
+                    (H.rope, H.RopeArgs(kb, dec.pos_buf, 1, hkv, d, s.theta)),
+                    (H.kvAppend, H.KvAppendArgs(kb, vb, kc, vc, H.DTYPE_F16, pos, 1, hkv, d, cap))]
+            attn = [(H.gqaAttention, H.AttnArgs(qb, kc, vc, H.DTYPE_F16, out, pos, 1, hq, hkv, d, cap, s.scale))]
+            self.calls += {"prep": prep, "attn": attn, "all": prep + attn}[part]
+
+    def sweep(self):
+        for fn, a in self.calls:
+            fn(self.ctx, a)
+
+
+class PagedSweep:
+    """C4: n_layers of batched paged decode (32 sequences, 16-token pages)."""
+
+    def __init__(self, H, synth, ctx, config=4):
+        cfg = synth.CONFIGS[config]
+        self.H, self.ctx = H, ctx
+        s = self.s = cfg["shape"]
+        self.layers = cfg["layers"]
+        lay = self.lay = synth.paged_layout(cfg["n_seqs"], cfg["lo"], cfg["hi"], cfg["page_size"], seed=0)
+        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
+        B = self.B = cfg["n_seqs"]
+        self.slots = lay.n_pages * lay.page_size
+        pt, sl = ctx.from_numpy(lay.page_table), ctx.from_numpy(lay.seq_lens)
+        self.args, self.host, self.pools, self.outs = [], [], [], []
+        for layer in range(self.layers):
+            kp, vp = ctx.createBuffer(2 * hkv * self.slots * d), ctx.createBuffer(2 * hkv * self.slots * d)
+            ctx.fill_normal_f16(kp, hkv * self.slots * d, seed=(config << 20) + 2 * layer + 1)
+            ctx.fill_normal_f16(vp, hkv * self.slots * d, seed=(config << 20) + 2 * layer + 2)
+            q, k, v, qn, kn = synth.step_inputs(config, layer, B, s)
+            out = ctx.createBuffer(B * hq * d * 4)
+            self.host.append((q, k, v, qn, kn))
+            self.pools.append((kp, vp))
+            self.outs.append(out)
+            self.args.append(H.PagedDecodeArgs(ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v),
+                                               ctx.from_numpy(qn), ctx.from_numpy(kn), kp, vp, pt, sl, out, B, hq,
+                                               hkv, d, lay.page_size, lay.n_pages, lay.max_pages,
+                                               int(lay.seq_lens.max()), s.eps, s.theta, 1.0, s.scale))
+        pages = ((lay.seq_lens.astype(np.int64) + lay.page_size - 1) // lay.page_size).sum()
+        self.bytes_per_layer = int(sum(decode_bytes(hq, hkv, d, int(L)) - 8 * d for L in lay.seq_lens)
+                                   + 8 * d + 4 * pages)
+
+    def pool_host(self, layer):
+        shape = (self.s.n_kv_heads, self.slots, self.s.head_dim)
+        kp, vp = self.pools[layer]
+        return self.ctx.to_numpy(kp, np.uint16, shape), self.ctx.to_numpy(vp, np.uint16, shape)
+
     def sweep(self):
         for a in self.args:
-            self.H.attentionStep(self.ctx, a)
+            self.H.pagedDecode(self.ctx, a)
+
+
+class Prefill:
+    """C2: causal prefill of 2048 tokens into an empty f16 cache, one layer
+    (fused: the attention step; separate: the six ops)."""
+
+    def __init__(self, H, synth, ctx, config=2, fused=True):
+        cfg = synth.CONFIGS[config]
+        self.H, self.ctx, self.fused = H, ctx, fused
+        s = self.s = cfg["shape"]
+        T = self.T = cfg["tokens"]
+        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
+        self.host = synth.step_inputs(config, 0, T, s, f16_exact=True)
+        q, k, v, qn, kn = self.host
+        self.kc, self.vc = ctx.createBuffer(2 * hkv * T * d), ctx.createBuffer(2 * hkv * T * d)
+        self.out = ctx.createBuffer(T * hq * d * 4)
+        qb, kb, vb, qnb, knb = (ctx.from_numpy(a) for a in (q, k, v, qn, kn))
+        pb = ctx.from_numpy(np.arange(T, dtype=np.int32))
+        self.args = H.AttentionStepArgs(qb, kb, vb, qnb, knb, pb, self.kc, self.vc, self.out, H.DTYPE_F16, 0, T, hq,
+                                        hkv, d, T, s.eps, s.theta, 1.0, s.scale)
+        self.calls = [(H.rmsNorm, H.RmsNormArgs(qb, qnb, qb, T * hq, d, s.eps)),
+                      (H.rmsNorm, H.RmsNormArgs(kb, knb, kb, T * hkv, d, s.eps)),
+                      (H.rope, H.RopeArgs(qb, pb, T, hq, d, s.theta)),
+                      (H.rope, H.RopeArgs(kb, pb, T, hkv, d, s.theta)),
+                      (H.kvAppend, H.KvAppendArgs(kb, vb, self.kc, self.vc, H.DTYPE_F16, 0, T, hkv, d, T)),
+                      (H.gqaAttention, H.AttnArgs(qb, self.kc, self.vc, H.DTYPE_F16, self.out, 0, T, hq, hkv, d, T,
+                                                  s.scale))]
+        self.flops = prefill_flops(hq, d, T)
+
+    def sweep(self):
+        if self.fused:
+            self.H.attentionStep(self.ctx, self.args)
+        else:
+            for fn, a in self.calls:
+                fn(self.ctx, a)
+
+
+class FloorSweep:
+    """The floors of one decode layer: 48 launches of an empty kernel (one
+    dependent launch each), 48 bare once-reads of a distinct 16 MiB buffer (a
+    C1 layer's K and V), or both per layer (the launch count of split + merge)."""
+
+    def __init__(self, H, ctx, layers=48, nbytes=16 << 20, mode="read"):
+        self.ctx, self.layers, self.mode, self.nbytes = ctx, layers, mode, nbytes
+        self.bufs = []
+        if mode != "empty":
+            for layer in range(layers):
+                b = ctx.createBuffer(nbytes)
+                ctx.fill_normal_f16(b, nbytes // 2, seed=(9 << 20) + layer)
+                self.bufs.append(b)
+        self.sink = ctx.createBuffer(16)
+
+    def sweep(self):
+        for layer in range(self.layers):
+            if self.mode != "empty":
+                self.ctx.stream_read(self.bufs[layer], self.nbytes, self.sink)
+            if self.mode != "read":
+                self.ctx.empty_launch(256)
 
 
 class ProjSweep:
@@ -219,64 +370,30 @@ class ProjPrefill:
         self.H.matmulGroup(self.ctx, self.args)
 
 
-class PagedSweep:
-    """C4: n_layers of batched paged decode (32 sequences, 16-token pages)."""
+# ---------------------------------------------------------------------------
+# Timing helpers
+# ---------------------------------------------------------------------------
 
-    def __init__(self, H, synth, ctx, config=4):
-        cfg = synth.CONFIGS[config]
-        self.H, self.ctx = H, ctx
-        s = self.s = cfg["shape"]
-        self.layers = cfg["layers"]
-        lay = self.lay = synth.paged_layout(cfg["n_seqs"], cfg["lo"], cfg["hi"], cfg["page_size"], seed=0)
-        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
-        B = cfg["n_seqs"]
-        slots = lay.n_pages * lay.page_size
-        pt, sl = ctx.from_numpy(lay.page_table), ctx.from_numpy(lay.seq_lens)
-        self.args = []
-        for layer in range(self.layers):
-            kp, vp = ctx.createBuffer(2 * hkv * slots * d), ctx.createBuffer(2 * hkv * slots * d)
-            ctx.fill_normal_f16(kp, hkv * slots * d, seed=(config << 20) + 2 * layer + 1)
-            ctx.fill_normal_f16(vp, hkv * slots * d, seed=(config << 20) + 2 * layer + 2)
-            q, k, v, qn, kn = synth.step_inputs(config, layer, B, s)
-            out = ctx.createBuffer(B * hq * d * 4)
-            self.args.append(H.PagedDecodeArgs(ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v),
-                                               ctx.from_numpy(qn), ctx.from_numpy(kn), kp, vp, pt, sl, out, B, hq,
-                                               hkv, d, lay.page_size, lay.n_pages, lay.max_pages,
-                                               int(lay.seq_lens.max()), s.eps, s.theta, 1.0, s.scale))
-        pages = ((lay.seq_lens.astype(np.int64) + lay.page_size - 1) // lay.page_size).sum()
-        self.bytes_per_layer = int(sum(decode_bytes(hq, hkv, d, int(L)) - 8 * d for L in lay.seq_lens)
-                                   + 8 * d + 4 * pages)
-
-    def sweep(self):
-        for a in self.args:
-            self.H.pagedDecode(self.ctx, a)
-
-
-class Prefill:
-    """C2: causal prefill of 2048 tokens into an empty f16 cache, one layer."""
-
-    def __init__(self, H, synth, ctx, config=2):
-        cfg = synth.CONFIGS[config]
-        self.H, self.ctx = H, ctx
-        s = self.s = cfg["shape"]
-        T = self.T = cfg["tokens"]
-        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
-        q, k, v, qn, kn = synth.step_inputs(config, 0, T, s, f16_exact=True)
-        kc, vc = ctx.createBuffer(2 * hkv * T * d), ctx.createBuffer(2 * hkv * T * d)
-        out = ctx.createBuffer(T * hq * d * 4)
-        self.args = H.AttentionStepArgs(ctx.from_numpy(q), ctx.from_numpy(k), ctx.from_numpy(v), ctx.from_numpy(qn),
-                                        ctx.from_numpy(kn), ctx.from_numpy(np.arange(T, dtype=np.int32)), kc, vc,
-                                        out, H.DTYPE_F16, 0, T, hq, hkv, d, T, s.eps, s.theta, 1.0, s.scale)
-        self.flops = prefill_flops(hq, d, T)
-
-    def sweep(self):
-        self.H.attentionStep(self.ctx, self.args)
+USE_GRAPHS = True  # --no-graph: sweeps run eagerly (profiling runs; the profiler's graph interception is unstable)
 
 
 def time_graph(ctx, work, steps, warmup):
-    """Capture work.sweep() once, replay warmup + steps times; returns seconds of the timed replays."""
+    """Capture work.sweep() once, replay warmup + steps times; returns (device seconds
+    of the timed replays from events on the context stream, wall seconds). Without
+    graphs (--no-graph) the sweeps are enqueued eagerly instead."""
     work.sweep()                      # eager once: sizes the split-K workspace
     ctx.submit()
+    if not USE_GRAPHS:
+        for _ in range(warmup):
+            work.sweep()
+        ctx.submit()
+        ctx.begin()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            work.sweep()
+        ctx.submit()
+        wall = time.perf_counter() - t0
+        return ctx.gpuElapsedNs() * 1e-9, wall
     g = ctx.capture(work.sweep)
     try:
         for _ in range(warmup):
@@ -293,18 +410,39 @@ def time_graph(ctx, work, steps, warmup):
         g.destroy()
 
 
-def kernel_mean_ns(ctx, work, kernel, reps):
-    """Mean device duration of `kernel` over `reps` eager sweeps, from HIP events
-    recorded around each launch on the context stream."""
+def replays_for(seconds_per_step, min_seconds, floor):
+    return max(floor, int(min_seconds / max(seconds_per_step, 1e-9)) + 1)
+
+
+def kernel_stats(ctx, work, kernels, min_seconds=0.3, max_reps=2000):
+    """Mean device duration (ns) and launch count of each named kernel over eager
+    sweeps (at least min_seconds of them), each launch timed by start/stop events
+    attached to its own dispatch."""
     ctx.set_kernel_timing(True)
     try:
-        for _ in range(reps):
+        t0, reps = time.perf_counter(), 0
+        while reps < max_reps and (reps < 2 or time.perf_counter() - t0 < min_seconds):
             work.sweep()
+            reps += 1
+            if reps % 4 == 0:
+                ctx.kernel_time(kernels[0])  # resolves the pending event pairs (bounded event pool)
         ctx.submit()
-        n, total = ctx.kernel_time(kernel)
+        out = {}
+        for k in kernels:
+            n, total = ctx.kernel_time(k)
+            out[k] = (total / n if n else float("nan"), n)
     finally:
         ctx.set_kernel_timing(False)
-    return (total / n if n else float("nan")), n
+    return out
+
+
+def rocprof_kernel_us(workload, kernel):
+    """The rocprofv3 kernel-trace average (us) of `kernel` in the committed summary
+    for `workload` (profiles/rocprof_kernel_us.json), or None."""
+    if not os.path.exists(ROCPROF_JSON):
+        return None
+    with open(ROCPROF_JSON) as f:
+        return json.load(f).get(workload, {}).get(kernel, {}).get("avg_us")
 
 
 def measured_traffic(kernel, workload):
@@ -319,43 +457,152 @@ def measured_traffic(kernel, workload):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def cpu_baseline_c1(synth, seconds):
-    """Oracle (single-threaded C restatement of kernels_a/b.zig) on C1 layers."""
-    from oracle import oracle as O
-    cfg = synth.CONFIGS[1]
-    s, cap, pos = cfg["shape"], cfg["cap"], cfg["pos"]
-    data = []
-    for layer in range(3):
-        q, k, v, qn, kn = synth.step_inputs(1, layer, 1, s)
-        kc, vc = synth.cache_f16(1, layer, s, cap, pos)
-        data.append((q, k, v, qn, kn, kc, vc))
-    n, t_total = 0, 0.0
-    while t_total < seconds:
-        q, k, v, qn, kn, kc, vc = data[n % len(data)]
-        t0 = time.perf_counter()
-        O.attention_step(q, k, v, qn, kn, np.array([pos], np.int32), kc, vc, kv_dtype=1, pos=pos, n_tokens=1,
-                         n_q_heads=s.n_q_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, max_ctx=cap,
-                         eps=s.eps, theta=s.theta, scale=s.scale)
-        t_total += time.perf_counter() - t0
-        n += 1
-    us = t_total / n * 1e6
-    return dict(us_per_layer=us, layers=n, seconds=t_total)
+def ingest_rocprof(stats_csv, workload):
+    """Record the per-kernel averages of a rocprofv3 --stats kernel_stats.csv under
+    `workload` in profiles/rocprof_kernel_us.json."""
+    data = json.load(open(ROCPROF_JSON)) if os.path.exists(ROCPROF_JSON) else {}
+    entry = {}
+    import subprocess
+    with open(stats_csv) as f:
+        for row in csv.DictReader(f):
+            name = row["Name"]
+            if name.startswith("_ZN12_GLOBAL__N_1"):  # (anonymous namespace)::<len><name>...
+                rest = name[len("_ZN12_GLOBAL__N_1"):]
+                digits = len(rest) - len(rest.lstrip("0123456789"))
+                name = rest[digits:digits + int(rest[:digits])]
+            elif name.startswith("_Z"):
+                name = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip() or name
+            name = name.replace("(anonymous namespace)::", "")
+            if name.startswith("void "):
+                name = name[5:]
+            name = name.split("(")[0].split("<")[0].strip().split("::")[-1]
+            calls = int(row["Calls"])
+            avg = float(row["AverageNs"]) / 1e3
+            prev = entry.get(name)
+            if prev is None or calls > prev["calls"]:
+                entry[name] = dict(avg_us=round(avg, 3), calls=calls, min_us=round(float(row["MinNs"]) / 1e3, 3),
+                                   max_us=round(float(row["MaxNs"]) / 1e3, 3))
+    data[workload] = entry
+    with open(ROCPROF_JSON, "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)
+        f.write("\n")
+    print(json.dumps({workload: entry}))
 
+
+# ---------------------------------------------------------------------------
+# Parity and the CPU legs (the oracle: tests infrastructure, used here only as
+# the checker and the CPU baseline)
+# ---------------------------------------------------------------------------
+
+def parity(got, want, got_rows=None, want_rows=None):
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    err = float(np.max(np.abs(got - want)))
+    cos = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want)))
+    r = dict(max_abs=float(f"{err:.3e}"), cosine=round(cos, 9), ok=bool(err <= OUT_ATOL and cos >= OUT_COS
+                                                                         and np.all(np.isfinite(got))))
+    if got_rows is not None:
+        def mono(x):
+            x = np.asarray(x, np.uint16).astype(np.int32)
+            return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + x)
+        ulp = int(np.max(np.abs(mono(got_rows) - mono(want_rows))))
+        r["kv_ulp_max"] = ulp
+        r["ok"] = r["ok"] and ulp <= 1
+    return r
+
+
+def oracle_decode(O, s, host, kc, vc, pos, cap):
+    q, k, v, qn, kn = host
+    kc, vc = kc.copy(), vc.copy()
+    out, _, _ = O.attention_step(q, k, v, qn, kn, np.array([pos], np.int32), kc, vc, kv_dtype=1, pos=pos,
+                                 n_tokens=1, n_q_heads=s.n_q_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim,
+                                 max_ctx=cap, eps=s.eps, theta=s.theta, scale=s.scale)
+    return out, kc[:, pos], vc[:, pos]
+
+
+def cpu_decode_leg(O, w, layers, seconds):
+    """The oracle on `layers` of a DecodeSweep, cycling until `seconds` have passed
+    (at least one pass); returns (us per layer, layer-steps, seconds, {layer: reference})."""
+    samples = {layer: w.cache_host(layer) for layer in layers}
+    refs, n, t = {}, 0, 0.0
+    while n < len(layers) or t < seconds:
+        layer = layers[n % len(layers)]
+        kc, vc = samples[layer]
+        t0 = time.perf_counter()
+        r = oracle_decode(O, w.s, w.host[layer], kc, vc, w.pos, w.cap)
+        t += time.perf_counter() - t0
+        refs[layer] = r
+        n += 1
+    return t / n * 1e6, n, t, refs
+
+
+def cpu_paged_leg(O, w, layer=0):
+    """The oracle on every sequence of one C4 layer: gather the sequence's pages
+    into a contiguous cache, then the decode step (the reduction the parity tests
+    use). Returns (us for the layer, seconds, references)."""
+    s, lay = w.s, w.lay
+    kp, vp = w.pool_host(layer)
+    q, k, v, qn, kn = w.host[layer]
+    refs, t = [], 0.0
+    for b in range(w.B):
+        L = int(lay.seq_lens[b])
+        kc = O.paged_gather_f16(kp, lay.page_table[b], lay.page_size, L)
+        vc = O.paged_gather_f16(vp, lay.page_table[b], lay.page_size, L)
+        t0 = time.perf_counter()
+        r = oracle_decode(O, s, (q[b:b + 1], k[b:b + 1], v[b:b + 1], qn, kn), kc, vc, L - 1, L)
+        t += time.perf_counter() - t0
+        refs.append(r)
+    return t * 1e6, t, refs
+
+
+def cpu_prefill_leg(O, p, group=0):
+    """The oracle on one GQA group of C2 (q heads of kv head `group`, all 2048
+    tokens); the layer's CPU time is that times the number of kv heads."""
+    s, T = p.s, p.T
+    hg = s.n_q_heads // s.n_kv_heads
+    q, k, v, qn, kn = p.host
+    qg = np.ascontiguousarray(q[:, group * hg:(group + 1) * hg])
+    kg = np.ascontiguousarray(k[:, group:group + 1])
+    vg = np.ascontiguousarray(v[:, group:group + 1])
+    kc = np.zeros((1, T, s.head_dim), np.uint16)
+    vc = np.zeros((1, T, s.head_dim), np.uint16)
+    t0 = time.perf_counter()
+    out, _, _ = O.attention_step(qg, kg, vg, qn, kn, np.arange(T, dtype=np.int32), kc, vc, kv_dtype=1, pos=0,
+                                 n_tokens=T, n_q_heads=hg, n_kv_heads=1, head_dim=s.head_dim, max_ctx=T, eps=s.eps,
+                                 theta=s.theta, scale=s.scale)
+    t = time.perf_counter() - t0
+    return t * 1e6 * s.n_kv_heads, t, (out.reshape(T, hg, s.head_dim), kc[0], vc[0])
+
+
+# ---------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50, help="timed 48-layer sweeps")
+    ap.add_argument("--steps", type=int, default=50, help="timed 48-layer sweeps (C1)")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", default="C1,C2,C3,C4,QKV,WO,MOE,QKVP",
-                    help="comma list of configs to run (C1 is the headline; QKV / QKVP: the decode / prefill "
-                         "q/k/v projections; WO: the decode output projection and residual; MOE: the decode MoE block)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU legs (and the parity figures)")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time per cycled decode leg (C0, C1)")
+    ap.add_argument("--leg-seconds", type=float, default=0.5,
+                    help="minimum device time of each secondary timed leg (graph replays / eager kernel timing)")
+    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,QKVP",
+                    help="comma list of legs: C0-C4 (BASELINE configs; C1 is the headline), FLOOR (launch and "
+                         "bare-read floors), SIX (C1 through the six separate ops), QKV / QKVP (decode / prefill "
+                         "q/k/v projections), WO (output projection + residual), MOE (decode MoE block)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="enqueue the timed sweeps eagerly instead of replaying captured graphs (for profiler runs)")
+    ap.add_argument("--ingest-rocprof", nargs=2, metavar=("KERNEL_STATS_CSV", "WORKLOAD"),
+                    help="record a rocprofv3 --stats kernel_stats.csv under WORKLOAD in "
+                         "profiles/rocprof_kernel_us.json and exit (no GPU)")
     args = ap.parse_args()
+    if args.ingest_rocprof:
+        ingest_rocprof(*args.ingest_rocprof)
+        return
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(layers/heads/sequences would shard across GPUs; no multi-GPU path is built)", file=sys.stderr)
@@ -373,88 +620,244 @@ def main():
         ctx.copy_device(dst, src, nb)
         ctx.submit()
         log(f"[bench] calibration copy of {args.calibrate_copy} MiB done")
-    extra = {}
-    result = None
 
-    if "C1" in only:
-        log("[bench] C1: building 48 layers (8192-token f16 caches)")
-        w = DecodeSweep(H, synth, ctx, 1)
-        elapsed, wall = time_graph(ctx, w, args.steps, args.warmup)
+    # ---- 1. build the device workloads
+    W = {}
+    for c in (0, 1, 3):
+        if f"C{c}" in only or (c == 1 and "SIX" in only):
+            log(f"[bench] C{c}: building {synth.CONFIGS[c]['layers']} layers")
+            # C0 is one layer: a step is replayed 100 times per graph so that the
+            # figure is the device's per-step time, not one graph launch's host cost
+            W[c] = DecodeSweep(H, synth, ctx, c, repeat=100 if c == 0 else 1)
+    if "C4" in only:
+        log("[bench] C4: building 48 layers of paged pools (32 sequences)")
+        W[4] = PagedSweep(H, synth, ctx)
+    if "C2" in only:
+        log("[bench] C2: prefill 2048 tokens")
+        W[2] = Prefill(H, synth, ctx)
+    ctx.submit()
+
+    # ---- 2. CPU legs (before the GPU legs): the oracle, one core, on bounded samples
+    cpu, refs = {}, {}
+    O = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        O.lib()
+        for c, layers in ((0, [0]), (1, [0, 1, 2]), (3, [0])):
+            if c in W and f"C{c}" in only:
+                secs = args.cpu_seconds if c != 3 else 0.0
+                us, n, t, refs[c] = cpu_decode_leg(O, W[c], layers, secs)
+                cpu[c] = dict(us_per_layer=round(us, 1), cores=1, kind="port",
+                              sample=f"{n} decode layer-steps over layers {layers} through oracle/ds5_oracle.c "
+                                     f"ds5o_attention_step, {t:.1f} s")
+                log(f"[bench] CPU C{c}: {us:.1f} us/layer ({n} layer-steps, {t:.1f} s)")
+        if 4 in W:
+            us, t, refs[4] = cpu_paged_leg(O, W[4])
+            cpu[4] = dict(us_per_layer=round(us, 1), cores=1, kind="port",
+                          sample=f"layer 0, all {W[4].B} sequences (pages gathered, then ds5o_attention_step), "
+                                 f"{t:.1f} s")
+            log(f"[bench] CPU C4: {us:.1f} us/layer ({t:.1f} s)")
+        if 2 in W:
+            us, t, refs[2] = cpu_prefill_leg(O, W[2])
+            cpu[2] = dict(us_per_layer=round(us, 1), cores=1, kind="port",
+                          sample=f"one GQA group of 4 (kv head 0, 8 q heads, all 2048 tokens) through "
+                                 f"ds5o_attention_step in {t:.1f} s, times 4 for the layer")
+            log(f"[bench] CPU C2: {us / 1e6:.2f} s/layer (one group {t:.1f} s)")
+
+    # ---- 3. GPU legs; each config's parity (its GPU outputs vs the oracle's) is read
+    #         right after its leg, before a later leg can touch its caches
+    configs, extra, result = {}, {}, None
+    leg = args.leg_seconds
+
+    def parity_decode(c):
+        if c not in refs:
+            return
+        w, pr = W[c], []
+        for layer, (wout, wk, wv) in refs[c].items():
+            got = ctx.to_numpy(w.outs[layer], np.float32)
+            gk, gv = w.cache_host(layer)
+            pr.append(parity(got, wout, np.stack([gk[:, w.pos], gv[:, w.pos]]), np.stack([wk, wv])))
+        configs[f"C{c}"]["parity"] = dict(layers=sorted(refs[c]), max_abs=max(x["max_abs"] for x in pr),
+                                          cosine_min=min(x["cosine"] for x in pr),
+                                          kv_ulp_max=max(x["kv_ulp_max"] for x in pr), ok=all(x["ok"] for x in pr))
+
+    def parity_c4():
+        if 4 not in refs:
+            return
+        w = W[4]
+        got = ctx.to_numpy(w.outs[0], np.float32).reshape(w.B, -1)
+        kp, vp = w.pool_host(0)
+        pr = []
+        for b, (wout, wk, wv) in enumerate(refs[4]):
+            slot = w.lay.slot(b, int(w.lay.seq_lens[b]) - 1)
+            pr.append(parity(got[b], wout, np.stack([kp[:, slot], vp[:, slot]]), np.stack([wk, wv])))
+        configs["C4"]["parity"] = dict(sequences=w.B, max_abs=max(x["max_abs"] for x in pr),
+                                       cosine_min=min(x["cosine"] for x in pr),
+                                       kv_ulp_max=max(x["kv_ulp_max"] for x in pr), ok=all(x["ok"] for x in pr))
+
+    def parity_c2():
+        if 2 not in refs:
+            return
+        p = W[2]
+        s, T = p.s, p.T
+        hg = s.n_q_heads // s.n_kv_heads
+        wout, wk, wv = refs[2]
+        got = ctx.to_numpy(p.out, np.float32).reshape(T, s.n_q_heads, s.head_dim)[:, :hg]
+        shape = (s.n_kv_heads, T, s.head_dim)
+        gk, gv = ctx.to_numpy(p.kc, np.uint16, shape)[0], ctx.to_numpy(p.vc, np.uint16, shape)[0]
+        configs["C2"]["parity"] = dict(parity(got, wout, np.stack([gk, gv]), np.stack([wk, wv])),
+                                       sample="kv head 0: its 8 q heads x 2048 tokens and its 2048 cache rows")
+
+    def decode_leg(c, steps, warmup):
+        w = W[c]
+        elapsed, wall = time_graph(ctx, w, steps, warmup)
+        us = elapsed / (w.layers * getattr(w, "repeat", 1) * steps) * 1e6
+        ks = kernel_stats(ctx, w, ("decode_split_kernel", "decode_merge_kernel"), leg)
+        split_ns, n_split = ks["decode_split_kernel"]
+        merge_ns, _ = ks["decode_merge_kernel"]
+        r = dict(us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 1),
+                 frac=round(w.bytes_per_layer / (us * 1e3) / HBM_PEAK_GBS, 4), bytes_per_layer=w.bytes_per_layer,
+                 steps=steps, layers=w.layers, kernel_us=dict(decode_split_kernel=round(split_ns / 1e3, 3),
+                                                               decode_merge_kernel=round(merge_ns / 1e3, 3)),
+                 kernel_frac=round(w.bytes_per_layer / split_ns / HBM_PEAK_GBS, 4), kernel_launches=n_split)
+        ru = rocprof_kernel_us(f"C{c}", "decode_split_kernel")
+        if ru:
+            r["rocprof_kernel_us"] = ru
+            r["rocprof_kernel_frac"] = round(w.bytes_per_layer / (ru * 1e3) / HBM_PEAK_GBS, 4)
+        return r, elapsed, wall, split_ns
+
+    if 1 in W and "C1" in only:
+        w = W[1]
+        r, elapsed, wall, split_ns = decode_leg(1, args.steps, args.warmup)
         layers = w.layers * args.steps
-        us_layer = elapsed / layers * 1e6
-        gbs = w.bytes_per_layer * layers / elapsed / 1e9
-        log(f"[bench] C1 graph sweep: {us_layer:.3f} us/layer, {gbs:.1f} GB/s (wall {wall / layers * 1e6:.3f} us/layer)")
-        ns_split, n_split = kernel_mean_ns(ctx, w, "decode_split_kernel", max(2, args.steps // 10))
-        achieved = w.bytes_per_layer / ns_split  # bytes/ns == GB/s
-        log(f"[bench] C1 decode_split_kernel mean {ns_split / 1e3:.3f} us over {n_split} launches -> {achieved:.1f} GB/s")
+        log(f"[bench] C1 graph sweep: {r['us_per_layer']:.3f} us/layer, {r['gbs']:.1f} GB/s "
+            f"(wall {wall / layers * 1e6:.3f} us/layer); decode_split_kernel {split_ns / 1e3:.3f} us")
         ctx.submit()
         ctx.begin()
         for _ in range(args.steps):
             w.sweep()
         ctx.submit()
-        eager_us = ctx.gpuElapsedNs() / (w.layers * args.steps) / 1e3
-        log(f"[bench] C1 eager (no graph) sweep: {eager_us:.3f} us/layer")
+        r["us_per_layer_eager"] = round(ctx.gpuElapsedNs() / (w.layers * args.steps) / 1e3, 3)
+        configs["C1"] = dict(workload="decode, 48 layers, 32q/4kv, d128, L 8192, f16 cache, fused step", gpu=r)
+        achieved = w.bytes_per_layer / split_ns  # bytes/ns == GB/s
+        roof = dict(bound="hbm", achieved=round(achieved, 2), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic("decode_split_kernel", "c1"),
+                    kernel="decode_split_kernel", kernel_mean_us=round(split_ns / 1e3, 4),
+                    algorithmic_bytes_per_launch=w.bytes_per_layer)
+        if "rocprof_kernel_us" in r:
+            roof["rocprof_kernel_mean_us"] = r["rocprof_kernel_us"]
+            roof["rocprof_frac"] = r["rocprof_kernel_frac"]
         result = dict(
             metric="decode attn µs/layer & HBM GB/s (32q/4kv,d128,8K ctx f16 KV); prefill TFLOP/s",
-            value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+            value=r["gbs"], unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
             ms_per_step=round(elapsed / args.steps * 1e3, 4), higher_is_better=True, scaling="weak",
             vs_baseline=None, dtype="f16 KV / f32 compute", data="synthetic",
             config=dict(workload="C1: decode 1 token x 48 independent layers, Qwen3-30B-A3B attention "
                                  "(32q/4kv, d128), f16 KV cache 8192 tokens/layer, fused qk-norm+rope+append+attention",
                         layers=w.layers, ctx_len=w.pos + 1, n_q_heads=32, n_kv_heads=4, head_dim=128,
                         parallelism="single GPU"),
-            us_per_layer=round(us_layer, 4),
-            us_per_layer_eager=round(eager_us, 4),
-            roofline=dict(bound="hbm", achieved=round(achieved, 2), peak=HBM_PEAK_GBS, unit="GB/s",
-                          frac=round(achieved / HBM_PEAK_GBS, 4),
-                          traffic=measured_traffic("decode_split_kernel", "c1"),
-                          kernel="decode_split_kernel", kernel_mean_us=round(ns_split / 1e3, 4),
-                          algorithmic_bytes_per_launch=w.bytes_per_layer),
-        )
-        del w
+            us_per_layer=r["us_per_layer"], us_per_layer_eager=r["us_per_layer_eager"], roofline=roof)
+        parity_decode(1)
 
-    if "C2" in only:
-        log("[bench] C2: prefill 2048 tokens")
-        p = Prefill(H, synth, ctx)
-        elapsed, _ = time_graph(ctx, p, max(5, args.steps // 5), 2)
-        n_rep = max(5, args.steps // 5)
-        e2e_us = elapsed / n_rep * 1e6
-        ns_pf, _ = kernel_mean_ns(ctx, p, "prefill_attention_kernel", 5)
+    if 1 in W and "SIX" in only:
+        six = {}
+        for part in ("prep", "attn", "all"):
+            sw = SixOpSweep(H, ctx, W[1], part)
+            el, _ = time_graph(ctx, sw, max(5, args.steps // 2), 2)
+            six[part] = round(el / (sw.layers * max(5, args.steps // 2)) * 1e6, 3)
+            if part == "all":
+                names = ("rms_norm_rows_kernel", "rope_kernel", "kv_append_kernel", "decode_split_kernel",
+                         "decode_merge_kernel")
+                ks = kernel_stats(ctx, sw, names, leg)
+                six["kernel_us"] = {k: round(ks[k][0] / 1e3, 3) for k in names}
+            del sw
+        fused = configs.get("C1", {}).get("gpu", {}).get("us_per_layer")
+        extra["C1_six_ops"] = dict(
+            norm_rope_append_us_per_layer=six["prep"], attention_us_per_layer=six["attn"],
+            six_ops_us_per_layer=six["all"], fused_step_us_per_layer=fused, six_ops_kernel_us=six["kernel_us"],
+            note="(i) rmsNorm q, rmsNorm k, rope q, rope k, kvAppend (five launches); (ii) gqaAttention "
+                 "(split + merge); (iii) the fused step (norm/rope/append inside the split kernel)")
+        log(f"[bench] C1 six ops: norm/rope/append {six['prep']:.3f}, attention {six['attn']:.3f}, all six "
+            f"{six['all']:.3f} us/layer; fused step {fused}; kernels {six['kernel_us']}")
+
+    if "FLOOR" in only:
+        fl = {}
+        for mode in ("empty", "read", "both"):
+            fw = FloorSweep(H, ctx, mode=mode)
+            el, _ = time_graph(ctx, fw, max(5, args.steps), 2)
+            fl[mode] = round(el / (fw.layers * max(5, args.steps)) * 1e6, 3)
+            del fw
+        extra["floors"] = dict(
+            empty_launch_us=fl["empty"], read_16MiB_us=fl["read"], read_plus_empty_us=fl["both"],
+            read_16MiB_gbs=round((16 << 20) / (fl["read"] * 1e3), 1),
+            note="per layer in a 48-layer graph: one dependent launch of an empty kernel; one launch reading a "
+                 "distinct 16 MiB buffer once (C1's K+V per layer) with the decode's 16-byte non-temporal loads; "
+                 "both (the split + merge launch count)")
+        log(f"[bench] floors: empty launch {fl['empty']:.3f} us, 16 MiB read {fl['read']:.3f} us, "
+            f"read + empty {fl['both']:.3f} us per layer")
+
+    if 0 in W and "C0" in only:
+        w = W[0]
+        el1, _ = time_graph(ctx, w, 2, 1)
+        reps = replays_for(el1 / 2, leg, 20)
+        r, _, _, _ = decode_leg(0, reps, 5)
+        configs["C0"] = dict(workload="decode, 1 layer, 32q/4kv, d128, 31 cached + 1 appended, f16 cache, fused step",
+                             gpu=r, note="launch-bound: us per step (100 dependent steps per graph replay) is the "
+                                         "figure; GB/s is not meaningful at 103 KB per step")
+        log(f"[bench] C0 {r['us_per_layer']:.3f} us/step (graph of 100 steps, {reps} replays)")
+        parity_decode(0)
+
+    if 2 in W and "C2" in only:
+        p = W[2]
+        el1, _ = time_graph(ctx, p, 5, 2)
+        reps = replays_for(el1 / 5, leg, 10)
+        elapsed, _ = time_graph(ctx, p, reps, 2)
+        e2e_us = elapsed / reps * 1e6
+        ks = kernel_stats(ctx, p, ("prefill_prep_kernel", "prefill_attention_kernel"), leg)
+        ns_pf = ks["prefill_attention_kernel"][0]
         tf = p.flops / ns_pf / 1e3
-        extra["C2_prefill"] = dict(kernel="prefill_attention_kernel", kernel_us=round(ns_pf / 1e3, 3), tflops=round(tf, 2),
-                                   frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(e2e_us, 3),
-                                   flops=p.flops, peak_tflops=F16_MFMA_PEAK_TFLOPS)
-        log(f"[bench] C2 prefill_attention_kernel {ns_pf / 1e3:.2f} us -> {tf:.1f} TFLOP/s; end-to-end {e2e_us:.2f} us")
-        del p
+        sep = Prefill(H, synth, ctx, fused=False)
+        el_sep, _ = time_graph(ctx, sep, max(10, reps // 4), 2)
+        r = dict(end_to_end_us=round(e2e_us, 3), kernel_us=dict(prefill_prep_kernel=round(ks["prefill_prep_kernel"][0] / 1e3, 3),
+                                                               prefill_attention_kernel=round(ns_pf / 1e3, 3)),
+                 tflops=round(tf, 2), frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+                 tflops_end_to_end=round(p.flops / (e2e_us * 1e3) / 1e3, 2), flops=p.flops,
+                 peak_tflops=F16_MFMA_PEAK_TFLOPS, six_ops_end_to_end_us=round(el_sep / max(10, reps // 4) * 1e6, 3))
+        ru = rocprof_kernel_us("C2", "prefill_attention_kernel")
+        if ru:
+            r["rocprof_kernel_us"] = ru
+            r["rocprof_frac"] = round(p.flops / (ru * 1e3) / 1e3 / F16_MFMA_PEAK_TFLOPS, 4)
+        configs["C2"] = dict(workload="causal prefill 2048 tokens, 32q/4kv, d128, empty f16 cache, fused step",
+                             gpu=r)
+        extra["C2_prefill"] = dict(kernel="prefill_attention_kernel", kernel_us=round(ns_pf / 1e3, 3),
+                                   tflops=r["tflops"], frac=r["frac"], end_to_end_us=r["end_to_end_us"])
+        log(f"[bench] C2 prefill_attention_kernel {ns_pf / 1e3:.2f} us -> {tf:.1f} TFLOP/s; end-to-end {e2e_us:.2f} us; "
+            f"six ops {r['six_ops_end_to_end_us']:.2f} us")
+        del sep
+        parity_c2()
 
-    if "C3" in only:
-        log("[bench] C3: building 47 layers (32768-token f16 caches, 64q/4kv)")
-        w = DecodeSweep(H, synth, ctx, 3)
-        steps3 = max(5, args.steps // 4)
-        elapsed, _ = time_graph(ctx, w, steps3, 2)
-        us = elapsed / (w.layers * steps3) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "decode_split_kernel", 2)
-        extra["C3_decode"] = dict(us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
-                                  kernel_us=round(ns_k / 1e3, 3),
-                                  kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),
-                                  bytes_per_layer=w.bytes_per_layer)
-        log(f"[bench] C3 {us:.3f} us/layer; kernel {ns_k / 1e3:.3f} us")
-        del w
+    if 3 in W and "C3" in only:
+        w = W[3]
+        el1, _ = time_graph(ctx, w, 2, 1)
+        r, _, _, _ = decode_leg(3, replays_for(el1 / 2, leg, max(5, args.steps // 4)), 2)
+        configs["C3"] = dict(workload="decode, 47 layers, 64q/4kv, d128, L 32768, theta 5e6, f16 cache, fused step",
+                             gpu=r)
+        extra["C3_decode"] = dict(us_per_layer=r["us_per_layer"], gbs=r["gbs"],
+                                  kernel_us=r["kernel_us"]["decode_split_kernel"], kernel_frac=r["kernel_frac"])
+        log(f"[bench] C3 {r['us_per_layer']:.3f} us/layer; kernel {r['kernel_us']}")
+        parity_decode(3)
 
-    if "C4" in only:
-        log("[bench] C4: building 48 layers of paged pools (32 sequences)")
-        w = PagedSweep(H, synth, ctx)
-        steps4 = max(3, args.steps // 10)
-        elapsed, _ = time_graph(ctx, w, steps4, 1)
-        us = elapsed / (w.layers * steps4) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "decode_split_kernel", 1)
-        extra["C4_paged_decode"] = dict(us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2),
-                                        kernel_us=round(ns_k / 1e3, 3),
-                                        kernel_frac=round(w.bytes_per_layer / ns_k / HBM_PEAK_GBS, 4),
-                                        bytes_per_layer=w.bytes_per_layer,
-                                        total_tokens=int(w.lay.seq_lens.sum()))
-        log(f"[bench] C4 {us:.3f} us/layer; kernel {ns_k / 1e3:.3f} us")
-        del w
+    if 4 in W and "C4" in only:
+        w = W[4]
+        el1, _ = time_graph(ctx, w, 1, 1)
+        r, _, _, _ = decode_leg(4, replays_for(el1, leg, max(3, args.steps // 10)), 1)
+        r["total_tokens"] = int(w.lay.seq_lens.sum())
+        configs["C4"] = dict(workload="paged decode, 32 sequences L ~ U[512, 16384], 16-token pages, 48 layers",
+                             gpu=r)
+        extra["C4_paged_decode"] = dict(us_per_layer=r["us_per_layer"], gbs=r["gbs"],
+                                        kernel_us=r["kernel_us"]["decode_split_kernel"], kernel_frac=r["kernel_frac"])
+        log(f"[bench] C4 {r['us_per_layer']:.3f} us/layer; kernel {r['kernel_us']}")
+        parity_c4()
 
     if "QKV" in only:
         log("[bench] QKV: decode q/k/v projections, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048], 48 layers")
@@ -462,7 +865,7 @@ def main():
         w = ProjSweep(H, ctx)
         elapsed, _ = time_graph(ctx, w, stepsq, 2)
         us = elapsed / (w.layers * stepsq) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "matmul_rows_kernel", 2)
+        ns_k = kernel_stats(ctx, w, ("matmul_rows_kernel",), leg)["matmul_rows_kernel"][0]
         del w
         w = ProjSweep(H, ctx, grouped=False)
         elapsed, _ = time_graph(ctx, w, stepsq, 2)
@@ -482,7 +885,7 @@ def main():
         w = WoSweep(H, ctx)
         elapsed, _ = time_graph(ctx, w, stepsw, 2)
         us = elapsed / (w.layers * stepsw) * 1e6
-        ns_k, _ = kernel_mean_ns(ctx, w, "matmul_rows_kernel", 2)
+        ns_k = kernel_stats(ctx, w, ("matmul_rows_kernel",), leg)["matmul_rows_kernel"][0]
         bpl = w.bytes_per_layer
         del w
         w = WoSweep(H, ctx, fused=False)
@@ -504,8 +907,9 @@ def main():
         stepsm = max(5, args.steps // 4)
         elapsed, _ = time_graph(ctx, w, stepsm, 2)
         us = elapsed / (w.layers * stepsm) * 1e6
-        per = {kn: kernel_mean_ns(ctx, w, kn, 2)[0] / 1e3 for kn in
-               ("router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel")}
+        names = ("router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel")
+        ks = kernel_stats(ctx, w, names, leg)
+        per = {k: ks[k][0] / 1e3 for k in names}
         extra["moe_block_decode"] = dict(
             us_per_layer=round(us, 3), gbs=round(w.bytes_per_layer / (us * 1e3), 2), bytes_per_layer=w.bytes_per_layer,
             kernel_us={k: round(v, 3) for k, v in per.items()},
@@ -520,8 +924,8 @@ def main():
         p = ProjPrefill(H, ctx)
         n_rep = max(5, args.steps // 5)
         elapsed, _ = time_graph(ctx, p, n_rep, 2)
-        ns_k, _ = kernel_mean_ns(ctx, p, "matmul_q8_mfma_kernel", 5)
-        ns_split, _ = kernel_mean_ns(ctx, p, "matmul_x_split_kernel", 5)
+        ks = kernel_stats(ctx, p, ("matmul_q8_mfma_kernel", "matmul_x_split_kernel"), leg)
+        ns_k, ns_split = ks["matmul_q8_mfma_kernel"][0], ks["matmul_x_split_kernel"][0]
         tf = p.flops / ns_k / 1e3
         extra["qkv_projection_prefill"] = dict(
             kernel="matmul_q8_mfma_kernel", kernel_us=round(ns_k / 1e3, 3), tflops=round(tf, 2),
@@ -533,19 +937,27 @@ def main():
         log(f"[bench] QKVP matmul_q8_mfma_kernel {ns_k / 1e3:.2f} us -> {tf:.1f} TFLOP/s (useful)")
         del p
 
+    for c, r in cpu.items():
+        if f"C{c}" in configs:
+            configs[f"C{c}"]["cpu"] = r
+            g = configs[f"C{c}"]["gpu"]
+            gus = g.get("us_per_layer", g.get("end_to_end_us"))
+            if gus:
+                r["gpu_speedup"] = round(r["us_per_layer"] / gus, 1)
+    for name, cfg in configs.items():
+        if "parity" in cfg:
+            log(f"[bench] parity {name}: {cfg['parity']}")
+
     if result is None:
-        result = dict(metric="partial run", value=None, extra=extra)
-    else:
-        result["extra"] = extra
-        if not args.no_cpu:
-            log(f"[bench] CPU baseline: oracle on C1 layers for ~{args.cpu_seconds:.0f} s (1 core)")
-            cb = cpu_baseline_c1(synth, args.cpu_seconds)
-            bpl = decode_bytes(32, 4, 128, 8192)
-            result["cpu_baseline"] = dict(
-                value=round(bpl / (cb["us_per_layer"] * 1e3), 4), unit="GB/s", cores=1, kind="port",
-                us_per_layer=round(cb["us_per_layer"], 1), host_nproc=os.cpu_count(),
-                sample=f"{cb['layers']} C1 decode layer-steps (3 distinct seeded layers, 8192-token f16 cache) "
-                       f"through oracle/ds5_oracle.c ds5o_attention_step, {cb['seconds']:.1f} s")
+        result = dict(metric="partial run", value=None)
+    result["configs"] = configs
+    result["extra"] = extra
+    if 1 in cpu:
+        bpl = decode_bytes(32, 4, 128, 8192)
+        c1 = cpu[1]
+        result["cpu_baseline"] = dict(value=round(bpl / (c1["us_per_layer"] * 1e3), 4), unit="GB/s", cores=1,
+                                      kind="port", us_per_layer=c1["us_per_layer"], host_nproc=os.cpu_count(),
+                                      sample="C1: " + c1["sample"])
     ctx.deinit()
     print(json.dumps(result), flush=True)
 

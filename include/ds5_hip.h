@@ -472,6 +472,16 @@ int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t 
  * traffic counters (FETCH_SIZE / WRITE_SIZE) it reports. */
 int ds5_hip_copy_device(ds5_hip_ctx* ctx, ds5_buf dst, ds5_buf src, uint64_t len);
 
+/* Floor measurements for the benchmark: one launch that reads `len` bytes of
+ * buf once (len % 16 == 0, 16-byte aligned view) with the decode kernel's
+ * contiguous access -- 16-byte non-temporal loads, 64 KiB per 256-thread
+ * workgroup -- and computes nothing (sink: 4 bytes, written only for one bit
+ * pattern of the data); and one launch of an empty kernel over n_workgroups
+ * workgroups. Captured per layer into a graph they give the cost of one
+ * dependent launch and of one bare read of a layer's K/V. */
+int ds5_hip_stream_read(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t len, ds5_buf sink);
+int ds5_hip_empty_launch(ds5_hip_ctx* ctx, uint32_t n_workgroups);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 // Device side: vector types, MFMA wrappers, wavefront reductions.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -74,9 +75,9 @@ struct ds5_hip_ctx {
     std::map<std::string, std::pair<double, uint64_t>> kernel_ns;  // name -> (total ns, launches)
 };
 
-// Brackets one kernel launch with timing events when timing is enabled.
-int ds5_timer_start(ds5_hip_ctx* ctx, hipEvent_t* ev);
-void ds5_timer_stop(ds5_hip_ctx* ctx, const char* name, hipEvent_t start);
+// Per-kernel timing: a pooled event pair per launch, resolved at submit / query time.
+hipEvent_t ds5_next_event(ds5_hip_ctx* ctx);
+void ds5_timer_record(ds5_hip_ctx* ctx, const char* name, hipEvent_t start, hipEvent_t end);
 int ds5_timers_resolve(ds5_hip_ctx* ctx);
 
 int ds5_fail(ds5_hip_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
@@ -88,13 +89,24 @@ int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out);
 int ds5_scratch_init(ds5_hip_ctx* ctx);
 void ds5_rope_table(float theta, uint32_t head_dim, RopeTable* t);
 
-#define DS5_TIMED_LAUNCH(ctx, name, ...)        \
-    do {                                        \
-        hipEvent_t ds5_t0_ = nullptr;           \
-        ds5_timer_start((ctx), &ds5_t0_);       \
-        hipLaunchKernelGGL(__VA_ARGS__);        \
-        ds5_timer_stop((ctx), (name), ds5_t0_); \
-    } while (0)
+// Launches a kernel on `stream`. With timing enabled the launch carries its own
+// start/stop events (hipExtLaunchKernelGGL: the events belong to the dispatch
+// itself, so they time the kernel's execution, as a profiler's kernel trace
+// does, not the dispatch latency around it).
+template <typename K, typename... Args>
+inline void ds5_launch(ds5_hip_ctx* ctx, const char* name, K kernel, dim3 grid, dim3 block, uint32_t shmem,
+                       hipStream_t stream, Args... args) {
+    if (ctx->kernel_timing) {
+        hipEvent_t start = ds5_next_event(ctx), stop = ds5_next_event(ctx);
+        if (start && stop) {
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, start, stop, 0u, args...);
+            ds5_timer_record(ctx, name, start, stop);
+            return;
+        }
+    }
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+}
+#define DS5_TIMED_LAUNCH(ctx, name, ...) ds5_launch((ctx), (name), __VA_ARGS__)
 
 static inline void* ds5_ptr(ds5_buf b) { return (char*)b.handle + b.offset; }
 
@@ -274,6 +286,8 @@ struct PrefillLaunch {
 int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a);
 
 int launch_fill_normal_f16(ds5_hip_ctx* ctx, f16* out, uint64_t n, uint64_t seed);
+int launch_stream_read(ds5_hip_ctx* ctx, const void* src, uint64_t len, uint32_t* sink);
+int launch_empty(ds5_hip_ctx* ctx, uint32_t n_workgroups);
 
 // ---------------------------------------------------------------------------
 // Device helpers

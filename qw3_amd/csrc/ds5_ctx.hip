@@ -71,7 +71,7 @@ int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
     return DS5_OK;
 }
 
-static hipEvent_t next_event(ds5_hip_ctx* ctx) {
+hipEvent_t ds5_next_event(ds5_hip_ctx* ctx) {
     if (ctx->event_next == ctx->event_pool.size()) {
         hipEvent_t e = nullptr;
         if (hipEventCreate(&e) != hipSuccess) return nullptr;
@@ -80,19 +80,7 @@ static hipEvent_t next_event(ds5_hip_ctx* ctx) {
     return ctx->event_pool[ctx->event_next++];
 }
 
-int ds5_timer_start(ds5_hip_ctx* ctx, hipEvent_t* ev) {
-    *ev = nullptr;
-    if (!ctx->kernel_timing) return DS5_OK;
-    *ev = next_event(ctx);
-    if (*ev) (void)hipEventRecord(*ev, ctx->stream);
-    return DS5_OK;
-}
-
-void ds5_timer_stop(ds5_hip_ctx* ctx, const char* name, hipEvent_t start) {
-    if (!ctx->kernel_timing || !start) return;
-    hipEvent_t end = next_event(ctx);
-    if (!end) return;
-    (void)hipEventRecord(end, ctx->stream);
+void ds5_timer_record(ds5_hip_ctx* ctx, const char* name, hipEvent_t start, hipEvent_t end) {
     ctx->pending.push_back({name, start, end});
 }
 

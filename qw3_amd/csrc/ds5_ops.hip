@@ -769,6 +769,21 @@ int ds5_hip_copy_device(ds5_hip_ctx* ctx, ds5_buf dst, ds5_buf src, uint64_t len
                           "copy_device");
 }
 
+int ds5_hip_stream_read(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t len, ds5_buf sink) {
+    if (len % 16 != 0 || !covers(buf, len) || !aligned16(buf))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "stream_read: len must be a multiple of 16 in a 16-byte aligned view");
+    if (!covers(sink, 4) || ((uintptr_t)ds5_ptr(sink) & 3u))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "stream_read: sink must be a 4-byte aligned view of 4 bytes");
+    if (int rc = set_device(ctx)) return rc;
+    return launch_stream_read(ctx, ds5_ptr(buf), len, (uint32_t*)ds5_ptr(sink));
+}
+
+int ds5_hip_empty_launch(ds5_hip_ctx* ctx, uint32_t n_workgroups) {
+    if (n_workgroups == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "empty_launch: no workgroups");
+    if (int rc = set_device(ctx)) return rc;
+    return launch_empty(ctx, n_workgroups);
+}
+
 int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t seed) {
     if (!covers(buf, n * 2)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "fill_normal_f16: buffer too small");
     if (int rc = set_device(ctx)) return rc;

@@ -18,11 +18,64 @@
 
 namespace {
 
-constexpr int kRowsPerBlock = 64;  // one wavefront, one row per lane
+constexpr int kRowsPerBlock = 64;  // large-dim kernel: one wavefront, one row per lane
 constexpr int kColTile = 64;
+constexpr int kNormThreads = 256;
+constexpr int kNormTile = 4096;    // floats of a block's rows staged in LDS (rows of up to 4096 elements)
 
-// Serial sum of squares of 64 rows, one row per lane, in element order.
-// The tile is staged transposed through LDS so global reads stay coalesced.
+// Rows of at most kNormTile elements: R = kNormTile / dim rows per block (at
+// most 64). The block loads its R rows (contiguous in memory) with every load
+// in flight into LDS at a row stride of dim + 1 floats; thread r then adds row
+// r's squares in element order -- the reference's serial sum, each square
+// rounded on its own -- reading one LDS word per step (the stride puts the R
+// rows' words in distinct banks); then the block writes (v * inv) * w.
+__global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float* x, const float* __restrict__ w,
+                                                                     float* out, uint32_t n_rows, uint32_t dim,
+                                                                     uint32_t rows_per_block, float eps) {
+    __shared__ float s_x[kNormTile + 64];
+    __shared__ float s_inv[64];
+    const uint32_t row0 = blockIdx.x * rows_per_block;
+    const uint32_t nr = min(rows_per_block, n_rows - row0);
+    const uint32_t n = nr * dim;
+    const uint32_t stride = dim + 1;
+    const float* src = x + (uint64_t)row0 * dim;
+    constexpr int kPer = kNormTile / kNormThreads;  // elements per thread
+    float v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+        const uint32_t i = threadIdx.x + k * kNormThreads;
+        v[k] = src[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+        const uint32_t i = threadIdx.x + k * kNormThreads;
+        if (i < n) s_x[(i / dim) * stride + i % dim] = v[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < nr) {
+        const float* row = s_x + threadIdx.x * stride;
+        float sumsq = 0.0f;
+        for (uint32_t j = 0; j < dim; j++) {
+            const float e = row[j];
+            sumsq += e * e;
+        }
+        s_inv[threadIdx.x] = rms_inv(sumsq, (float)dim, eps);
+    }
+    __syncthreads();
+    // out may alias x: every element of the block's rows was read above.
+    float* dst = out + (uint64_t)row0 * dim;
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+        const uint32_t i = threadIdx.x + k * kNormThreads;
+        if (i < n) {
+            const uint32_t r = i / dim, c = i % dim;
+            dst[i] = v[k] * s_inv[r] * w[c];
+        }
+    }
+}
+
+// Rows longer than kNormTile: one row per lane, the row's columns staged in
+// tiles transposed through LDS so global reads stay coalesced.
 __device__ void rows_sumsq(const float* __restrict__ x, uint32_t row0, uint32_t n_rows, uint32_t dim,
                            float (*tile)[kColTile + 1], float* sumsq_out) {
     const int lane = threadIdx.x;
@@ -68,25 +121,35 @@ __global__ __launch_bounds__(kRowsPerBlock) void rms_norm_kernel(const float* x,
     }
 }
 
-__global__ __launch_bounds__(256) void rope_kernel(float* x, const int32_t* __restrict__ positions,
-                                                   uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim,
-                                                   float freq_scale, RopeTable table) {
+// One block per token group: the token's cos/sin (one per pair index, shared by
+// all heads) go to LDS first, then every head's pairs rotate.
+constexpr int kRopeThreads = 256;
+constexpr int kRopeHalfMax = DS5_MAX_ROPE_HALF;
+
+__global__ __launch_bounds__(kRopeThreads) void rope_kernel(float* x, const int32_t* __restrict__ positions,
+                                                            uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim,
+                                                            float freq_scale, RopeTable table) {
+    __shared__ float s_cos[kRopeHalfMax], s_sin[kRopeHalfMax];
     const uint32_t half = head_dim / 2;
-    const uint64_t total = (uint64_t)n_tokens * n_heads * half;
-    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t i = idx % half;
-        const uint64_t th = idx / half;  // t * n_heads + h
-        const uint32_t t = th / n_heads;
+    for (uint32_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
         const float pos = (float)positions[t];
-        const float angle = pos * freq_scale * table.inv[i];
-        const float c = cosf(angle);
-        const float s = sinf(angle);
-        float* head = x + th * head_dim;
-        const float x0 = head[i];
-        const float x1 = head[i + half];
-        head[i] = x0 * c - x1 * s;
-        head[i + half] = x0 * s + x1 * c;
+        for (uint32_t i = threadIdx.x; i < half; i += kRopeThreads) {
+            const float angle = pos * freq_scale * table.inv[i];
+            s_cos[i] = cosf(angle);
+            s_sin[i] = sinf(angle);
+        }
+        __syncthreads();
+        float* tok = x + (uint64_t)t * n_heads * head_dim;
+        for (uint32_t j = threadIdx.x; j < n_heads * half; j += kRopeThreads) {
+            const uint32_t h = j / half, i = j % half;
+            float* head = tok + (uint64_t)h * head_dim;
+            const float c = s_cos[i], s = s_sin[i];
+            const float x0 = head[i];
+            const float x1 = head[i + half];
+            head[i] = x0 * c - x1 * s;
+            head[i + half] = x0 * s + x1 * c;
+        }
+        __syncthreads();
     }
 }
 
@@ -128,6 +191,13 @@ inline uint32_t grid_for(uint64_t total, uint32_t block) {
 
 int launch_rms_norm(ds5_hip_ctx* ctx, const RmsNormLaunch& a) {
     if (a.n_rows == 0) return DS5_OK;
+    if (a.dim <= kNormTile) {
+        const uint32_t rpb = std::min<uint32_t>(64, kNormTile / a.dim);
+        const uint32_t blocks = (a.n_rows + rpb - 1) / rpb;
+        DS5_TIMED_LAUNCH(ctx, "rms_norm_rows_kernel", rms_norm_rows_kernel, dim3(blocks), dim3(kNormThreads), 0,
+                         ctx->stream, a.x, a.w, a.out, a.n_rows, a.dim, rpb, a.eps);
+        return ds5_after_launch(ctx, "rms_norm_rows_kernel");
+    }
     const uint32_t blocks = (a.n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
     DS5_TIMED_LAUNCH(ctx, "rms_norm_kernel", rms_norm_kernel, dim3(blocks), dim3(kRowsPerBlock), 0, ctx->stream, a.x, a.w, a.out,
                        a.n_rows, a.dim, a.eps);
@@ -137,8 +207,9 @@ int launch_rms_norm(ds5_hip_ctx* ctx, const RmsNormLaunch& a) {
 int launch_rope(ds5_hip_ctx* ctx, const RopeLaunch& a) {
     const uint64_t total = (uint64_t)a.n_tokens * a.n_heads * (a.head_dim / 2);
     if (total == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "rope_kernel", rope_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, a.x, a.positions,
-                       a.n_tokens, a.n_heads, a.head_dim, a.freq_scale, *a.table);
+    const uint32_t blocks = std::min<uint32_t>(a.n_tokens, 65535u * 16u);
+    DS5_TIMED_LAUNCH(ctx, "rope_kernel", rope_kernel, dim3(blocks), dim3(kRopeThreads), 0, ctx->stream, a.x, a.positions,
+                     a.n_tokens, a.n_heads, a.head_dim, a.freq_scale, *a.table);
     return ds5_after_launch(ctx, "rope_kernel");
 }
 

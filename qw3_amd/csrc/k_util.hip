@@ -1,4 +1,6 @@
-// k_util.hip -- device-side synthetic data for benchmarks: N(0,1) f16 values
+// k_util.hip -- benchmark utilities.
+//
+// Device-side synthetic data: N(0,1) f16 values
 // from a counter-based generator, so multi-GB KV caches need no host
 // generation or PCIe transfer. Value i depends only on (seed, i):
 //   u64 z = splitmix64(seed * 0x9E3779B97F4A7C15 + (i >> 1));
@@ -30,7 +32,44 @@ __global__ __launch_bounds__(256) void fill_normal_f16_kernel(f16* out, uint64_t
     }
 }
 
+// Floor measurements (no reference counterpart): one launch that reads a view
+// once -- the decode kernel's contiguous K/V access, 16-byte non-temporal loads,
+// 64 KiB per 256-thread workgroup, all loads of a thread in flight together --
+// and an empty launch. The sink store depends on every loaded word, so the
+// loads stay; it only happens for one bit pattern.
+constexpr int kReadLoads = 16;
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* src, uint64_t n16, uint32_t* sink) {
+    const uint64_t base = (uint64_t)blockIdx.x * (256 * kReadLoads) + threadIdx.x;
+    u32x4 v[kReadLoads];
+#pragma unroll
+    for (int i = 0; i < kReadLoads; i++) {
+        const uint64_t j = base + (uint64_t)i * 256;
+        v[i] = __builtin_nontemporal_load(src + (j < n16 ? j : n16 - 1));
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < kReadLoads; i++) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+__global__ void empty_kernel() {}
+
 }  // namespace
+
+int launch_stream_read(ds5_hip_ctx* ctx, const void* src, uint64_t len, uint32_t* sink) {
+    const uint64_t n16 = len / 16;
+    if (n16 == 0) return DS5_OK;
+    const uint64_t blocks = (n16 + 256 * kReadLoads - 1) / (256 * kReadLoads);
+    DS5_TIMED_LAUNCH(ctx, "stream_read_kernel", stream_read_kernel, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream,
+                     (const u32x4*)src, n16, sink);
+    return ds5_after_launch(ctx, "stream_read_kernel");
+}
+
+int launch_empty(ds5_hip_ctx* ctx, uint32_t n_workgroups) {
+    DS5_TIMED_LAUNCH(ctx, "empty_kernel", empty_kernel, dim3(n_workgroups), dim3(256), 0, ctx->stream);
+    return ds5_after_launch(ctx, "empty_kernel");
+}
 
 int launch_fill_normal_f16(ds5_hip_ctx* ctx, f16* out, uint64_t n, uint64_t seed) {
     if (n == 0) return DS5_OK;

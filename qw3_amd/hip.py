@@ -207,6 +207,8 @@ SIGNATURES = {
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
     "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
     "ds5_hip_copy_device": ([_P, Buf, Buf, C.c_uint64], C.c_int),
+    "ds5_hip_stream_read": ([_P, Buf, C.c_uint64, Buf], C.c_int),
+    "ds5_hip_empty_launch": ([_P, C.c_uint32], C.c_int),
 }
 
 
@@ -339,6 +341,13 @@ class Ctx:
 
     def copy_device(self, dst: Buf, src: Buf, length: int) -> None:
         self.check(LIB.ds5_hip_copy_device(self._h, dst, src, length))
+
+    def stream_read(self, buf: Buf, length: int, sink: Buf) -> None:
+        """One launch reading `length` bytes of buf once (the decode's contiguous K/V access, nothing computed)."""
+        self.check(LIB.ds5_hip_stream_read(self._h, buf, length, sink))
+
+    def empty_launch(self, n_workgroups: int = 256) -> None:
+        self.check(LIB.ds5_hip_empty_launch(self._h, n_workgroups))
 
 
 class Graph:
