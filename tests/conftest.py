@@ -53,3 +53,17 @@ def f16_ulp_diff(a_bits, b_bits) -> np.ndarray:
         x = np.asarray(x, np.uint16).astype(np.int32)
         return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + x)
     return np.abs(mono(a_bits) - mono(b_bits))
+
+
+def attention_f64(q, kc_bits, vc_bits, scale):
+    """Causal softmax(q k^T * scale) v in float64 for one head: q [T, d] f32, caches
+    [T, d] f16 bits (the token at row t attends rows 0..t)."""
+    qd = np.asarray(q, np.float64)
+    kd = np.asarray(kc_bits, np.uint16).view(np.float16).astype(np.float64)
+    vd = np.asarray(vc_bits, np.uint16).view(np.float16).astype(np.float64)
+    s = (qd @ kd.T) * float(np.float32(scale))
+    T = s.shape[0]
+    s[np.triu_indices(T, 1)] = -np.inf
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    return (p @ vd) / p.sum(axis=1, keepdims=True)

@@ -698,3 +698,21 @@ def test_expert_mlp_rejections(oracle):
     assert call(da=bank[:31]) == oracle.SHAPE_MISMATCH
     assert call(pairs=np.array([(0, 1, 1.0)], oracle.PAIR_DTYPE)) == oracle.SHAPE_MISMATCH
     assert call(pairs=np.array([(1, 0, 1.0)], oracle.PAIR_DTYPE)) == oracle.SHAPE_MISMATCH
+
+
+def test_attention_f64_checker_matches_oracle(oracle):
+    """The float64 causal attention the full-size GPU prefill test checks every head
+    against agrees with the oracle's f16-cache attention (and fails on a shifted mask)."""
+    from conftest import attention_f64
+    g = np.random.default_rng(3)
+    T, d = 96, 128
+    q = g.standard_normal((T, 1, d)).astype(np.float32)
+    kc = oracle.f32_to_f16_bits(g.standard_normal((1, T, d)).astype(np.float32))
+    vc = oracle.f32_to_f16_bits(g.standard_normal((1, T, d)).astype(np.float32))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    want = oracle.gqa_attention(q, kc, vc, 1, 0, T, 1, 1, d, T, scale).reshape(T, d)
+    got = attention_f64(q[:, 0], kc[0], vc[0], scale)
+    assert np.max(np.abs(got - want)) < 1e-5
+    # a mask one position too wide must not pass
+    bad = attention_f64(q[1:, 0], kc[0, 1:], vc[0, 1:], scale)
+    assert np.max(np.abs(bad - want[1:])) > 1e-3
