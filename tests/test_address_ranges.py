@@ -1,0 +1,361 @@
+"""Host replicas of the device kernels' load/store address arithmetic (no GPU).
+
+Each replica restates, per lane, the byte offsets a kernel reads or writes --
+with the same clamps, wrap-free unsigned arithmetic and launch geometry as the
+kernel source it cites -- and the tests assert that every access of every
+workgroup stays inside its view at the BASELINE shapes (C0-C4) and at the
+Q8_0 shapes whose blocks start 2 bytes off a dword. A GPU memory fault once came
+from exactly such arithmetic (an offset that went negative and wrapped as an
+unsigned 32-bit value); a replica catches that class of mistake on the CPU.
+
+Replicated:
+  qw3_amd/csrc/k_decode.hip  decode_geometry_of, issue_tile, the q-operand and
+                             new-row accesses and the partial stores of
+                             decode_split_kernel (contiguous and paged caches)
+  qw3_amd/csrc/k_matmul.hip  load_block of matmul_q8_mfma_kernel (x planes, Q8_0
+                             runs and scales) and matmul_path's slack rule
+  qw3_amd/csrc/k_prefill.hip DmaPlan / dma_tile of prefill_attention_kernel (every
+                             direct-to-LDS load of every round) and its q-operand
+                             loads
+"""
+import numpy as np
+import pytest
+
+from qw3_amd import synth
+
+U32 = 1 << 32
+
+
+# ---------------------------------------------------------------------------
+# decode_split_kernel (k_decode.hip)
+# ---------------------------------------------------------------------------
+
+K_TILE, K_WAVES, K_HEADS = 32, 4, 16
+
+
+def decode_geometry(n_seqs, n_kv_heads, n_sub, max_len, cu_count=256, decode_chunk=0):
+    """decode_geometry_of: (chunk, n_splits)."""
+    step = K_WAVES * K_TILE
+    chunk = decode_chunk
+    if chunk == 0:
+        units = n_seqs * n_kv_heads * n_sub
+        target = 4 * cu_count
+        chunk = min((max_len * units + target - 1) // target, max_len)
+    chunk = max((chunk + step - 1) // step * step, step)
+    chunk = max(chunk, (max_len + 63) // 64)
+    chunk = (chunk + step - 1) // step * step
+    return chunk, (max_len + chunk - 1) // chunk
+
+
+def tile_rows(p0, end, D, paged, page_row=None):
+    """issue_tile: the cache rows (positions, or pool slots when paged) of the K and V
+    loads of the tile starting at p0, and each load's element offset inside its row:
+    K: lane (g, c16), half st, step kk -> row (p0 + 16 st + c16 clamped), dims kk*32 + 8g;
+    V: chunk c = lane + 64 r -> row p0 + c / RC (clamped), dims (c % RC) * 8."""
+    KK, RC = D // 32, D // 8
+    VC = K_TILE * RC // 64
+    lane = np.arange(64)
+    g, c16 = lane >> 4, lane & 15
+    krow, kcol, vrow, vcol = [], [], [], []
+    for st in range(2):
+        for kk in range(KK):
+            if paged:
+                krow.append(page_row(p0, st) + c16)
+            else:
+                krow.append(np.minimum(p0 + 16 * st + c16, end - 1))
+            kcol.append(kk * 32 + 8 * g)
+    for r in range(VC):
+        c = lane + 64 * r
+        tr = c // RC
+        if paged:
+            vrow.append(page_row(p0, 0 if r < VC // 2 else 1) + (tr & 15))
+        else:
+            vrow.append(np.minimum(p0 + tr, end - 1))
+        vcol.append((c % RC) * 8)
+    return (np.concatenate(krow), np.concatenate(kcol), np.concatenate(vrow), np.concatenate(vcol))
+
+
+def check_decode(n_seqs, hq, hkv, D, lens, cache_stride, page_size=0, page_table=None, n_pages=0, max_len=None,
+                 fused=True):
+    """Every access of one decode launch. lens: attended positions per sequence (the
+    contiguous cache passes one length). Returns the number of checked 16-byte loads."""
+    group = hq // hkv
+    n_sub = (group + K_HEADS - 1) // K_HEADS
+    max_len = max_len if max_len is not None else int(max(lens))
+    chunk, n_splits = decode_geometry(n_seqs, hkv, n_sub, max_len)
+    paged = page_table is not None
+    cache_elems = hkv * cache_stride * D            # per K (and V) cache, f16 elements
+    q_elems = n_seqs * hq * D
+    part_elems = n_seqs * hq * n_splits * D if n_splits > 1 else 0
+    TPH = D // 8
+    checked = 0
+    for b in range(n_seqs):
+        L = int(lens[b]) if len(lens) > 1 else int(lens[0])
+        if paged and not (1 <= L <= max_len):
+            continue  # poisoned sequence: only its output is written
+        for kv in range(hkv):
+            for sub in range(n_sub):
+                n0 = sub * K_HEADS
+                NS = min(K_HEADS, group - n0)
+                qrow0 = b * hq + kv * group + n0
+                # q-operand loads: thread t reads 4 floats at (qrow0 + min(t / TPH, NS - 1)) * D + 4 (t % TPH) (+ D/2)
+                t = np.arange(256)
+                qoff = (qrow0 + np.minimum(t // TPH, NS - 1)) * D + 4 * (t % TPH)
+                assert qoff.min() >= 0 and (qoff + D // 2 + 4).max() <= q_elems
+                for split in range(n_splits):
+                    start = split * chunk
+                    if start >= L:
+                        continue
+                    end = min(L, start + chunk)
+                    n_tiles = (end - start + K_TILE - 1) // K_TILE
+                    newpos = L - 1
+
+                    def page_row(p0, st):
+                        pos = p0 if st == 0 else min(p0 + 16, end - 1)
+                        idx = b * page_table.shape[1] + pos // page_size
+                        assert 0 <= idx < page_table.size  # the page-table read itself
+                        pg = int(page_table.reshape(-1)[idx])
+                        base = (pg if 0 <= pg < n_pages else 0) * page_size
+                        return base + (p0 + 16 * st) % page_size
+
+                    for wave in range(K_WAVES):
+                        # the first tile is issued unconditionally (clamped), then one ahead
+                        tiles = [start + min(wave, n_tiles - 1) * K_TILE]
+                        it = wave
+                        while it < n_tiles and it + K_WAVES < n_tiles:
+                            it += K_WAVES
+                            tiles.append(start + it * K_TILE)
+                        for p0 in tiles:
+                            kr, kc, vr, vc = tile_rows(p0, end, D, paged, page_row if paged else None)
+                            for rows, cols in ((kr, kc), (vr, vc)):
+                                off = ((kv * cache_stride + rows) * D + cols).astype(np.int64)
+                                assert off.min() >= 0 and (off + 8).max() <= cache_elems, (b, kv, split, p0)
+                                checked += off.size
+                    if fused and start <= newpos < end:
+                        slot = newpos
+                        if paged:
+                            idx = b * page_table.shape[1] + newpos // page_size
+                            pg = int(page_table.reshape(-1)[idx])
+                            slot = (pg if 0 <= pg < n_pages else 0) * page_size + newpos % page_size
+                        off = (kv * cache_stride + slot) * D + np.arange(D)
+                        assert off.min() >= 0 and off.max() < cache_elems
+                    if n_splits > 1:
+                        qi = qrow0 + np.arange(NS)
+                        off = ((qi * n_splits + split) * D)[:, None] + np.arange(0, D, 4)[None, :]
+                        assert off.min() >= 0 and (off + 4).max() <= part_elems
+    return checked
+
+
+@pytest.mark.parametrize("config", [0, 1, 3])
+def test_decode_contiguous_addresses(config):
+    cfg = synth.CONFIGS[config]
+    s = cfg["shape"]
+    n = check_decode(1, s.n_q_heads, s.n_kv_heads, s.head_dim, [cfg["pos"] + 1], cfg["cap"])
+    assert n > 0
+
+
+@pytest.mark.parametrize("L,cap,hq,hkv,D", [
+    (1, 1, 32, 4, 128), (33, 40, 32, 4, 128), (129, 129, 8, 2, 64), (1000, 1024, 64, 4, 128),
+    (8191, 8192, 32, 4, 128), (4097, 5000, 6, 3, 128), (300, 300, 40, 2, 128),
+])
+def test_decode_contiguous_addresses_edges(L, cap, hq, hkv, D):
+    """Lengths that leave partial tiles, single tiles, and a group of 20 heads (two head sub-groups)."""
+    assert check_decode(1, hq, hkv, D, [L], cap) > 0
+
+
+def test_decode_paged_addresses_config4():
+    cfg = synth.CONFIGS[4]
+    s = cfg["shape"]
+    lay = synth.paged_layout(cfg["n_seqs"], cfg["lo"], cfg["hi"], cfg["page_size"], seed=0)
+    n = check_decode(cfg["n_seqs"], s.n_q_heads, s.n_kv_heads, s.head_dim, lay.seq_lens, lay.n_pages * 16, 16,
+                     lay.page_table, lay.n_pages, int(lay.seq_lens.max()))
+    assert n > 0
+
+
+def test_decode_paged_addresses_invalid_entries():
+    """Page ids outside the pool and lengths outside [1, max_len] (the device-side
+    entries the host cannot check) are never used as addresses."""
+    lay = synth.paged_layout(5, 40, 300, 16, seed=11)
+    table, lens = lay.page_table.copy(), lay.seq_lens.copy()
+    max_len = int(lens.max())
+    table[1, 0] = lay.n_pages + 3
+    table[4, :] = -7
+    lens[2] = 0
+    lens[3] = max_len + 1
+    assert check_decode(5, 32, 4, 128, lens, lay.n_pages * 16, 16, table, lay.n_pages, max_len) > 0
+
+
+def test_decode_replica_catches_a_wrapped_offset():
+    """A plausible mistake -- the half-tile row taken as p0 - 16 + c16 instead of
+    p0 + 16 + c16, wrapping below zero for the first tile -- is caught."""
+    kr, kc, _, _ = tile_rows(0, 100, 128, paged=False)
+    bad = np.minimum(0 - 16 + (np.arange(64) & 15), 99) % U32  # unsigned 32-bit wrap
+    assert kr.min() >= 0 and bad.max() >= U32 - 16
+
+
+# ---------------------------------------------------------------------------
+# matmul_q8_mfma_kernel load_block (k_matmul.hip)
+# ---------------------------------------------------------------------------
+
+Q8 = 34
+
+
+def gemm_path_ok(w_addr, n, k, w_len):
+    """matmul_path's Q8_0 requirements of the weight view for the fast kernels."""
+    end = n * (k // 32) * Q8
+    return w_addr % 4 == 0 and ((w_addr + end) % 4 == 0 or w_len >= end + 2)
+
+
+def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
+    """Every x-plane and weight byte load_block reads for each block b of every tile."""
+    threads = WM * WN * 64
+    a_per, b_per = BM * 8 // threads, BN * 4 // threads
+    nb = k // 32
+    row_bytes = nb * Q8
+    b = np.arange(nb)[:, None]
+    # x planes: c = thread + threads u; row = min(m0 + (c / 4) % BM, m - 1); halves row*k + 32b + 8 (c % 4), 8 halves
+    c = (np.arange(threads)[:, None] + threads * np.arange(a_per)[None, :]).ravel()
+    for m0 in range(0, m, BM):
+        row = np.minimum(m0 + ((c >> 2) % BM), m - 1)
+        off = row[None, :] * k + 32 * b + 8 * (c[None, :] & 3)
+        assert off.min() >= 0 and (off + 8).max() <= m * k
+    # q runs: row = min(n0 + c / 4, n - 1); s = row*row_bytes + b*34 + 2 + 8 (c % 4); dwords from s - (s & 3)
+    c = (np.arange(threads)[:, None] + threads * np.arange(b_per)[None, :]).ravel()
+    lo, hi = None, None
+    for n0 in range(0, n, BN):
+        row = np.minimum(n0 + (c >> 2), n - 1)
+        blk = row[None, :] * row_bytes + b * Q8
+        s = blk + 2 + 8 * (c[None, :] & 3)
+        sh = (w_addr + s) & 3                      # the kernel's qsh (w itself is 4-byte aligned)
+        first = s - sh
+        last = first + np.where(sh != 0, 12, 8)    # the third dword only when the run straddles it
+        scale_end = blk + 2                        # part-0 threads read the block's f16 scale
+        lo = min(first.min(), blk.min()) if lo is None else min(lo, first.min(), blk.min())
+        hi = max(last.max(), scale_end.max()) if hi is None else max(hi, last.max(), scale_end.max())
+    assert lo >= 0
+    return int(hi)
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (16, 512, 2048), (2048, 4096, 2048), (2048, 512, 2048), (200, 300, 96), (130, 70, 32 * 65),
+    (17, 256, 256), (16, 5, 32 * 3), (33, 129, 32 * 7),
+])
+@pytest.mark.parametrize("tile", [(128, 128, 4, 2), (32, 64, 2, 2)])
+def test_gemm_load_block_addresses(m, n, k, tile):
+    """Both GEMM tiles; odd block counts put every other row's blocks at 2 mod 4."""
+    end = n * (k // 32) * Q8
+    for w_len in (end, end + 2):
+        if not gemm_path_ok(0, n, k, w_len):
+            continue  # matmul_path sends this view to the serial kernel
+        hi = check_gemm(m, n, k, 0, w_len, *tile)
+        assert hi <= w_len, (hi, w_len)
+
+
+def test_gemm_slack_rule_is_needed():
+    """Without matmul_path's rule the last run of an odd-block view ending at 2 mod 4
+    reads 2 bytes past the view: the rule is what keeps the GEMM inside it."""
+    n, k = 129, 32 * 7
+    end = n * (k // 32) * Q8
+    assert end % 4 == 2 and not gemm_path_ok(0, n, k, end)
+    assert check_gemm(64, n, k, 0, end, 32, 64, 2, 2) == end + 2
+
+
+# ---------------------------------------------------------------------------
+# prefill_attention_kernel DMA (k_prefill.hip)
+# ---------------------------------------------------------------------------
+
+P_HEADS, P_SETS, P_QROWS, P_KTILE = 4, 2, 32, 64
+
+
+def dma_plan(D, RS, B):
+    """DmaPlan: per head slot hw and load i, each lane's byte offset inside a 64-row
+    tile (or None past the stage's loads)."""
+    NB = P_KTILE * RS // 1024
+    plans = {}
+    for hw in range(P_HEADS):
+        offs = []
+        for i in range(B):
+            b = hw + P_HEADS * i
+            if b >= NB:
+                break
+            pos = 1024 * b + 16 * np.arange(64)
+            r, c = pos // RS, (pos % RS) // 16
+            offs.append(r * 2 * D + np.where(c < D // 8, 16 * c, 0))
+        plans[hw] = np.concatenate(offs) if offs else np.zeros(0, np.int64)
+    return plans
+
+
+def dma_extent(D, plan, key0, kv_end):
+    """dma_tile: byte range [lo, hi) read from the kv head's rows for one call."""
+    offs = np.concatenate(list(plan.values()))
+    if key0 + P_KTILE <= kv_end:  # whole tile: scalar tile base + offset
+        a = key0 * 2 * D + offs
+    else:
+        r, col = offs // (2 * D), offs % (2 * D)
+        key = np.minimum(key0 + r, kv_end - 1)
+        a = key * 2 * D + col
+    return int(a.min()), int(a.max()) + 16
+
+
+def check_prefill(pos, T, hq, hkv, D, max_ctx):
+    """Every direct-to-LDS load and q-operand load of one prefill launch."""
+    RB = 2 * D
+    RSK, RSV = RB + 16, RB + 64
+    BK = (P_KTILE * RSK // 1024 + P_HEADS - 1) // P_HEADS
+    BV = (P_KTILE * RSV // 1024 + P_HEADS - 1) // P_HEADS
+    pk, pv = dma_plan(D, RSK, BK), dma_plan(D, RSV, BV)
+    group = hq // hkv
+    n_qtiles = (T + P_QROWS - 1) // P_QROWS
+    n_pairs = (n_qtiles + 1) // 2
+    n_hgroups = (group + P_HEADS - 1) // P_HEADS
+    head_bytes = max_ctx * 2 * D
+    calls = set()
+    for pair in range(n_pairs):
+        heavy = n_qtiles - 1 - pair
+        has_light = pair < heavy
+        kv_end_light = pos + min(T, pair * P_QROWS + P_QROWS)
+        n_kt_light = (kv_end_light + P_KTILE - 1) // P_KTILE
+        for sel in range(2):
+            if sel == 1 and not has_light:
+                break
+            qt = heavy if sel == 0 else pair
+            q0 = qt * P_QROWS
+            kv_end = pos + min(T, q0 + P_QROWS)
+            n_kt = (kv_end + P_KTILE - 1) // P_KTILE
+            for st in range(P_SETS):
+                if sel == 0:
+                    calls.add((st * P_KTILE, kv_end))
+                prefetch_light = sel == 0 and has_light and st < n_kt_light
+                for r in range((n_kt + 1) // 2):
+                    j = 2 * r + st
+                    if j >= n_kt:
+                        continue
+                    own_next = j + 2 < n_kt
+                    if own_next or prefetch_light:
+                        calls.add(((j + 2) * P_KTILE if own_next else st * P_KTILE,
+                                   kv_end if own_next else kv_end_light))
+            # q operand: lane (r32, h): row min(q0 + r32, T - 1), head hq, halves 8h + 16 ks .. + 8
+            tc = np.minimum(q0 + np.arange(32), T - 1)
+            for hg in range(n_hgroups):
+                for hw in range(P_HEADS):
+                    hin = hg * P_HEADS + hw
+                    for kvh in range(hkv):
+                        hqi = kvh * group + (hin if hin < group else 0)
+                        off = (tc * hq + hqi) * D
+                        assert off.min() >= 0 and (off + D).max() <= T * hq * D
+    for key0, end in calls:
+        assert 0 < end <= max_ctx
+        for plan in (pk, pv):
+            lo, hi = dma_extent(D, plan, key0, end)
+            assert lo >= 0 and hi <= head_bytes, (key0, end, lo, hi)
+    return len(calls)
+
+
+@pytest.mark.parametrize("pos,T,hq,hkv,D,cap", [
+    (0, 2048, 32, 4, 128, 2048),     # C2
+    (0, 300, 32, 4, 128, 307), (100, 130, 32, 4, 128, 237), (5, 77, 32, 4, 64, 89), (0, 2, 32, 4, 128, 9),
+    (0, 97, 32, 4, 128, 104), (31, 200, 64, 4, 128, 238), (3, 96, 6, 3, 128, 106), (0, 65, 8, 8, 64, 72),
+])
+def test_prefill_dma_addresses(pos, T, hq, hkv, D, cap):
+    """C2 and the GPU parity suite's prefill shapes (chunked continuations, odd q-tile counts)."""
+    assert check_prefill(pos, T, hq, hkv, D, cap) > 0
