@@ -472,6 +472,12 @@ int ds5_hip_fill_normal_f16(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t n, uint64_t 
  * traffic counters (FETCH_SIZE / WRITE_SIZE) it reports. */
 int ds5_hip_copy_device(ds5_hip_ctx* ctx, ds5_buf dst, ds5_buf src, uint64_t len);
 
+/* Zero `len` bytes of a view on the context stream with a fill kernel: no host
+ * copy and no synchronisation (the reference zeroes the MoE accumulator with a
+ * host upload, forward.zig:452-454; a device-resident engine step does it here),
+ * and no memset node when the call is captured into a graph. */
+int ds5_hip_zero(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t len);
+
 /* Floor measurements for the benchmark: one launch that reads `len` bytes of
  * buf once (len % 16 == 0, 16-byte aligned view) with the decode kernel's
  * contiguous access -- 16-byte non-temporal loads, 64 KiB per 256-thread

@@ -90,11 +90,17 @@ class Engine:
             q = O.matmul(h, self._w(li, "attn_q.weight"), tensor_dtype(self._w(li, "attn_q.weight")), n, q_dim, hidden)
             k = O.matmul(h, self._w(li, "attn_k.weight"), tensor_dtype(self._w(li, "attn_k.weight")), n, kv_dim, hidden)
             v = O.matmul(h, self._w(li, "attn_v.weight"), tensor_dtype(self._w(li, "attn_v.weight")), n, kv_dim, hidden)
+            tr(li, "q_proj", q)
+            tr(li, "k_proj", k)
+            tr(li, "v_proj", v)
             q = O.rms_norm(q, self._w(li, "attn_q_norm.weight"), eps, n * hq, hd)
             k = O.rms_norm(k, self._w(li, "attn_k_norm.weight"), eps, n * hkv, hd)
+            tr(li, "q_norm", q)
+            tr(li, "k_norm", k)
             q = O.rope(q.reshape(n, hq, hd), positions, c["rope_theta"])
             k = O.rope(k.reshape(n, hkv, hd), positions, c["rope_theta"])
             tr(li, "rope_q", q)
+            tr(li, "rope_k", k)
             O.kv_append(k, v, self.k_cache[li], self.v_cache[li], self.kv_dtype, self.pos, n, hkv, hd, self.capacity)
             attn = O.gqa_attention(q, self.k_cache[li], self.v_cache[li], self.kv_dtype, self.pos, n, hq, hkv, hd,
                                    self.capacity, scale).reshape(n, q_dim)
@@ -103,6 +109,7 @@ class Engine:
             x = O.add(x, O.matmul(attn, wo, tensor_dtype(wo), n, hidden, q_dim))
             tr(li, "attn_resid", x)
             h2 = O.rms_norm(x, self._w(li, "ffn_norm.weight"), eps, n, hidden)
+            tr(li, "ffn_norm", h2)
             router = self._w(li, "ffn_gate_inp.weight")
             ids, wts = O.router_topk(h2, router, tensor_dtype(router), n, hidden, c["n_experts"], c["top_k"],
                                      c["norm_topk_prob"])
@@ -114,6 +121,7 @@ class Engine:
             x = O.add(x, proj)
             tr(li, "block", x)
         h = O.rms_norm(x, self.w["output_norm.weight"], eps, n, hidden)
+        tr(-1, "output_norm", h)
         out_w = self.w["output.weight"]
         logits = O.matmul(h, out_w, tensor_dtype(out_w), n, c["vocab_size"], hidden)
         tr(-1, "logits", logits)
@@ -124,3 +132,30 @@ class Engine:
 def argmax(logits: np.ndarray) -> int:
     """forward.zig:518-528: the first index of the maximum (ties to the lower token id)."""
     return int(np.argmax(logits))
+
+
+# forward.zig's trace points of one layer, in the order they fire (forward.zig:334-470)
+LAYER_TRACE_OPS = ("attn_norm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm", "rope_q", "rope_k", "attn",
+                   "attn_resid", "ffn_norm", "experts", "block")
+
+
+def trace_order(n_layers: int):
+    """Every (layer, op) trace point of a forward pass in firing order."""
+    pts = [(-1, "embed")]
+    for li in range(n_layers):
+        pts += [(li, op) for op in LAYER_TRACE_OPS]
+    return pts + [(-1, "output_norm"), (-1, "logits")]
+
+
+def first_divergence(want: dict, got: dict, n_layers: int, atol: float, rtol: float, logits_tol=None):
+    """The first trace point, in firing order, where `got` leaves `want`'s tolerance
+    (|a - o| <= atol + rtol |o|, NaN fails) -- test_forward.zig:304-330's firstDivergence
+    over every point both traces hold. Returns (layer, op, compare result) or None."""
+    for key in trace_order(n_layers):
+        if key not in want or key not in got:
+            continue
+        a, t = (atol, rtol) if key[1] != "logits" or logits_tol is None else logits_tol
+        r = O.compare(np.asarray(want[key], np.float32).reshape(-1), np.asarray(got[key], np.float32).reshape(-1), a, t)
+        if not r.passed:
+            return key[0], key[1], r
+    return None

@@ -288,6 +288,7 @@ int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a);
 int launch_fill_normal_f16(ds5_hip_ctx* ctx, f16* out, uint64_t n, uint64_t seed);
 int launch_stream_read(ds5_hip_ctx* ctx, const void* src, uint64_t len, uint32_t* sink);
 int launch_empty(ds5_hip_ctx* ctx, uint32_t n_workgroups);
+int launch_zero(ds5_hip_ctx* ctx, void* p, uint64_t len);
 
 // ---------------------------------------------------------------------------
 // Device helpers

@@ -778,6 +778,12 @@ int ds5_hip_stream_read(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t len, ds5_buf sin
     return launch_stream_read(ctx, ds5_ptr(buf), len, (uint32_t*)ds5_ptr(sink));
 }
 
+int ds5_hip_zero(ds5_hip_ctx* ctx, ds5_buf buf, uint64_t len) {
+    if (!covers(buf, len)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "zero: view too small");
+    if (int rc = set_device(ctx)) return rc;
+    return launch_zero(ctx, ds5_ptr(buf), len);
+}
+
 int ds5_hip_empty_launch(ds5_hip_ctx* ctx, uint32_t n_workgroups) {
     if (n_workgroups == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "empty_launch: no workgroups");
     if (int rc = set_device(ctx)) return rc;

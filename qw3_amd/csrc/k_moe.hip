@@ -28,6 +28,8 @@
 
 namespace {
 
+constexpr int kMaxDevices = 64;  // per-device one-time kernel attributes
+
 constexpr int kRouterThreads = 256;
 constexpr int kMoeWaves = 8;  // wavefronts (weight rows) per GEMV workgroup
 
@@ -636,13 +638,14 @@ static int launch_router_t(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     const size_t smem = ((size_t)((a.dim + 3) & ~3u)) * sizeof(float) + (size_t)rows * a.row_bytes;
     if (smem > 131072)  // nothing is enqueued yet: the router is the first launch of its calls
         return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "router: dim %u needs %zu bytes of LDS (131072 at most)", a.dim, smem);
-    static bool big_lds = false;  // allow the 64 KiB of rows plus x (up to 128 KiB) once per instantiation
-    if (!big_lds) {
+    static bool big_lds[kMaxDevices] = {};  // allow the 64 KiB of rows plus x (up to 128 KiB), once per device
+    if (ctx->device >= kMaxDevices) return ds5_fail(ctx, DS5_DEVICE_FAILURE, "router: device index %d", ctx->device);
+    if (!big_lds[ctx->device]) {
         if (int rc = ds5_hip_status(ctx, hipFuncSetAttribute((const void*)router_logits_kernel<DT, CP>,
                                                              hipFuncAttributeMaxDynamicSharedMemorySize, 131072),
                                     "router lds"))
             return rc;
-        big_lds = true;
+        big_lds[ctx->device] = true;
     }
     const dim3 grid(a.n_tokens, (a.n_experts + rows - 1) / rows);
     DS5_TIMED_LAUNCH(ctx, "router_logits_kernel", (router_logits_kernel<DT, CP>), grid, dim3(kRouterThreads), smem,
@@ -664,6 +667,15 @@ int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
              : a.w_dtype == DS5_DTYPE_F16 ? launch_router_dt<DS5_DTYPE_F16>(ctx, a)
                                           : launch_router_dt<DS5_DTYPE_Q8_0>(ctx, a);
     if (rc) return rc;
+    // the token's probabilities in dynamic LDS: n_experts * 4 bytes, up to 64 KiB (16384 experts)
+    static bool select_lds[kMaxDevices] = {};
+    if (!select_lds[ctx->device]) {
+        if (int rc2 = ds5_hip_status(ctx, hipFuncSetAttribute((const void*)router_select_kernel,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize, 65536),
+                                     "router select lds"))
+            return rc2;
+        select_lds[ctx->device] = true;
+    }
     DS5_TIMED_LAUNCH(ctx, "router_select_kernel", router_select_kernel, dim3(a.n_tokens), dim3(64),
                      (size_t)a.n_experts * sizeof(float), ctx->stream, a.logits, a.n_experts, a.top_k, (uint32_t)a.norm,
                      a.ids, a.weights, a.pairs);

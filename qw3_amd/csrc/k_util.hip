@@ -55,6 +55,17 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* src, uint
 
 __global__ void empty_kernel() {}
 
+// Zero fill: words when the view is 4-byte aligned and sized, else bytes.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+__global__ __launch_bounds__(256) void zero_bytes_kernel(uint8_t* p, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
 }  // namespace
 
 int launch_stream_read(ds5_hip_ctx* ctx, const void* src, uint64_t len, uint32_t* sink) {
@@ -64,6 +75,20 @@ int launch_stream_read(ds5_hip_ctx* ctx, const void* src, uint64_t len, uint32_t
     DS5_TIMED_LAUNCH(ctx, "stream_read_kernel", stream_read_kernel, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream,
                      (const u32x4*)src, n16, sink);
     return ds5_after_launch(ctx, "stream_read_kernel");
+}
+
+int launch_zero(ds5_hip_ctx* ctx, void* p, uint64_t len) {
+    if (len == 0) return DS5_OK;
+    const bool words = ((uintptr_t)p % 4 == 0) && len % 4 == 0;
+    const uint64_t n = words ? len / 4 : len;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n + 255) / 256, 4096);
+    if (words)
+        DS5_TIMED_LAUNCH(ctx, "zero_words_kernel", zero_words_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
+                         (uint32_t*)p, n);
+    else
+        DS5_TIMED_LAUNCH(ctx, "zero_bytes_kernel", zero_bytes_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
+                         (uint8_t*)p, n);
+    return ds5_after_launch(ctx, "zero_kernel");
 }
 
 int launch_empty(ds5_hip_ctx* ctx, uint32_t n_workgroups) {

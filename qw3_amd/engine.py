@@ -29,8 +29,15 @@ from . import hip as H
 
 
 def _dtype_of(a: np.ndarray) -> int:
-    """GGUF weights as the engine binds them: Q8_0 rows (uint8 [rows, k/32*34]) or f32."""
-    return H.DTYPE_Q8_0 if a.dtype == np.uint8 else H.DTYPE_F32
+    """The GGUF tensor type of a weight as the engine binds it (forward.zig:81-118 takes
+    it from the tensor descriptor): Q8_0 rows (uint8 [rows, k/32*34]), f16 or f32."""
+    if a.dtype == np.uint8:
+        return H.DTYPE_Q8_0
+    if a.dtype == np.float16:
+        return H.DTYPE_F16
+    if a.dtype == np.float32:
+        return H.DTYPE_F32
+    raise H.UnsupportedDtype(f"weight dtype {a.dtype}: the provider takes f32, f16 or Q8_0")
 
 
 class Weights:
@@ -137,6 +144,10 @@ class Engine:
                 H.matmul(ctx, H.MatmulArgs(self.h, wq, dq, self.q, n, q_dim, hidden))
                 H.matmul(ctx, H.MatmulArgs(self.h, wk, dk, self.k, n, kv_dim, hidden))
                 H.matmul(ctx, H.MatmulArgs(self.h, wv, dv, self.v, n, kv_dim, hidden))
+            self._trace(li, "q_proj", self.q, n * q_dim)
+            self._trace(li, "k_proj", self.k, n * kv_dim)
+            self._trace(li, "v_proj", self.v, n * kv_dim)
+            # fused: q_norm, k_norm, rope_q and rope_k happen inside attentionStep (no trace points)
             if self.fused:
                 H.attentionStep(ctx, H.AttentionStepArgs(
                     self.q, self.k, self.v, q_norm, k_norm, self.positions, self.k_cache[li], self.v_cache[li],
@@ -145,9 +156,12 @@ class Engine:
             else:
                 H.rmsNorm(ctx, H.RmsNormArgs(self.q, q_norm, self.q, n * hq, hd, eps))
                 H.rmsNorm(ctx, H.RmsNormArgs(self.k, k_norm, self.k, n * hkv, hd, eps))
+                self._trace(li, "q_norm", self.q, n * q_dim)
+                self._trace(li, "k_norm", self.k, n * kv_dim)
                 H.rope(ctx, H.RopeArgs(self.q, self.positions, n, hq, hd, c["rope_theta"]))
                 H.rope(ctx, H.RopeArgs(self.k, self.positions, n, hkv, hd, c["rope_theta"]))
                 self._trace(li, "rope_q", self.q, n * q_dim)
+                self._trace(li, "rope_k", self.k, n * kv_dim)
                 H.kvAppend(ctx, H.KvAppendArgs(self.k, self.v, self.k_cache[li], self.v_cache[li], self.kv_dtype,
                                                self.pos, n, hkv, hd, self.capacity))
                 H.gqaAttention(ctx, H.AttnArgs(self.q, self.k_cache[li], self.v_cache[li], self.kv_dtype,
@@ -164,12 +178,18 @@ class Engine:
 
             ffn_norm, _ = self.w.layer(li, "ffn_norm.weight")
             H.rmsNorm(ctx, H.RmsNormArgs(self.x, ffn_norm, self.h2, n, hidden, eps))
+            self._trace(li, "ffn_norm", self.h2, n * hidden)
             router, dr = self.w.layer(li, "ffn_gate_inp.weight")
             gate, dg = self.w.layer(li, "ffn_gate_exps.weight")
             up, _ = self.w.layer(li, "ffn_up_exps.weight")
             down, _ = self.w.layer(li, "ffn_down_exps.weight")
-            # proj doubles as the MoE accumulator and must start at zero (forward.zig:452-454)
-            ctx.upload(self.proj, 0, self.zeros[:n * hidden])
+            # proj doubles as the MoE accumulator and must start at zero (forward.zig:452-454):
+            # the eight-op mode uploads zeros as the reference does; the fused mode clears it
+            # on the device (no host copy or synchronisation inside the layer)
+            if self.fused:
+                ctx.zero(self.proj, n * hidden * 4)
+            else:
+                ctx.upload(self.proj, 0, self.zeros[:n * hidden])
             if self.fused:
                 H.moe(ctx, H.MoeArgs(self.h2, router, dr, gate, up, down, dg, self.proj, H.Buf(), H.Buf(), n,
                                      hidden, c["expert_ffn_dim"], c["n_experts"], c["top_k"],

@@ -207,6 +207,7 @@ SIGNATURES = {
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
     "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
     "ds5_hip_copy_device": ([_P, Buf, Buf, C.c_uint64], C.c_int),
+    "ds5_hip_zero": ([_P, Buf, C.c_uint64], C.c_int),
     "ds5_hip_stream_read": ([_P, Buf, C.c_uint64, Buf], C.c_int),
     "ds5_hip_empty_launch": ([_P, C.c_uint32], C.c_int),
 }
@@ -341,6 +342,10 @@ class Ctx:
 
     def copy_device(self, dst: Buf, src: Buf, length: int) -> None:
         self.check(LIB.ds5_hip_copy_device(self._h, dst, src, length))
+
+    def zero(self, buf: Buf, length: int) -> None:
+        """Zero `length` bytes of buf on the context stream (fill kernel, no host copy)."""
+        self.check(LIB.ds5_hip_zero(self._h, buf, length))
 
     def stream_read(self, buf: Buf, length: int, sink: Buf) -> None:
         """One launch reading `length` bytes of buf once (the decode's contiguous K/V access, nothing computed)."""

@@ -113,3 +113,39 @@ def test_planted_mistake_is_caught(oracle, model):
         oracle.add = real_add
     layer, _, _, x_out, atol, rtol = [c for c in S.block_cases() if c[0] == 2][0]
     assert not oracle.compare(x_out.reshape(-1), seen[(2, "block")].reshape(-1), atol, rtol).passed
+
+
+def test_trace_points_and_first_divergence(oracle, model):
+    """The oracle engine fires forward.zig's 16 trace points in its order
+    (forward.zig:316-492), and the ported first-divergence walk
+    (test_forward.zig:304-330) names the planted mistake's point: the third residual
+    add dropped is layer 1's attn_resid."""
+    from oracle import engine as OE
+    cfg, w, prompts = model
+    toks = prompts[0]["token_ids"]
+    order, clean = [], {}
+
+    def keep(store):
+        return lambda layer, op, a: store.__setitem__((layer, op), np.array(a, np.float32, copy=True))
+
+    def both(layer, op, a):
+        order.append((layer, op))
+        keep(clean)(layer, op, a)
+
+    _engine(model, oracle.F32).forward(toks, trace=both)
+    assert order == OE.trace_order(cfg["n_layers"])
+    assert len({op for _, op in order}) == 16
+    real_add, calls, bad = oracle.add, [], {}
+
+    def bad_add(x, y):
+        calls.append(1)
+        return np.array(x, np.float32, copy=True) if len(calls) == 3 else real_add(x, y)
+
+    oracle.add = bad_add
+    try:
+        _engine(model, oracle.F32).forward(toks, trace=keep(bad))
+    finally:
+        oracle.add = real_add
+    assert OE.first_divergence(clean, clean, cfg["n_layers"], 2e-3, 1e-2) is None
+    layer, op, r = OE.first_divergence(clean, bad, cfg["n_layers"], 2e-3, 1e-2)
+    assert (layer, op) == (1, "attn_resid") and not r.passed

@@ -817,6 +817,23 @@ def test_router_vs_oracle(ctx, hip, oracle, dt, off):
     assert np.all(rel <= 1e-6)
 
 
+@pytest.mark.parametrize("E,K", [(300, 8), (128, 80), (16384, 8), (257, 64)])
+def test_router_wide_selects(ctx, hip, oracle, E, K):
+    """router_select_kernel beyond its register path (more than 256 experts or more than
+    64 picks) and at the 16384-expert limit of its LDS: ids equal to the oracle's,
+    weights within 1e-6."""
+    g = np.random.default_rng(E + K)
+    T, dim = 3, 64
+    w = (g.standard_normal((E, dim)) * 0.05).astype(np.float32)
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    ids, wts = hip.routerTopK(ctx, ctx.from_numpy(x), ctx.from_numpy(w), hip.DTYPE_F32, T, dim, E, K, True)
+    oi, ow = oracle.router_topk(x, w, oracle.F32, T, dim, E, K, True)
+    assert np.array_equal(ids, oi)
+    rel = np.abs(wts - ow) / np.abs(ow)
+    print(f"  E={E} K={K}: weights vs oracle max rel {rel.max():.2e}", flush=True)
+    assert np.all(rel <= 1e-6)
+
+
 @pytest.mark.parametrize("i", range(3))
 def test_expert_mlp_fixtures(ctx, hip, oracle, i):
     """kernels_c.zig:320-401 through the GPU: Q8_0 banks, token-major pairs, the case tolerance."""
