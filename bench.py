@@ -370,6 +370,46 @@ class ProjPrefill:
         self.H.matmulGroup(self.ctx, self.args)
 
 
+class BlockPrefill:
+    """The attention block of a 2048-token prefill (forward.zig:337-412): x [T, hidden]
+    f32 through the Q8_0 q/k/v projections, then the attention step into an empty f16
+    cache. fused: ds5_hip_attention_block (the pre-pass in the projection GEMM's
+    epilogue); otherwise ds5_hip_matmul_group then ds5_hip_attention_step."""
+
+    def __init__(self, H, synth, ctx, fused=True, hidden=2048, seed=12):
+        self.H, self.ctx, self.fused = H, ctx, fused
+        s = self.s = synth.CONFIGS[2]["shape"]
+        T = self.T = synth.CONFIGS[2]["tokens"]
+        hq, hkv, d = s.n_q_heads, s.n_kv_heads, s.head_dim
+        g = np.random.default_rng(seed)
+        nb = hidden // 32
+        x = ctx.from_numpy(g.standard_normal((T, hidden)).astype(np.float32))
+        ws = []
+        for n in (hq * d, hkv * d, hkv * d):
+            w = g.integers(0, 256, (n, nb, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.02], np.float16).view(np.uint8)
+            ws.append(ctx.from_numpy(w.reshape(n, nb * 34)))
+        _, _, _, qn, kn = synth.step_inputs(2, 0, 1, s)
+        q, k, v = (ctx.createBuffer(T * h * d * 4) for h in (hq, hkv, hkv))
+        self.kc, self.vc = ctx.createBuffer(2 * hkv * T * d), ctx.createBuffer(2 * hkv * T * d)
+        self.out = ctx.createBuffer(T * hq * d * 4)
+        pb = ctx.from_numpy(np.arange(T, dtype=np.int32))
+        self.step = H.AttentionStepArgs(q, k, v, ctx.from_numpy(qn), ctx.from_numpy(kn), pb, self.kc, self.vc,
+                                        self.out, H.DTYPE_F16, 0, T, hq, hkv, d, T, s.eps, s.theta, 1.0, s.scale)
+        self.block = H.AttentionBlockArgs(x, *ws, H.DTYPE_Q8_0, hidden, self.step)
+        self.group = H.MatmulGroupArgs.of(x, H.DTYPE_Q8_0, T, hidden, [(ws[0], q, hq * d), (ws[1], k, hkv * d),
+                                                                        (ws[2], v, hkv * d)])
+        self.proj_flops = 2 * T * (hq + 2 * hkv) * d * hidden
+        self.attn_flops = prefill_flops(hq, d, T)
+
+    def sweep(self):
+        if self.fused:
+            self.H.attentionBlock(self.ctx, self.block)
+        else:
+            self.H.matmulGroup(self.ctx, self.group)
+            self.H.attentionStep(self.ctx, self.step)
+
+
 # ---------------------------------------------------------------------------
 # Timing helpers
 # ---------------------------------------------------------------------------
@@ -585,10 +625,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time per cycled decode leg (C0, C1)")
     ap.add_argument("--leg-seconds", type=float, default=0.5,
                     help="minimum device time of each secondary timed leg (graph replays / eager kernel timing)")
-    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,QKVP",
+    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,QKVP,BLK",
                     help="comma list of legs: C0-C4 (BASELINE configs; C1 is the headline), FLOOR (launch and "
                          "bare-read floors), SIX (C1 through the six separate ops), QKV / QKVP (decode / prefill "
-                         "q/k/v projections), WO (output projection + residual), MOE (decode MoE block)")
+                         "q/k/v projections), WO (output projection + residual), MOE (decode MoE block), BLK (prefill "
+                         "attention block: projections + step, fused vs the two calls)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -936,6 +977,27 @@ def main():
                   "(2 matrix-core products per useful one)")
         log(f"[bench] QKVP matmul_q8_mfma_kernel {ns_k / 1e3:.2f} us -> {tf:.1f} TFLOP/s (useful)")
         del p
+
+    if "BLK" in only:
+        log("[bench] BLK: prefill attention block, 2048 tokens: Q8_0 q/k/v projections (hidden 2048) + step")
+        legs = {}
+        for fused in (True, False):
+            p = BlockPrefill(H, synth, ctx, fused=fused)
+            n_rep = max(5, args.steps // 5)
+            elapsed, _ = time_graph(ctx, p, n_rep, 2)
+            names = ("matmul_x_split_kernel", "matmul_q8_mfma_kernel", "prefill_prep_kernel",
+                     "prefill_attention_kernel")
+            ks = kernel_stats(ctx, p, names, leg)
+            legs[fused] = dict(end_to_end_us=round(elapsed / n_rep * 1e6, 3),
+                               kernel_us={k: round(ks[k][0] / 1e3, 3) for k in names if ks[k][1]})
+            del p
+        extra["attention_block_prefill"] = dict(
+            fused=legs[True], two_calls=legs[False],
+            shape="T 2048, hidden 2048, wq [4096 x 2048] + wk, wv [512 x 2048] Q8_0, 32q/4kv d128, empty f16 "
+                  "cache; fused = ds5_hip_attention_block (norm, rope, f16 append and the q operand in the "
+                  "projection GEMM's epilogue), two_calls = ds5_hip_matmul_group + ds5_hip_attention_step")
+        log(f"[bench] BLK fused {legs[True]['end_to_end_us']:.2f} us ({legs[True]['kernel_us']}); two calls "
+            f"{legs[False]['end_to_end_us']:.2f} us ({legs[False]['kernel_us']})")
 
     for c, r in cpu.items():
         if f"C{c}" in configs:

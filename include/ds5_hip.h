@@ -395,6 +395,30 @@ typedef struct ds5_attention_step_args {
 } ds5_attention_step_args;
 int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* args);
 
+/* The attention block of a layer, forward.zig:337-412 as one call (no
+ * reference counterpart: the reference makes nine provider calls): the q/k/v
+ * projections of x (K.matmul by wq, wk, wv; kernels_a.zig:136-163), then the
+ * attention step. The results -- cache rows and attention output -- are those
+ * of ds5_hip_matmul_group(x; wq, wk, wv -> step.q, step.k, step.v) followed by
+ * ds5_hip_attention_step(&step), bit for bit, and the preconditions are
+ * theirs, in that order. For a prefill whose Q8_0 projections take the
+ * matrix-core GEMM path (n_tokens >= 16, or hidden above 8192), with an f16
+ * cache and head_dim 128, the step's pre-pass runs in
+ * the projection GEMM's epilogue -- per-head RMSNorm, rope, f16 k/v append
+ * and the f16 q operand -- so q, k and v are never written in f32 and no
+ * pre-pass launches; every other case runs the two calls. step.q / step.k /
+ * step.v are scratch. */
+typedef struct ds5_attention_block_args {
+    ds5_buf x;         /* f32 [n_tokens, hidden]: the attn_norm output */
+    ds5_buf wq;        /* [n_q_heads * head_dim rows of hidden] in w_dtype */
+    ds5_buf wk;        /* [n_kv_heads * head_dim rows of hidden] */
+    ds5_buf wv;        /* [n_kv_heads * head_dim rows of hidden] */
+    uint32_t w_dtype;  /* DS5_DTYPE_F32 or DS5_DTYPE_Q8_0 */
+    uint32_t hidden;
+    ds5_attention_step_args step; /* q/k/v scratch, norms, positions, caches, out, shapes */
+} ds5_attention_block_args;
+int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* args);
+
 /* No reference counterpart. For callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): ds5_hip_attention_step with the same kernels, arguments,

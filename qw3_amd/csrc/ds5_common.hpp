@@ -140,6 +140,28 @@ struct MatmulGroupLaunch {
     uint32_t n[kMatmulGroupMax];
 };
 int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const MatmulPath* paths);
+// The attention block's q/k/v projections with the prefill pre-pass in the GEMM's
+// epilogue (Q8_0 weights, head_dim 128, m >= 16): k / v rows into the f16 caches
+// at pos, the f16 q operand into q16. ws: qkv_prep_workspace_bytes (x split and
+// the rope cos / sin of every token).
+struct QkvPrepLaunch {
+    const float* x;
+    const uint8_t *wq, *wk, *wv;
+    uint32_t m, k, n_q_heads, n_kv_heads, head_dim;
+    const int32_t* positions;
+    float freq_scale;
+    const RopeTable* table;
+    const float* q_norm;
+    const float* k_norm;
+    f16* q16;
+    f16* k_cache;
+    f16* v_cache;
+    uint32_t pos, max_ctx;
+    float eps, q_scale;
+    void* ws;
+};
+size_t qkv_prep_workspace_bytes(uint32_t m, uint32_t k, uint32_t head_dim);
+int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a);
 // Residual add out = x + y over n f32 elements (any views; out may be x or y).
 int launch_add(ds5_hip_ctx* ctx, const void* x, const void* y, void* out, uint64_t n);
 
@@ -402,4 +424,64 @@ DS5_DEVICE_INLINE float sqrt_rn(float x) { return (float)__builtin_sqrt((double)
 // RMSNorm scale of kernels_a.zig:87.
 DS5_DEVICE_INLINE float rms_inv(float sumsq, float dim, float eps) {
     return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sumsq, dim) + eps));
+}
+
+// The q/k arithmetic of a prefill step, shared by every kernel that produces the
+// cache rows and the attention q operand (the pre-pass and the projection GEMM's
+// epilogue), each operation rounded on its own so they agree bit for bit:
+//   qk_serial_sumsq: sum of squares in element order (kernels_a.zig:85-86)
+//   qk_norm_mul:     (v * inv) * w                  (kernels_a.zig:89)
+//   qk_rope_angle:   (pos * freq_scale) * inv_freq   (kernels_a.zig:120)
+//   qk_rotate:       x0 c - x1 s, x0 s + x1 c        (kernels_a.zig:125-126)
+//   qk_pairs_sumsq:  one lane's share of a q head's sum of squares, 8 rope
+//                    pairs (i, i + D/2); q only feeds attention, so the head's
+//                    lanes then add their shares in a fixed xor order
+//   qk_scaled_f16:   f16 of the f32 product y * s, rounded twice (to f32, then
+//                    to f16). The backend turns a product that is converted
+//                    to f16 into one mixed-precision fma (v_fma_mixlo_f16, a
+//                    single rounding) in some kernels and not in others, even
+//                    with contraction off; an empty asm that takes the product
+//                    as a register value keeps the two roundings everywhere
+DS5_DEVICE_INLINE float qk_serial_sumsq(const float* row, int dim) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+    for (int i = 0; i < dim; i += 4) {
+        const float4 v = *(const float4*)(row + i);
+        acc += v.x * v.x;
+        acc += v.y * v.y;
+        acc += v.z * v.z;
+        acc += v.w * v.w;
+    }
+    return acc;
+}
+
+DS5_DEVICE_INLINE float qk_norm_mul(float v, float inv, float w) {
+#pragma clang fp contract(off)
+    return v * inv * w;
+}
+
+DS5_DEVICE_INLINE float qk_rope_angle(float pos, float freq_scale, float inv) {
+#pragma clang fp contract(off)
+    return pos * freq_scale * inv;
+}
+
+DS5_DEVICE_INLINE void qk_rotate(float x0, float x1, float c, float s, float& y0, float& y1) {
+#pragma clang fp contract(off)
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+
+DS5_DEVICE_INLINE _Float16 qk_scaled_f16(float y, float s) {
+#pragma clang fp contract(off)
+    float p = y * s;
+    asm volatile("" : "+v"(p));
+    return (_Float16)p;
+}
+
+DS5_DEVICE_INLINE float qk_pairs_sumsq(const float (&x0)[8], const float (&x1)[8]) {
+#pragma clang fp contract(off)
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss += x0[j] * x0[j] + x1[j] * x1[j];
+    return ss;
 }

@@ -552,10 +552,10 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
     return launch_generic_attention(ctx, g);
 }
 
-int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
-    if (!a) return DS5_SHAPE_MISMATCH;
+// The attention step's preconditions: rmsNorm(q), rmsNorm(k), rope(q), rope(k),
+// kvAppend and gqaAttention checks, in that order.
+static int check_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
     const uint64_t T = a->n_tokens, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
-    // rmsNorm(q), rmsNorm(k), rope(q), rope(k), kvAppend, gqaAttention checks, in that order.
     if (hd == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: head_dim == 0");
     if (!covers(a->q, T * hq * hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: q too small");
     if (!covers(a->q_norm, hd * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: q_norm too small");
@@ -571,6 +571,16 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
     if (int rc = check_attention(ctx, &at)) return rc;
     if (T == 0) return DS5_OK;
     if (hd > 2 * DS5_MAX_ROPE_HALF) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "step: head_dim > 512");
+    return DS5_OK;
+}
+
+int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    if (int rc = check_step(ctx, a)) return rc;
+    const uint64_t T = a->n_tokens, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
+    const ds5_attn_args at{a->q, a->k_cache, a->v_cache, a->kv_dtype, a->out, a->pos, a->n_tokens,
+                           a->n_q_heads, a->n_kv_heads, a->head_dim, a->max_ctx, a->scale};
+    if (T == 0) return DS5_OK;
     if (int rc = set_device(ctx)) return rc;
     const RopeTable* table = rope_table_for(a->theta, a->head_dim);
 
@@ -654,6 +664,87 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
                                                        a->n_kv_heads, a->head_dim, a->max_ctx});
     if (!rc) rc = ds5_hip_gqa_attention(ctx, &at);
     return rc;
+}
+
+int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* a) {
+    if (!a) return DS5_SHAPE_MISMATCH;
+    const ds5_attention_step_args& s = a->step;
+    const uint32_t hd = s.head_dim;
+    ds5_matmul_group_args g{};
+    g.x = a->x;
+    g.w_dtype = a->w_dtype;
+    g.m = s.n_tokens;
+    g.k = a->hidden;
+    g.count = 3;
+    g.w[0] = a->wq;
+    g.w[1] = a->wk;
+    g.w[2] = a->wv;
+    g.out[0] = s.q;
+    g.out[1] = s.k;
+    g.out[2] = s.v;
+    g.n[0] = s.n_q_heads * hd;
+    g.n[1] = g.n[2] = s.n_kv_heads * hd;
+    // the calls' preconditions, in their order: the three projections, then the step
+    for (uint32_t e = 0; e < 3; e++)
+        if (int rc = check_matmul(ctx, "attention_block", g.x, g.w[e], g.w_dtype, g.out[e], g.m, g.n[e], g.k)) return rc;
+    if (int rc = check_step(ctx, &s)) return rc;
+    if (s.n_tokens == 0) return DS5_OK;
+    if (int rc = set_device(ctx)) return rc;
+    // Fused: the prefill pre-pass in the projection GEMM's epilogue (the paths the two
+    // calls would take: the GEMM for every weight, the fused MFMA prefill step).
+    bool fused = a->w_dtype == DS5_DTYPE_Q8_0 && hd == 128 && s.n_tokens >= 2 &&
+                 mfma_shape(s.kv_dtype, hd, {s.q, s.k, s.v, s.k_cache, s.v_cache, s.out}) &&
+                 prefill_prep_supported(s.n_kv_heads, hd) && aligned16(a->x);
+    for (uint32_t e = 0; fused && e < 3; e++) {
+        const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(g.w[e]), true,
+                             (float*)ds5_ptr(g.out[e]), g.m, g.n[e], g.k};
+        fused = matmul_path(l, g.w[e].len) == MatmulPath::Gemm;
+    }
+    if (!fused) {
+        if (int rc = ds5_hip_matmul_group(ctx, &g)) return rc;
+        return ds5_hip_attention_step(ctx, &s);
+    }
+    const uint64_t T = s.n_tokens;
+    const size_t q16_bytes = (size_t)T * s.n_q_heads * hd * sizeof(uint16_t);
+    const size_t prep_bytes = qkv_prep_workspace_bytes(s.n_tokens, a->hidden, hd);
+    void* ws = nullptr;
+    if (int rc = ds5_workspace(ctx, q16_bytes + prep_bytes, &ws)) return rc;
+    QkvPrepLaunch qp{};
+    qp.x = (const float*)ds5_ptr(a->x);
+    qp.wq = (const uint8_t*)ds5_ptr(a->wq);
+    qp.wk = (const uint8_t*)ds5_ptr(a->wk);
+    qp.wv = (const uint8_t*)ds5_ptr(a->wv);
+    qp.m = s.n_tokens;
+    qp.k = a->hidden;
+    qp.n_q_heads = s.n_q_heads;
+    qp.n_kv_heads = s.n_kv_heads;
+    qp.head_dim = hd;
+    qp.positions = (const int32_t*)ds5_ptr(s.positions);
+    qp.freq_scale = s.freq_scale;
+    qp.table = rope_table_for(s.theta, hd);
+    qp.q_norm = (const float*)ds5_ptr(s.q_norm);
+    qp.k_norm = (const float*)ds5_ptr(s.k_norm);
+    qp.q16 = (f16*)ws;
+    qp.k_cache = (f16*)ds5_ptr(s.k_cache);
+    qp.v_cache = (f16*)ds5_ptr(s.v_cache);
+    qp.pos = s.pos;
+    qp.max_ctx = s.max_ctx;
+    qp.eps = s.eps;
+    qp.q_scale = s.scale * kLog2e;
+    qp.ws = (char*)ws + q16_bytes;
+    if (int rc = launch_qkv_prep(ctx, qp)) return rc;
+    PrefillLaunch l{};
+    l.q16 = (const f16*)ws;
+    l.k_cache = qp.k_cache;
+    l.v_cache = qp.v_cache;
+    l.out = (float*)ds5_ptr(s.out);
+    l.pos = s.pos;
+    l.n_tokens = s.n_tokens;
+    l.n_q_heads = s.n_q_heads;
+    l.n_kv_heads = s.n_kv_heads;
+    l.head_dim = hd;
+    l.max_ctx = s.max_ctx;
+    return launch_prefill(ctx, l);
 }
 
 // Workspace bytes ds5_hip_attention_step takes for these arguments: the same

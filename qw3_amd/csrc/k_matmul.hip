@@ -201,14 +201,35 @@ constexpr int kXExpBias = 14;  // scaled rows have max |x'| in [2^14, 2^15)
 // Workspace bytes of the split x: hi and lo planes of m x k halves, m exponents.
 inline size_t x_split_bytes(uint32_t m, uint32_t k) { return (size_t)m * k * 4 + (size_t)m * 4; }
 
+// The rope angles of a prefill's tokens, made by the x split of the attention
+// block's projection (one workgroup per token): cs[t] holds cos then sin of
+// (pos_t * freq_scale) * inv_freq[i], i < half.
+struct XSplitRope {
+    const int32_t* positions;
+    float* cs;
+    uint32_t half;
+    float freq_scale;
+};
+
 // One workgroup per x row: max |x|, its exponent E, then hi / lo of x * 2^(14 - E).
-// A row of zeros (or with a non-finite maximum) keeps E = 0.
+// A row of zeros (or with a non-finite maximum) keeps E = 0. ROPE: also the
+// row's token's rope cos / sin.
+template <bool ROPE>
 __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const float* __restrict__ x,
                                                                        uint16_t* __restrict__ hi,
                                                                        uint16_t* __restrict__ lo,
-                                                                       int* __restrict__ row_exp, uint32_t k) {
+                                                                       int* __restrict__ row_exp, uint32_t k,
+                                                                       XSplitRope rope, RopeTable table) {
     __shared__ float red[kSplitThreads / 64];
     const uint64_t row = blockIdx.x;
+    if constexpr (ROPE) {
+        const float pos = (float)rope.positions[row];
+        for (uint32_t i = threadIdx.x; i < rope.half; i += kSplitThreads) {
+            const float ang = qk_rope_angle(pos, rope.freq_scale, table.inv[i]);
+            rope.cs[row * 2 * rope.half + i] = cosf(ang);
+            rope.cs[row * 2 * rope.half + rope.half + i] = sinf(ang);
+        }
+    }
     const float4* xr = (const float4*)(x + row * k);
     const uint32_t kc = k / 4;
     float mx = 0.0f;
@@ -253,16 +274,36 @@ __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t u) {
     return uint2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
 
-template <int BM, int BN, int WM, int WN>
+// EPI = 1: the attention block's q / k / v projections (entries 0, 1, 2 of the
+// group), 128 x 128 tiles: a tile is 128 tokens of one head's 128 dims, and
+// the epilogue turns it into what the prefill attention reads -- k: RMSNorm
+// (serial sum) and rotation, f16 into the cache row pos + t of its kv head; v:
+// f16 into the cache; q: RMSNorm, rotation, times q_scale, f16 into the q
+// operand [t, n_q_heads, 128] -- with the pre-pass's arithmetic (the qk_*
+// helpers), so the results equal the separate projection and step.
+struct AttnPrepEpi {
+    const float* q_norm;
+    const float* k_norm;
+    const float* cs;  // [m, 128]: cos of pairs 0..63, then sin
+    f16* q16;
+    f16* k_cache;
+    f16* v_cache;
+    uint32_t pos, n_q_heads, max_ctx;
+    float eps, q_scale;
+};
+
+template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
-                                                                      const WeightGroup g, uint32_t m, uint32_t k) {
+                                                                      const WeightGroup g, uint32_t m, uint32_t k,
+                                                                      const AttnPrepEpi ep) {
     // this workgroup's entry and column tile (uniform); out may be the residual itself
     const uint8_t* __restrict__ w = g.w[0];
     float* out = g.out[0];
     const float* res = g.res[0];
     uint32_t n = g.n[0], tile = blockIdx.x;
+    int entry = 0;
 #pragma unroll
     for (int e = 1; e < kMatmulGroupMax; e++)
         if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
@@ -271,6 +312,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
             res = g.res[e];
             n = g.n[e];
             tile = blockIdx.x - g.wg0[e];
+            entry = e;
         }
     constexpr int kThreads = WM * WN * 64;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
@@ -279,9 +321,16 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     constexpr int kBPer = BN * 4 / kThreads;  // 8-byte q runs per thread and block
     static_assert(kAPer >= 1 && kBPer >= 1, "at least one staging unit per thread");
 
-    __shared__ u32x4_t As[2][2][BM * 4];  // [buffer][hi, lo][row * 4 + swizzled chunk]
-    __shared__ u32x4_t Bs[2][BN * 4];
-    __shared__ float Ss[2][BN];
+    // LDS: As [buffer][hi, lo][row * 4 + swizzled chunk], Bs [buffer][row * 4 +
+    // swizzled chunk], Ss [buffer][row]; EPI 1 reuses the bytes for the f32 tile
+    constexpr int kAsBytes = 2 * 2 * BM * 4 * 16, kBsBytes = 2 * BN * 4 * 16, kSsBytes = 2 * BN * 4;
+    constexpr int kMainBytes = kAsBytes + kBsBytes + kSsBytes;
+    constexpr int kTileRow = BN + 4;  // EPI 1 tile row stride in floats (16-byte rows, rows 4 banks apart)
+    constexpr int kLdsBytes = EPI == 1 && BM * kTileRow * 4 > kMainBytes ? BM * kTileRow * 4 : kMainBytes;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsBytes];
+    auto& As = *reinterpret_cast<u32x4_t(*)[2][2][BM * 4]>(smem);
+    auto& Bs = *reinterpret_cast<u32x4_t(*)[2][BN * 4]>(smem + kAsBytes);
+    auto& Ss = *reinterpret_cast<float(*)[2][BN]>(smem + kAsBytes + kBsBytes);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -376,6 +425,99 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
         __syncthreads();
     }
 
+    if constexpr (EPI == 1) {
+        // The whole 128 x 128 tile (one head of 128 tokens) goes through LDS once;
+        // then thread t takes rows t / 8 and t / 8 + 64, dims k8 + [0, 8) and
+        // 64 + k8 + [0, 8) (8 rope pairs), k8 = 8 (t % 8). Its norm weights and
+        // rope cos / sin are loaded before the tile is written, so their
+        // latency overlaps the tile's LDS round trip.
+        static_assert(BM == 128 && BN == 128 && WM == 4 && WN == 2, "one head of 128 dims per tile");
+        constexpr int D = 128, HALF = 64, TROW = kTileRow;
+        const uint32_t head = tile;  // BN = D: tile j of an entry is head j
+        const int r0 = threadIdx.x / 8, k8 = 8 * (threadIdx.x % 8);
+        const float* nw = entry == 0 ? ep.q_norm : ep.k_norm;
+        float w0[8], w1[8], c[2][8], sn[2][8];
+        if (entry != 2) {
+            *(float4*)&w0[0] = *(const float4*)(nw + k8);
+            *(float4*)&w0[4] = *(const float4*)(nw + k8 + 4);
+            *(float4*)&w1[0] = *(const float4*)(nw + HALF + k8);
+            *(float4*)&w1[4] = *(const float4*)(nw + HALF + k8 + 4);
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++) {
+                const uint32_t tok = min(m0 + r0 + 64 * rr, m - 1);
+                const float* cs = ep.cs + (uint64_t)tok * D;
+                *(float4*)&c[rr][0] = *(const float4*)(cs + k8);
+                *(float4*)&c[rr][4] = *(const float4*)(cs + k8 + 4);
+                *(float4*)&sn[rr][0] = *(const float4*)(cs + HALF + k8);
+                *(float4*)&sn[rr][4] = *(const float4*)(cs + HALF + k8 + 4);
+            }
+        }
+        // the main loop ended on a barrier after every wavefront's last LDS read
+        float* tl = reinterpret_cast<float*>(smem);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int lr = wm0 + 16 * i + 4 * grp + e;
+                const uint32_t row = m0 + lr;
+                const int sh = row < m ? row_exp[row] - kXExpBias : 0;
+#pragma unroll
+                for (int j = 0; j < TN; j++) tl[lr * TROW + wn0 + 16 * j + r16] = __builtin_ldexpf(acc[i][j][e], sh);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 2; rr++) {
+            const int r = r0 + 64 * rr;
+            const uint32_t tok = m0 + r;
+            const bool ok = tok < m;
+            const float* trow = tl + r * TROW;
+            float x0[8], x1[8];
+            *(float4*)&x0[0] = *(const float4*)(trow + k8);
+            *(float4*)&x0[4] = *(const float4*)(trow + k8 + 4);
+            *(float4*)&x1[0] = *(const float4*)(trow + HALF + k8);
+            *(float4*)&x1[4] = *(const float4*)(trow + HALF + k8 + 4);
+            f16x8_t y0v, y1v;
+            f16* dst;
+            if (entry == 2) {  // v: f16 append
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    y0v[j] = (f16)x0[j];
+                    y1v[j] = (f16)x1[j];
+                }
+                dst = ep.v_cache + ((uint64_t)head * ep.max_ctx + ep.pos + tok) * D;
+            } else {
+                float inv;
+                if (entry == 0) {  // q: the head's lanes add their shares in xor order
+                    float ss = qk_pairs_sumsq(x0, x1);
+#pragma unroll
+                    for (int mm = 1; mm < 8; mm <<= 1) ss += __shfl_xor(ss, mm, 64);
+                    inv = rms_inv(ss, (float)D, ep.eps);
+                } else {  // k: the reference's serial sum of the row
+                    inv = rms_inv(qk_serial_sumsq(trow, D), (float)D, ep.eps);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    float y0, y1;
+                    qk_rotate(qk_norm_mul(x0[j], inv, w0[j]), qk_norm_mul(x1[j], inv, w1[j]), c[rr][j], sn[rr][j],
+                              y0, y1);
+                    if (entry == 0) {
+                        y0v[j] = qk_scaled_f16(y0, ep.q_scale);
+                        y1v[j] = qk_scaled_f16(y1, ep.q_scale);
+                    } else {
+                        y0v[j] = (f16)y0;
+                        y1v[j] = (f16)y1;
+                    }
+                }
+                dst = entry == 0 ? ep.q16 + ((uint64_t)tok * ep.n_q_heads + head) * D
+                                 : ep.k_cache + ((uint64_t)head * ep.max_ctx + ep.pos + tok) * D;
+            }
+            if (ok) {
+                *(f16x8_t*)(dst + k8) = y0v;
+                *(f16x8_t*)(dst + HALF + k8) = y1v;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -493,8 +635,8 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     uint16_t* hi = (uint16_t*)ws;
     uint16_t* lo = hi + (size_t)a.m * a.k;
     int* row_exp = (int*)(lo + (size_t)a.m * a.k);
-    DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel, dim3(a.m), dim3(kSplitThreads), 0, ctx->stream,
-                     a.x, hi, lo, row_exp, a.k);
+    DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(a.m), dim3(kSplitThreads), 0,
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{});
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     uint32_t tiles = 0;
@@ -508,12 +650,45 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
         g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
     }
     if (tiles == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN>), dim3(tiles, (a.m + BM - 1) / BM),
-                     dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k);
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0>),
+                     dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
+                     AttnPrepEpi{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
 
 }  // namespace
+
+size_t qkv_prep_workspace_bytes(uint32_t m, uint32_t k, uint32_t head_dim) {
+    return x_split_bytes(m, k) + (size_t)m * head_dim * sizeof(float);
+}
+
+int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
+    constexpr int BM = 128, BN = 128, WM = 4, WN = 2;
+    uint16_t* hi = (uint16_t*)a.ws;
+    uint16_t* lo = hi + (size_t)a.m * a.k;
+    int* row_exp = (int*)(lo + (size_t)a.m * a.k);
+    float* cs = (float*)(row_exp + a.m);  // 4-byte aligned: the planes and exponents are whole dwords
+    XSplitRope rope{a.positions, cs, a.head_dim / 2, a.freq_scale};
+    DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<true>, dim3(a.m), dim3(kSplitThreads), 0,
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table);
+    if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
+    WeightGroup g{};
+    const uint32_t ns[3] = {a.n_q_heads * a.head_dim, a.n_kv_heads * a.head_dim, a.n_kv_heads * a.head_dim};
+    const uint8_t* ws[3] = {a.wq, a.wk, a.wv};
+    uint32_t tiles = 0;
+    for (int e = 0; e < 3; e++) {
+        g.w[e] = ws[e];
+        g.n[e] = ns[e];
+        g.wg0[e] = tiles;
+        tiles += ns[e] / BN;
+    }
+    g.count = 3;
+    AttnPrepEpi ep{a.q_norm, a.k_norm, cs, a.q16, a.k_cache, a.v_cache, a.pos, a.n_q_heads, a.max_ctx, a.eps, a.q_scale};
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1>),
+                     dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
+                     ep);
+    return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
+}
 
 // Tokens from which Q8_0 products run on the matrix cores (below, the row
 // kernel's passes of up to 4 tokens re-read the weights less often than the

@@ -45,35 +45,6 @@ namespace {
 constexpr int kPrepThreads = 256;
 constexpr int kPrepMaxRow = 2048;  // n_kv_heads * head_dim floats staged per token
 
-__device__ __forceinline__ float serial_sumsq(const float* row, int dim) {
-#pragma clang fp contract(off)
-    float acc = 0.0f;
-    for (int i = 0; i < dim; i += 4) {
-        const float4 v = *(const float4*)(row + i);
-        acc += v.x * v.x;
-        acc += v.y * v.y;
-        acc += v.z * v.z;
-        acc += v.w * v.w;
-    }
-    return acc;
-}
-
-__device__ __forceinline__ float norm_mul(float v, float inv, float w) {
-#pragma clang fp contract(off)
-    return v * inv * w;
-}
-
-__device__ __forceinline__ void rotate(float x0, float x1, float c, float s, float& y0, float& y1) {
-#pragma clang fp contract(off)
-    y0 = x0 * c - x1 * s;
-    y1 = x0 * s + x1 * c;
-}
-
-__device__ __forceinline__ float rope_angle(float pos, float freq_scale, float inv) {
-#pragma clang fp contract(off)
-    return pos * freq_scale * inv;
-}
-
 // Token t: cos/sin of its rope angles (kernels_a.zig:119-122); every kv head's
 // k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX rotation (:125-126),
 // f16 append at slot pos + t (:196-210); v rows f16. Then the q rows of every
@@ -107,12 +78,12 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
     float4 v0 = tid < H * D / 4 ? vrow[tid] : float4{};
     const float pos = (float)a.positions[t];
     for (uint32_t i = tid; i < half; i += kPrepThreads) {
-        const float ang = rope_angle(pos, a.freq_scale, table.inv[i]);
+        const float ang = qk_rope_angle(pos, a.freq_scale, table.inv[i]);
         s_cos[i] = cosf(ang);
         s_sin[i] = sinf(ang);
     }
     __syncthreads();
-    for (uint32_t h = tid; h < H; h += kPrepThreads) s_inv[h] = rms_inv(serial_sumsq(s_k + h * D, (int)D), (float)D, a.eps);
+    for (uint32_t h = tid; h < H; h += kPrepThreads) s_inv[h] = rms_inv(qk_serial_sumsq(s_k + h * D, (int)D), (float)D, a.eps);
     // v rows: f16 append
     for (uint32_t e = tid; e < H * D / 4; e += kPrepThreads) {
         const float4 v = e == tid ? v0 : vrow[e];
@@ -130,9 +101,7 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
             *(float4*)&x1[0] = *(const float4*)(row + half);
             *(float4*)&x1[4] = *(const float4*)(row + half + 4);
         }
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) ss += x0[j] * x0[j] + x1[j] * x1[j];
+        float ss = qk_pairs_sumsq(x0, x1);
 #pragma unroll
         for (uint32_t m = 1; m < TPH; m <<= 1) ss += __shfl_xor(ss, (int)m, 64);
         const float inv = rms_inv(ss, (float)D, a.eps);
@@ -141,10 +110,10 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
         for (int j = 0; j < 8; j++) {
             const uint32_t i = k8 + j;
             float y0, y1;
-            rotate(norm_mul(x0[j], inv, a.q_norm[i]), norm_mul(x1[j], inv, a.q_norm[i + half]), s_cos[i], s_sin[i], y0,
-                   y1);
-            y0v[j] = (f16)(y0 * a.q_scale);
-            y1v[j] = (f16)(y1 * a.q_scale);
+            qk_rotate(qk_norm_mul(x0[j], inv, a.q_norm[i]), qk_norm_mul(x1[j], inv, a.q_norm[i + half]), s_cos[i],
+                      s_sin[i], y0, y1);
+            y0v[j] = qk_scaled_f16(y0, a.q_scale);
+            y1v[j] = qk_scaled_f16(y1, a.q_scale);
         }
         f16* dst = q16 + ((uint64_t)t * HQ + hq) * D;
         *(f16x8*)(dst + k8) = y0v;
@@ -155,10 +124,10 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
     for (uint32_t e = tid; e < H * half; e += kPrepThreads) {
         const uint32_t h = e / half, i = e % half;
         const float inv = s_inv[h];
-        const float y0n = norm_mul(s_k[h * D + i], inv, a.k_norm[i]);
-        const float y1n = norm_mul(s_k[h * D + i + half], inv, a.k_norm[i + half]);
+        const float y0n = qk_norm_mul(s_k[h * D + i], inv, a.k_norm[i]);
+        const float y1n = qk_norm_mul(s_k[h * D + i + half], inv, a.k_norm[i + half]);
         float y0, y1;
-        rotate(y0n, y1n, s_cos[i], s_sin[i], y0, y1);
+        qk_rotate(y0n, y1n, s_cos[i], s_sin[i], y0, y1);
         f16* dst = a.k_cache + ((uint64_t)h * a.max_ctx + a.pos + t) * D;
         dst[i] = (f16)y0;
         dst[i + half] = (f16)y1;
@@ -169,8 +138,9 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
 __global__ __launch_bounds__(256) void q_pack_kernel(const float* q, f16* q16, uint64_t n8, float q_scale) {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n8; i += (uint64_t)gridDim.x * 256) {
         const float4 a = *(const float4*)(q + 8 * i), b = *(const float4*)(q + 8 * i + 4);
-        const f16x8 y = {(f16)(a.x * q_scale), (f16)(a.y * q_scale), (f16)(a.z * q_scale), (f16)(a.w * q_scale),
-                         (f16)(b.x * q_scale), (f16)(b.y * q_scale), (f16)(b.z * q_scale), (f16)(b.w * q_scale)};
+        const f16x8 y = {qk_scaled_f16(a.x, q_scale), qk_scaled_f16(a.y, q_scale), qk_scaled_f16(a.z, q_scale),
+                         qk_scaled_f16(a.w, q_scale), qk_scaled_f16(b.x, q_scale), qk_scaled_f16(b.y, q_scale),
+                         qk_scaled_f16(b.z, q_scale), qk_scaled_f16(b.w, q_scale)};
         *(f16x8*)(q16 + 8 * i) = y;
     }
 }

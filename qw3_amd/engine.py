@@ -14,9 +14,12 @@ Two modes:
 - `fused=False`: exactly the eight provider ops of `assertKernelApi`
   (src/shared/contracts.zig:356-367), one call per reference call;
 - `fused=True`: the optional decls the engine takes via `@hasDecl`: the q/k/v
-  projections as one `matmulGroup`, the q/k norm + rope + append + attention as one
-  `attentionStep`, Wo and its residual as one `matmulAdd`, and the MoE block as one
-  `moe` (router and experts with the pairs kept on the device).
+  projections and the q/k norm + rope + append + attention as one `attentionBlock`
+  (at a prefill the pre-pass runs in the projection GEMM's epilogue, so q, k and v
+  are never written in f32; with a trace callback set, the same work as its two
+  calls, `matmulGroup` then `attentionStep`, which the block equals bit for bit, so
+  the projection trace points exist), Wo and its residual as one `matmulAdd`, and
+  the MoE block as one `moe` (router and experts with the pairs kept on the device).
 Both produce the residual stream of forward.zig within the reference's layer
 tolerance; the per-op calls of the fused mode are bit-identical to the separate ones
 where the ABI says so (matmulGroup, matmulAdd, moe).
@@ -137,7 +140,15 @@ class Engine:
                                             ("attn_q.weight", "attn_k.weight", "attn_v.weight"))
             q_norm, _ = self.w.layer(li, "attn_q_norm.weight")
             k_norm, _ = self.w.layer(li, "attn_k_norm.weight")
-            if self.fused and dq == dk == dv:
+            step = None
+            if self.fused:
+                step = H.AttentionStepArgs(
+                    self.q, self.k, self.v, q_norm, k_norm, self.positions, self.k_cache[li], self.v_cache[li],
+                    self.attn, self.kv_dtype, self.pos, n, hq, hkv, hd, self.capacity, eps, c["rope_theta"], 1.0,
+                    scale)
+            if self.fused and dq == dk == dv and self.trace is None:
+                H.attentionBlock(ctx, H.AttentionBlockArgs(self.h, wq, wk, wv, dq, hidden, step))
+            elif self.fused and dq == dk == dv:
                 H.matmulGroup(ctx, H.MatmulGroupArgs.of(self.h, dq, n, hidden, [
                     (wq, self.q, q_dim), (wk, self.k, kv_dim), (wv, self.v, kv_dim)]))
             else:
@@ -147,12 +158,10 @@ class Engine:
             self._trace(li, "q_proj", self.q, n * q_dim)
             self._trace(li, "k_proj", self.k, n * kv_dim)
             self._trace(li, "v_proj", self.v, n * kv_dim)
-            # fused: q_norm, k_norm, rope_q and rope_k happen inside attentionStep (no trace points)
+            # fused: q_norm, k_norm, rope_q and rope_k happen inside the step (no trace points)
             if self.fused:
-                H.attentionStep(ctx, H.AttentionStepArgs(
-                    self.q, self.k, self.v, q_norm, k_norm, self.positions, self.k_cache[li], self.v_cache[li],
-                    self.attn, self.kv_dtype, self.pos, n, hq, hkv, hd, self.capacity, eps, c["rope_theta"], 1.0,
-                    scale))
+                if not (dq == dk == dv and self.trace is None):
+                    H.attentionStep(ctx, step)
             else:
                 H.rmsNorm(ctx, H.RmsNormArgs(self.q, q_norm, self.q, n * hq, hd, eps))
                 H.rmsNorm(ctx, H.RmsNormArgs(self.k, k_norm, self.k, n * hkv, hd, eps))

@@ -162,6 +162,12 @@ class AttentionStepArgs(C.Structure):
                [(n, C.c_float) for n in ("eps", "theta", "freq_scale", "scale")]
 
 
+class AttentionBlockArgs(C.Structure):
+    """ds5_attention_block_args: the q/k/v projections of x then the attention step."""
+    _fields_ = [("x", Buf), ("wq", Buf), ("wk", Buf), ("wv", Buf), ("w_dtype", C.c_uint32), ("hidden", C.c_uint32),
+                ("step", AttentionStepArgs)]
+
+
 class PagedDecodeArgs(C.Structure):
     _fields_ = [(n, Buf) for n in ("q", "k", "v", "q_norm", "k_norm", "k_pool", "v_pool", "page_table",
                                    "seq_lens", "out")] + \
@@ -203,6 +209,7 @@ SIGNATURES = {
     "ds5_hip_moe": ([_P, C.POINTER(MoeArgs)], C.c_int),
     "ds5_hip_attention_step": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
     "ds5_hip_attention_step_noalloc": ([_P, C.POINTER(AttentionStepArgs)], C.c_int),
+    "ds5_hip_attention_block": ([_P, C.POINTER(AttentionBlockArgs)], C.c_int),
     "ds5_hip_paged_decode": ([_P, C.POINTER(PagedDecodeArgs)], C.c_int),
     "ds5_hip_rope_table": ([C.c_float, C.c_uint32, C.c_void_p], C.c_int),
     "ds5_hip_fill_normal_f16": ([_P, Buf, C.c_uint64, C.c_uint64], C.c_int),
@@ -440,6 +447,12 @@ def matmulGroup(ctx: Ctx, args: MatmulGroupArgs) -> None:
 def attentionStep(ctx: Ctx, args: AttentionStepArgs) -> None:
     """Fused q/k norm + rope + kvAppend + gqaAttention (one engine layer's attention block)."""
     ctx.check(LIB.ds5_hip_attention_step(ctx.handle, C.byref(args)))
+
+
+def attentionBlock(ctx: Ctx, args: AttentionBlockArgs) -> None:
+    """The q/k/v projections of x then attentionStep, as one call (prefill: the pre-pass
+    runs in the projection GEMM's epilogue). No reference counterpart."""
+    ctx.check(LIB.ds5_hip_attention_block(ctx.handle, C.byref(args)))
 
 
 # DS5_NOALLOC_SCRATCH_BYTES (include/ds5_hip.h): the static scratch of the allocation-free entry point

@@ -36,6 +36,7 @@ STRUCTS = {
     "ds5_buf": "Buf", "ds5_rms_norm_args": "RmsNormArgs", "ds5_rope_args": "RopeArgs",
     "ds5_kv_append_args": "KvAppendArgs", "ds5_attn_args": "AttnArgs",
     "ds5_attention_step_args": "AttentionStepArgs", "ds5_paged_decode_args": "PagedDecodeArgs",
+    "ds5_attention_block_args": "AttentionBlockArgs",
     "ds5_matmul_args": "MatmulArgs", "ds5_matmul_group_args": "MatmulGroupArgs", "ds5_add_args": "AddArgs",
     "ds5_matmul_add_args": "MatmulAddArgs", "ds5_router_args": "RouterArgs", "ds5_pair": "Pair",
     "ds5_expert_mlp_args": "ExpertMlpArgs", "ds5_moe_args": "MoeArgs",
