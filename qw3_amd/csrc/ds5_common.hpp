@@ -60,8 +60,10 @@ struct ds5_hip_ctx {
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     bool use_scratch = false;
-    // Decode tuning: positions per split-K workgroup (0 = heuristic).
+    // Decode tuning: positions per split-K workgroup (0 = heuristic); paged
+    // plan: workgroups per launch the plan aims at (0 = two per CU).
     uint32_t decode_chunk = 0;
+    uint32_t plan_items = 0;
     // Optional per-kernel timing: events recorded around every launch on the
     // context stream, resolved at submit / query time.
     bool kernel_timing = false;

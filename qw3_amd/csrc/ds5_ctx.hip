@@ -124,6 +124,7 @@ int ds5_hip_init(int device_index, ds5_hip_ctx** out) {
         return rc;
     }
     if (const char* s = getenv("DS5_HIP_DECODE_CHUNK")) ctx->decode_chunk = (uint32_t)strtoul(s, nullptr, 10);
+    if (const char* s = getenv("DS5_HIP_PLAN_ITEMS")) ctx->plan_items = (uint32_t)strtoul(s, nullptr, 10);
     *out = ctx;
     return DS5_OK;
 }

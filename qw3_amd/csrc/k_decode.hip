@@ -30,7 +30,8 @@
 //
 // Splits combine through a workspace: each workgroup writes its unnormalised
 // O, its reference max and its sum; decode_merge_kernel combines the splits of
-// every (sequence, q head) with one load per split and lane. A single split
+// every (sequence, q head) (one split per lane, or split slots per thread when
+// the rows are many). A single split
 // writes the output directly. Cross-workgroup combining inside one launch was
 // measured to be slower on this part than the second launch.
 //
@@ -48,6 +49,8 @@ constexpr int kWaves = 4;   // wavefronts per workgroup (one per SIMD)
 constexpr int kThreads = kWaves * 64;
 constexpr int kHeads = 16;  // q heads per workgroup (the MFMA N dimension)
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (p <= 2^8 between rescales)
+constexpr uint32_t kMaxSplits = 64;   // splits per sequence at most
+constexpr uint32_t kPlanMaxSeqs = 4096;  // paged plan: lengths staged in the V staging area
 
 struct DecodeParams {
     const float* q;
@@ -68,6 +71,10 @@ struct DecodeParams {
     uint32_t ctx_len, max_len, chunk, n_splits;
     uint32_t n_q_heads, n_kv_heads, group, n_sub;
     float scale_log2, eps, freq_scale;
+    // paged plan (see paged_plan): plan != nullptr when the workgroups take their
+    // (sequence, split) from it; plan[0] receives the chunk for the merge
+    uint32_t* plan;
+    uint32_t plan_cap, n_seqs;
 };
 
 template <int D>
@@ -349,6 +356,126 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Paged plan. Sequence lengths differ, so splits of one size taken over the
+// longest sequence leave most workgroups short or idle and the longest splits
+// set the launch time. Every workgroup of a paged launch computes the same plan
+// from the device-side lengths (no extra launch, no host round trip): the
+// smallest chunk c -- a multiple of 128, at least max_len / kMaxSplits -- whose
+// item count sum_b ceil(L_b / c) fits plan_cap items (the grid's x extent);
+// workgroup x takes item x. A length outside [1, max_len] counts one item
+// (split 0 poisons that sequence's output).
+struct PagedItem {
+    int32_t b;  // -1: no item for this workgroup
+    uint32_t split, chunk;
+};
+
+__device__ __forceinline__ uint32_t plan_items(uint32_t len, uint32_t c) { return len == 0 ? 1u : (len + c - 1) / c; }
+
+// s_len: n_seqs words of LDS; s_red: kThreads / 64 + 2 words
+__device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_len, uint32_t* s_red) {
+    constexpr int NW = kThreads / 64;
+    constexpr uint32_t kStep = kWaves * kTile;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t n = p.n_seqs;
+    for (uint32_t i = tid; i < n; i += kThreads) {
+        const int32_t len = p.seq_lens[i];
+        s_len[i] = (len < 1 || (uint32_t)len > p.max_len) ? 0u : (uint32_t)len;
+    }
+    __syncthreads();
+    // thread t owns sequences [b0, b1)
+    const uint32_t per = (n + kThreads - 1) / kThreads;
+    const uint32_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
+    auto count = [&](uint32_t c) {
+        uint32_t k = 0;
+        for (uint32_t i = b0; i < b1; i++) k += plan_items(s_len[i], c);
+        return k;
+    };
+    auto block_sum = [&](uint32_t v) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        __syncthreads();  // s_red's previous readers are done
+        if (lane == 0) s_red[wave] = v;
+        __syncthreads();
+        uint32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) t += s_red[w];
+        return t;
+    };
+    // binary search over c = cmin + kStep k: the count does not grow with c, and
+    // c = max_len (rounded up) gives one item per sequence, which the cap admits
+    const uint32_t cmin = max(kStep, (p.max_len + kMaxSplits - 1) / kMaxSplits + kStep - 1) / kStep * kStep;
+    uint32_t lo = 0, hi = ((p.max_len + kStep - 1) / kStep * kStep - min(cmin, (p.max_len + kStep - 1) / kStep * kStep)) / kStep;
+    while (lo < hi) {  // uniform
+        const uint32_t mid = (lo + hi) / 2;
+        if (block_sum(count(cmin + kStep * mid)) <= p.plan_cap)
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    const uint32_t chunk = cmin + kStep * lo;
+    // Item order: every sequence's whole chunks first (in sequence order), then the
+    // partial last chunks (and poisoned sequences): consecutive workgroups go to
+    // consecutive XCDs, so the equal-sized items spread evenly over the XCDs and
+    // start first. Exclusive prefixes of both counts over the owners, then the
+    // owner of item x.
+    uint32_t mf = 0, mt = 0;
+    for (uint32_t i = b0; i < b1; i++) {
+        const uint32_t L = s_len[i];
+        mf += L / chunk;
+        mt += (L == 0 || L % chunk != 0) ? 1u : 0u;
+    }
+    auto block_scan = [&](uint32_t v, uint32_t& total) {
+        uint32_t incl = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        __syncthreads();
+        if (lane == 63) s_red[wave] = incl;
+        __syncthreads();
+        uint32_t base = 0;
+        total = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            base += w < wave ? s_red[w] : 0u;
+            total += s_red[w];
+        }
+        return base + incl - v;
+    };
+    uint32_t F, T;
+    const uint32_t ef = block_scan(mf, F);
+    const uint32_t et = block_scan(mt, T);
+    __syncthreads();  // s_red's scan readers are done
+    if (x < F && x >= ef && x < ef + mf) {  // whole chunk
+        uint32_t acc = ef;
+        for (uint32_t i = b0; i < b1; i++) {
+            const uint32_t k = s_len[i] / chunk;
+            if (x < acc + k) {
+                s_red[NW] = i;
+                s_red[NW + 1] = x - acc;
+                break;
+            }
+            acc += k;
+        }
+    } else if (x >= F && x - F >= et && x - F < et + mt) {  // partial last chunk
+        uint32_t acc = et;
+        for (uint32_t i = b0; i < b1; i++) {
+            const uint32_t L = s_len[i];
+            if (L == 0 || L % chunk != 0) {
+                if (x - F == acc) {
+                    s_red[NW] = i;
+                    s_red[NW + 1] = L / chunk;
+                    break;
+                }
+                acc++;
+            }
+        }
+    }
+    __syncthreads();
+    return PagedItem{x < F + T ? (int32_t)s_red[NW] : -1, s_red[NW + 1], chunk};
+}
+
 // ONE: every wavefront has at most one tile (chunk <= kWaves * kTile). That case
 // gets a kernel of its own without the prefetch loop: the loop's four tile
 // bodies double the code, and a decode launch is short enough for instruction
@@ -391,9 +518,22 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
-    const uint32_t split = blockIdx.x;
+    uint32_t split = blockIdx.x, b = blockIdx.z, chunk = p.chunk;
     const uint32_t kvh = blockIdx.y / p.n_sub, sub = blockIdx.y % p.n_sub;
-    const uint32_t b = blockIdx.z;
+    if constexpr (PAGED) {
+        if (p.plan) {
+            __shared__ uint32_t s_plan[kThreads / 64 + 2];
+            static_assert(kPlanMaxSeqs * 4 <= sizeof(s_big), "the plan's lengths fit the staging area");
+            const PagedItem it = paged_plan(p, blockIdx.x, (uint32_t*)s_big, s_plan);
+            if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) p.plan[0] = it.chunk;  // for the merge
+            if (it.b < 0) return;  // uniform: no item
+            // uniform values read from LDS: scalar registers, so the page-table
+            // lookups stay scalar loads (outside the vector loads' issue order)
+            b = (uint32_t)__builtin_amdgcn_readfirstlane(it.b);
+            split = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.split);
+            chunk = (uint32_t)__builtin_amdgcn_readfirstlane((int)it.chunk);
+        }
+    }
     const uint32_t n0 = sub * kHeads;
     const int NS = (int)min((uint32_t)kHeads, p.group - n0);
     const uint32_t hq0 = kvh * p.group + n0;  // first q head of this workgroup
@@ -410,9 +550,9 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
         }
         L = (uint32_t)len;
     }
-    const uint32_t start = split * p.chunk;
+    const uint32_t start = split * chunk;
     if (start >= L) return;  // uniform: this split is past the sequence
-    const uint32_t end = min(L, start + p.chunk);
+    const uint32_t end = min(L, start + chunk);
     const uint32_t n_tiles = (end - start + kTile - 1) / kTile;
     const uint32_t newpos = L - 1;
     const bool has_new = FUSED && newpos >= start && newpos < end;
@@ -613,7 +753,7 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     bool poison = false;
 #pragma unroll
     for (int w = 0; w < W; w++) poison |= s_badw[w] != 0;
-    const bool single = p.n_splits == 1;
+    const bool single = L <= chunk;  // the sequence's only split writes the output itself
     for (int q4 = tid; q4 < NS * (D / 4); q4 += kThreads) {
         const int n = q4 / (D / 4), d0 = (q4 % (D / 4)) * 4;
         float M = s_m[0][n];
@@ -640,12 +780,15 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     }
 }
 
-// Split merge: block = 4 wavefronts = 4 groups of 4 output dims of one
-// (sequence, q head); lane s holds split s (n_splits <= 64). One load per
-// lane, then fixed-order DPP / permlane reductions (VALU only), so results are
-// deterministic.
+// Split merge, two forms; both fold the splits of one (sequence, q head) in a
+// fixed order, so results are deterministic.
+//
+// Lanes (at most 64 splits; few rows): block = 4 wavefronts = 4 groups of 4
+// output dims of one (sequence, q head); lane s holds split s. One load per
+// lane, then DPP / permlane reductions (VALU only): the shortest chain, for
+// a grid of rows x D/16 workgroups that fills the chip at most a few times.
 template <int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+__device__ __forceinline__ void merge_lanes(const DecodeParams& p) {
     const uint64_t qi = blockIdx.x;  // sequence * n_q_heads + head
     const uint32_t b = (uint32_t)(qi / p.n_q_heads);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -656,7 +799,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
         if (len < 1 || (uint32_t)len > p.max_len) return;  // poisoned by the split kernel
         L = (uint32_t)len;
     }
-    const uint32_t ns = (L + p.chunk - 1) / p.chunk;
+    const uint32_t chunk = p.plan ? p.plan[0] : p.chunk;
+    const uint32_t ns = (L + chunk - 1) / chunk;
+    if (ns <= 1) return;  // written by its split
     float m = -INFINITY, l = 0.0f;
     float4 o = {0.f, 0.f, 0.f, 0.f};
     if ((uint32_t)lane < ns) {
@@ -678,6 +823,77 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
     o.z = wave_allreduce(o.z, OpAdd{});
     o.w = wave_allreduce(o.w, OpAdd{});
     if (lane == 0) *(float4*)(p.out + qi * D + d0) = float4{o.x / l, o.y / l, o.z / l, o.w / l};
+}
+
+// Slots (any number of splits; many rows): one workgroup per (sequence, q
+// head). Thread (slot, column) takes splits slot, slot + SLOTS, ... of one
+// float4 column of O, eight loads in flight at a time, and folds them in split
+// order with a running maximum; the slots then combine through LDS in slot order.
+template <int D>
+__device__ __forceinline__ void merge_slots(const DecodeParams& p) {
+    constexpr int COLS = D / 4, SLOTS = 256 / COLS, BATCH = 8;
+    __shared__ float4 s_o[SLOTS][COLS];
+    __shared__ float2 s_ml[SLOTS];
+    const uint64_t qi = blockIdx.x;  // sequence * n_q_heads + head
+    const uint32_t b = (uint32_t)(qi / p.n_q_heads);
+    const int col = threadIdx.x % COLS, slot = threadIdx.x / COLS;
+    uint32_t L = p.ctx_len;
+    if (p.seq_lens) {
+        const int32_t len = p.seq_lens[b];
+        if (len < 1 || (uint32_t)len > p.max_len) return;  // poisoned by the split kernel
+        L = (uint32_t)len;
+    }
+    const uint32_t chunk = p.plan ? p.plan[0] : p.chunk;
+    const uint32_t ns = (L + chunk - 1) / chunk;
+    if (ns <= 1) return;  // written by its split
+    const float2* ml_row = (const float2*)p.part_ml + qi * p.n_splits;
+    const float* o_row = p.part_o + qi * p.n_splits * D + 4 * col;
+    float m = -INFINITY, l = 0.0f;
+    float4 o = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s0 = slot; s0 < ns; s0 += SLOTS * BATCH) {
+        float2 ml[BATCH];
+        float4 os[BATCH];
+#pragma unroll
+        for (int k = 0; k < BATCH; k++) {  // unconditional loads, clamped to a valid split
+            const uint32_t s = min(s0 + SLOTS * k, ns - 1);
+            ml[k] = ml_row[s];
+            os[k] = *(const float4*)(o_row + (uint64_t)s * D);
+        }
+#pragma unroll
+        for (int k = 0; k < BATCH; k++) {
+            if (s0 + SLOTS * k >= ns) break;
+            const float mn = fmaxf(m, ml[k].x);       // every split has a position: ml.x is finite
+            const float a = fast_exp2(m - mn), w = fast_exp2(ml[k].x - mn);  // m = -inf: a = 0
+            l = l * a + ml[k].y * w;
+            o = o * a + os[k] * w;
+            m = mn;
+        }
+    }
+    s_o[slot][col] = o;
+    if (col == 0) s_ml[slot] = float2{m, l};
+    __syncthreads();
+    if (slot == 0) {
+        float M = s_ml[0].x;
+#pragma unroll
+        for (int t = 1; t < SLOTS; t++) M = fmaxf(M, s_ml[t].x);  // slot 0 always has split 0
+        float lt = 0.0f;
+        float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < SLOTS; t++) {
+            const float w = fast_exp2(s_ml[t].x - M);  // an empty slot: -inf - M, weight 0
+            lt += s_ml[t].y * w;
+            acc += s_o[t][col] * w;
+        }
+        *(float4*)(p.out + qi * D + 4 * col) = acc / lt;
+    }
+}
+
+template <int D, bool SLOTS_FORM>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+    if constexpr (SLOTS_FORM)
+        merge_slots<D>(p);
+    else
+        merge_lanes<D>(p);
 }
 
 template <int D, bool FUSED, bool PAGED, bool PACK, bool ONE>
@@ -703,7 +919,8 @@ int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams&
     const bool paged = a.page_table != nullptr;
     const RopeTable& tab = a.fused ? *a.table : RopeTable{};
     // groups of at most 8 heads use the packed hi/lo columns (half the products)
-    const bool pack = prm.group <= kHeads / 2, one = prm.chunk <= kWaves * kTile;
+    // (a planned launch's chunk is chosen on the device: the looping kernel)
+    const bool pack = prm.group <= kHeads / 2, one = prm.plan == nullptr && prm.chunk <= kWaves * kTile;
     if (pack && one)
         launch_split<D, true, true>(ctx, a.fused, paged, prm, tab, grid);
     else if (pack)
@@ -714,16 +931,21 @@ int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams&
         launch_split<D, false, false>(ctx, a.fused, paged, prm, tab, grid);
     int rc = ds5_after_launch(ctx, "decode_split_kernel");
     if (rc || prm.n_splits == 1) return rc;
-    DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", decode_merge_kernel<D>, dim3(a.n_seqs * a.n_q_heads, D / 16), dim3(256), 0,
-                     ctx->stream, prm);
+    const uint64_t rows = (uint64_t)a.n_seqs * a.n_q_heads;
+    if (prm.n_splits <= 64 && rows * (D / 16) <= 4ull * (ctx->cu_count > 0 ? ctx->cu_count : 256))
+        DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", (decode_merge_kernel<D, false>), dim3(rows, D / 16), dim3(256), 0,
+                         ctx->stream, prm);
+    else
+        DS5_TIMED_LAUNCH(ctx, "decode_merge_kernel", (decode_merge_kernel<D, true>), dim3(rows), dim3(256), 0,
+                         ctx->stream, prm);
     return ds5_after_launch(ctx, "decode_merge_kernel");
 }
 
 }  // namespace
 
 // Positions per split: about four workgroups per CU over the longest sequence,
-// whole 128-position steps (one 32-position tile per wavefront), at most 64
-// splits (the merge kernel's lane count).
+// whole 128-position steps (one 32-position tile per wavefront), at most
+// kMaxSplits splits (bounds the partials).
 static DecodeGeometry decode_geometry_of(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_kv_heads, uint32_t n_sub,
                                          uint32_t max_len) {
     constexpr uint32_t kStep = kWaves * kTile;
@@ -734,7 +956,7 @@ static DecodeGeometry decode_geometry_of(const ds5_hip_ctx* ctx, uint32_t n_seqs
         chunk = (uint32_t)std::min<uint64_t>((max_len * units + target - 1) / target, max_len);
     }
     chunk = std::max<uint32_t>((chunk + kStep - 1) / kStep * kStep, kStep);
-    chunk = std::max<uint32_t>(chunk, (max_len + 63) / 64);
+    chunk = std::max<uint32_t>(chunk, (max_len + kMaxSplits - 1) / kMaxSplits);
     chunk = (chunk + kStep - 1) / kStep * kStep;
     return DecodeGeometry{chunk, (max_len + chunk - 1) / chunk};
 }
@@ -754,8 +976,23 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
     const uint32_t n_sub = (group + kHeads - 1) / kHeads;
     const uint32_t max_len = a.max_len;
     if (a.n_seqs == 0 || max_len == 0) return DS5_OK;
-    const DecodeGeometry geo = decode_geometry_of(ctx, a.n_seqs, a.n_kv_heads, n_sub, max_len);
-    const uint32_t chunk = geo.chunk, n_splits = geo.n_splits;
+    const bool planned = a.page_table != nullptr && a.n_seqs <= kPlanMaxSeqs;
+    const uint32_t cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const uint32_t units = a.n_kv_heads * n_sub;
+    // planned: about two workgroups per CU (measured at C4 against one, three and
+    // four: one and two are equal and fastest), at least one item per sequence
+    const uint32_t target = ctx->plan_items ? ctx->plan_items : 2 * cu;
+    const uint32_t plan_cap = planned ? std::max<uint32_t>((target + units - 1) / units, a.n_seqs) : 0;
+    const DecodeGeometry geo = planned ? DecodeGeometry{0, kMaxSplits}
+                                       : decode_geometry_of(ctx, a.n_seqs, a.n_kv_heads, n_sub, max_len);
+    const uint32_t chunk = geo.chunk;
+    // planned: the partials' layout keeps kMaxSplits slots per row; a launch whose
+    // smallest chunk covers max_len has one split per sequence
+    constexpr uint32_t kStep = kWaves * kTile;
+    const bool may_split = planned ? (max_len + kStep - 1) / kStep * kStep >
+                                         std::max(kStep, (max_len + kMaxSplits - 1) / kMaxSplits + kStep - 1) / kStep * kStep
+                                   : geo.n_splits > 1;
+    const uint32_t n_splits = may_split ? geo.n_splits : 1;
 
     DecodeParams prm{};
     prm.q = a.q;
@@ -784,15 +1021,18 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
     prm.scale_log2 = a.scale * kLog2e;
     prm.eps = a.eps;
     prm.freq_scale = a.freq_scale;
-    if (n_splits > 1) {
-        const size_t n_part = (size_t)a.n_seqs * a.n_q_heads * n_splits;
+    prm.n_seqs = a.n_seqs;
+    prm.plan_cap = plan_cap;
+    if (n_splits > 1 || planned) {
+        const size_t n_part = n_splits > 1 ? (size_t)a.n_seqs * a.n_q_heads * n_splits : 0;
         void* ws = nullptr;
-        int rc = ds5_workspace(ctx, n_part * ((size_t)a.head_dim + 2) * sizeof(float), &ws);
+        int rc = ds5_workspace(ctx, n_part * ((size_t)a.head_dim + 2) * sizeof(float) + 16, &ws);
         if (rc) return rc;
         prm.part_o = (float*)ws;
         prm.part_ml = prm.part_o + n_part * a.head_dim;
+        if (planned) prm.plan = (uint32_t*)(prm.part_ml + 2 * n_part);
     }
-    const dim3 grid(n_splits, a.n_kv_heads * n_sub, a.n_seqs);
+    const dim3 grid = planned ? dim3(plan_cap, units, 1) : dim3(n_splits, units, a.n_seqs);
     if (a.head_dim == 128) return launch_decode_d<128>(ctx, a, prm, grid);
     return launch_decode_d<64>(ctx, a, prm, grid);
 }

@@ -9,7 +9,7 @@ from exactly such arithmetic (an offset that went negative and wrapped as an
 unsigned 32-bit value); a replica catches that class of mistake on the CPU.
 
 Replicated:
-  qw3_amd/csrc/k_decode.hip  decode_geometry_of, issue_tile, the q-operand and
+  qw3_amd/csrc/k_decode.hip  decode_geometry_of, paged_plan, issue_tile, the q-operand and
                              new-row accesses and the partial stores of
                              decode_split_kernel (contiguous and paged caches)
   qw3_amd/csrc/k_matmul.hip  load_block of matmul_q8_mfma_kernel (x planes, Q8_0
@@ -47,6 +47,24 @@ def decode_geometry(n_seqs, n_kv_heads, n_sub, max_len, cu_count=256, decode_chu
     return chunk, (max_len + chunk - 1) // chunk
 
 
+def paged_plan(lens, max_len, n_kv_units, cu_count=256, max_splits=64):
+    """paged_plan (k_decode.hip): the smallest chunk (a multiple of 128, at least
+    max_len / max_splits) whose item count sum_b ceil(L_b / chunk) fits the cap; a
+    length outside [1, max_len] counts one item. Returns (chunk, cap, items)."""
+    step = K_WAVES * K_TILE
+    cap = max((2 * cu_count + n_kv_units - 1) // n_kv_units, len(lens))
+    lens = [int(L) if 1 <= int(L) <= max_len else 0 for L in lens]
+    cmin = max(step, -(-max_len // max_splits) + step - 1) // step * step
+    cmax = -(-max_len // step) * step
+    count = lambda c: sum(1 if L == 0 else -(-L // c) for L in lens)
+    chunk = next(c for c in range(cmin, cmax + 1, step) if count(c) <= cap)
+    # whole chunks of every sequence first, then the partial last chunks (and poisoned sequences)
+    items = [(b, sp) for b, L in enumerate(lens) for sp in range(L // chunk)]
+    items += [(b, L // chunk) for b, L in enumerate(lens) if L == 0 or L % chunk]
+    assert len(items) <= cap
+    return chunk, cap, items
+
+
 def tile_rows(p0, end, D, paged, page_row=None):
     """issue_tile: the cache rows (positions, or pool slots when paged) of the K and V
     loads of the tile starting at p0, and each load's element offset inside its row:
@@ -82,13 +100,19 @@ def check_decode(n_seqs, hq, hkv, D, lens, cache_stride, page_size=0, page_table
     group = hq // hkv
     n_sub = (group + K_HEADS - 1) // K_HEADS
     max_len = max_len if max_len is not None else int(max(lens))
-    chunk, n_splits = decode_geometry(n_seqs, hkv, n_sub, max_len)
     paged = page_table is not None
+    if paged:  # planned launch: chunk from the lengths, kMaxSplits partial slots per row
+        chunk, _, items = paged_plan(lens, max_len, hkv * n_sub)
+        n_splits = 64
+        assert all(sp < n_splits for _, sp in items)
+    else:
+        chunk, n_splits = decode_geometry(n_seqs, hkv, n_sub, max_len)
     cache_elems = hkv * cache_stride * D            # per K (and V) cache, f16 elements
     q_elems = n_seqs * hq * D
     part_elems = n_seqs * hq * n_splits * D if n_splits > 1 else 0
     TPH = D // 8
     checked = 0
+    item_set = set(items) if paged else set()
     for b in range(n_seqs):
         L = int(lens[b]) if len(lens) > 1 else int(lens[0])
         if paged and not (1 <= L <= max_len):
@@ -106,6 +130,7 @@ def check_decode(n_seqs, hq, hkv, D, lens, cache_stride, page_size=0, page_table
                     start = split * chunk
                     if start >= L:
                         continue
+                    assert not paged or (b, split) in item_set  # every split the kernel reads has a workgroup
                     end = min(L, start + chunk)
                     n_tiles = (end - start + K_TILE - 1) // K_TILE
                     newpos = L - 1
@@ -170,6 +195,23 @@ def test_decode_paged_addresses_config4():
     n = check_decode(cfg["n_seqs"], s.n_q_heads, s.n_kv_heads, s.head_dim, lay.seq_lens, lay.n_pages * 16, 16,
                      lay.page_table, lay.n_pages, int(lay.seq_lens.max()))
     assert n > 0
+
+
+def test_paged_plan_fits_and_is_smallest():
+    """The plan's chunk is the smallest admissible one: the next smaller multiple of
+    128 (when admissible) overflows the cap. C4's lengths give ~2 workgroups per CU."""
+    cfg = synth.CONFIGS[4]
+    lay = synth.paged_layout(cfg["n_seqs"], cfg["lo"], cfg["hi"], cfg["page_size"], seed=0)
+    max_len = int(lay.seq_lens.max())
+    chunk, cap, items = paged_plan(lay.seq_lens, max_len, 4)
+    assert cap == 128 and len(items) <= cap and chunk % 128 == 0
+    smaller = chunk - 128
+    if smaller >= max(128, -(-max_len // 64)):
+        assert sum(-(-int(L) // smaller) for L in lay.seq_lens) > cap
+    # every position of every sequence is in exactly one item
+    for b, L in enumerate(lay.seq_lens):
+        spans = sorted(sp for bb, sp in items if bb == b)
+        assert spans == list(range(-(-int(L) // chunk)))
 
 
 def test_decode_paged_addresses_invalid_entries():
