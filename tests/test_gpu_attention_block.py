@@ -150,3 +150,33 @@ def test_attention_block_errors(ctx, hip, oracle):
     ctx.submit()
     assert np.array_equal(ctx.to_numpy(a.k_cache, np.uint16, inp.kc.shape), inp.kc)
     assert np.array_equal(ctx.to_numpy(a.v_cache, np.uint16, inp.vc.shape), inp.vc)
+
+
+@pytest.mark.parametrize("case", ["t300_64q", "t8_rows"])
+def test_attention_block_graph_replays(ctx, hip, oracle, case):
+    """The block captured into a HIP graph (fused prefill path and the two-call path),
+    replayed three times with eager work and synchronisations between the replays:
+    every replay's output and cache rows equal the eager call's, bit for bit."""
+    inp = _Inputs(ctx, hip, oracle, case)
+    a = inp.step_args(ctx, hip)
+    block = hip.AttentionBlockArgs(inp.xb, *inp.wb, inp.dtype, inp.hidden, a)
+    hip.attentionBlock(ctx, block)  # eager; also sizes the workspace before the capture
+    want = inp.results(ctx, a)
+    other = inp.step_args(ctx, hip)
+    g = ctx.capture(lambda: hip.attentionBlock(ctx, block))
+    try:
+        for r in range(3):
+            ctx.upload(a.out, 0, np.zeros(inp.T * inp.hq * inp.hd, np.float32))
+            ctx.upload(a.k_cache, 0, inp.kc)  # the replay appends the same rows again
+            ctx.upload(a.v_cache, 0, inp.vc)
+            hip.attentionBlock(ctx, hip.AttentionBlockArgs(inp.xb, *inp.wb, inp.dtype, inp.hidden, other))
+            ctx.submit()
+            g.launch()
+            ctx.submit()
+            got = inp.results(ctx, a)
+            same = [np.array_equal(x.view(np.uint8), y.view(np.uint8)) for x, y in zip(got, want)]
+            print(f"  replay {r}: out/k/v bit-identical {same}", flush=True)
+            assert all(same)
+        assert all(np.array_equal(x.view(np.uint8), y.view(np.uint8)) for x, y in zip(inp.results(ctx, other), want))
+    finally:
+        g.destroy()
