@@ -408,6 +408,14 @@ def test_paged_decode_config4_geometry(ctx, hip, oracle):
     _paged_case(ctx, hip, oracle, 32, 512, 16384, seed=0)
 
 
+def test_paged_decode_large_batch_unplanned(ctx, hip, oracle):
+    """More sequences than the device-side plan stages (4096): the launch falls back to
+    the (split, kv head, sequence) grid sized from the longest sequence, here one split
+    per sequence whose workgroup writes the output itself. A sample of sequences
+    against the oracle; every pool row outside the new slots byte-identical."""
+    _paged_case(ctx, hip, oracle, 4100, 1, 40, seed=9, check_seqs=[0, 1, 777, 2048, 4095, 4096, 4099])
+
+
 def test_paged_decode_invalid_entries(ctx, hip, oracle):
     """Device-side entries the host cannot check: a page id outside the pool and
     sequence lengths outside [1, max_seq_len] are never dereferenced; those
