@@ -2,9 +2,9 @@
  * ds5_hip.h -- C ABI of the MI355X (gfx950) backend for DS5's attention path.
  *
  * libds5hip.so is a third kernel backend beside DS5's `cpu` and `metal`
- * providers. The Zig host binds it with @cImport (the binding is shown in
- * INTEGRATION.md); every entry point takes plain pointers, sizes and the
- * structs below, never a torch type.
+ * providers. The Zig host binds it with @cImport of this header; every entry
+ * point takes plain pointers, sizes and the structs below, never a torch
+ * type.
  *
  * Two groups of entry points:
  *   1. the device context, one per engine, replacing the frozen GPU API
