@@ -181,9 +181,14 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
 // context workspace; matmul_q8_mfma_kernel then only copies x tiles.
 //
 // GEMM workgroup: BM tokens x BN weight rows, WM x WN wavefronts, each with
-// TM x TN tiles of 16 x 16. Per block, the workgroup stages x (hi and lo
-// planes) and q (as f16) and the BN scales in LDS, double-buffered: the next
-// block's global loads are in flight while the current block is multiplied.
+// TM x TN tiles of 16 x 16. Per block the workgroup stages x (hi and lo
+// planes), q (as f16) and the BN scales in LDS. The loop is bound by memory
+// latency, not by the matrix cores: every load is issued two blocks before the
+// block is multiplied. x goes HBM/L2 -> LDS with direct-to-LDS loads into a
+// ring of three stages; each thread's 8-byte q run and its row's scale go to
+// registers (three sets) and are converted to f16 into LDS one block ahead.
+// One workgroup barrier per block. The loads are inline asm with explicit
+// vmcnt waits (the compiler's waits would cover the later blocks' loads too).
 // LDS rows are 32 halves (four 16-byte chunks) with chunk c of row r stored at
 // c ^ ((r >> 2) & 3), so a 16-lane group reading one chunk of 16 rows hits 16
 // distinct bank groups.
@@ -274,6 +279,44 @@ __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t u) {
     return uint2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
 
+// Workgroup barrier that orders LDS only: global loads stay in flight across it.
+__device__ __forceinline__ void gemm_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ uint32_t gemm_lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p;
+}
+
+// Wave-uniform 64-bit value made explicitly scalar (an asm "s" operand).
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+
+// Wait until at most N vector-memory operations of this wavefront are
+// outstanding (the compiler does not count inline-asm loads).
+template <int N>
+__device__ __forceinline__ void wait_vm_only() {
+    static_assert(N >= 0 && N < 16, "vmcnt field");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Direct-to-LDS load: 16 (DW = 4) or 4 (DW = 1) bytes per lane from base + off
+// to LDS address lds + lane * 4 DW.
+template <int DW>
+__device__ __forceinline__ void lds_dma(uint32_t off, uint64_t base, uint32_t lds) {
+    if constexpr (DW == 4)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                     : "m0", "memory");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds)
+                     : "m0", "memory");
+}
+
 // EPI = 1: the attention block's q / k / v projections (entries 0, 1, 2 of the
 // group), 128 x 128 tiles: a tile is 128 tokens of one head's 128 dims, and
 // the epilogue turns it into what the prefill attention reads -- k: RMSNorm
@@ -292,7 +335,7 @@ struct AttnPrepEpi {
     float eps, q_scale;
 };
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, int PD>
 __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
@@ -317,20 +360,23 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     constexpr int kThreads = WM * WN * 64;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "tile split");
-    constexpr int kAPer = BM * 8 / kThreads;  // 16-byte x chunks (both planes) per thread and block
     constexpr int kBPer = BN * 4 / kThreads;  // 8-byte q runs per thread and block
-    static_assert(kAPer >= 1 && kBPer >= 1, "at least one staging unit per thread");
+    static_assert(kBPer >= 1, "at least one q run per thread");
 
-    // LDS: As [buffer][hi, lo][row * 4 + swizzled chunk], Bs [buffer][row * 4 +
-    // swizzled chunk], Ss [buffer][row]; EPI 1 reuses the bytes for the f32 tile
-    constexpr int kAsBytes = 2 * 2 * BM * 4 * 16, kBsBytes = 2 * BN * 4 * 16, kSsBytes = 2 * BN * 4;
-    constexpr int kMainBytes = kAsBytes + kBsBytes + kSsBytes;
+    // LDS: As [stage][hi, lo][row * 4 + swizzled chunk], raw q [stage][row][9 dwords],
+    // Bs [buffer][row * 4 + swizzled chunk], Ss [buffer][row]; EPI 1 reuses the bytes
+    // for the f32 tile
+    static_assert(PD == 1 || PD == 2, "prefetch depth");
+    constexpr int kStages = PD + 2;
+    constexpr int kAsBytes = kStages * 2 * BM * 4 * 16, kRawBytes = kStages * BN * 36, kBsBytes = 2 * BN * 4 * 16,
+                  kSsBytes = 2 * BN * 4;
+    constexpr int kMainBytes = kAsBytes + kRawBytes + kBsBytes + kSsBytes;
     constexpr int kTileRow = BN + 4;  // EPI 1 tile row stride in floats (16-byte rows, rows 4 banks apart)
     constexpr int kLdsBytes = EPI == 1 && BM * kTileRow * 4 > kMainBytes ? BM * kTileRow * 4 : kMainBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsBytes];
-    auto& As = *reinterpret_cast<u32x4_t(*)[2][2][BM * 4]>(smem);
-    auto& Bs = *reinterpret_cast<u32x4_t(*)[2][BN * 4]>(smem + kAsBytes);
-    auto& Ss = *reinterpret_cast<float(*)[2][BN]>(smem + kAsBytes + kBsBytes);
+    auto& As = *reinterpret_cast<u32x4_t(*)[kStages][2][BM * 4]>(smem);
+    auto& Bs = *reinterpret_cast<u32x4_t(*)[2][BN * 4]>(smem + kAsBytes + kRawBytes);
+    auto& Ss = *reinterpret_cast<float(*)[2][BN]>(smem + kAsBytes + kRawBytes + kBsBytes);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -338,49 +384,120 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     const uint32_t nb = k / 32;
     const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
 
-    // ---- staging: this thread's x chunks and q runs of one block -------------
-    u32x4_t xa[kAPer];
-    uint32_t qd[kBPer][3];
-    uint32_t qsh[kBPer];
-    uint32_t sbits[kBPer];  // scale bits of the run's block (read by part-0 threads)
-    auto load_block = [&](uint32_t b) {
+    // ---- staging ------------------------------------------------------------------
+    // All global loads are direct-to-LDS, issued ahead and awaited explicitly:
+    // iteration b issues x of block b + PD + 1 and the raw q of block b + PD + 2
+    // (one group of loads), converts block b + 1's raw q to f16, multiplies
+    // block b, then waits until at most its last PD groups are outstanding and
+    // meets the barrier, so a load has PD iterations to land. Block j uses x
+    // stage j % (PD + 2), raw q stage j % (PD + 2) and f16 q buffer j % 2.
+    constexpr int kXStage = 2 * BM * 64;  // bytes: hi plane rows, then lo plane rows
+    constexpr int kRowDw = 9;             // raw q row: the 9 dwords covering a 34-byte block
+    constexpr int kQStage = BN * kRowDw * 4;
+    constexpr int W = WM * WN;
+    constexpr int NX = kXStage / 1024 / W;  // x loads per wavefront and block
+    static_assert(NX >= 1 && NX * 1024 * W == kXStage, "whole 1 KB x loads per wavefront");
+    static_assert((BM * 64) % 1024 == 0, "an x load stays inside one plane");
+    constexpr int kQLoads = (BN * kRowDw + 63) / 64;  // raw q loads (256 bytes each) per workgroup and block
+    constexpr int NQ = (kQLoads + W - 1) / W;         // at most, per wavefront
+    static_assert(BN * kRowDw % 64 == 0 && NQ <= 3, "raw q stage in whole loads");
+    const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+    const bool q_extra = wave_u + W * (NQ - 1) < (uint32_t)kQLoads;  // uniform: this wavefront issues NQ, else NQ - 1
+    const uint32_t smem_lds = gemm_lds_addr(smem);
+
+    // x: load i of this wavefront fills stage bytes [1024 (wave + W i), +1024), lane L
+    // the 16 bytes at +16 L: plane, row r, slot L % 4 holding chunk (L % 4) ^ ((r >> 2) & 3).
+    uint32_t xoff[NX];  // byte offset in the plane: row min(m0 + r, m - 1), chunk c, block 0
 #pragma unroll
-        for (int u = 0; u < kAPer; u++) {
-            const uint32_t c = threadIdx.x + kThreads * u;  // plane c / (4 BM), row (c / 4) % BM, chunk c % 4
-            const uint32_t row = min(m0 + ((c >> 2) % BM), m - 1);
-            const uint16_t* src = c < 4 * BM ? xhi : xlo;
-            xa[u] = *(const u32x4_t*)(src + (uint64_t)row * k + 32 * b + 8 * (c & 3));
-        }
+    for (int i = 0; i < NX; i++) {
+        const uint32_t o = 1024u * (wave_u + W * i) + 16u * lane;
+        const uint32_t r = (o % (BM * 64)) / 64, c = (uint32_t)(lane & 3) ^ ((r >> 2) & 3);
+        xoff[i] = min(m0 + r, m - 1) * k * 2 + 16 * c;
+    }
+    auto issue_x = [&](uint32_t b, int stage) {
 #pragma unroll
-        for (int u = 0; u < kBPer; u++) {
-            const uint32_t c = threadIdx.x + kThreads * u;  // row c / 4, q bytes 8 (c % 4) ..
-            const uint32_t row = min(n0 + (c >> 2), n - 1);
-            const uint64_t blk = row * row_bytes + (uint64_t)b * kQ8Bytes;
-            const uint64_t s = blk + 2 + 8 * (c & 3);
-            qsh[u] = (uint32_t)s & 3u;  // w is 4-byte aligned: 0 or 2
-            const uint32_t* p = (const uint32_t*)(w + (s - qsh[u]));
-            qd[u][0] = p[0];
-            qd[u][1] = p[1];
-            qd[u][2] = qsh[u] ? p[2] : 0u;  // the third dword only when the run straddles it
-            sbits[u] = (c & 3) == 0 ? *(const uint16_t*)(w + blk) : 0u;
+        for (int i = 0; i < NX; i++) {
+            const uint32_t blk = wave_u + W * i;  // uniform
+            const uint16_t* plane = blk * 1024 < BM * 64 ? xhi : xlo;
+            lds_dma<4>(xoff[i], uniform_u64((uint64_t)(uintptr_t)plane + 64ull * b),
+                       (uint32_t)__builtin_amdgcn_readfirstlane(smem_lds + stage * kXStage + 1024 * blk));
         }
     };
-    auto stage_block = [&](int buf) {
+
+    // raw q: dword d = 64 (wave + W i) + lane of the stage is dword d % 9 of tile row
+    // d / 9, from the dword boundary at or below the row's block: weight row
+    // wr = min(n0 + d / 9, n - 1), rb = wr * row_bytes, block b at byte rb + 34 b of
+    // the weights. 34 b is 0 mod 4 for even b and 2 mod 4 for odd b, so the
+    // dwords start at 34 b + (rb & ~3) (even) or 34 b - 2 + ((rb + 2) & ~3) (odd):
+    // scalar base w + 34 b or w + 34 b - 2, lane offsets per parity (both sums of
+    // non-negative terms: no unsigned wrap).
+    uint32_t qoff_e[NQ], qoff_o[NQ];
 #pragma unroll
-        for (int u = 0; u < kAPer; u++) {
-            const uint32_t c = threadIdx.x + kThreads * u;
-            const uint32_t row = (c >> 2) % BM;
-            As[buf][c < 4 * BM ? 0 : 1][row * 4 + ((c & 3) ^ ((row >> 2) & 3))] = xa[u];
+    for (int i = 0; i < NQ; i++) {
+        const uint32_t d = min(64u * (wave_u + W * i) + lane, (uint32_t)(BN * kRowDw - 1));
+        const uint32_t rb = min(n0 + d / kRowDw, n - 1) * (uint32_t)row_bytes;
+        qoff_e[i] = (rb & ~3u) + 4 * (d % kRowDw);
+        qoff_o[i] = ((rb + 2) & ~3u) + 4 * (d % kRowDw);
+    }
+    auto issue_q = [&](uint32_t b, int stage) {
+        const bool odd = b & 1;
+        const uint64_t base = uniform_u64((uint64_t)(uintptr_t)w + (uint64_t)kQ8Bytes * b - (odd ? 2u : 0u));
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const uint32_t blk = wave_u + W * i;  // uniform
+            if (i == NQ - 1 && !q_extra) break;
+            lds_dma<1>(odd ? qoff_o[i] : qoff_e[i], base,
+                       (uint32_t)__builtin_amdgcn_readfirstlane(smem_lds + kStages * kXStage + stage * kQStage + 256 * blk));
         }
+    };
+    // load instructions of one group of this wavefront, and the wait that leaves
+    // at most n of them outstanding (n uniform)
+    const uint32_t nq_w = q_extra ? NQ : NQ - 1;
+    auto group_ops = [&](bool x_issued, bool q_issued) { return (x_issued ? NX : 0) + (q_issued ? nq_w : 0); };
+    auto wait_outstanding = [&](uint32_t n) {
+        static_assert(2 * (NX + NQ) <= 12, "wait cases below");
+        switch (n) {
+            case 0: wait_vm_only<0>(); break;
+            case 1: wait_vm_only<1>(); break;
+            case 2: wait_vm_only<2>(); break;
+            case 3: wait_vm_only<3>(); break;
+            case 4: wait_vm_only<4>(); break;
+            case 5: wait_vm_only<5>(); break;
+            case 6: wait_vm_only<6>(); break;
+            case 7: wait_vm_only<7>(); break;
+            case 8: wait_vm_only<8>(); break;
+            case 9: wait_vm_only<9>(); break;
+            case 10: wait_vm_only<10>(); break;
+            case 11: wait_vm_only<11>(); break;
+            default: wait_vm_only<12>(); break;
+        }
+    };
+
+    // f16 q: thread c = tid + threads u takes tile row c / 4, bytes 2 + 8 (c % 4) .. + 8
+    // of its block: raw-row bytes (s & 3) + 2 + 8 (c % 4) .. + 8, inside the three
+    // dwords 2 (c % 4) .. + 3 of the raw row (bytes 2..9 of them when s & 3 = 0, bytes
+    // 4..11 when it is 2). Part 0's first dword also holds the scale (bytes s & 3, + 1).
+    const unsigned char* qraw = smem + kStages * kXStage;
+    uint32_t rbp[kBPer], qrd[kBPer];  // (weight row * row_bytes) & 3; byte of the lane's dwords in a raw stage
+#pragma unroll
+    for (int u = 0; u < kBPer; u++) {
+        const uint32_t c = threadIdx.x + kThreads * u;
+        rbp[u] = (min(n0 + (c >> 2), n - 1) * (uint32_t)row_bytes) & 3u;
+        qrd[u] = (c >> 2) * (kRowDw * 4) + 8 * (c & 3);
+    }
+    auto convert_q = [&](uint32_t b, int stage, int buf) {
 #pragma unroll
         for (int u = 0; u < kBPer; u++) {
             const uint32_t c = threadIdx.x + kThreads * u;
             const uint32_t row = c >> 2, part = c & 3;
-            const uint32_t sel = qsh[u] ? 0x05040302u : 0x03020100u;
-            const uint2 a = i8x4_to_f16x4(__builtin_amdgcn_perm(qd[u][1], qd[u][0], sel));
-            const uint2 b = i8x4_to_f16x4(__builtin_amdgcn_perm(qd[u][2], qd[u][1], sel));
-            Bs[buf][row * 4 + (part ^ ((row >> 2) & 3))] = u32x4_t{a.x, a.y, b.x, b.y};
-            if (part == 0) Ss[buf][row] = f16_bits_to_f32(sbits[u]);
+            const bool s2 = (rbp[u] + 2 * b) & 2u;  // s & 3 == 2
+            const uint32_t* rw = (const uint32_t*)(qraw + stage * kQStage + qrd[u]);
+            const uint32_t d0 = rw[0], d1 = rw[1], d2 = rw[2];
+            const uint32_t sel = s2 ? 0x07060504u : 0x05040302u;
+            const uint2 a = i8x4_to_f16x4(__builtin_amdgcn_perm(d1, d0, sel));
+            const uint2 bb = i8x4_to_f16x4(__builtin_amdgcn_perm(d2, d1, sel));
+            Bs[buf][row * 4 + (part ^ ((row >> 2) & 3))] = u32x4_t{a.x, a.y, bb.x, bb.y};
+            if (part == 0) Ss[buf][row] = f16_bits_to_f32(s2 ? d0 >> 16 : d0 & 0xffffu);
         }
     };
 
@@ -393,26 +510,21 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    load_block(0);
-    stage_block(0);
-    __syncthreads();
-    for (uint32_t b = 0; b < nb; b++) {
-        const int cur = b & 1;
-        if (b + 1 < nb) load_block(b + 1);
+    auto multiply = [&](int stage, int buf) {
         f16x8_t bv[TN];
         float sv[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int row = wn0 + 16 * j + r16;
-            bv[j] = __builtin_bit_cast(f16x8_t, Bs[cur][row * 4 + (grp ^ ((row >> 2) & 3))]);
-            sv[j] = Ss[cur][row];
+            bv[j] = __builtin_bit_cast(f16x8_t, Bs[buf][row * 4 + (grp ^ ((row >> 2) & 3))]);
+            sv[j] = Ss[buf][row];
         }
 #pragma unroll
         for (int i = 0; i < TM; i++) {
             const int row = wm0 + 16 * i + r16;
             const int slot = row * 4 + (grp ^ ((row >> 2) & 3));
-            const f16x8_t ah = __builtin_bit_cast(f16x8_t, As[cur][0][slot]);
-            const f16x8_t al = __builtin_bit_cast(f16x8_t, As[cur][1][slot]);
+            const f16x8_t ah = __builtin_bit_cast(f16x8_t, As[stage][0][slot]);
+            const f16x8_t al = __builtin_bit_cast(f16x8_t, As[stage][1][slot]);
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv[j], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
@@ -421,8 +533,41 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                 for (int e = 0; e < 4; e++) acc[i][j][e] = __builtin_fmaf(sv[j], t[e], acc[i][j][e]);
             }
         }
-        if (b + 1 < nb) stage_block(cur ^ 1);
-        __syncthreads();
+    };
+
+    // prologue: group 0 = x 0, raw q 0 and 1; group g <= PD = x g, raw q g + 1. Once
+    // group 0 has landed, block 0's q is converted.
+    issue_x(0, 0);
+    issue_q(0, 0);
+    if (nb > 1) issue_q(1, 1);
+    uint32_t ops[2] = {0, 0};  // load instructions of the last two groups (ops[0] the latest)
+#pragma unroll
+    for (uint32_t g = 1; g <= (uint32_t)PD; g++) {
+        const bool xi = g < nb, qi = g + 1 < nb;
+        if (xi) issue_x(g, g);
+        if (qi) issue_q(g + 1, g + 1);
+        ops[1] = ops[0];
+        ops[0] = group_ops(xi, qi);
+    }
+    wait_outstanding(PD == 1 ? ops[0] : ops[0] + ops[1]);
+    gemm_lds_sync();
+    convert_q(0, 0, 0);
+    gemm_lds_sync();
+    // iteration b: stage b % (PD + 2) (uniform)
+    uint32_t st = 0;
+    for (uint32_t b = 0; b < nb; b++) {
+        const uint32_t st1 = st == kStages - 1 ? 0 : st + 1;          // (b + 1) % S
+        const uint32_t stx = st == 0 ? kStages - 1 : st - 1;          // (b + PD + 1) % S = (b - 1) % S
+        const bool xi = b + PD + 1 < nb, qi = b + PD + 2 < nb;
+        if (xi) issue_x(b + PD + 1, stx);
+        if (qi) issue_q(b + PD + 2, st);  // (b + PD + 2) % S = b % S: raw q stage of block b, converted last iteration
+        if (b + 1 < nb) convert_q(b + 1, st1, (b + 1) & 1);
+        multiply(st, b & 1);
+        ops[1] = ops[0];
+        ops[0] = group_ops(xi, qi);
+        wait_outstanding(PD == 1 ? ops[0] : ops[0] + ops[1]);  // x b + 1 and raw q b + 2 have landed
+        gemm_lds_sync();
+        st = st1;
     }
 
     if constexpr (EPI == 1) {
@@ -628,7 +773,7 @@ int launch_rows_q(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
 }
 
 // The split x is made once and shared by the group's products.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int PD>
 int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, x_split_bytes(a.m, a.k), &ws)) return rc;
@@ -650,7 +795,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
         g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
     }
     if (tiles == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0>),
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, PD>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      AttnPrepEpi{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
@@ -684,7 +829,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     }
     g.count = 3;
     AttnPrepEpi ep{a.q_norm, a.k_norm, cs, a.q16, a.k_cache, a.v_cache, a.pos, a.n_q_heads, a.max_ctx, a.eps, a.q_scale};
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1>),
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1, 1>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      ep);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
@@ -702,7 +847,12 @@ constexpr uint32_t kGemmMinM = 16;
 // view only if the weights end on a dword boundary or the view has 2 more bytes.
 // The GEMM reads x as float4 (x 16-byte aligned), stores single floats (out
 // 4-byte aligned) and reads q in 8-byte runs from the dword boundary at or below
-// them, with the same end condition.
+// them, with the same end condition. Its loads address an x plane and the
+// weights with 32-bit byte offsets from a scalar base.
+static bool gemm_offsets_fit(uint32_t m, uint32_t k, uint64_t w_end) {
+    return (uint64_t)m * k * 2 < (1ull << 32) && w_end + 2 < (1ull << 32);
+}
+
 MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len) {
     const uintptr_t x_addr = (uintptr_t)a.x, out_addr = (uintptr_t)a.out, w_addr = (uintptr_t)a.w;
     if (a.k % 32 != 0 || (x_addr & 15u)) return MatmulPath::Generic;
@@ -710,9 +860,10 @@ MatmulPath matmul_path(const MatmulLaunch& a, uint64_t w_len) {
                                                                                          : MatmulPath::Generic;
     const uint64_t end = (uint64_t)a.n * (a.k / 32) * kQ8Bytes;
     if ((w_addr & 3u) || !((w_addr + end) % 4 == 0 || w_len >= end + 2)) return MatmulPath::Generic;
-    if (a.m >= kGemmMinM && (out_addr & 3u) == 0) return MatmulPath::Gemm;
+    const bool gemm = (out_addr & 3u) == 0 && gemm_offsets_fit(a.m, a.k, end);
+    if (a.m >= kGemmMinM && gemm) return MatmulPath::Gemm;
     if (a.k / 32 <= 256 && (out_addr & 15u) == 0) return MatmulPath::Rows;
-    return (out_addr & 3u) == 0 ? MatmulPath::Gemm : MatmulPath::Generic;
+    return gemm ? MatmulPath::Gemm : MatmulPath::Generic;
 }
 
 static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bool q8, float* out, const float* res,
@@ -727,7 +878,7 @@ static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bo
 static int launch_same_path(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, MatmulPath path) {
     if (path == MatmulPath::Rows) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
     if (path == MatmulPath::Gemm)
-        return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);
+        return a.m >= 128 ? launch_gemm<128, 128, 4, 2, 1>(ctx, a) : launch_gemm<32, 64, 2, 2, 1>(ctx, a);
     for (uint32_t e = 0; e < a.count; e++)
         if (a.n[e])
             if (int rc = launch_generic(ctx, a.x, a.w[e], a.q8, a.out[e], a.res[e], a.m, a.n[e], a.k)) return rc;

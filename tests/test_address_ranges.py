@@ -12,8 +12,8 @@ Replicated:
   qw3_amd/csrc/k_decode.hip  decode_geometry_of, paged_plan, issue_tile, the q-operand and
                              new-row accesses and the partial stores of
                              decode_split_kernel (contiguous and paged caches)
-  qw3_amd/csrc/k_matmul.hip  load_block of matmul_q8_mfma_kernel (x planes, Q8_0
-                             runs and scales) and matmul_path's slack rule
+  qw3_amd/csrc/k_matmul.hip  the direct-to-LDS loads of matmul_q8_mfma_kernel (x
+                             planes, raw Q8_0 rows) and matmul_path's slack rule
   qw3_amd/csrc/k_prefill.hip DmaPlan / dma_tile of prefill_attention_kernel (every
                              direct-to-LDS load of every round) and its q-operand
                              loads
@@ -236,46 +236,75 @@ def test_decode_replica_catches_a_wrapped_offset():
 
 
 # ---------------------------------------------------------------------------
-# matmul_q8_mfma_kernel load_block (k_matmul.hip)
+# matmul_q8_mfma_kernel direct-to-LDS loads (k_matmul.hip)
 # ---------------------------------------------------------------------------
 
 Q8 = 34
 
 
-def gemm_path_ok(w_addr, n, k, w_len):
-    """matmul_path's Q8_0 requirements of the weight view for the fast kernels."""
+def gemm_path_ok(w_addr, n, k, w_len, m=1):
+    """matmul_path's Q8_0 requirements of the weight view for the GEMM: the row
+    kernel's end condition, and plane and weight offsets that fit 32 bits
+    (gemm_offsets_fit)."""
     end = n * (k // 32) * Q8
-    return w_addr % 4 == 0 and ((w_addr + end) % 4 == 0 or w_len >= end + 2)
+    fits = m * k * 2 < U32 and end + 2 < U32
+    return w_addr % 4 == 0 and ((w_addr + end) % 4 == 0 or w_len >= end + 2) and fits
 
 
 def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
-    """Every x-plane and weight byte load_block reads for each block b of every tile."""
-    threads = WM * WN * 64
-    a_per, b_per = BM * 8 // threads, BN * 4 // threads
+    """Every x-plane and weight byte the GEMM's direct-to-LDS loads read, for each
+    block b of every tile; returns one past the highest weight byte read."""
+    W = WM * WN
     nb = k // 32
     row_bytes = nb * Q8
     b = np.arange(nb)[:, None]
-    # x planes: c = thread + threads u; row = min(m0 + (c / 4) % BM, m - 1); halves row*k + 32b + 8 (c % 4), 8 halves
-    c = (np.arange(threads)[:, None] + threads * np.arange(a_per)[None, :]).ravel()
+    lane = np.arange(64)
+    # x: load i of wavefront w: stage byte o = 1024 (w + W i) + 16 lane -> plane o / (64 BM),
+    # row r = (o % (64 BM)) / 64, chunk (lane % 4) ^ ((r / 4) % 4); plane byte
+    # min(m0 + r, m - 1) * 2k + 16 chunk + 64 b, 16 bytes; the offset is a 32-bit lane value
+    nx = 2 * BM * 64 // 1024 // W
+    assert nx >= 1 and nx * 1024 * W == 2 * BM * 64
     for m0 in range(0, m, BM):
-        row = np.minimum(m0 + ((c >> 2) % BM), m - 1)
-        off = row[None, :] * k + 32 * b + 8 * (c[None, :] & 3)
-        assert off.min() >= 0 and (off + 8).max() <= m * k
-    # q runs: row = min(n0 + c / 4, n - 1); s = row*row_bytes + b*34 + 2 + 8 (c % 4); dwords from s - (s & 3)
-    c = (np.arange(threads)[:, None] + threads * np.arange(b_per)[None, :]).ravel()
-    lo, hi = None, None
+        for w in range(W):
+            for i in range(nx):
+                o = 1024 * (w + W * i) + 16 * lane
+                plane = o // (BM * 64)
+                assert (plane == plane[0]).all()  # one plane per load
+                r = (o % (BM * 64)) // 64
+                c = (lane & 3) ^ ((r >> 2) & 3)
+                off = np.minimum(m0 + r, m - 1) * k * 2 + 16 * c
+                assert off.max() < 2 ** 32
+                byte = off[None, :] + 64 * b
+                assert byte.min() >= 0 and (byte + 16).max() <= m * k * 2
+    # raw q: 9 dwords per tile row from the dword boundary at or below the row's
+    # block; dword d = 64 (w + W i) + lane (clamped to the last) is dword d % 9 of row
+    # d / 9, rb = min(n0 + d / 9, n - 1) * row_bytes: weight byte (34 b) + (rb & ~3)
+    # + 4 (d % 9) for even b, (34 b - 2) + ((rb + 2) & ~3) + 4 (d % 9) for odd b --
+    # a scalar base plus a 32-bit lane offset, 4 bytes
+    n_loads = (BN * 9 + 63) // 64
+    hi = None
     for n0 in range(0, n, BN):
-        row = np.minimum(n0 + (c >> 2), n - 1)
-        blk = row[None, :] * row_bytes + b * Q8
-        s = blk + 2 + 8 * (c[None, :] & 3)
-        sh = (w_addr + s) & 3                      # the kernel's qsh (w itself is 4-byte aligned)
-        first = s - sh
-        last = first + np.where(sh != 0, 12, 8)    # the third dword only when the run straddles it
-        scale_end = blk + 2                        # part-0 threads read the block's f16 scale
-        lo = min(first.min(), blk.min()) if lo is None else min(lo, first.min(), blk.min())
-        hi = max(last.max(), scale_end.max()) if hi is None else max(hi, last.max(), scale_end.max())
-    assert lo >= 0
-    return int(hi)
+        for w in range(W):
+            for i in range((n_loads + W - 1) // W):
+                blk = w + W * i
+                if blk >= n_loads:
+                    continue
+                d = np.minimum(64 * blk + lane, BN * 9 - 1)
+                rb = np.minimum(n0 + d // 9, n - 1) * row_bytes
+                even = (rb & ~3) + 4 * (d % 9)        # lane offsets: sums of non-negative terms
+                odd = ((rb + 2) & ~3) + 4 * (d % 9)
+                assert min(even.min(), odd.min()) >= 0 and max(even.max(), odd.max()) < 2 ** 32
+                base = Q8 * b - (b % 2) * 2               # the scalar base (non-negative: b >= 1 when odd)
+                assert base.min() >= 0
+                byte = base + np.where(b % 2 == 0, even[None, :], odd[None, :])
+                # the bytes are those of the dword boundary at or below the block
+                want = (rb[None, :] + Q8 * b) // 4 * 4 + 4 * (d % 9)[None, :]
+                assert (byte == want).all()
+                assert ((w_addr + byte) % 4 == 0).all()  # dword loads stay aligned
+                assert byte.min() >= 0
+                top = int((byte + 4).max())
+                hi = top if hi is None else max(hi, top)
+    return hi
 
 
 @pytest.mark.parametrize("m,n,k", [
@@ -287,7 +316,7 @@ def test_gemm_load_block_addresses(m, n, k, tile):
     """Both GEMM tiles; odd block counts put every other row's blocks at 2 mod 4."""
     end = n * (k // 32) * Q8
     for w_len in (end, end + 2):
-        if not gemm_path_ok(0, n, k, w_len):
+        if not gemm_path_ok(0, n, k, w_len, m):
             continue  # matmul_path sends this view to the serial kernel
         hi = check_gemm(m, n, k, 0, w_len, *tile)
         assert hi <= w_len, (hi, w_len)
