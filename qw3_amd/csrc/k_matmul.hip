@@ -335,7 +335,7 @@ struct AttnPrepEpi {
     float eps, q_scale;
 };
 
-template <int BM, int BN, int WM, int WN, int EPI, int PD>
+template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
@@ -363,18 +363,16 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     constexpr int kBPer = BN * 4 / kThreads;  // 8-byte q runs per thread and block
     static_assert(kBPer >= 1, "at least one q run per thread");
 
-    // LDS: As [stage][hi, lo][row * 4 + swizzled chunk], raw q [stage][row][9 dwords],
-    // Bs [buffer][row * 4 + swizzled chunk], Ss [buffer][row]; EPI 1 reuses the bytes
-    // for the f32 tile
-    static_assert(PD == 1 || PD == 2, "prefetch depth");
-    constexpr int kStages = PD + 2;
-    constexpr int kAsBytes = kStages * 2 * BM * 4 * 16, kRawBytes = kStages * BN * 36, kBsBytes = 2 * BN * 4 * 16,
-                  kSsBytes = 2 * BN * 4;
+    // LDS: As [stage][hi, lo][row * 4 + swizzled chunk], raw q [stage][wavefront][rows of
+    // 9 dwords], Bs [buffer][row * 4 + swizzled chunk], Ss [buffer][row]; EPI 1 reuses
+    // the bytes for the f32 tile
+    constexpr int kRawBytes = 2 * WM * WN * ((16 * (BN * 4 / (WM * WN * 64)) * 9 + 63) / 64) * 256;
+    constexpr int kAsBytes = 3 * 2 * BM * 4 * 16, kBsBytes = 2 * BN * 4 * 16, kSsBytes = 2 * BN * 4;
     constexpr int kMainBytes = kAsBytes + kRawBytes + kBsBytes + kSsBytes;
     constexpr int kTileRow = BN + 4;  // EPI 1 tile row stride in floats (16-byte rows, rows 4 banks apart)
     constexpr int kLdsBytes = EPI == 1 && BM * kTileRow * 4 > kMainBytes ? BM * kTileRow * 4 : kMainBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsBytes];
-    auto& As = *reinterpret_cast<u32x4_t(*)[kStages][2][BM * 4]>(smem);
+    auto& As = *reinterpret_cast<u32x4_t(*)[3][2][BM * 4]>(smem);
     auto& Bs = *reinterpret_cast<u32x4_t(*)[2][BN * 4]>(smem + kAsBytes + kRawBytes);
     auto& Ss = *reinterpret_cast<float(*)[2][BN]>(smem + kAsBytes + kRawBytes + kBsBytes);
 
@@ -385,24 +383,25 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
 
     // ---- staging ------------------------------------------------------------------
-    // All global loads are direct-to-LDS, issued ahead and awaited explicitly:
-    // iteration b issues x of block b + PD + 1 and the raw q of block b + PD + 2
-    // (one group of loads), converts block b + 1's raw q to f16, multiplies
-    // block b, then waits until at most its last PD groups are outstanding and
-    // meets the barrier, so a load has PD iterations to land. Block j uses x
-    // stage j % (PD + 2), raw q stage j % (PD + 2) and f16 q buffer j % 2.
+    // All global loads are direct-to-LDS, issued two blocks ahead and awaited
+    // explicitly. Iteration b issues x and the raw q of block b + 2 (one group of
+    // loads), multiplies block b, waits until only that group is outstanding
+    // (block b + 1 has landed), converts block b + 1's raw q to f16 and meets
+    // the barrier. Each wavefront loads the raw rows its own threads convert, so
+    // the conversion needs only the wavefront's own wait. Block j uses x stage
+    // j % 3, raw q stage j % 2 and f16 q buffer j % 2.
     constexpr int kXStage = 2 * BM * 64;  // bytes: hi plane rows, then lo plane rows
     constexpr int kRowDw = 9;             // raw q row: the 9 dwords covering a 34-byte block
-    constexpr int kQStage = BN * kRowDw * 4;
     constexpr int W = WM * WN;
     constexpr int NX = kXStage / 1024 / W;  // x loads per wavefront and block
     static_assert(NX >= 1 && NX * 1024 * W == kXStage, "whole 1 KB x loads per wavefront");
     static_assert((BM * 64) % 1024 == 0, "an x load stays inside one plane");
-    constexpr int kQLoads = (BN * kRowDw + 63) / 64;  // raw q loads (256 bytes each) per workgroup and block
-    constexpr int NQ = (kQLoads + W - 1) / W;         // at most, per wavefront
-    static_assert(BN * kRowDw % 64 == 0 && NQ <= 3, "raw q stage in whole loads");
+    constexpr int kWRows = 16 * kBPer;                   // tile rows whose runs a wavefront converts
+    constexpr int NQ = (kWRows * kRowDw + 63) / 64;      // raw q loads (256 bytes) per wavefront and block
+    constexpr int kQWave = NQ * 256;                     // a wavefront's raw q area in a stage
+    constexpr int kQStage = W * kQWave;
+    constexpr int kVmPerBlock = NX + NQ;
     const uint32_t wave_u = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
-    const bool q_extra = wave_u + W * (NQ - 1) < (uint32_t)kQLoads;  // uniform: this wavefront issues NQ, else NQ - 1
     const uint32_t smem_lds = gemm_lds_addr(smem);
 
     // x: load i of this wavefront fills stage bytes [1024 (wave + W i), +1024), lane L
@@ -424,66 +423,46 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
         }
     };
 
-    // raw q: dword d = 64 (wave + W i) + lane of the stage is dword d % 9 of tile row
-    // d / 9, from the dword boundary at or below the row's block: weight row
-    // wr = min(n0 + d / 9, n - 1), rb = wr * row_bytes, block b at byte rb + 34 b of
-    // the weights. 34 b is 0 mod 4 for even b and 2 mod 4 for odd b, so the
-    // dwords start at 34 b + (rb & ~3) (even) or 34 b - 2 + ((rb + 2) & ~3) (odd):
-    // scalar base w + 34 b or w + 34 b - 2, lane offsets per parity (both sums of
-    // non-negative terms: no unsigned wrap).
+    // raw q: the wavefront's local row lr < 16 kBPer is tile row 16 wave + (threads / 4)
+    // (lr / 16) + lr % 16 (the rows of its threads' runs). Dword d = 64 i + lane of its
+    // area (clamped to the last, d < 9 * 16 kBPer) is dword d % 9 of local row d / 9, from
+    // the dword boundary at or below the row's block: weight row wr = min(n0 + row,
+    // n - 1), rb = wr * row_bytes, block b at byte rb + 34 b of the weights. 34 b is
+    // 0 mod 4 for even b and 2 mod 4 for odd b, so the dwords start at 34 b + (rb & ~3)
+    // (even) or 34 b - 2 + ((rb + 2) & ~3) (odd): scalar base w + 34 b or w + 34 b - 2,
+    // lane offsets per parity (both sums of non-negative terms: no unsigned wrap).
     uint32_t qoff_e[NQ], qoff_o[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
-        const uint32_t d = min(64u * (wave_u + W * i) + lane, (uint32_t)(BN * kRowDw - 1));
-        const uint32_t rb = min(n0 + d / kRowDw, n - 1) * (uint32_t)row_bytes;
+        const uint32_t d = min(64u * i + lane, (uint32_t)(kWRows * kRowDw - 1));
+        const uint32_t lr = d / kRowDw;
+        const uint32_t row = 16 * wave_u + (kThreads / 4) * (lr / 16) + lr % 16;
+        const uint32_t rb = min(n0 + row, n - 1) * (uint32_t)row_bytes;
         qoff_e[i] = (rb & ~3u) + 4 * (d % kRowDw);
         qoff_o[i] = ((rb + 2) & ~3u) + 4 * (d % kRowDw);
     }
+    const uint32_t q_lds = smem_lds + 3 * kXStage + wave_u * kQWave;
     auto issue_q = [&](uint32_t b, int stage) {
         const bool odd = b & 1;
         const uint64_t base = uniform_u64((uint64_t)(uintptr_t)w + (uint64_t)kQ8Bytes * b - (odd ? 2u : 0u));
 #pragma unroll
-        for (int i = 0; i < NQ; i++) {
-            const uint32_t blk = wave_u + W * i;  // uniform
-            if (i == NQ - 1 && !q_extra) break;
+        for (int i = 0; i < NQ; i++)
             lds_dma<1>(odd ? qoff_o[i] : qoff_e[i], base,
-                       (uint32_t)__builtin_amdgcn_readfirstlane(smem_lds + kStages * kXStage + stage * kQStage + 256 * blk));
-        }
-    };
-    // load instructions of one group of this wavefront, and the wait that leaves
-    // at most n of them outstanding (n uniform)
-    const uint32_t nq_w = q_extra ? NQ : NQ - 1;
-    auto group_ops = [&](bool x_issued, bool q_issued) { return (x_issued ? NX : 0) + (q_issued ? nq_w : 0); };
-    auto wait_outstanding = [&](uint32_t n) {
-        static_assert(2 * (NX + NQ) <= 12, "wait cases below");
-        switch (n) {
-            case 0: wait_vm_only<0>(); break;
-            case 1: wait_vm_only<1>(); break;
-            case 2: wait_vm_only<2>(); break;
-            case 3: wait_vm_only<3>(); break;
-            case 4: wait_vm_only<4>(); break;
-            case 5: wait_vm_only<5>(); break;
-            case 6: wait_vm_only<6>(); break;
-            case 7: wait_vm_only<7>(); break;
-            case 8: wait_vm_only<8>(); break;
-            case 9: wait_vm_only<9>(); break;
-            case 10: wait_vm_only<10>(); break;
-            case 11: wait_vm_only<11>(); break;
-            default: wait_vm_only<12>(); break;
-        }
+                       (uint32_t)__builtin_amdgcn_readfirstlane(q_lds + stage * kQStage + 256 * i));
     };
 
-    // f16 q: thread c = tid + threads u takes tile row c / 4, bytes 2 + 8 (c % 4) .. + 8
-    // of its block: raw-row bytes (s & 3) + 2 + 8 (c % 4) .. + 8, inside the three
-    // dwords 2 (c % 4) .. + 3 of the raw row (bytes 2..9 of them when s & 3 = 0, bytes
-    // 4..11 when it is 2). Part 0's first dword also holds the scale (bytes s & 3, + 1).
-    const unsigned char* qraw = smem + kStages * kXStage;
-    uint32_t rbp[kBPer], qrd[kBPer];  // (weight row * row_bytes) & 3; byte of the lane's dwords in a raw stage
+    // f16 q: thread c = tid + threads u takes tile row c / 4 (local row 16 u + lane / 4 of
+    // its wavefront), bytes 2 + 8 (c % 4) .. + 8 of its block: raw-row bytes (s & 3) + 2
+    // + 8 (c % 4) .. + 8, inside the three dwords 2 (c % 4) .. + 3 of the raw row (bytes
+    // 2..9 of them when s & 3 = 0, bytes 4..11 when it is 2). Part 0's first dword also
+    // holds the scale (bytes s & 3, + 1).
+    const unsigned char* qraw = smem + 3 * kXStage + wave_u * kQWave;
+    uint32_t rbp[kBPer], qrd[kBPer];  // (weight row * row_bytes) & 3; byte of the lane's dwords in the area
 #pragma unroll
     for (int u = 0; u < kBPer; u++) {
         const uint32_t c = threadIdx.x + kThreads * u;
         rbp[u] = (min(n0 + (c >> 2), n - 1) * (uint32_t)row_bytes) & 3u;
-        qrd[u] = (c >> 2) * (kRowDw * 4) + 8 * (c & 3);
+        qrd[u] = (16 * u + (lane >> 2)) * (kRowDw * 4) + 8 * (lane & 3);
     }
     auto convert_q = [&](uint32_t b, int stage, int buf) {
 #pragma unroll
@@ -535,37 +514,31 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
         }
     };
 
-    // prologue: group 0 = x 0, raw q 0 and 1; group g <= PD = x g, raw q g + 1. Once
-    // group 0 has landed, block 0's q is converted.
+    // prologue: blocks 0 and 1 in flight; block 0's q converted once its loads have landed
     issue_x(0, 0);
     issue_q(0, 0);
-    if (nb > 1) issue_q(1, 1);
-    uint32_t ops[2] = {0, 0};  // load instructions of the last two groups (ops[0] the latest)
-#pragma unroll
-    for (uint32_t g = 1; g <= (uint32_t)PD; g++) {
-        const bool xi = g < nb, qi = g + 1 < nb;
-        if (xi) issue_x(g, g);
-        if (qi) issue_q(g + 1, g + 1);
-        ops[1] = ops[0];
-        ops[0] = group_ops(xi, qi);
+    if (nb > 1) {
+        issue_x(1, 1);
+        issue_q(1, 1);
+        wait_vm_only<kVmPerBlock>();
+    } else {
+        wait_vm_only<0>();
     }
-    wait_outstanding(PD == 1 ? ops[0] : ops[0] + ops[1]);
-    gemm_lds_sync();
     convert_q(0, 0, 0);
     gemm_lds_sync();
-    // iteration b: stage b % (PD + 2) (uniform)
+    // iteration b: x stage b % 3 (uniform)
     uint32_t st = 0;
     for (uint32_t b = 0; b < nb; b++) {
-        const uint32_t st1 = st == kStages - 1 ? 0 : st + 1;          // (b + 1) % S
-        const uint32_t stx = st == 0 ? kStages - 1 : st - 1;          // (b + PD + 1) % S = (b - 1) % S
-        const bool xi = b + PD + 1 < nb, qi = b + PD + 2 < nb;
-        if (xi) issue_x(b + PD + 1, stx);
-        if (qi) issue_q(b + PD + 2, st);  // (b + PD + 2) % S = b % S: raw q stage of block b, converted last iteration
-        if (b + 1 < nb) convert_q(b + 1, st1, (b + 1) & 1);
+        const uint32_t st1 = st == 2 ? 0 : st + 1, st2 = st == 0 ? 2 : st - 1;  // (b + 1) % 3, (b + 2) % 3
+        const bool ahead = b + 2 < nb;  // uniform
+        if (ahead) {
+            issue_x(b + 2, st2);  // the stage of block b - 1, read before the last barrier
+            issue_q(b + 2, b & 1);  // the raw stage of block b, converted before the last barrier
+        }
         multiply(st, b & 1);
-        ops[1] = ops[0];
-        ops[0] = group_ops(xi, qi);
-        wait_outstanding(PD == 1 ? ops[0] : ops[0] + ops[1]);  // x b + 1 and raw q b + 2 have landed
+        if (ahead) wait_vm_only<kVmPerBlock>();  // block b + 1 has landed
+        else wait_vm_only<0>();
+        if (b + 1 < nb) convert_q(b + 1, (b + 1) & 1, (b + 1) & 1);
         gemm_lds_sync();
         st = st1;
     }
@@ -773,7 +746,7 @@ int launch_rows_q(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
 }
 
 // The split x is made once and shared by the group's products.
-template <int BM, int BN, int WM, int WN, int PD>
+template <int BM, int BN, int WM, int WN>
 int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, x_split_bytes(a.m, a.k), &ws)) return rc;
@@ -795,7 +768,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
         g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
     }
     if (tiles == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, PD>),
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      AttnPrepEpi{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
@@ -829,7 +802,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     }
     g.count = 3;
     AttnPrepEpi ep{a.q_norm, a.k_norm, cs, a.q16, a.k_cache, a.v_cache, a.pos, a.n_q_heads, a.max_ctx, a.eps, a.q_scale};
-    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1, 1>),
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      ep);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
@@ -878,7 +851,7 @@ static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bo
 static int launch_same_path(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, MatmulPath path) {
     if (path == MatmulPath::Rows) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
     if (path == MatmulPath::Gemm)
-        return a.m >= 128 ? launch_gemm<128, 128, 4, 2, 1>(ctx, a) : launch_gemm<32, 64, 2, 2, 1>(ctx, a);
+        return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);
     for (uint32_t e = 0; e < a.count; e++)
         if (a.n[e])
             if (int rc = launch_generic(ctx, a.x, a.w[e], a.q8, a.out[e], a.res[e], a.m, a.n[e], a.k)) return rc;

@@ -276,21 +276,26 @@ def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
                 assert off.max() < 2 ** 32
                 byte = off[None, :] + 64 * b
                 assert byte.min() >= 0 and (byte + 16).max() <= m * k * 2
-    # raw q: 9 dwords per tile row from the dword boundary at or below the row's
-    # block; dword d = 64 (w + W i) + lane (clamped to the last) is dword d % 9 of row
-    # d / 9, rb = min(n0 + d / 9, n - 1) * row_bytes: weight byte (34 b) + (rb & ~3)
-    # + 4 (d % 9) for even b, (34 b - 2) + ((rb + 2) & ~3) + 4 (d % 9) for odd b --
-    # a scalar base plus a 32-bit lane offset, 4 bytes
-    n_loads = (BN * 9 + 63) // 64
+    # raw q: 9 dwords per tile row from the dword boundary at or below the row's block,
+    # each wavefront loading the rows of its own threads' runs: local row lr < 16 b_per
+    # is tile row 16 w + (threads / 4) (lr / 16) + lr % 16; dword d = 64 i + lane
+    # (clamped to the last) is dword d % 9 of local row d / 9; rb = min(n0 + row, n - 1)
+    # * row_bytes: weight byte (34 b) + (rb & ~3) + 4 (d % 9) for even b, (34 b - 2) +
+    # ((rb + 2) & ~3) + 4 (d % 9) for odd b -- a scalar base plus a 32-bit lane offset
+    threads = W * 64
+    b_per = BN * 4 // threads
+    w_rows = 16 * b_per
+    nq = (w_rows * 9 + 63) // 64
     hi = None
     for n0 in range(0, n, BN):
         for w in range(W):
-            for i in range((n_loads + W - 1) // W):
-                blk = w + W * i
-                if blk >= n_loads:
-                    continue
-                d = np.minimum(64 * blk + lane, BN * 9 - 1)
-                rb = np.minimum(n0 + d // 9, n - 1) * row_bytes
+            covered = set()
+            for i in range(nq):
+                d = np.minimum(64 * i + lane, w_rows * 9 - 1)
+                lr = d // 9
+                row = 16 * w + (threads // 4) * (lr // 16) + lr % 16
+                covered.update(row.tolist())
+                rb = np.minimum(n0 + row, n - 1) * row_bytes
                 even = (rb & ~3) + 4 * (d % 9)        # lane offsets: sums of non-negative terms
                 odd = ((rb + 2) & ~3) + 4 * (d % 9)
                 assert min(even.min(), odd.min()) >= 0 and max(even.max(), odd.max()) < 2 ** 32
@@ -304,6 +309,9 @@ def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
                 assert byte.min() >= 0
                 top = int((byte + 4).max())
                 hi = top if hi is None else max(hi, top)
+            # the wavefront loaded exactly the rows its threads convert (thread c: row c / 4)
+            conv = {(c + threads * u) // 4 for c in range(64 * w, 64 * w + 64) for u in range(b_per)}
+            assert covered == conv
     return hi
 
 
@@ -311,7 +319,7 @@ def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
     (16, 512, 2048), (2048, 4096, 2048), (2048, 512, 2048), (200, 300, 96), (130, 70, 32 * 65),
     (17, 256, 256), (16, 5, 32 * 3), (33, 129, 32 * 7),
 ])
-@pytest.mark.parametrize("tile", [(128, 128, 4, 2), (32, 64, 2, 2)])
+@pytest.mark.parametrize("tile", [(128, 128, 4, 2), (32, 64, 2, 2), (64, 128, 2, 2), (128, 128, 2, 2)])
 def test_gemm_load_block_addresses(m, n, k, tile):
     """Both GEMM tiles; odd block counts put every other row's blocks at 2 mod 4."""
     end = n * (k // 32) * Q8
