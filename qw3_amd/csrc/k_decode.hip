@@ -515,6 +515,19 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeParams p, 
     __shared__ float s_m[W][kHeads], s_l[W][kHeads];
     __shared__ int s_badw[W];
 
+    // Every argument the first loads need, read in one scalar round trip: left to
+    // itself the compiler loads only what the first early-exit test needs, waits,
+    // and loads the rest after the branch -- a second dependent round trip (~0.9 us
+    // on a cold argument buffer) before the first K/V load.
+    if constexpr (PAGED)
+        asm volatile("" ::"s"(p.k_cache), "s"(p.v_cache), "s"(p.cache_stride), "s"(p.q), "s"(p.chunk), "s"(p.n_sub),
+                     "s"(p.group), "s"(p.n_q_heads), "s"(p.n_kv_heads), "s"(p.k_new), "s"(p.v_new), "s"(p.q_norm),
+                     "s"(p.k_norm), "s"(p.plan), "s"(p.seq_lens), "s"(p.max_len), "s"(p.page_table), "s"(p.page_size),
+                     "s"(p.max_pages), "s"(p.n_pages), "s"(p.plan_cap), "s"(p.n_seqs), "s"(p.out));
+    else
+        asm volatile("" ::"s"(p.k_cache), "s"(p.v_cache), "s"(p.cache_stride), "s"(p.q), "s"(p.chunk), "s"(p.n_sub),
+                     "s"(p.group), "s"(p.n_q_heads), "s"(p.n_kv_heads), "s"(p.k_new), "s"(p.v_new), "s"(p.q_norm),
+                     "s"(p.k_norm), "s"(p.ctx_len), "s"(p.positions));
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
@@ -890,6 +903,9 @@ __device__ __forceinline__ void merge_slots(const DecodeParams& p) {
 
 template <int D, bool SLOTS_FORM>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+    // every argument in one scalar round trip (see decode_split_kernel)
+    asm volatile("" ::"s"(p.seq_lens), "s"(p.plan), "s"(p.n_q_heads), "s"(p.ctx_len), "s"(p.max_len), "s"(p.chunk),
+                 "s"(p.part_ml), "s"(p.part_o), "s"(p.n_splits), "s"(p.out));
     if constexpr (SLOTS_FORM)
         merge_slots<D>(p);
     else
