@@ -34,6 +34,16 @@ struct WeightGroup {
     uint32_t count;
 };
 
+// Every field of a group in one scalar round trip: the entry selection below
+// would otherwise load each entry's fields only after testing the previous
+// entry (a chain of dependent argument loads before the first memory access).
+#define DS5_GROUP_ARGS(g) \
+    "s"((g).w[0]), "s"((g).w[1]), "s"((g).w[2]), "s"((g).w[3]), "s"((g).out[0]), "s"((g).out[1]), "s"((g).out[2]), \
+        "s"((g).out[3]), "s"((g).res[0]), "s"((g).res[1]), "s"((g).res[2]), "s"((g).res[3]), "s"((g).n[0]), \
+        "s"((g).n[1]), "s"((g).n[2]), "s"((g).n[3]), "s"((g).wg0[0]), "s"((g).wg0[1]), "s"((g).wg0[2]), \
+        "s"((g).wg0[3]), "s"((g).count)
+static_assert(kMatmulGroupMax == 4, "DS5_GROUP_ARGS lists four entries");
+
 // MT tokens per pass, JB blocks per lane (k <= 2048 * JB).
 // Launch: grid.x = sum of ceil(n[e] / 8), one pass of tokens m0..m0+MT-1. Rows
 // past n (an entry's last workgroup) load row n - 1 and store nothing: every
@@ -41,21 +51,22 @@ struct WeightGroup {
 template <int MT, int JB, bool Q8>
 __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const WeightGroup g,
                                                                  uint32_t m, uint32_t k, uint32_t m0) {
-    // this workgroup's entry (uniform; selected without indexing the argument arrays)
+    // this workgroup's entry (uniform; selected without indexing the argument arrays,
+    // with selects rather than branches so that every field loads in one round trip)
     // (out may be the residual itself: each output is read, then written, by one lane)
     const uint8_t* __restrict__ w = g.w[0];
     float* out = g.out[0];
     const float* res = g.res[0];
     uint32_t n = g.n[0], wg = blockIdx.x;
 #pragma unroll
-    for (int e = 1; e < kMatmulGroupMax; e++)
-        if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
-            w = g.w[e];
-            out = g.out[e];
-            res = g.res[e];
-            n = g.n[e];
-            wg = blockIdx.x - g.wg0[e];
-        }
+    for (int e = 1; e < kMatmulGroupMax; e++) {
+        const bool take = (uint32_t)e < g.count && blockIdx.x >= g.wg0[e];
+        w = take ? g.w[e] : w;
+        out = take ? g.out[e] : out;
+        res = take ? g.res[e] : res;
+        n = take ? g.n[e] : n;
+        wg = take ? blockIdx.x - g.wg0[e] : wg;
+    }
 
     // x in LDS: float4 chunk i of block b of token t at t * kXChunks + 8 b + (i ^ (b & 7)),
     // so the 16-byte reads of 8 consecutive lanes (one block each) hit distinct banks
@@ -341,6 +352,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                                                                       const int* __restrict__ row_exp,
                                                                       const WeightGroup g, uint32_t m, uint32_t k,
                                                                       const AttnPrepEpi ep) {
+    asm volatile("" ::DS5_GROUP_ARGS(g), "s"(xhi), "s"(xlo), "s"(row_exp), "s"(m), "s"(k));
     // this workgroup's entry and column tile (uniform); out may be the residual itself
     const uint8_t* __restrict__ w = g.w[0];
     float* out = g.out[0];

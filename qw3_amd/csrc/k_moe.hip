@@ -400,6 +400,9 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(const float
                                                                      float* __restrict__ h, uint32_t n_pairs,
                                                                      uint32_t dim, uint32_t ffn, uint64_t row_h,
                                                                      uint64_t stride) {
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(x), "s"(gate), "s"(up), "s"(pairs), "s"(h), "s"(n_pairs), "s"(dim), "s"(ffn), "s"(row_h),
+                 "s"(stride));
     extern __shared__ __attribute__((aligned(16))) float moe_xs[];
     const int lane = threadIdx.x & 63;
     const uint64_t r0 = (uint64_t)blockIdx.x * kMoeWaves, r = r0 + (threadIdx.x >> 6);
@@ -466,6 +469,9 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* _
                                                                   const ds5_pair* __restrict__ pairs,
                                                                   float* __restrict__ y, uint32_t n_pairs, uint32_t dim,
                                                                   uint32_t ffn, uint64_t row_f, uint64_t stride) {
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(h), "s"(down), "s"(pairs), "s"(y), "s"(n_pairs), "s"(dim), "s"(ffn), "s"(row_f),
+                 "s"(stride));
     const int lane = threadIdx.x & 63;
     const uint64_t r = (uint64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
     if (r >= (uint64_t)n_pairs * dim) return;  // wave-uniform
@@ -488,6 +494,9 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offsets, uint32_t top_k, float* __restrict__ out,
     uint32_t dim, uint32_t ffn, uint64_t row_f, uint64_t stride) {
 #pragma clang fp contract(off)
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(h), "s"(down), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(dim),
+                 "s"(ffn), "s"(row_f), "s"(stride));
     __shared__ float ys[kMoeWaves][kDownRows], wts[kMoeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t groups = dim / kDownRows;
@@ -570,6 +579,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
                                                           const uint32_t* __restrict__ offsets, uint32_t top_k,
                                                           float* __restrict__ out, uint32_t n_tokens, uint32_t dim) {
 #pragma clang fp contract(off)
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(y), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(n_tokens), "s"(dim));
     const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (id >= (uint64_t)n_tokens * dim) return;
     const uint32_t t = (uint32_t)(id / dim), i = (uint32_t)(id % dim);

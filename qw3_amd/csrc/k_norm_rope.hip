@@ -129,6 +129,8 @@ constexpr int kRopeHalfMax = DS5_MAX_ROPE_HALF;
 __global__ __launch_bounds__(kRopeThreads) void rope_kernel(float* x, const int32_t* __restrict__ positions,
                                                             uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim,
                                                             float freq_scale, RopeTable table) {
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(x), "s"(positions), "s"(n_tokens), "s"(n_heads), "s"(head_dim), "s"(freq_scale));
     __shared__ float s_cos[kRopeHalfMax], s_sin[kRopeHalfMax];
     const uint32_t half = head_dim / 2;
     for (uint32_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
@@ -169,9 +171,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
                                                         const float* __restrict__ v_new, T* k_cache, T* v_cache,
                                                         uint32_t pos, uint32_t n_tokens, uint32_t n_kv_heads,
                                                         uint32_t head_dim, uint32_t max_ctx) {
+    // the arguments in one scalar round trip (before the first early exit)
+    asm volatile("" ::"s"(k_new), "s"(v_new), "s"(k_cache), "s"(v_cache), "s"(pos), "s"(n_tokens), "s"(n_kv_heads),
+                 "s"(head_dim), "s"(max_ctx), "s"(gridDim.x));
     const uint64_t total = (uint64_t)n_tokens * n_kv_heads * head_dim;
-    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (uint64_t)gridDim.x * blockDim.x) {
+    for (uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (uint64_t)gridDim.x * 256) {
         const uint32_t d = idx % head_dim;
         const uint64_t th = idx / head_dim;
         const uint32_t h = th % n_kv_heads;
