@@ -30,11 +30,13 @@
 // workgroups of one kv head are placed on the same XCD (workgroup b runs on
 // XCD b % 8), so each XCD's L2 holds one kv head's K/V.
 //
-// Fused mode: the pre-pass (prefill_prep_kernel) writes the normalised,
-// rotated f16 k rows and the f16 v rows into the cache and a (cos, sin) table
-// per (token, pair); the attention kernel takes raw q, applies the per-head
-// RMSNorm (the row's sum of squares reduced across the two lanes that hold
-// it) and the rotation, and rounds q to f16.
+// Fused mode: the pre-pass (prefill_prep_kernel, one workgroup per token)
+// writes the normalised, rotated f16 k rows and the f16 v rows into the cache,
+// and the attention kernel's q operand: q normalised, rotated, times softmax
+// scale * log2(e), rounded to f16 ([n_tokens, n_q_heads, head_dim]). The
+// separate-op path packs an already normalised and rotated q the same way
+// (q_pack_kernel). The attention block's projection GEMM can do the pre-pass
+// in its epilogue instead (k_matmul.hip).
 #include "ds5_common.hpp"
 
 namespace {
