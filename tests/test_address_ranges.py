@@ -318,6 +318,7 @@ def check_gemm(m, n, k, w_addr, w_len, BM, BN, WM, WN):
 @pytest.mark.parametrize("m,n,k", [
     (16, 512, 2048), (2048, 4096, 2048), (2048, 512, 2048), (200, 300, 96), (130, 70, 32 * 65),
     (17, 256, 256), (16, 5, 32 * 3), (33, 129, 32 * 7),
+    (128, 256, 32), (130, 128, 64), (256, 384, 96), (136, 200, 160),
 ])
 @pytest.mark.parametrize("tile", [(128, 128, 4, 2), (32, 64, 2, 2), (64, 128, 2, 2), (128, 128, 2, 2)])
 def test_gemm_load_block_addresses(m, n, k, tile):

@@ -604,6 +604,10 @@ def test_matmul_f32_hand_case(ctx, hip):
     (33, 130, 4096),   # small tiles, ragged tokens and rows
     (128, 512, 2048),  # large tiles, exact
     (200, 300, 2080),  # large tiles, ragged tokens, rows and an odd block count
+    (128, 256, 32),    # large tiles, one block: nothing loaded ahead
+    (130, 128, 64),    # large tiles, two blocks: one block ahead only
+    (256, 384, 96),    # large tiles, three blocks: the pipeline's first full iteration
+    (136, 200, 160),   # large tiles, five blocks, ragged rows: each stage and raw area reused
 ])
 def test_matmul_q8_0_and_f32_vs_oracle(ctx, hip, oracle, m, n, k):
     """Q8_0 rows and their dequantised f32 rows against the oracle, within the bound
