@@ -6,12 +6,14 @@
 // h / group; softmax(scale * q.k) in f32.
 //
 // prefill_attention_kernel. A workgroup serves 4 q heads of one GQA group
-// with 8 wavefronts: two sets of four (one head each), set s taking the key
-// tiles 2r + s, so each SIMD runs two wavefronts whose MFMA, exponential and
-// LDS phases overlap. A wavefront owns 32 query rows of its head. Each set
-// streams 64-position K/V tiles into its own pair of LDS stages with gfx950's
-// direct-to-LDS loads (global_load_lds_dwordx4, no register staging); the next
-// tile's loads are in flight while the current one is consumed. Per tile:
+// and a pair of 32-row q tiles with 8 wavefronts: two sets of four (one head
+// each), so each SIMD runs two wavefronts whose MFMA, exponential and LDS
+// phases overlap. Set 0 takes the first half of the heavy q tile's key tiles;
+// set 1 the light q tile's key tiles, then the rest of the heavy tile's. Each
+// set streams 64-position K/V tiles into its own pair of LDS stages with
+// gfx950's direct-to-LDS loads (global_load_lds_dwordx4, no register staging);
+// the next tile's loads are in flight while the current one is consumed. Per
+// tile:
 //   S^T[32 keys x 32 q] = K . Q^T         v_mfma_f32_32x32x16_f16 (x2)
 //   O^T[D x 32 q]      += V^T . P^T       v_mfma_f32_32x32x16_f16
 // With S transposed a lane holds 16 scores of one query row, so row max/sum
@@ -21,9 +23,9 @@
 // chunks so both read patterns are bank-conflict free. q (pre-scaled by
 // scale * log2 e) and p are rounded to f16 for the products; the softmax state
 // is f32 in the log2 domain with a lazy reference max (rescale only on growth
-// > 2^8); the row sum adds the f16 weights the products use. Causal masking
-// runs only on tiles that cross the diagonal. The two sets' (max, sum, O)
-// merge through LDS at the end of a q tile.
+// > 2^8); the row sum adds the f32 weights. Causal masking runs only on tiles
+// that cross the diagonal. Set 1 writes the light tile's rows itself; the two
+// sets' (max, sum, O) of the heavy tile merge through LDS at the end.
 //
 // Load balance: q tiles are paired heaviest with lightest (tile NQ-1-i with
 // tile i) so every workgroup carries the same number of key tiles, and the
@@ -316,193 +318,222 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const DmaPlan<D, RSK, G::BK> dk(hw, lane);
     const DmaPlan<D, RSV, G::BV> dv(hw, lane);
 
+    // Key-tile schedule of the q-tile pair (heavy tile NQ-1-i with H key tiles, light
+    // tile i with L): set 0 takes the heavy tile's key tiles [0, k0), set 1 the light
+    // tile's L key tiles and then the heavy tile's [k0, H), k0 = ceil((H + L) / 2). Both
+    // sets run k0 rounds; the light tile's rows are written by set 1 alone and only the
+    // heavy tile's two partials merge, when set 1 reaches that tile.
     const uint32_t heavy = p.n_qtiles - 1 - pair;
     const bool has_light = pair < heavy;  // the middle tile of an odd count is processed once
-    // Keys of the light q tile, and the stage parity its first round starts on for
-    // this set (its first tile is loaded during the heavy tile's last round).
-    const uint32_t kv_end_light = p.pos + min(p.n_tokens, pair * kQRows + kQRows);
-    const uint32_t n_kt_light = (kv_end_light + kKTile - 1) / kKTile;
-    const uint32_t n_kt_heavy = (p.pos + min(p.n_tokens, heavy * kQRows + kQRows) + kKTile - 1) / kKTile;
-    // Stage parity of set s's first round in q tile sel: 0 for the heavy tile; for the
-    // light tile, the stage its first tile was loaded into (the one after the heavy
-    // tile's last round of set s).
-    auto sb_of = [&](int sel, int s) -> uint32_t {
-        if (sel == 0) return 0;
-        const uint32_t rl = n_kt_heavy > (uint32_t)s ? (n_kt_heavy - 1 - s) / 2 : 0;
-        return (rl + 1) & 1;
+    auto kv_end_of = [&](uint32_t qtile) -> uint32_t {  // keys the q tile needs (exclusive)
+        return p.pos + min(p.n_tokens, qtile * kQRows + kQRows);
     };
-    for (int sel = 0; sel < 2; sel++) {
-        const uint32_t qt = sel == 0 ? heavy : pair;
-        if (sel == 1 && !has_light) break;
-        const uint32_t q0 = qt * kQRows;
-        const uint32_t t = q0 + r32;
-        const uint32_t tc = min(t, p.n_tokens - 1);
-        const bool keep = live && t < p.n_tokens;
-        const uint64_t t_abs = (uint64_t)p.pos + t;
-        const uint32_t kv_end = p.pos + min(p.n_tokens, q0 + kQRows);  // keys this tile needs (exclusive)
-        const uint32_t n_kt = (kv_end + kKTile - 1) / kKTile;
-        const uint32_t n_full = (p.pos + q0 + 1) / kKTile;             // tiles with no masked key
-        const uint32_t n_rounds = (n_kt + 1) / 2;                      // set s takes tiles 2 r + s
-        const uint32_t sb = sb_of(sel, set);
-        // in its last round the set loads the light tile's first tile (set 0: key tile 0, set 1: 1)
-        const bool prefetch_light = sel == 0 && has_light && (uint32_t)set < n_kt_light;
+    const uint32_t H = (kv_end_of(heavy) + kKTile - 1) / kKTile;
+    const uint32_t L = has_light ? (kv_end_of(pair) + kKTile - 1) / kKTile : 0;
+    const uint32_t k0 = (H + L + 1) / 2;  // rounds; L <= H, so k0 <= H
+    const uint32_t n_items = set == 0 ? k0 : L + H - k0;
+    const bool merge = H > k0;  // set 1 ends on the heavy tile
+    // item i of this set: its q tile and key tile
+    auto item_qt = [&](uint32_t i) -> uint32_t { return set == 1 && i < L ? pair : heavy; };
+    auto item_kt = [&](uint32_t i) -> uint32_t { return set == 0 ? i : (i < L ? i : k0 + i - L); };
 
-        // ---- q operand first (vmcnt retires in issue order), then the first tile.
-        // lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
+    // the wavefront's q tile: lane (r32, h) holds query row t
+    uint32_t qt = item_qt(0);
+    uint32_t t = qt * kQRows + r32;
+    bool keep = live && t < p.n_tokens;
+    uint32_t n_full = (p.pos + qt * kQRows + 1) / kKTile;  // key tiles with no masked key
+
+    // q operand of lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
+    f16x8 qop[KS], qnext[KS];
+    auto load_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
+        const uint32_t tc = min(qtile * kQRows + r32, p.n_tokens - 1);
         const f16* qrow = p.q16 + ((uint64_t)tc * p.n_q_heads + hq) * D + 8 * h;
-        f16x8 qop[KS];
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) qop[ks] = *(const f16x8*)(qrow + 16 * ks);
-        if (sel == 0) {  // the light tile's first tiles are already in LDS
-            dma_tile(k_lds, kc, set * kKTile, kv_end, dk, hw, lane);
-            dma_tile(v_lds, vc, set * kKTile, kv_end, dv, hw, lane);
-        }
-        if (!keep) {
+        for (int ks = 0; ks < KS; ks++) dst[ks] = *(const f16x8*)(qrow + 16 * ks);
+    };
+    // ---- q operand first (vmcnt retires in issue order), then the first tile
+    load_q(qop, qt);
+    if (n_items > 0) {
+        dma_tile(k_lds, kc, item_kt(0) * kKTile, kv_end_of(qt), dk, hw, lane);
+        dma_tile(v_lds, vc, item_kt(0) * kKTile, kv_end_of(qt), dv, hw, lane);
+    }
+    if (!keep) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
-        }
+        for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
+    }
 
-        f32x16 O[DT];
+    f32x16 O[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
-        float m_ref = -INFINITY, l_sum = 0.0f;
+        for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
+    float m_ref = -INFINITY, l_sum = 0.0f;
 
-        wait_vm<0>();
-        lds_sync();
-        // Round r: this set's tile j = 2 r + set sits in its stage (r + sb) % 2; the
-        // tile of round r + 1 streams into the other stage meanwhile (that stage
-        // was last read in round r - 1, before the previous barrier). In the set's
-        // last round the other stage receives the light q tile's first tile instead.
-        for (uint32_t r = 0; r < n_rounds; r++) {
-            const uint32_t j = 2 * r + set;
-            const uint32_t kcur = ((r + sb) & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
-            const uint32_t vcur = ((r + sb) & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
-            const bool own_next = j + 2 < n_kt;
-            const bool load_next = own_next || prefetch_light;
-            const uint32_t nkey0 = own_next ? (j + 2) * kKTile : (uint32_t)set * kKTile;
-            const uint32_t nend = own_next ? kv_end : kv_end_light;
-            // The next tile's loads are issued in two halves inside the round (a
-            // burst from all eight wavefronts right after the barrier would stall
-            // their issue); with no tile this round there is none next round.
-            if (j < n_kt) {
-                const uint32_t key0 = j * kKTile;
-                const char* sk = k_st + kcur + kb;
-                f32x16 S[2];  // S^T of the tile's two 32-key halves
-#pragma unroll
-                for (int kh = 0; kh < 2; kh++) {
-#pragma unroll
-                    for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
-#pragma unroll
-                    for (int ks = 0; ks < KS; ks++) {
-                        const f16x8 a = *(const f16x8*)(sk + 32 * kh * RSK + 32 * ks);
-                        S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
-                    }
-                }
-                if (load_next) dma_tile(k_lds + knxt, kc, nkey0, nend, dk, hw, lane);
-                // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
-                if (j >= n_full) {  // causal mask on tiles that reach past the first row
-#pragma unroll
-                    for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                        for (int i = 0; i < 16; i++) {
-                            const uint64_t key = key0 + 32 * kh + 8 * (i / 4) + 4 * h + (i % 4);
-                            if (key > t_abs) S[kh][i] = -INFINITY;
-                        }
-                }
-                float mx = S[0][0];
-#pragma unroll
-                for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) mx = fmaxf(mx, S[kh][i]);
-                mx = max_xor32(mx);
-                if (__ballot(mx > m_ref + kRescaleLog2) != 0) {  // lazy rescale (also the first tile)
-                    const float m_new = mx > m_ref + kRescaleLog2 ? mx : m_ref;
-                    const float alpha = m_new == m_ref ? 1.0f : fast_exp2(m_ref - m_new);  // -inf - -inf would be NaN
-                    l_sum *= alpha;
-#pragma unroll
-                    for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
-                    m_ref = m_new;
-                }
-                // A row with every key so far masked (possible in set 1, whose first
-                // tile is key tile 1) keeps m_ref = -inf; its weights are 0.
-                const float m_exp = m_ref == -INFINITY ? 0.0f : m_ref;
-                f16x8 pop[4];  // P^T operand of key step m: scores i = 8 (m % 2) + jj of half m / 2
-                // Row sum in f32 adds of the f32 weights: v_dot2 of the f16 weights would
-                // share the matrix core with the other wavefront's products on this SIMD.
-                float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int m = 0; m < 4; m++)
-#pragma unroll
-                    for (int jj = 0; jj < 8; jj++) {
-                        const float e = fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
-                        pop[m][jj] = (f16)e;
-                        ps[m] += e;
-                    }
-                l_sum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-                if (load_next) dma_tile(v_lds + vnxt, vc, nkey0, nend, dv, hw, lane);
-                // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
-                // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
-                // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
-                const char* sv = v_st + vcur + vb;
-#pragma unroll
-                for (int m = 0; m < 4; m++)
-#pragma unroll
-                    for (int dt = 0; dt < DT; dt++) {
-                        const f16x4 lo = lds_read_tr16(sv + 16 * m * RSV + 64 * dt);
-                        const f16x4 hi = lds_read_tr16(sv + (16 * m + 8) * RSV + 64 * dt);
-                        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
-                    }
-            }
-            wait_vm<0>();
-            lds_sync();
-        }
-
-        // ---- merge set 1 into set 0 through LDS: head slot hw uses a stage freed by
-        // the last round (slots 0, 1: set 0's K and V stages of its last round's
-        // parity; 2, 3: set 1's), so the light tile's prefetched stages stay intact.
-        // [float4 index][lane]
-        constexpr int NV4 = DT * 4 + 1;  // O as float4s, then (m, l, -, -)
-        static_assert(NV4 * 64 * 16 <= G::KSTAGE && G::KSTAGE <= G::VSTAGE, "a merge slot fits a stage");
-        const int ms = hw >> 1;  // set whose stage holds this slot
-        const uint32_t r_last_ms = n_kt > (uint32_t)ms ? (n_kt - 1 - ms) / 2 : 0;
-        const uint32_t lp_ms = (r_last_ms + sb_of(sel, ms)) & 1;
-        char* const slot = s_kv + ms * G::SET_BYTES +
-                           ((hw & 1) == 0 ? lp_ms * G::KSTAGE : 2 * G::KSTAGE + lp_ms * G::VSTAGE);
-        float4* mrg = (float4*)slot + lane;
-        if (set == 1) {
+    // The wavefront's rows of its q tile when every key of the tile went through it:
+    // O over its own row sum. Wave-uniform call (the row sum crosses lanes).
+    auto write_rows = [&]() {
+        const float l = sum_xor32(l_sum);
+        if (keep) {
+            const float inv_l = 1.0f / l;
+            float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int i4 = 0; i4 < 4; i4++)
-                    mrg[(dt * 4 + i4) * 64] = float4{O[dt][4 * i4], O[dt][4 * i4 + 1], O[dt][4 * i4 + 2], O[dt][4 * i4 + 3]};
-            mrg[DT * 4 * 64] = float4{m_ref, l_sum, 0.0f, 0.0f};
+                    *(float4*)(out + dt * 32 + 8 * i4 + 4 * h) =
+                        float4{O[dt][4 * i4] * inv_l, O[dt][4 * i4 + 1] * inv_l, O[dt][4 * i4 + 2] * inv_l,
+                               O[dt][4 * i4 + 3] * inv_l};
         }
-        lds_sync();
-        if (set == 0) {
-            const float4 ml = mrg[DT * 4 * 64];
-            const float m = fmaxf(m_ref, ml.x);  // m_ref is finite (key 0 is visible to set 0)
-            const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(ml.x - m);  // set 1 with no tile: m1 = -inf, a1 = 0
-            const float l = sum_xor32(l_sum * a0 + ml.y * a1);
-            if (keep) {
-                const float inv_l = 1.0f / l;
-                float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
+    };
+
+    wait_vm<0>();
+    lds_sync();
+    // Round r: item r of each set sits in stage r % 2; item r + 1 streams into the other
+    // stage meanwhile (that stage was last read in round r - 1, before the previous barrier).
+    for (uint32_t r = 0; r < k0; r++) {
+        const uint32_t kcur = (r & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
+        const uint32_t vcur = (r & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
+        if (set == 1 && L > 0 && L < n_items) {
+            // set 1 moves from the light tile to the heavy one: the heavy q operand loads
+            // one round ahead (drained by that round's barrier wait); at round L the light
+            // rows are written and the softmax state restarts
+            if (r + 1 == L) load_q(qnext, heavy);
+            if (r == L) {
+                write_rows();
+                qt = heavy;
+                t = qt * kQRows + r32;
+                keep = live && t < p.n_tokens;
+                n_full = (p.pos + qt * kQRows + 1) / kKTile;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) qop[ks] = keep ? qnext[ks] : f16x8{};
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-                    for (int i4 = 0; i4 < 4; i4++) {
-                        const float4 o1 = mrg[(dt * 4 + i4) * 64];
-                        const int d = dt * 32 + 8 * i4 + 4 * h;
-                        *(float4*)(out + d) = float4{(O[dt][4 * i4] * a0 + o1.x * a1) * inv_l,
-                                                     (O[dt][4 * i4 + 1] * a0 + o1.y * a1) * inv_l,
-                                                     (O[dt][4 * i4 + 2] * a0 + o1.z * a1) * inv_l,
-                                                     (O[dt][4 * i4 + 3] * a0 + o1.w * a1) * inv_l};
-                    }
+                    for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
+                m_ref = -INFINITY;
+                l_sum = 0.0f;
             }
         }
-        lds_sync();  // the merge slots are stages again for the light tile
+        const bool load_next = r + 1 < n_items;
+        const uint32_t nkey0 = item_kt(r + 1) * kKTile, nend = kv_end_of(item_qt(r + 1));
+        // The next tile's loads are issued in two halves inside the round (a burst from
+        // all eight wavefronts right after the barrier would stall their issue).
+        if (r < n_items) {
+            const uint32_t j = item_kt(r);
+            const uint32_t key0 = j * kKTile;
+            const uint64_t t_abs = (uint64_t)p.pos + t;
+            const char* sk = k_st + kcur + kb;
+            f32x16 S[2];  // S^T of the tile's two 32-key halves
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const f16x8 a = *(const f16x8*)(sk + 32 * kh * RSK + 32 * ks);
+                    S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
+                }
+            }
+            if (load_next) dma_tile(k_lds + knxt, kc, nkey0, nend, dk, hw, lane);
+            // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
+            if (j >= n_full) {  // causal mask on tiles that reach past the first row
+#pragma unroll
+                for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const uint64_t key = key0 + 32 * kh + 8 * (i / 4) + 4 * h + (i % 4);
+                        if (key > t_abs) S[kh][i] = -INFINITY;
+                    }
+            }
+            float mx = S[0][0];
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) mx = fmaxf(mx, S[kh][i]);
+            mx = max_xor32(mx);
+            if (__ballot(mx > m_ref + kRescaleLog2) != 0) {  // lazy rescale (also the first tile)
+                const float m_new = mx > m_ref + kRescaleLog2 ? mx : m_ref;
+                const float alpha = m_new == m_ref ? 1.0f : fast_exp2(m_ref - m_new);  // -inf - -inf would be NaN
+                l_sum *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
+                m_ref = m_new;
+            }
+            // A row with every key so far masked (possible in set 1, whose part of the
+            // heavy tile starts at key tile k0) keeps m_ref = -inf; its weights are 0.
+            const float m_exp = m_ref == -INFINITY ? 0.0f : m_ref;
+            f16x8 pop[4];  // P^T operand of key step m: scores i = 8 (m % 2) + jj of half m / 2
+            // Row sum in f32 adds of the f32 weights: v_dot2 of the f16 weights would
+            // share the matrix core with the other wavefront's products on this SIMD.
+            float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    const float e = fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
+                    pop[m][jj] = (f16)e;
+                    ps[m] += e;
+                }
+            l_sum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+            if (load_next) dma_tile(v_lds + vnxt, vc, nkey0, nend, dv, hw, lane);
+            // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
+            // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
+            // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
+            const char* sv = v_st + vcur + vb;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    const f16x4 lo = lds_read_tr16(sv + 16 * m * RSV + 64 * dt);
+                    const f16x4 hi = lds_read_tr16(sv + (16 * m + 8) * RSV + 64 * dt);
+                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
+                }
+        }
+        wait_vm<0>();
+        lds_sync();
+    }
+
+    if (!merge) {
+        if (set == 0 || L > 0) write_rows();  // set 0: the heavy tile; set 1: the light tile
+        return;
+    }
+    // ---- merge set 1 (the heavy tile's keys [k0, H)) into set 0 through LDS; every stage
+    // is free after the last round. Head slot hw: [float4 index][lane].
+    constexpr int NV4 = DT * 4 + 1;  // O as float4s, then (m, l, -, -)
+    static_assert(NV4 * 64 * 16 <= G::KSTAGE && G::KSTAGE <= G::VSTAGE, "a merge slot fits a stage");
+    char* const slot = s_kv + (hw >> 1) * G::SET_BYTES + ((hw & 1) == 0 ? 0 : 2 * G::KSTAGE);
+    float4* mrg = (float4*)slot + lane;
+    if (set == 1) {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; i4++)
+                mrg[(dt * 4 + i4) * 64] = float4{O[dt][4 * i4], O[dt][4 * i4 + 1], O[dt][4 * i4 + 2], O[dt][4 * i4 + 3]};
+        mrg[DT * 4 * 64] = float4{m_ref, l_sum, 0.0f, 0.0f};
+    }
+    lds_sync();
+    if (set == 0) {
+        const float4 ml = mrg[DT * 4 * 64];
+        const float m = fmaxf(m_ref, ml.x);  // m_ref is finite (key 0 is visible to set 0)
+        // a row whose keys in set 1's range were all masked has ml.x = -inf: a1 = 0
+        const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(ml.x - m);
+        const float l = sum_xor32(l_sum * a0 + ml.y * a1);
+        if (keep) {
+            const float inv_l = 1.0f / l;
+            float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; i4++) {
+                    const float4 o1 = mrg[(dt * 4 + i4) * 64];
+                    const int d = dt * 32 + 8 * i4 + 4 * h;
+                    *(float4*)(out + d) = float4{(O[dt][4 * i4] * a0 + o1.x * a1) * inv_l,
+                                                 (O[dt][4 * i4 + 1] * a0 + o1.y * a1) * inv_l,
+                                                 (O[dt][4 * i4 + 2] * a0 + o1.z * a1) * inv_l,
+                                                 (O[dt][4 * i4 + 3] * a0 + o1.w * a1) * inv_l};
+                }
+        }
     }
 }
 

@@ -390,30 +390,28 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
     n_hgroups = (group + P_HEADS - 1) // P_HEADS
     head_bytes = max_ctx * 2 * D
     calls = set()
+    kv_end_of = lambda qt: pos + min(T, qt * P_QROWS + P_QROWS)
     for pair in range(n_pairs):
         heavy = n_qtiles - 1 - pair
         has_light = pair < heavy
-        kv_end_light = pos + min(T, pair * P_QROWS + P_QROWS)
-        n_kt_light = (kv_end_light + P_KTILE - 1) // P_KTILE
+        H = (kv_end_of(heavy) + P_KTILE - 1) // P_KTILE
+        L = (kv_end_of(pair) + P_KTILE - 1) // P_KTILE if has_light else 0
+        k0 = (H + L + 1) // 2
+        # schedule: set 0 takes heavy key tiles [0, k0), set 1 light [0, L) then heavy [k0, H)
+        items = {0: [(heavy, j) for j in range(k0)],
+                 1: [(pair, j) for j in range(L)] + [(heavy, j) for j in range(k0, H)]}
+        assert len(items[1]) <= k0 and k0 <= H
+        done = items[0] + items[1]
+        want = [(heavy, j) for j in range(H)] + [(pair, j) for j in range(L)]
+        assert sorted(done) == sorted(want) and len(set(done)) == len(done)  # every key tile once
+        for st in range(P_SETS):
+            for qt, j in items[st]:
+                calls.add((j * P_KTILE, kv_end_of(qt)))
         for sel in range(2):
             if sel == 1 and not has_light:
                 break
             qt = heavy if sel == 0 else pair
             q0 = qt * P_QROWS
-            kv_end = pos + min(T, q0 + P_QROWS)
-            n_kt = (kv_end + P_KTILE - 1) // P_KTILE
-            for st in range(P_SETS):
-                if sel == 0:
-                    calls.add((st * P_KTILE, kv_end))
-                prefetch_light = sel == 0 and has_light and st < n_kt_light
-                for r in range((n_kt + 1) // 2):
-                    j = 2 * r + st
-                    if j >= n_kt:
-                        continue
-                    own_next = j + 2 < n_kt
-                    if own_next or prefetch_light:
-                        calls.add(((j + 2) * P_KTILE if own_next else st * P_KTILE,
-                                   kv_end if own_next else kv_end_light))
             # q operand: lane (r32, h): row min(q0 + r32, T - 1), head hq, halves 8h + 16 ks .. + 8
             tc = np.minimum(q0 + np.arange(32), T - 1)
             for hg in range(n_hgroups):
