@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void q_pack_kernel(const float* q, f16* q16, u
 // Attention.
 // ---------------------------------------------------------------------------
 constexpr int kHeads = 4;      // q heads per workgroup
-constexpr int kSets = 2;       // wavefront sets, each takes every other key tile
+constexpr int kSets = 2;       // wavefront sets (set 0: heavy q tile's first key tiles; set 1: the rest)
 constexpr int kWaves = kHeads * kSets;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA N)
