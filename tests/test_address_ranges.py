@@ -432,7 +432,7 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
 @pytest.mark.parametrize("pos,T,hq,hkv,D,cap", [
     (0, 2048, 32, 4, 128, 2048),     # C2
     (0, 300, 32, 4, 128, 307), (100, 130, 32, 4, 128, 237), (5, 77, 32, 4, 64, 89), (0, 2, 32, 4, 128, 9),
-    (0, 97, 32, 4, 128, 104), (31, 200, 64, 4, 128, 238), (3, 96, 6, 3, 128, 106), (0, 65, 8, 8, 64, 72),
+    (0, 97, 32, 4, 128, 104), (48, 160, 32, 4, 128, 215), (31, 200, 64, 4, 128, 238), (3, 96, 6, 3, 128, 106), (0, 65, 8, 8, 64, 72),
 ])
 def test_prefill_dma_addresses(pos, T, hq, hkv, D, cap):
     """C2 and the GPU parity suite's prefill shapes (chunked continuations, odd q-tile counts)."""

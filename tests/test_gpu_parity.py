@@ -315,6 +315,7 @@ def test_decode_step_configs(ctx, hip, oracle, config, layer, fused):
     (77, 5, 64, 32, 4),     # head_dim 64
     (2, 0, 128, 32, 4),     # one key tile: the second wavefront set idles
     (97, 0, 128, 32, 4),    # odd q-tile count: the middle tile runs once
+    (160, 48, 128, 32, 4),  # middle tile whose first 16 rows see no key in set 1's key tiles
     (200, 31, 128, 64, 4),  # 16-head group: four head groups per kv head
     (96, 3, 128, 6, 3),     # 2-head group: half the wavefronts have no head
     (65, 0, 64, 8, 8),      # no grouping, head_dim 64
