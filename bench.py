@@ -417,6 +417,24 @@ class BlockPrefill:
 USE_GRAPHS = True  # --no-graph: sweeps run eagerly (profiling runs; the profiler's graph interception is unstable)
 
 
+# Single-layer legs (C2, QKVP, BLK) capture this many back-to-back sweeps per graph: a graph
+# launch costs ~5-35 us of device idle per replay here (measured: BLK 228 us per sweep with
+# one sweep per graph, 195 with eight, 194 eager), which a multi-layer graph amortises and an
+# op inside a real forward graph never pays on its own.
+SWEEPS_PER_GRAPH = 8
+
+
+class Repeat:
+    """n back-to-back sweeps of `work` as one sweep (one captured graph holds all n)."""
+
+    def __init__(self, work, n):
+        self.work, self.n = work, n
+
+    def sweep(self):
+        for _ in range(self.n):
+            self.work.sweep()
+
+
 def time_graph(ctx, work, steps, warmup):
     """Capture work.sweep() once, replay warmup + steps times; returns (device seconds
     of the timed replays from events on the context stream, wall seconds). Without
@@ -850,20 +868,24 @@ def main():
 
     if 2 in W and "C2" in only:
         p = W[2]
-        el1, _ = time_graph(ctx, p, 5, 2)
-        reps = replays_for(el1 / 5, leg, 10)
-        elapsed, _ = time_graph(ctx, p, reps, 2)
-        e2e_us = elapsed / reps * 1e6
+        pr = Repeat(p, SWEEPS_PER_GRAPH)
+        el1, _ = time_graph(ctx, pr, 3, 1)
+        reps = replays_for(el1 / 3, leg, 5)
+        elapsed, _ = time_graph(ctx, pr, reps, 2)
+        e2e_us = elapsed / (reps * SWEEPS_PER_GRAPH) * 1e6
         ks = kernel_stats(ctx, p, ("prefill_prep_kernel", "prefill_attention_kernel"), leg)
         ns_pf = ks["prefill_attention_kernel"][0]
         tf = p.flops / ns_pf / 1e3
         sep = Prefill(H, synth, ctx, fused=False)
-        el_sep, _ = time_graph(ctx, sep, max(10, reps // 4), 2)
+        n_sep = max(5, reps // 4)
+        el_sep, _ = time_graph(ctx, Repeat(sep, SWEEPS_PER_GRAPH), n_sep, 2)
         r = dict(end_to_end_us=round(e2e_us, 3), kernel_us=dict(prefill_prep_kernel=round(ks["prefill_prep_kernel"][0] / 1e3, 3),
                                                                prefill_attention_kernel=round(ns_pf / 1e3, 3)),
                  tflops=round(tf, 2), frac=round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                  tflops_end_to_end=round(p.flops / (e2e_us * 1e3) / 1e3, 2), flops=p.flops,
-                 peak_tflops=F16_MFMA_PEAK_TFLOPS, six_ops_end_to_end_us=round(el_sep / max(10, reps // 4) * 1e6, 3))
+                 peak_tflops=F16_MFMA_PEAK_TFLOPS,
+                 six_ops_end_to_end_us=round(el_sep / (n_sep * SWEEPS_PER_GRAPH) * 1e6, 3),
+                 sweeps_per_graph=SWEEPS_PER_GRAPH)
         ru = rocprof_kernel_us("C2", "prefill_attention_kernel")
         if ru:
             r["rocprof_kernel_us"] = ru
@@ -963,8 +985,9 @@ def main():
     if "QKVP" in only:
         log("[bench] QKVP: prefill q/k/v projections, 2048 tokens, Q8_0 wq [4096 x 2048] + wk, wv [512 x 2048]")
         p = ProjPrefill(H, ctx)
-        n_rep = max(5, args.steps // 5)
-        elapsed, _ = time_graph(ctx, p, n_rep, 2)
+        n_rep = max(10, args.steps // 3)
+        elapsed, _ = time_graph(ctx, Repeat(p, SWEEPS_PER_GRAPH), n_rep, 2)
+        elapsed /= SWEEPS_PER_GRAPH
         ks = kernel_stats(ctx, p, ("matmul_q8_mfma_kernel", "matmul_x_split_kernel"), leg)
         ns_k, ns_split = ks["matmul_q8_mfma_kernel"][0], ks["matmul_x_split_kernel"][0]
         tf = p.flops / ns_k / 1e3
@@ -983,12 +1006,13 @@ def main():
         legs = {}
         for fused in (True, False):
             p = BlockPrefill(H, synth, ctx, fused=fused)
-            n_rep = max(5, args.steps // 5)
-            elapsed, _ = time_graph(ctx, p, n_rep, 2)
+            n_rep = max(10, args.steps // 3)
+            elapsed, _ = time_graph(ctx, Repeat(p, SWEEPS_PER_GRAPH), n_rep, 2)
+            elapsed /= SWEEPS_PER_GRAPH
             names = ("matmul_x_split_kernel", "matmul_q8_mfma_kernel", "prefill_prep_kernel",
                      "prefill_attention_kernel")
             ks = kernel_stats(ctx, p, names, leg)
-            legs[fused] = dict(end_to_end_us=round(elapsed / n_rep * 1e6, 3),
+            legs[fused] = dict(end_to_end_us=round(elapsed / n_rep * 1e6, 3), sweeps_per_graph=SWEEPS_PER_GRAPH,
                                kernel_us={k: round(ks[k][0] / 1e3, 3) for k in names if ks[k][1]})
             del p
         extra["attention_block_prefill"] = dict(
