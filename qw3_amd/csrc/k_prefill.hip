@@ -49,6 +49,36 @@ namespace {
 constexpr int kPrepThreads = 256;
 constexpr int kPrepMaxRow = 2048;  // n_kv_heads * head_dim floats staged per token
 
+// Elementwise squares (each rounded to f32, as the reference's acc += v * v rounds the
+// product before the add).
+__device__ __forceinline__ float4 sq4(float4 v) {
+#pragma clang fp contract(off)
+    return float4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+}
+
+// Serial-order sum of D squares held in LDS (kernels_a.zig:85-86's order): the reads
+// go out four 16-byte chunks at a time ahead of their adds, so the dependent chain
+// waits for one LDS round trip per batch rather than per chunk.
+template <int D>
+__device__ __forceinline__ float serial_sum_sq(const float* sq) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int b = 0; b < D; b += 16) {
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = *(const float4*)(sq + b + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            acc += v[j].x;
+            acc += v[j].y;
+            acc += v[j].z;
+            acc += v[j].w;
+        }
+    }
+    return acc;
+}
+
 // Token t: cos/sin of its rope angles (kernels_a.zig:119-122); every kv head's
 // k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX rotation (:125-126),
 // f16 append at slot pos + t (:196-210); v rows f16. Then the q rows of every
@@ -58,38 +88,58 @@ constexpr int kPrepMaxRow = 2048;  // n_kv_heads * head_dim floats staged per to
 template <int D>
 __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, f16* q16, RopeTable table) {
     __shared__ __attribute__((aligned(16))) float s_k[kPrepMaxRow];
+    __shared__ __attribute__((aligned(16))) float s_ksq[kPrepMaxRow];  // the k squares, formed in parallel
     __shared__ float s_cos[D / 2], s_sin[D / 2];
     __shared__ float s_inv[kPrepMaxRow / 64];
     constexpr uint32_t half = D / 2;
     constexpr uint32_t TPH = D / 16;  // q: threads per head, thread k takes dims 8k + [0, 8) and half + 8k + [0, 8)
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t H = a.n_kv_heads, HQ = a.n_q_heads;
-    // Every global load of the token is issued up front (k to LDS, the first q
-    // chunk and v quad of this thread to registers), so one memory round trip
-    // covers them all.
-    const float* krow = a.k + (uint64_t)t * H * D;
-    for (uint32_t e = tid; e < H * D / 4; e += kPrepThreads) ((float4*)s_k)[e] = ((const float4*)krow)[e];
+    // Every load of the token is issued up front, with no wait in between (this
+    // thread's k and v quads, its first q chunk, the position and its inverse
+    // frequency; each unconditional with a clamped index, since a load under a
+    // branch makes the compiler wait at the join), so one memory round trip covers
+    // them all. (Staging k in LDS straight from its loads made every thread wait
+    // for k before issuing q and v: three round trips instead of one.)
+    const float pos = (float)a.positions[t];
+    const float inv_freq = table.inv[min(tid, half - 1)];  // the threads < half use it
+    static_assert(D / 2 <= kPrepThreads, "one rope angle per thread");
+    static_assert(kPrepMaxRow / 4 <= 2 * kPrepThreads, "k quads: two per thread at most");
+    const uint32_t nk4 = H * D / 4;
+    const float4* krow = (const float4*)(a.k + (uint64_t)t * H * D);
+    const float4 kq0 = krow[min(tid, nk4 - 1)];
+    const float4 kq1 = krow[min(tid + kPrepThreads, nk4 - 1)];
     const float* qbase = a.q + (uint64_t)t * HQ * D;
     float x0[8], x1[8];
-    if (tid < HQ * TPH) {
-        const float* row = qbase + (tid / TPH) * D + 8 * (tid % TPH);
+    {
+        const uint32_t e = min(tid, HQ * TPH - 1);
+        const float* row = qbase + (e / TPH) * D + 8 * (e % TPH);
         *(float4*)&x0[0] = *(const float4*)(row);
         *(float4*)&x0[4] = *(const float4*)(row + 4);
         *(float4*)&x1[0] = *(const float4*)(row + half);
         *(float4*)&x1[4] = *(const float4*)(row + half + 4);
     }
     const float4* vrow = (const float4*)(a.v + (uint64_t)t * H * D);
-    float4 v0 = tid < H * D / 4 ? vrow[tid] : float4{};
-    const float pos = (float)a.positions[t];
-    for (uint32_t i = tid; i < half; i += kPrepThreads) {
-        const float ang = qk_rope_angle(pos, a.freq_scale, table.inv[i]);
-        s_cos[i] = cosf(ang);
-        s_sin[i] = sinf(ang);
+    const float4 v0 = vrow[min(tid, nk4 - 1)];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < half) {
+        const float ang = qk_rope_angle(pos, a.freq_scale, inv_freq);
+        s_cos[tid] = cosf(ang);
+        s_sin[tid] = sinf(ang);
+    }
+    if (tid < nk4) {
+        ((float4*)s_k)[tid] = kq0;
+        ((float4*)s_ksq)[tid] = sq4(kq0);
+    }
+    if (tid + kPrepThreads < nk4) {
+        ((float4*)s_k)[tid + kPrepThreads] = kq1;
+        ((float4*)s_ksq)[tid + kPrepThreads] = sq4(kq1);
     }
     __syncthreads();
-    for (uint32_t h = tid; h < H; h += kPrepThreads) s_inv[h] = rms_inv(qk_serial_sumsq(s_k + h * D, (int)D), (float)D, a.eps);
+    for (uint32_t h = tid; h < H; h += kPrepThreads) s_inv[h] = rms_inv(serial_sum_sq<D>(s_ksq + h * D), (float)D, a.eps);
     // v rows: f16 append
-    for (uint32_t e = tid; e < H * D / 4; e += kPrepThreads) {
+    for (uint32_t e = tid; e < nk4; e += kPrepThreads) {
         const float4 v = e == tid ? v0 : vrow[e];
         const uint32_t h = (4 * e) / D, i = (4 * e) % D;
         const f16x4 y = {(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
