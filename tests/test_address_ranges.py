@@ -197,6 +197,16 @@ def test_decode_paged_addresses_config4():
     assert n > 0
 
 
+@pytest.mark.parametrize("page_size", [32, 64])
+def test_decode_paged_addresses_larger_pages(page_size):
+    """The GPU suite's 32- and 64-position page cases (7 sequences, lengths 1..700)."""
+    s = synth.Shape()
+    lay = synth.paged_layout(7, 1, 700, page_size, seed=11)
+    n = check_decode(7, s.n_q_heads, s.n_kv_heads, s.head_dim, lay.seq_lens, lay.n_pages * page_size, page_size,
+                     lay.page_table, lay.n_pages, int(lay.seq_lens.max()))
+    assert n > 0
+
+
 def test_paged_plan_fits_and_is_smallest():
     """The plan's chunk is the smallest admissible one: the next smaller multiple of
     128 (when admissible) overflows the cap. C4's lengths give ~2 workgroups per CU."""

@@ -365,11 +365,11 @@ def test_prefill_config2_full(ctx, hip, oracle, fused):
 # paged decode (C4 layout)
 # ---------------------------------------------------------------------------
 
-def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None):
+def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None, page_size=16):
     s = synth.Shape()
-    lay = synth.paged_layout(n_seqs, lo, hi, 16, seed=seed)
+    lay = synth.paged_layout(n_seqs, lo, hi, page_size, seed=seed)
     hq, hkv, hd = s.n_q_heads, s.n_kv_heads, s.head_dim
-    slots = lay.n_pages * 16
+    slots = lay.n_pages * page_size
     g = np.random.default_rng(seed)
     kpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
     vpool = oracle.f32_to_f16_bits(g.standard_normal((hkv, slots, hd)).astype(np.float32))
@@ -379,7 +379,7 @@ def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None):
     max_len = int(lay.seq_lens.max())
     hip.pagedDecode(ctx, hip.PagedDecodeArgs(dev(ctx, q), dev(ctx, k), dev(ctx, v), dev(ctx, qn), dev(ctx, kn), kpb,
                                              vpb, dev(ctx, lay.page_table), dev(ctx, lay.seq_lens), out, n_seqs, hq,
-                                             hkv, hd, 16, lay.n_pages, lay.max_pages, max_len, s.eps, s.theta, 1.0,
+                                             hkv, hd, page_size, lay.n_pages, lay.max_pages, max_len, s.eps, s.theta, 1.0,
                                              s.scale))
     got = ctx.to_numpy(out, np.float32).reshape(n_seqs, hq * hd)
     gk, gv = host(ctx, kpb, kpool), host(ctx, vpb, vpool)
@@ -389,8 +389,8 @@ def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None):
     assert np.array_equal(gk[:, mask], kpool[:, mask]) and np.array_equal(gv[:, mask], vpool[:, mask])
     for b in (range(n_seqs) if check_seqs is None else check_seqs):
         L = int(lay.seq_lens[b])
-        kc = oracle.paged_gather_f16(kpool, lay.page_table[b], 16, L)
-        vc = oracle.paged_gather_f16(vpool, lay.page_table[b], 16, L)
+        kc = oracle.paged_gather_f16(kpool, lay.page_table[b], page_size, L)
+        vc = oracle.paged_gather_f16(vpool, lay.page_table[b], page_size, L)
         wout, wk, wv = _oracle_step(oracle, q[b:b + 1], k[b:b + 1], v[b:b + 1], qn, kn, np.array([L - 1], np.int32),
                                     kc, vc, L - 1, s)
         ulp_k = f16_ulp_diff(gk[:, new_slots[b]], wk[:, L - 1])
@@ -401,6 +401,13 @@ def _paged_case(ctx, hip, oracle, n_seqs, lo, hi, seed, check_seqs=None):
 
 def test_paged_decode_small(ctx, hip, oracle):
     _paged_case(ctx, hip, oracle, 7, 1, 300, seed=5)
+
+
+@pytest.mark.parametrize("page_size", [32, 64])
+def test_paged_decode_larger_pages(ctx, hip, oracle, page_size):
+    """Pages of 32 and 64 positions (the ABI takes any multiple of 16): a 32-position
+    tile then lies inside one page, and page boundaries fall inside a split."""
+    _paged_case(ctx, hip, oracle, 7, 1, 700, seed=11, page_size=page_size)
 
 
 def test_paged_decode_config4_geometry(ctx, hip, oracle):
