@@ -995,7 +995,7 @@ def main():
             kernel="matmul_q8_mfma_kernel", kernel_us=round(ns_k / 1e3, 3), tflops=round(tf, 2),
             frac=round(tf / BF16_MFMA_PEAK_TFLOPS, 4), end_to_end_us=round(elapsed / n_rep * 1e6, 3),
             flops=p.flops, peak_tflops=BF16_MFMA_PEAK_TFLOPS,
-            split_us=round(ns_split / 1e3, 3),
+            split_us=round(ns_split / 1e3, 3), sweeps_per_graph=SWEEPS_PER_GRAPH,
             shape="m 2048, n 4096 + 512 + 512, k 2048, Q8_0, one grouped call; x split into f16 hi and lo "
                   "(2 matrix-core products per useful one)")
         log(f"[bench] QKVP matmul_q8_mfma_kernel {ns_k / 1e3:.2f} us -> {tf:.1f} TFLOP/s (useful)")
