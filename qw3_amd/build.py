@@ -30,13 +30,22 @@ CXXFLAGS = [
 ]
 
 
+# Per-file extra flags. k_prefill.hip: MFMA accumulators in VGPRs. The attention
+# kernel reads its scores with VALU instructions, which cannot take AGPRs; with
+# the AGPR form the backend copied the O accumulators between the register files
+# every round.
+EXTRA_FLAGS = {
+    "k_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CXXFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CXXFLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -5,27 +5,29 @@
 // position pos + t) of q head h attends cache positions 0..pos+t of kv head
 // h / group; softmax(scale * q.k) in f32.
 //
-// prefill_attention_kernel. A workgroup serves 4 q heads of one GQA group
-// and a pair of 32-row q tiles with 8 wavefronts: two sets of four (one head
-// each), so each SIMD runs two wavefronts whose MFMA, exponential and LDS
-// phases overlap. Set 0 takes the first half of the heavy q tile's key tiles;
-// set 1 the light q tile's key tiles, then the rest of the heavy tile's. Each
-// set streams 64-position K/V tiles into its own pair of LDS stages with
-// gfx950's direct-to-LDS loads (global_load_lds_dwordx4, no register staging);
-// the next tile's loads are in flight while the current one is consumed. Per
-// tile:
-//   S^T[32 keys x 32 q] = K . Q^T         v_mfma_f32_32x32x16_f16 (x2)
-//   O^T[D x 32 q]      += V^T . P^T       v_mfma_f32_32x32x16_f16
-// With S transposed a lane holds 16 scores of one query row, so row max/sum
-// need one lane swap (v_permlane32_swap), and the P^T operand is the lane's
-// own scores. V^T operands come from LDS through the transpose read
-// (ds_read_b64_tr_b16). LDS rows are unpadded with XOR-swizzled 16-byte
-// chunks so both read patterns are bank-conflict free. q (pre-scaled by
-// scale * log2 e) and p are rounded to f16 for the products; the softmax state
-// is f32 in the log2 domain with a lazy reference max (rescale only on growth
-// > 2^8); the row sum adds the f32 weights. Causal masking runs only on tiles
-// that cross the diagonal. Set 1 writes the light tile's rows itself; the two
-// sets' (max, sum, O) of the heavy tile merge through LDS at the end.
+// prefill_attention_kernel. A workgroup serves 4 q heads of one GQA group and a
+// pair of 32-row q tiles (the heavy tile NQ-1-i, then the light tile i, so every
+// workgroup carries the same number of key tiles) with 5 wavefronts: 4 compute
+// wavefronts, one head each, one per SIMD, and a producer wavefront that only
+// streams 64-position K/V tiles through a ring of 4 LDS stages with gfx950's
+// direct-to-LDS loads (global_load_lds_dwordx4, no register staging), three tiles
+// ahead of their use. Per key tile and head, in two 32-key halves:
+//   S^T[32 keys x 32 q] = onecol . mneg + K . Q^T    v_mfma_f32_32x32x16_f16 (1 + D/16)
+//   O^T[D x 32 q]      += V^T . P^T                  v_mfma_f32_32x32x16_f16 (D/32 per key step)
+//   l^T[32 x 32 q]     += ones . P^T                 v_mfma_f32_32x32x16_f16 (1 per key step)
+// With S transposed a lane holds 16 scores of one query row, so the row max needs one
+// lane swap (v_permlane32_swap), and the P^T operand is the lane's own weights. The
+// first product of the scores adds -m (the row's lazy reference max, an f16 value),
+// so the weights are exp2 of the products' result; the row sums come from the matrix
+// core too. V^T operands come from LDS through the transpose read
+// (ds_read_b64_tr_b16). LDS rows are padded (K: +16 bytes, V: +64 bytes) so both read
+// patterns are bank-conflict free. q (pre-scaled by scale * log2 e) and p are rounded
+// to f16 for the products; the softmax state is f32 in the log2 domain, rescaled only
+// when a row's max grows by more than 2^8. Each compute wavefront issues the next
+// half's score products beside the current half's exponentials and the PV products
+// beside the next half's row max, so its matrix-core and VALU work overlap in one
+// instruction stream. Causal masking runs only on the halves that cross the diagonal,
+// in rounds of their own; the other rounds run a branch-free form.
 //
 // Load balance: q tiles are paired heaviest with lightest (tile NQ-1-i with
 // tile i) so every workgroup carries the same number of key tiles, and the
@@ -39,6 +41,8 @@
 // separate-op path packs an already normalised and rotated q the same way
 // (q_pack_kernel). The attention block's projection GEMM can do the pre-pass
 // in its epilogue instead (k_matmul.hip).
+#include <type_traits>
+
 #include "ds5_common.hpp"
 
 namespace {
@@ -202,12 +206,13 @@ __global__ __launch_bounds__(256) void q_pack_kernel(const float* q, f16* q16, u
 // ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
-constexpr int kHeads = 4;      // q heads per workgroup
-constexpr int kSets = 2;       // wavefront sets (set 0: heavy q tile's first key tiles; set 1: the rest)
-constexpr int kWaves = kHeads * kSets;
-constexpr int kThreads = kWaves * 64;
+constexpr int kHeads = 4;      // q heads per workgroup, one compute wavefront each
+constexpr int kThreads = (kHeads + 1) * 64;  // + the producer wavefront
 constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA N)
 constexpr int kKTile = 64;     // keys per LDS stage
+constexpr int kStages = 4;     // K/V ring: a stage is refilled three rounds ahead of its use
+constexpr int kAhead = kStages - 1;
+constexpr int kOpAhead = 3;    // LDS operand reads in flight ahead of their product
 constexpr float kRescaleLog2 = 8.0f;
 
 struct PrefillParams {
@@ -232,12 +237,11 @@ struct PGeo {
     // read address is then a per-lane base plus an immediate.
     static constexpr int RSK = RB + 16;
     static constexpr int RSV = RB + 64;
-    static constexpr int KSTAGE = kKTile * RSK;    // bytes per K stage
-    static constexpr int VSTAGE = kKTile * RSV;    // bytes per V stage
+    static constexpr int KSTAGE = kKTile * RSK;    // bytes of K per stage
+    static constexpr int VSTAGE = kKTile * RSV;    // bytes of V per stage
+    static constexpr int STAGE = KSTAGE + VSTAGE;
     static constexpr int NBK = KSTAGE / 1024, NBV = VSTAGE / 1024;  // 1 KiB direct-to-LDS loads per stage
     static_assert(KSTAGE % 1024 == 0 && VSTAGE % 1024 == 0, "stages are whole 1 KiB loads");
-    static constexpr int BK = (NBK + kHeads - 1) / kHeads, BV = (NBV + kHeads - 1) / kHeads;  // per wavefront
-    static constexpr int SET_BYTES = 2 * (KSTAGE + VSTAGE);  // double-buffered K and V of one wavefront set
 };
 
 __device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_ptr) {
@@ -261,67 +265,81 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// max / sum of v over lanes l and l ^ 32 (one VALU swap, no LDS round trip)
+// max(a, b, c) as one v_max3_f32. Written as asm so that the chain stays where it
+// is issued (between the products) and takes the raw MFMA results: compiled from
+// fmaxf the chain is either gathered after the last product or, pinned in place,
+// given a canonicalizing v_max per operand. No NaN reaches it. Every caller reads
+// scores whose last product was issued at least two products earlier, past the
+// matrix core's result latency (an asm statement gets no hazard wait states).
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// max of v over lanes l and l ^ 32 (one VALU swap, no LDS round trip)
 __device__ __forceinline__ float max_xor32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Direct-to-LDS loads of the 64 K (or V) rows starting at key0 into one stage
 // with row stride RS. Load b fills stage bytes [1024 b, +1024), lane L the 16
 // bytes at 1024 b + 16 L: row r, chunk slot c of that row, or the row padding
 // (such a lane re-reads the row's first chunk; the padding is never read).
-// Loads b = wave, wave + 4, ... are this wavefront's. DmaPlan keeps the lane's
-// byte offset inside the tile for each of its loads: whole tiles (all 64 rows
-// below kv_end) are fetched with a scalar tile base plus that offset; the last
-// tile clamps rows past kv_end to kv_end - 1 (valid memory, weighted 0).
-template <int D, int RS, int B>
-struct DmaPlan {
-    uint32_t off[B];
-    __device__ __forceinline__ DmaPlan(int wave, int lane) {
+// TilePlan keeps the lane's byte offset inside the tile for every load: a load
+// takes the scalar tile base plus that offset; on the last tile of a q tile,
+// rows past kv_end are clamped to kv_end - 1 (valid memory, weighted 0).
+template <int D, int RS>
+struct TilePlan {
+    static constexpr int NB = kKTile * RS / 1024;
+    uint32_t off[NB];
+    __device__ __forceinline__ explicit TilePlan(int lane) {
 #pragma unroll
-        for (int i = 0; i < B; i++) {
-            const int pos = 1024 * (wave + kHeads * i) + 16 * lane;
+        for (int b = 0; b < NB; b++) {
+            const int pos = 1024 * b + 16 * lane;
             const int r = pos / RS, c = (pos % RS) / 16;
-            off[i] = (uint32_t)(r * 2 * D + (c < D / 8 ? 16 * c : 0));
+            off[b] = (uint32_t)(r * 2 * D + (c < D / 8 ? 16 * c : 0));
         }
     }
 };
 
-template <int D, int RS, int B>
+// A wave-uniform pointer made explicitly scalar (readfirstlane returns int: each
+// half goes through uint32_t so that the low half is zero-extended when the
+// pointer is rebuilt).
+__device__ __forceinline__ uint64_t scalar_ptr(const void* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+
+template <int D, int RS>
 __device__ __forceinline__ void dma_tile(uint32_t stage_lds, const f16* base, uint32_t key0, uint32_t kv_end,
-                                         const DmaPlan<D, RS, B>& dp, int wave, int lane) {
-    constexpr int NB = kKTile * RS / 1024;
-    // wave-uniform operands made explicitly scalar (else the compiler wraps each
-    // asm statement in a loop over the distinct lane values)
-    // (readfirstlane returns int: each half goes through uint32_t so that the low
-    // half is zero-extended, not sign-extended, when the pointer is rebuilt)
-    const uint64_t tb = (uint64_t)(base + (uint64_t)key0 * D);
-    const uint32_t tb_hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(tb >> 32));
-    const uint32_t tb_lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)tb);
-    const uint64_t tile = ((uint64_t)tb_hi << 32) | (uint64_t)tb_lo;
-    const bool whole = key0 + kKTile <= kv_end;  // uniform
+                                         const TilePlan<D, RS>& tp) {
+    constexpr int NB = TilePlan<D, RS>::NB;
+    const uint64_t tile = scalar_ptr(base + (uint64_t)key0 * D);
+    // Issued as inline asm: the compiler would otherwise make every later LDS read
+    // wait for all such loads (it cannot tell the stages apart). Completion is
+    // awaited explicitly (wait_vm) before the barrier that publishes a stage.
+    // (Two asm forms keep the clamp a real branch: whole tiles run no address
+    // arithmetic.)
+    if (key0 + kKTile <= kv_end) {  // uniform
 #pragma unroll
-    for (int i = 0; i < B; i++) {
-        const int b = wave + kHeads * i;
-        if (B * kHeads > NB && b >= NB) break;  // uniform: this wavefront has fewer loads
-        const uint32_t lds = __builtin_amdgcn_readfirstlane(stage_lds + 1024 * b);
-        // Issued as inline asm: the compiler would otherwise make every later
-        // LDS read wait for all such loads (it cannot tell the stages apart).
-        // Completion is awaited explicitly (wait_vm) before the barrier that
-        // publishes a stage.
-        if (whole) {
-            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(dp.off[i]), "s"(tile), "s"(lds)
+        for (int b = 0; b < NB; b++) {
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(stage_lds + 1024 * b);
+            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(tp.off[b]), "s"(tile),
+                         "s"(lds)
                          : "m0");
-        } else {
-            const uint32_t r = dp.off[i] / (2 * D), col = dp.off[i] % (2 * D);
-            const uint32_t key = min(key0 + r, kv_end - 1);
-            const char* src = (const char*)(base + (uint64_t)key * D) + col;
-            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
+        }
+    } else {
+        const uint32_t last_row = kv_end - key0 - 1;  // rows of this tile below kv_end, minus one
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(stage_lds + 1024 * b);
+            const uint32_t off = min(tp.off[b] / (2 * D), last_row) * (2 * D) + tp.off[b] % (2 * D);
+            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(tile), "s"(lds)
+                         : "m0");
         }
     }
 }
@@ -330,16 +348,27 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p;
 }
 
+// Causal flash attention. A workgroup serves 4 q heads of one GQA group and a pair
+// of 32-row q tiles: the heavy tile NQ-1-i, then the light tile i, so every
+// workgroup carries the same number of key tiles and nothing is merged. Four
+// compute wavefronts (one head each, one per SIMD) and one producer wavefront
+// that does nothing but stream key tiles through a ring of four LDS stages with
+// direct-to-LDS loads, three tiles ahead of their use: a direct-to-LDS load holds
+// up the wavefront that issues it until the CU's load path accepts it (~64 bytes
+// per clock per CU), and the producer takes those stalls in place of the compute
+// wavefronts. Round r works on item r (a key tile of the current q tile); within
+// a round each compute wavefront issues the next half tile's S products beside the
+// current half's exponentials and the current PV products beside the next half's
+// row max (see step), so its matrix-core and VALU work overlap in one instruction
+// stream.
 template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
     constexpr int KS = G::KS, DT = G::DT, RSK = G::RSK, RSV = G::RSV;
-    // LDS: per set, K stages 0 and 1 then V stages 0 and 1; reused by the set merge
-    __shared__ __attribute__((aligned(1024))) char s_kv[kSets * G::SET_BYTES];
+    __shared__ __attribute__((aligned(1024))) char s_kv[kStages * G::STAGE];  // stage s: K then V
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int set = wave / kHeads, hw = wave % kHeads;  // key-tile set, head slot
+    const int lane = threadIdx.x & 63;
+    const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head slot (kHeads: the producer)
     const int r32 = lane & 31, h = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
 
     // workgroup -> (kv head, head group, q-tile pair); one kv head per XCD where possible
@@ -348,15 +377,59 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     const uint32_t pair = item % p.n_pairs;
     const uint32_t hg = (item / p.n_pairs) % p.n_hgroups;
     const uint32_t kvh = item / (p.n_pairs * p.n_hgroups);
+
+    // Items: the heavy tile's key tiles 0 .. H-1, then the light tile's 0 .. L-1.
+    const uint32_t heavy = p.n_qtiles - 1 - pair;
+    const bool has_light = pair < heavy;  // the middle tile of an odd count is processed once
+    auto kv_end_of = [&](uint32_t qtile) -> uint32_t {  // keys the q tile needs (exclusive)
+        return p.pos + min(p.n_tokens, qtile * kQRows + kQRows);
+    };
+    const uint32_t H = (kv_end_of(heavy) + kKTile - 1) / kKTile;
+    const uint32_t L = has_light ? (kv_end_of(pair) + kKTile - 1) / kKTile : 0;
+    const uint32_t n_items = H + L;
+    auto item_qt = [&](uint32_t i) -> uint32_t { return i < H ? heavy : pair; };
+    auto item_kt = [&](uint32_t i) -> uint32_t { return i < H ? i : i - H; };
+    auto k_stage = [&](uint32_t i) -> uint32_t { return (i % kStages) * G::STAGE; };
+
+    if (hw == kHeads) {
+        // ---- producer: items 0 .. kAhead - 1 before the first barrier, then item
+        // r + kAhead in round r, into the stage item r - 1 left (every wavefront passed
+        // round r - 1's barrier). At the end of round r every item up to r + kAhead - 1
+        // has landed (items r + 1 and r + 2 are read in round r + 1); only item
+        // r + kAhead's loads stay in flight.
+        const f16* kc = p.k_cache + (uint64_t)kvh * p.max_ctx * D;
+        const f16* vc = p.v_cache + (uint64_t)kvh * p.max_ctx * D;
+        const uint32_t kv_lds = lds_addr(s_kv);
+        const TilePlan<D, RSK> tk(lane);
+        const TilePlan<D, RSV> tv(lane);
+        auto dma_item = [&](uint32_t i) {
+            const uint32_t key0 = item_kt(i) * kKTile, end = kv_end_of(item_qt(i));
+            dma_tile(kv_lds + k_stage(i), kc, key0, end, tk);
+            dma_tile(kv_lds + k_stage(i) + G::KSTAGE, vc, key0, end, tv);
+        };
+#pragma unroll
+        for (int i = 0; i < kAhead; i++)
+            if ((uint32_t)i < n_items) dma_item(i);
+        if (n_items >= kAhead)  // round 0 reads items 0 and 1; item 2 may still be in flight
+            wait_vm<(kAhead - 2) * (G::NBK + G::NBV)>();
+        else
+            wait_vm<0>();
+        lds_sync();
+        for (uint32_t r = 0; r + 1 < n_items; r++) {
+            if (r + kAhead < n_items) {
+                dma_item(r + kAhead);
+                wait_vm<G::NBK + G::NBV>();
+            } else {
+                wait_vm<0>();
+            }
+            lds_sync();
+        }
+        return;
+    }
+
     const uint32_t hin = hg * kHeads + hw;  // head index inside the group
     const bool live = hin < p.group;
     const uint32_t hq = kvh * p.group + (live ? hin : 0);
-    const f16* kc = p.k_cache + (uint64_t)kvh * p.max_ctx * D;
-    const f16* vc = p.v_cache + (uint64_t)kvh * p.max_ctx * D;
-    // this set's stages
-    char* const k_st = s_kv + set * G::SET_BYTES;
-    char* const v_st = k_st + 2 * G::KSTAGE;
-    const uint32_t k_lds = lds_addr(k_st), v_lds = lds_addr(v_st);
 
     // Per-lane LDS byte bases; every read adds an immediate. S operand of
     // (half kh, k-step ks): row 32 kh + r32, bytes 32 ks + 16 h of the row.
@@ -365,35 +438,14 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // group g16 reads row 16 m + 8 hi + 4 hh + i16 / 4, halves dt*32 + 16 (g16 & 1)
     // + 4 (i16 & 3), i.e. bytes 64 dt + 32 (g16 & 1) + 8 (i16 & 3) of the row.
     const int vb = (4 * (g16 >> 1) + (i16 >> 2)) * RSV + 32 * (g16 & 1) + 8 * (i16 & 3);
-    const DmaPlan<D, RSK, G::BK> dk(hw, lane);
-    const DmaPlan<D, RSV, G::BV> dv(hw, lane);
-
-    // Key-tile schedule of the q-tile pair (heavy tile NQ-1-i with H key tiles, light
-    // tile i with L): set 0 takes the heavy tile's key tiles [0, k0), set 1 the light
-    // tile's L key tiles and then the heavy tile's [k0, H), k0 = ceil((H + L) / 2). Both
-    // sets run k0 rounds; the light tile's rows are written by set 1 alone and only the
-    // heavy tile's two partials merge, when set 1 reaches that tile.
-    const uint32_t heavy = p.n_qtiles - 1 - pair;
-    const bool has_light = pair < heavy;  // the middle tile of an odd count is processed once
-    auto kv_end_of = [&](uint32_t qtile) -> uint32_t {  // keys the q tile needs (exclusive)
-        return p.pos + min(p.n_tokens, qtile * kQRows + kQRows);
-    };
-    const uint32_t H = (kv_end_of(heavy) + kKTile - 1) / kKTile;
-    const uint32_t L = has_light ? (kv_end_of(pair) + kKTile - 1) / kKTile : 0;
-    const uint32_t k0 = (H + L + 1) / 2;  // rounds; L <= H, so k0 <= H
-    const uint32_t n_items = set == 0 ? k0 : L + H - k0;
-    const bool merge = H > k0;  // set 1 ends on the heavy tile
-    // item i of this set: its q tile and key tile
-    auto item_qt = [&](uint32_t i) -> uint32_t { return set == 1 && i < L ? pair : heavy; };
-    auto item_kt = [&](uint32_t i) -> uint32_t { return set == 0 ? i : (i < L ? i : k0 + i - L); };
 
     // the wavefront's q tile: lane (r32, h) holds query row t
-    uint32_t qt = item_qt(0);
-    uint32_t t = qt * kQRows + r32;
+    uint32_t t = heavy * kQRows + r32;
     bool keep = live && t < p.n_tokens;
-    uint32_t n_full = (p.pos + qt * kQRows + 1) / kKTile;  // key tiles with no masked key
 
-    // q operand of lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step
+    // q operand of lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step.
+    // Rows past the last token and the heads of an unfilled group read clamped, valid
+    // q rows: their scores stay in their own columns of S and O and are never written.
     f16x8 qop[KS], qnext[KS];
     auto load_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
         const uint32_t tc = min(qtile * kQRows + r32, p.n_tokens - 1);
@@ -401,28 +453,177 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) dst[ks] = *(const f16x8*)(qrow + 16 * ks);
     };
-    // ---- q operand first (vmcnt retires in issue order), then the first tile
-    load_q(qop, qt);
-    if (n_items > 0) {
-        dma_tile(k_lds, kc, item_kt(0) * kKTile, kv_end_of(qt), dk, hw, lane);
-        dma_tile(v_lds, vc, item_kt(0) * kKTile, kv_end_of(qt), dv, hw, lane);
-    }
-    if (!keep) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qop[ks] = f16x8{};
-    }
 
     f32x16 O[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
-    float m_ref = -INFINITY, l_sum = 0.0f;
+    // The scores are kept relative to the row's reference m (the lazy running max,
+    // an f16 value): every score product starts with a 16-deep product whose only
+    // nonzero term is 1 x (-m) (onecol . mneg), so the products leave s - m and the
+    // weights are exp2(s - m) with no subtraction. thr: the rescale threshold on the
+    // relative max (-inf until a q tile has its first reference).
+    float m_sh = 0.0f, thr = -INFINITY;
+    f16x8 onecol, mneg;
+#pragma unroll
+    for (int i = 0; i < 8; i++) onecol[i] = mneg[i] = (f16)0.0f;
+    onecol[0] = h == 0 ? (f16)1.0f : (f16)0.0f;
+    // Row sums of the weights on the matrix core: Lsum^T += ones . P^T after each key
+    // step's PV products (every row of Lsum^T is the row-sum vector; element 0 is read).
+    // The sum is of the same f16 weights the products take.
+    f32x16 Lsum;
+#pragma unroll
+    for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
+    f16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = (f16)1.0f;
+    float mx = -INFINITY;  // row max of the scores computed one step ahead
+
+    // Causal mask of half kh of item i's scores, in place: lane (r32, h), score r of
+    // the half is key key0 + 32 kh + 8 (r / 4) + 4 h + r % 4; keys past the row's
+    // position are -inf. Needed when the half's last key lies past the q tile's first
+    // row.
+    auto masked_half = [&](uint32_t i, int kh) -> bool {
+        return item_kt(i) * kKTile + 32 * kh + 31 > p.pos + item_qt(i) * kQRows;
+    };
+    auto mask_half = [&](f32x16& s, uint32_t i, int kh) {
+        const int lim = (int)(p.pos + item_qt(i) * kQRows + r32) - (int)(item_kt(i) * kKTile + 32 * kh) - 4 * h;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            if (8 * (r / 4) + (r % 4) > lim) s[r] = -INFINITY;
+    };
+    // Row max of a half (lanes l and l ^ 32 hold the two key subsets of a row); a
+    // linear chain, which the backend turns into v_max3 on the raw MFMA results.
+    auto half_max = [&](const f32x16& s) -> float {
+        float a = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; r++) a = fmaxf(a, s[r]);
+        return max_xor32(a);
+    };
+    // V operand of key step m, dim block dt, from the stage at byte offset `st`. The
+    // k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4. Transpose read: lane
+    // i of a 16-lane group addresses row base + i/4, columns c0 + 4(i%4); lane j
+    // receives column c0 + j of the 4 rows.
+    auto vread = [&](uint32_t st, int m, int dt) -> f16x8 {
+        const char* sv = s_kv + st + G::KSTAGE + vb;
+        const f16x4 lo = lds_read_tr16(sv + 16 * m * RSV + 64 * dt);
+        const f16x4 hi = lds_read_tr16(sv + (16 * m + 8) * RSV + 64 * dt);
+        return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    // K operands of the scores in flight; the first AHEAD are read one step early.
+    constexpr int AHEAD = kOpAhead < KS ? kOpAhead : KS;
+    static_assert(8 % KS == 0 && 8 % DT == 0 && KS >= AHEAD && 2 * DT >= AHEAD, "schedule shape");
+    f16x8 kop[KS];
+    auto kptr = [&](uint32_t kst, int hn) -> const char* { return s_kv + kst + kb + 32 * hn * RSK; };
+
+    // One step = one 32-key half hc of the current item (scores Sc relative to the
+    // reference, their row max mx), in issue order:
+    //   - the 1 + KS products of the next half's scores Sn = -m + K . Q^T (K at sk)
+    //     when NEXT, beside the weights exp2(Sc) of the half's first 8 scores (the P^T
+    //     operand of key step 2 hc, rounded to f16);
+    //   - the lazy rescale check against mx: it is evaluated here, after those
+    //     weights, rather than before them, so the branch never waits for mx. The
+    //     weights were computed against the old reference; when the reference moves
+    //     (the half's max exceeds it by more than 2^kRescaleLog2, and at the start of
+    //     every q tile) O and the row sum are rescaled, Sc and Sn move to the new
+    //     reference and those 8 weights are computed again;
+    //   - the 2 DT products O^T += V^T . P^T (V tile in stage vst) and a row-sum
+    //     product per key step: the first DT (key step 2 hc) beside the weights of the
+    //     other 8 scores (key step 2 hc + 1, used by the last DT), the last DT beside
+    //     the row max of Sn.
+    // LDS operand reads run AHEAD products ahead of their use, across the steps too
+    // (the last products of a step read the first K operands of the next step's
+    // scores, at sk_after, when PRE), and scheduling fences keep this order, so the
+    // matrix cores and the VALU work at once and no product waits for its operand
+    // read.
+    auto step = [&](f32x16& Sc, f32x16& Sn, int hc, uint32_t vst, const char* sk, const char* sk_after,
+                    auto next, auto pre) {
+        constexpr bool NEXT = decltype(next)::value, PRE = decltype(pre)::value;
+        constexpr int NK = KS, NV = 2 * DT, E0 = 8 / NK, E1 = 8 / DT;
+        f16x8 vop[NV], pop[2];
+        float e[16];
+        auto vr = [&](int n) -> f16x8 { return vread(vst, 2 * hc + n / DT, n % DT); };
+        // (The empty asm statements pin each result where it is computed: without them
+        // the compiler sinks the weights below the rescale branch, or gathers the max
+        // chain after the last product, and nothing overlaps the matrix cores.)
+        auto weight = [&](int f) {  // score f of the half
+            e[f] = fast_exp2(Sc[f]);
+            if (f % 2 == 1) {
+                pop[f / 8][f % 8 - 1] = (f16)e[f - 1];
+                pop[f / 8][f % 8] = (f16)e[f];
+                if (f % 8 == 7) asm volatile("" : "+v"(pop[f / 8]));
+            }
+        };
+        if constexpr (!NEXT) {  // (a step with NEXT finds kop[0, AHEAD) read)
+#pragma unroll
+            for (int n = 0; n < AHEAD; n++) vop[n] = vr(n);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int n = 0; n < NK; n++) {
+            if constexpr (NEXT) {
+                if (n + AHEAD < NK)
+                    kop[n + AHEAD] = *(const f16x8*)(sk + 32 * (n + AHEAD));
+                else
+                    vop[n + AHEAD - NK] = vr(n + AHEAD - NK);
+                if (n == 0) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) Sn[r] = 0.0f;
+                    Sn = mfma_32x32x16(onecol, mneg, Sn);
+                }
+                Sn = mfma_32x32x16(kop[n], qop[n], Sn);
+            }
+#pragma unroll
+            for (int j = 0; j < E0; j++) weight(E0 * n + j);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (__builtin_expect(__ballot(mx > thr) != 0, 0)) {  // rare: the reference moves
+            // New reference: the row's max rounded to f16 (the shift operand is f16; the
+            // difference of two f16 values is exact in f32). The scores in flight (Sc,
+            // and Sn, whose products started from the old reference) move with it.
+            const float m_new = mx > thr ? (float)(f16)fminf(fmaxf(mx + m_sh, -65504.0f), 65504.0f) : m_sh;
+            const float delta = m_new - m_sh;
+            const float alpha = thr == -INFINITY ? 0.0f : fast_exp2(-delta);  // O and l are 0 at a q tile's start
+            Lsum[0] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
+            m_sh = m_new;
+            thr = kRescaleLog2;
+            mneg[0] = h == 0 ? (f16)(-m_sh) : (f16)0.0f;
+            Sc -= delta;
+            if constexpr (NEXT) Sn -= delta;
+#pragma unroll
+            for (int f = 0; f < 8; f++) weight(f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float a = NEXT ? Sn[0] : 0.0f;
+#pragma unroll
+        for (int n = 0; n < NV; n++) {
+            if (n + AHEAD < NV)
+                vop[n + AHEAD] = vr(n + AHEAD);
+            else if constexpr (PRE)
+                kop[n + AHEAD - NV] = *(const f16x8*)(sk_after + 32 * (n + AHEAD - NV));
+            O[n % DT] = mfma_32x32x16(vop[n], pop[n / DT], O[n % DT]);
+            if (n % DT == DT - 1) Lsum = mfma_32x32x16(ones, pop[n / DT], Lsum);
+            if (n < DT) {
+#pragma unroll
+                for (int j = 0; j < E1; j++) weight(8 + E1 * n + j);
+            } else if constexpr (NEXT) {
+#pragma unroll
+                for (int j = 1; j < 16; j += 2)  // Sn's max over the last DT products
+                    if ((j - 1) / 2 * DT / 8 == n - DT) a = vmax3(a, Sn[j], j + 1 < 16 ? Sn[j + 1] : Sn[j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (NEXT) mx = max_xor32(a);
+    };
 
     // The wavefront's rows of its q tile when every key of the tile went through it:
-    // O over its own row sum. Wave-uniform call (the row sum crosses lanes).
+    // O over its row sum.
     auto write_rows = [&]() {
-        const float l = sum_xor32(l_sum);
+        const float l = Lsum[0];
         if (keep) {
             const float inv_l = 1.0f / l;
             float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
@@ -436,157 +637,104 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         }
     };
 
+    // Half kh of item i on a tile that crosses the diagonal: its causal mask, in place,
+    // then its max again.
+    auto mask_if_needed = [&](f32x16& s, uint32_t i, int kh) {
+        if (__builtin_expect(masked_half(i, kh), 0)) {
+            mask_half(s, i, kh);
+            mx = half_max(s);
+        }
+    };
+
+    // ---- prologue: both q tiles' operands (the producer streams items 0 .. kAhead - 1
+    // meanwhile); the scores of item 0's first half and their row max before round 0.
+    load_q(qop, heavy);
+    f32x16 Sa, Sb;  // scores of the current item's first and second half
     wait_vm<0>();
     lds_sync();
-    // Round r: item r of each set sits in stage r % 2; item r + 1 streams into the other
-    // stage meanwhile (that stage was last read in round r - 1, before the previous barrier).
-    for (uint32_t r = 0; r < k0; r++) {
-        const uint32_t kcur = (r & 1) * G::KSTAGE, knxt = G::KSTAGE - kcur;
-        const uint32_t vcur = (r & 1) * G::VSTAGE, vnxt = G::VSTAGE - vcur;
-        if (set == 1 && L > 0 && L < n_items) {
-            // set 1 moves from the light tile to the heavy one: the heavy q operand loads
-            // one round ahead (drained by that round's barrier wait); at round L the light
-            // rows are written and the softmax state restarts
-            if (r + 1 == L) load_q(qnext, heavy);
-            if (r == L) {
-                write_rows();
-                qt = heavy;
-                t = qt * kQRows + r32;
-                keep = live && t < p.n_tokens;
-                n_full = (p.pos + qt * kQRows + 1) / kKTile;
+    {
+        const char* sk = s_kv + k_stage(0) + kb;
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) qop[ks] = keep ? qnext[ks] : f16x8{};
+        for (int r = 0; r < 16; r++) Sa[r] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) Sa = mfma_32x32x16(*(const f16x8*)(sk + 32 * ks), qop[ks], Sa);
+#pragma unroll
+        for (int n = 0; n < AHEAD; n++) kop[n] = *(const f16x8*)(kptr(k_stage(0), 1) + 32 * n);
+        mx = half_max(Sa);  // (a masked half's max is taken again after its mask)
+    }
+
+    // Round r (item r): step 0 (weights and PV of its first half; scores of its second
+    // half), then step 1 (weights and PV of its second half; scores of item r + 1's
+    // first half, from stage (r + 1) % kStages), then the round's barrier. A special
+    // round also masks the halves that cross the diagonal, loads the light tile's q
+    // operand or switches to the light tile; the others run the plain form, so the
+    // loop over a run of plain rounds has no branch but the rare rescale.
+    auto round = [&](uint32_t r, auto special) {
+        constexpr bool SPECIAL = decltype(special)::value;
+        const uint32_t st = k_stage(r), st1 = k_stage(r + 1);
+        if constexpr (SPECIAL) {
+            // The light tile's q operand loads one round in (not with the heavy tile's:
+            // at the start every workgroup loads its q at once, and that burst is time
+            // no product overlaps), or in round 0 when item 1 already starts the light
+            // tile.
+            if (has_light && r == min(1u, H - 1)) load_q(qnext, pair);
+            mask_if_needed(Sa, r, 0);
+        }
+        step(Sa, Sb, 0, st, kptr(st, 1), kptr(st1, 0), std::true_type{}, std::true_type{});
+        if constexpr (SPECIAL) {
+            if (r + 1 == H) {  // item H's scores (the next step) start the light tile
+                wait_vm<0>();
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) qop[ks] = qnext[ks];
+            }
+            mask_if_needed(Sb, r, 1);
+        }
+        step(Sb, Sa, 1, st, kptr(st1, 0), kptr(st1, 1), std::true_type{}, std::true_type{});
+        if constexpr (SPECIAL) {
+            if (r + 1 == H) {  // the heavy tile is done: its rows, then the light tile's state
+                write_rows();
+                t = pair * kQRows + r32;
+                keep = live && t < p.n_tokens;
 #pragma unroll
                 for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                     for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
-                m_ref = -INFINITY;
-                l_sum = 0.0f;
+                thr = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
             }
         }
-        const bool load_next = r + 1 < n_items;
-        const uint32_t nkey0 = item_kt(r + 1) * kKTile, nend = kv_end_of(item_qt(r + 1));
-        // The next tile's loads are issued in two halves inside the round (a burst from
-        // all eight wavefronts right after the barrier would stall their issue).
-        if (r < n_items) {
-            const uint32_t j = item_kt(r);
-            const uint32_t key0 = j * kKTile;
-            const uint64_t t_abs = (uint64_t)p.pos + t;
-            const char* sk = k_st + kcur + kb;
-            f32x16 S[2];  // S^T of the tile's two 32-key halves
-#pragma unroll
-            for (int kh = 0; kh < 2; kh++) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) S[kh][i] = 0.0f;
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    const f16x8 a = *(const f16x8*)(sk + 32 * kh * RSK + 32 * ks);
-                    S[kh] = mfma_32x32x16(a, qop[ks], S[kh]);
-                }
-            }
-            if (load_next) dma_tile(k_lds + knxt, kc, nkey0, nend, dk, hw, lane);
-            // lane: query row t; score r of half kh is key key0 + 32kh + 8(r/4) + 4h + r%4.
-            if (j >= n_full) {  // causal mask on tiles that reach past the first row
-#pragma unroll
-                for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        const uint64_t key = key0 + 32 * kh + 8 * (i / 4) + 4 * h + (i % 4);
-                        if (key > t_abs) S[kh][i] = -INFINITY;
-                    }
-            }
-            float mx = S[0][0];
-#pragma unroll
-            for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) mx = fmaxf(mx, S[kh][i]);
-            mx = max_xor32(mx);
-            if (__ballot(mx > m_ref + kRescaleLog2) != 0) {  // lazy rescale (also the first tile)
-                const float m_new = mx > m_ref + kRescaleLog2 ? mx : m_ref;
-                const float alpha = m_new == m_ref ? 1.0f : fast_exp2(m_ref - m_new);  // -inf - -inf would be NaN
-                l_sum *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) O[dt] *= alpha;
-                m_ref = m_new;
-            }
-            // A row with every key so far masked (possible in set 1, whose part of the
-            // heavy tile starts at key tile k0) keeps m_ref = -inf; its weights are 0.
-            const float m_exp = m_ref == -INFINITY ? 0.0f : m_ref;
-            f16x8 pop[4];  // P^T operand of key step m: scores i = 8 (m % 2) + jj of half m / 2
-            // Row sum in f32 adds of the f32 weights: v_dot2 of the f16 weights would
-            // share the matrix core with the other wavefront's products on this SIMD.
-            float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const float e = fast_exp2(S[m / 2][8 * (m % 2) + jj] - m_exp);
-                    pop[m][jj] = (f16)e;
-                    ps[m] += e;
-                }
-            l_sum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-            if (load_next) dma_tile(v_lds + vnxt, vc, nkey0, nend, dv, hw, lane);
-            // O^T += V^T . P^T; k-slot (h, jj) of step m is key 16m + 8(jj/4) + 4h + jj%4.
-            // Transpose read: lane i of a 16-lane group addresses row base + i/4, columns
-            // c0 + 4(i%4); lane j receives column c0 + j of the 4 rows.
-            const char* sv = v_st + vcur + vb;
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    const f16x4 lo = lds_read_tr16(sv + 16 * m * RSV + 64 * dt);
-                    const f16x4 hi = lds_read_tr16(sv + (16 * m + 8) * RSV + 64 * dt);
-                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    O[dt] = mfma_32x32x16(a, pop[m], O[dt]);
-                }
-        }
-        wait_vm<0>();
         lds_sync();
-    }
-
-    if (!merge) {
-        if (set == 0 || L > 0) write_rows();  // set 0: the heavy tile; set 1: the light tile
-        return;
-    }
-    // ---- merge set 1 (the heavy tile's keys [k0, H)) into set 0 through LDS; every stage
-    // is free after the last round. Head slot hw: [float4 index][lane].
-    constexpr int NV4 = DT * 4 + 1;  // O as float4s, then (m, l, -, -)
-    static_assert(NV4 * 64 * 16 <= G::KSTAGE && G::KSTAGE <= G::VSTAGE, "a merge slot fits a stage");
-    char* const slot = s_kv + (hw >> 1) * G::SET_BYTES + ((hw & 1) == 0 ? 0 : 2 * G::KSTAGE);
-    float4* mrg = (float4*)slot + lane;
-    if (set == 1) {
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int i4 = 0; i4 < 4; i4++)
-                mrg[(dt * 4 + i4) * 64] = float4{O[dt][4 * i4], O[dt][4 * i4 + 1], O[dt][4 * i4 + 2], O[dt][4 * i4 + 3]};
-        mrg[DT * 4 * 64] = float4{m_ref, l_sum, 0.0f, 0.0f};
-    }
-    lds_sync();
-    if (set == 0) {
-        const float4 ml = mrg[DT * 4 * 64];
-        const float m = fmaxf(m_ref, ml.x);  // m_ref is finite (key 0 is visible to set 0)
-        // a row whose keys in set 1's range were all masked has ml.x = -inf: a1 = 0
-        const float a0 = fast_exp2(m_ref - m), a1 = fast_exp2(ml.x - m);
-        const float l = sum_xor32(l_sum * a0 + ml.y * a1);
-        if (keep) {
-            const float inv_l = 1.0f / l;
-            float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-                for (int i4 = 0; i4 < 4; i4++) {
-                    const float4 o1 = mrg[(dt * 4 + i4) * 64];
-                    const int d = dt * 32 + 8 * i4 + 4 * h;
-                    *(float4*)(out + d) = float4{(O[dt][4 * i4] * a0 + o1.x * a1) * inv_l,
-                                                 (O[dt][4 * i4 + 1] * a0 + o1.y * a1) * inv_l,
-                                                 (O[dt][4 * i4 + 2] * a0 + o1.z * a1) * inv_l,
-                                                 (O[dt][4 * i4 + 3] * a0 + o1.w * a1) * inv_l};
-                }
+    };
+    // The special rounds: the light tile's q load (round min(1, H - 1)) and switch
+    // (round H - 1), and the items whose second half crosses a q tile's first row
+    // (key tile kt of q tile qt with 64 kt + 63 > pos + 32 qt, i.e. kt >= first_masked).
+    auto first_masked = [&](uint32_t qtile) -> uint32_t { return (p.pos + qtile * kQRows + 1) / kKTile; };
+    const uint32_t mh = min(first_masked(heavy), H), ml = H + first_masked(pair);
+    auto next_special = [&](uint32_t r) -> uint32_t {  // the first special round >= r
+        uint32_t ns = n_items;
+        if (has_light) {
+            ns = r <= min(1u, H - 1) ? min(1u, H - 1) : r <= H - 1 ? H - 1 : n_items;
+            ns = min(ns, max(r, ml));
         }
+        if (r < H && mh < H) ns = min(ns, max(r, mh));
+        return ns;
+    };
+    for (uint32_t r = 0; r + 1 < n_items;) {
+        const uint32_t stop = min(next_special(r), n_items - 1);
+        for (; r < stop; r++) round(r, std::false_type{});
+        if (r + 1 < n_items) round(r++, std::true_type{});
     }
+    // the last item: its second half's scores, then nothing ahead
+    {
+        const uint32_t r = n_items - 1, st = k_stage(r);
+        mask_if_needed(Sa, r, 0);
+        step(Sa, Sb, 0, st, kptr(st, 1), nullptr, std::true_type{}, std::false_type{});
+        mask_if_needed(Sb, r, 1);
+        step(Sb, Sa, 1, st, nullptr, nullptr, std::false_type{}, std::false_type{});
+    }
+    write_rows();
 }
-
 }  // namespace
 
 bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim) {

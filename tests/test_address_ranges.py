@@ -14,8 +14,8 @@ Replicated:
                              decode_split_kernel (contiguous and paged caches)
   qw3_amd/csrc/k_matmul.hip  the direct-to-LDS loads of matmul_q8_mfma_kernel (x
                              planes, raw Q8_0 rows) and matmul_path's slack rule
-  qw3_amd/csrc/k_prefill.hip DmaPlan / dma_tile of prefill_attention_kernel (every
-                             direct-to-LDS load of every round) and its q-operand
+  qw3_amd/csrc/k_prefill.hip TilePlan / dma_tile of prefill_attention_kernel (every
+                             direct-to-LDS load of every item) and its q-operand
                              loads
 """
 import numpy as np
@@ -354,36 +354,29 @@ def test_gemm_slack_rule_is_needed():
 # prefill_attention_kernel DMA (k_prefill.hip)
 # ---------------------------------------------------------------------------
 
-P_HEADS, P_SETS, P_QROWS, P_KTILE = 4, 2, 32, 64
+P_HEADS, P_QROWS, P_KTILE = 4, 32, 64
 
 
-def dma_plan(D, RS, B):
-    """DmaPlan: per head slot hw and load i, each lane's byte offset inside a 64-row
-    tile (or None past the stage's loads)."""
+def tile_plan(D, RS):
+    """TilePlan: each lane's byte offset inside a 64-row tile, for every 1 KiB load of
+    the stage (load b fills stage bytes [1024 b, +1024); a padding lane re-reads its
+    row's first chunk)."""
     NB = P_KTILE * RS // 1024
-    plans = {}
-    for hw in range(P_HEADS):
-        offs = []
-        for i in range(B):
-            b = hw + P_HEADS * i
-            if b >= NB:
-                break
-            pos = 1024 * b + 16 * np.arange(64)
-            r, c = pos // RS, (pos % RS) // 16
-            offs.append(r * 2 * D + np.where(c < D // 8, 16 * c, 0))
-        plans[hw] = np.concatenate(offs) if offs else np.zeros(0, np.int64)
-    return plans
+    offs = []
+    for b in range(NB):
+        pos = 1024 * b + 16 * np.arange(64)
+        r, c = pos // RS, (pos % RS) // 16
+        offs.append(r * 2 * D + np.where(c < D // 8, 16 * c, 0))
+    return np.concatenate(offs)
 
 
-def dma_extent(D, plan, key0, kv_end):
+def dma_extent(D, offs, key0, kv_end):
     """dma_tile: byte range [lo, hi) read from the kv head's rows for one call."""
-    offs = np.concatenate(list(plan.values()))
     if key0 + P_KTILE <= kv_end:  # whole tile: scalar tile base + offset
         a = key0 * 2 * D + offs
     else:
-        r, col = offs // (2 * D), offs % (2 * D)
-        key = np.minimum(key0 + r, kv_end - 1)
-        a = key * 2 * D + col
+        last_row = kv_end - key0 - 1
+        a = key0 * 2 * D + np.minimum(offs // (2 * D), last_row) * (2 * D) + offs % (2 * D)
     return int(a.min()), int(a.max()) + 16
 
 
@@ -391,9 +384,7 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
     """Every direct-to-LDS load and q-operand load of one prefill launch."""
     RB = 2 * D
     RSK, RSV = RB + 16, RB + 64
-    BK = (P_KTILE * RSK // 1024 + P_HEADS - 1) // P_HEADS
-    BV = (P_KTILE * RSV // 1024 + P_HEADS - 1) // P_HEADS
-    pk, pv = dma_plan(D, RSK, BK), dma_plan(D, RSV, BV)
+    pk, pv = tile_plan(D, RSK), tile_plan(D, RSV)
     group = hq // hkv
     n_qtiles = (T + P_QROWS - 1) // P_QROWS
     n_pairs = (n_qtiles + 1) // 2
@@ -406,16 +397,9 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
         has_light = pair < heavy
         H = (kv_end_of(heavy) + P_KTILE - 1) // P_KTILE
         L = (kv_end_of(pair) + P_KTILE - 1) // P_KTILE if has_light else 0
-        k0 = (H + L + 1) // 2
-        # schedule: set 0 takes heavy key tiles [0, k0), set 1 light [0, L) then heavy [k0, H)
-        items = {0: [(heavy, j) for j in range(k0)],
-                 1: [(pair, j) for j in range(L)] + [(heavy, j) for j in range(k0, H)]}
-        assert len(items[1]) <= k0 and k0 <= H
-        done = items[0] + items[1]
-        want = [(heavy, j) for j in range(H)] + [(pair, j) for j in range(L)]
-        assert sorted(done) == sorted(want) and len(set(done)) == len(done)  # every key tile once
-        for st in range(P_SETS):
-            for qt, j in items[st]:
+        # items: the heavy tile's key tiles 0 .. H - 1, then the light tile's 0 .. L - 1
+        for qt, n in ((heavy, H), (pair, L)):
+            for j in range(n):
                 calls.add((j * P_KTILE, kv_end_of(qt)))
         for sel in range(2):
             if sel == 1 and not has_light:
