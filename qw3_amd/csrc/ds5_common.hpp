@@ -231,27 +231,25 @@ struct KvAppendLaunch {
 int launch_kv_append(ds5_hip_ctx* ctx, const KvAppendLaunch& a);
 
 // Prefill pre-pass of the fused step: per token, the norm + rope + f16 append
-// of every kv head's k row, f16 append of v, and the attention kernel's q
-// operand: q RMSNorm + rope, times q_scale, f16 into q16 [n_tokens, n_q_heads, head_dim].
+// of every kv head's k row, f16 append of v, and the rope cos/sin of the token
+// into cs [n_tokens, head_dim] (cos of pairs 0 .. head_dim/2 - 1, then sin),
+// which the attention kernel rotates q with.
 constexpr float kLog2e = 1.4426950408889634f;  // softmax runs in the log2 domain
 
 struct KvPrepLaunch {
     const float* k;
     const float* v;
     const float* k_norm;
-    const float* q;
-    const float* q_norm;
     const int32_t* positions;
     f16* k_cache;
     f16* v_cache;
-    uint32_t pos, n_tokens, n_q_heads, n_kv_heads, head_dim, max_ctx;
-    float eps, freq_scale, q_scale;
+    float* cs;
+    uint32_t pos, n_tokens, n_kv_heads, head_dim, max_ctx;
+    float eps, freq_scale;
     const RopeTable* table;
 };
 bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim);
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, f16* q16);
-// Separate-op prefill: q16 = f16(q * q_scale) for n values (n % 8 == 0).
-int launch_q_pack(ds5_hip_ctx* ctx, const float* q, f16* q16, uint64_t n, float q_scale);
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a);
 
 // Generic causal GQA attention (any head_dim <= 512, f32 or f16 cache).
 struct GenericAttnLaunch {
@@ -300,8 +298,16 @@ size_t decode_workspace_bytes(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t 
                               uint32_t head_dim, uint32_t max_len);
 
 // Causal flash-attention prefill on f16 MFMA (head_dim 128 or 64).
+// The q operand is one of: q16 (a ready f16 operand, already scaled by softmax
+// scale * log2(e)); q with cs (the raw f32 projection: RMSNorm with q_norm and
+// eps, rotation with the pre-pass's cos/sin table, times q_scale); q alone (f32,
+// already normalised and rotated: times q_scale).
 struct PrefillLaunch {
-    const f16* q16;          // [n_tokens, n_q_heads, head_dim], already scaled by softmax scale * log2(e)
+    const f16* q16;          // [n_tokens, n_q_heads, head_dim] or null
+    const float* q;          // [n_tokens, n_q_heads, head_dim] f32 (q16 null)
+    const float* q_norm;     // [head_dim] (with cs)
+    const float* cs;         // [n_tokens, head_dim] or null
+    float eps, q_scale;      // q_scale = softmax scale * log2(e) (f32 q)
     const f16* k_cache;
     const f16* v_cache;
     float* out;

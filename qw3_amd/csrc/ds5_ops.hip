@@ -7,7 +7,7 @@
 //   rope          kernels_a.zig:97-130  -> rope_kernel
 //   kvAppend      kernels_a.zig:169-217 -> kv_append_kernel
 //   gqaAttention  kernels_b.zig:29-133  -> decode_split_kernel (+ merge),
-//                                          q_pack_kernel + prefill_attention_kernel,
+//                                          prefill_attention_kernel (f32 q),
 //                                          or the generic kernel
 #include <math.h>
 
@@ -528,13 +528,10 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
             l.scale = a->scale;
             return launch_decode(ctx, l);
         }
-        // f16 q operand (scaled by scale * log2 e) in the workspace
-        const uint64_t nq = (uint64_t)a->n_tokens * a->n_q_heads * a->head_dim;
-        void* ws = nullptr;
-        if (int rc = ds5_workspace(ctx, nq * sizeof(uint16_t), &ws)) return rc;
-        if (int rc = launch_q_pack(ctx, (const float*)ds5_ptr(a->q), (f16*)ws, nq, a->scale * kLog2e)) return rc;
+        // the kernel scales q (already normalised and rotated) into its f16 operand
         PrefillLaunch l{};
-        l.q16 = (const f16*)ws;
+        l.q = (const float*)ds5_ptr(a->q);
+        l.q_scale = a->scale * kLog2e;
         l.k_cache = (const f16*)ds5_ptr(a->k_cache);
         l.v_cache = (const f16*)ds5_ptr(a->v_cache);
         l.out = (float*)ds5_ptr(a->out);
@@ -550,6 +547,15 @@ int ds5_hip_gqa_attention(ds5_hip_ctx* ctx, const ds5_attn_args* a) {
                         a->kv_dtype, a->pos, a->n_tokens, a->n_q_heads, a->n_kv_heads, a->head_dim, a->max_ctx,
                         a->scale};
     return launch_generic_attention(ctx, g);
+}
+
+// Workspace of the fused prefill step: the pre-pass's rope cos/sin table [T, head_dim] f32.
+static size_t prefill_step_workspace_bytes(uint64_t T, uint64_t head_dim) { return (size_t)(T * head_dim * sizeof(float)); }
+// A multi-token step on the MFMA shapes runs fused (pre-pass + attention kernel) when
+// the pre-pass takes the kv width and q_norm is 16-byte aligned (the attention
+// kernel reads it in float4s); otherwise it runs the separate ops.
+static bool prefill_step_fused(const ds5_attention_step_args* a) {
+    return prefill_prep_supported(a->n_kv_heads, a->head_dim) && aligned16(a->q_norm);
 }
 
 // The attention step's preconditions: rmsNorm(q), rmsNorm(k), rope(q), rope(k),
@@ -610,32 +616,34 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* a) {
             l.table = table;
             return launch_decode(ctx, l);
         }
-        if (prefill_prep_supported(a->n_kv_heads, a->head_dim)) {
-            // the pre-pass's f16 q operand [n_tokens, n_q_heads, head_dim] in the workspace
+        if (prefill_step_fused(a)) {
+            // the pre-pass's rope cos/sin table [n_tokens, head_dim] in the workspace;
+            // the attention kernel normalises, rotates and scales q itself
             void* ws = nullptr;
-            if (int rc = ds5_workspace(ctx, (size_t)T * hq * hd * sizeof(uint16_t), &ws)) return rc;
+            if (int rc = ds5_workspace(ctx, prefill_step_workspace_bytes(T, hd), &ws)) return rc;
             KvPrepLaunch kp{};
             kp.k = (const float*)ds5_ptr(a->k);
             kp.v = (const float*)ds5_ptr(a->v);
             kp.k_norm = (const float*)ds5_ptr(a->k_norm);
-            kp.q = (const float*)ds5_ptr(a->q);
-            kp.q_norm = (const float*)ds5_ptr(a->q_norm);
             kp.positions = (const int32_t*)ds5_ptr(a->positions);
             kp.k_cache = (f16*)ds5_ptr(a->k_cache);
             kp.v_cache = (f16*)ds5_ptr(a->v_cache);
+            kp.cs = (float*)ws;
             kp.pos = a->pos;
             kp.n_tokens = a->n_tokens;
-            kp.n_q_heads = a->n_q_heads;
             kp.n_kv_heads = a->n_kv_heads;
             kp.head_dim = a->head_dim;
             kp.max_ctx = a->max_ctx;
             kp.eps = a->eps;
             kp.freq_scale = a->freq_scale;
-            kp.q_scale = a->scale * kLog2e;
             kp.table = table;
-            if (int rc = launch_kv_prep(ctx, kp, (f16*)ws)) return rc;
+            if (int rc = launch_kv_prep(ctx, kp)) return rc;
             PrefillLaunch l{};
-            l.q16 = (const f16*)ws;
+            l.q = (const float*)ds5_ptr(a->q);
+            l.q_norm = (const float*)ds5_ptr(a->q_norm);
+            l.cs = kp.cs;
+            l.eps = a->eps;
+            l.q_scale = a->scale * kLog2e;
             l.k_cache = (const f16*)ds5_ptr(a->k_cache);
             l.v_cache = (const f16*)ds5_ptr(a->v_cache);
             l.out = (float*)ds5_ptr(a->out);
@@ -694,7 +702,8 @@ int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* a)
     // calls would take: the GEMM for every weight, the fused MFMA prefill step).
     bool fused = a->w_dtype == DS5_DTYPE_Q8_0 && hd == 128 && s.n_tokens >= 2 &&
                  mfma_shape(s.kv_dtype, hd, {s.q, s.k, s.v, s.k_cache, s.v_cache, s.out}) &&
-                 prefill_prep_supported(s.n_kv_heads, hd) && aligned16(a->x);
+                 prefill_prep_supported(s.n_kv_heads, hd) && aligned16(a->x) && aligned16(s.q_norm) &&
+                 aligned16(s.k_norm);
     for (uint32_t e = 0; fused && e < 3; e++) {
         const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(g.w[e]), true,
                              (float*)ds5_ptr(g.out[e]), g.m, g.n[e], g.k};
@@ -754,12 +763,11 @@ static size_t step_workspace_bytes(const ds5_hip_ctx* ctx, const ds5_attention_s
     const uint64_t T = a->n_tokens, hq = a->n_q_heads, hkv = a->n_kv_heads, hd = a->head_dim;
     if (T == 0 || hkv == 0 || hd == 0) return 0;
     const bool fused = mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k, a->v, a->k_cache, a->v_cache, a->out});
-    if (fused && (T == 1 || prefill_prep_supported(a->n_kv_heads, a->head_dim)))
+    if (fused && (T == 1 || prefill_step_fused(a)))
         return T == 1 ? decode_workspace_bytes(ctx, 1, a->n_q_heads, a->n_kv_heads, a->head_dim, a->pos + 1)
-                      : (size_t)(T * hq * hd * sizeof(uint16_t));
+                      : prefill_step_workspace_bytes(T, hd);
     if (mfma_shape(a->kv_dtype, a->head_dim, {a->q, a->k_cache, a->v_cache, a->out}))
-        return T == 1 ? decode_workspace_bytes(ctx, 1, a->n_q_heads, a->n_kv_heads, a->head_dim, a->pos + 1)
-                      : (size_t)(T * hq * hd * sizeof(uint16_t));
+        return T == 1 ? decode_workspace_bytes(ctx, 1, a->n_q_heads, a->n_kv_heads, a->head_dim, a->pos + 1) : 0;
     return 0;
 }
 

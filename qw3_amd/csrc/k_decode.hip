@@ -980,6 +980,14 @@ static DecodeGeometry decode_geometry_of(const ds5_hip_ctx* ctx, uint32_t n_seqs
     return DecodeGeometry{chunk, (max_len + chunk - 1) / chunk};
 }
 
+// The workspace a launch requests for n_part partial rows: O and (m, l) per row,
+// then 16 bytes (the paged plan's chunk word).
+static size_t decode_request_bytes(size_t n_part, uint32_t head_dim) {
+    return n_part * ((size_t)head_dim + 2) * sizeof(float) + 16;
+}
+
+// What launch_decode requests for a contiguous cache (it requests nothing when one
+// split covers the sequences).
 size_t decode_workspace_bytes(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_q_heads, uint32_t n_kv_heads,
                               uint32_t head_dim, uint32_t max_len) {
     if (n_seqs == 0 || max_len == 0 || n_kv_heads == 0) return 0;
@@ -987,7 +995,7 @@ size_t decode_workspace_bytes(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t 
     const uint32_t n_sub = (group + kHeads - 1) / kHeads;
     const DecodeGeometry geo = decode_geometry_of(ctx, n_seqs, n_kv_heads, n_sub, max_len);
     if (geo.n_splits <= 1) return 0;
-    return (size_t)n_seqs * n_q_heads * geo.n_splits * ((size_t)head_dim + 2) * sizeof(float);
+    return decode_request_bytes((size_t)n_seqs * n_q_heads * geo.n_splits, head_dim);
 }
 
 int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
@@ -1045,7 +1053,7 @@ int launch_decode(ds5_hip_ctx* ctx, const DecodeLaunch& a) {
     if (n_splits > 1 || planned) {
         const size_t n_part = n_splits > 1 ? (size_t)a.n_seqs * a.n_q_heads * n_splits : 0;
         void* ws = nullptr;
-        int rc = ds5_workspace(ctx, n_part * ((size_t)a.head_dim + 2) * sizeof(float) + 16, &ws);
+        int rc = ds5_workspace(ctx, decode_request_bytes(n_part, a.head_dim), &ws);
         if (rc) return rc;
         prm.part_o = (float*)ws;
         prm.part_ml = prm.part_o + n_part * a.head_dim;

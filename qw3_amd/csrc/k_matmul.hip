@@ -788,8 +788,12 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
 
 }  // namespace
 
+// The rope table follows the x split at the next 16-byte boundary (the epilogue
+// reads it in float4s).
+static size_t qkv_prep_cs_offset(uint32_t m, uint32_t k) { return (x_split_bytes(m, k) + 15) & ~(size_t)15; }
+
 size_t qkv_prep_workspace_bytes(uint32_t m, uint32_t k, uint32_t head_dim) {
-    return x_split_bytes(m, k) + (size_t)m * head_dim * sizeof(float);
+    return qkv_prep_cs_offset(m, k) + (size_t)m * head_dim * sizeof(float);
 }
 
 int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
@@ -797,7 +801,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     uint16_t* hi = (uint16_t*)a.ws;
     uint16_t* lo = hi + (size_t)a.m * a.k;
     int* row_exp = (int*)(lo + (size_t)a.m * a.k);
-    float* cs = (float*)(row_exp + a.m);  // 4-byte aligned: the planes and exponents are whole dwords
+    float* cs = (float*)((char*)a.ws + qkv_prep_cs_offset(a.m, a.k));
     XSplitRope rope{a.positions, cs, a.head_dim / 2, a.freq_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<true>, dim3(a.m), dim3(kSplitThreads), 0,
                      ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table);

@@ -36,11 +36,14 @@
 //
 // Fused mode: the pre-pass (prefill_prep_kernel, one workgroup per token)
 // writes the normalised, rotated f16 k rows and the f16 v rows into the cache,
-// and the attention kernel's q operand: q normalised, rotated, times softmax
-// scale * log2(e), rounded to f16 ([n_tokens, n_q_heads, head_dim]). The
-// separate-op path packs an already normalised and rotated q the same way
-// (q_pack_kernel). The attention block's projection GEMM can do the pre-pass
-// in its epilogue instead (k_matmul.hip).
+// and every token's rope cos/sin ([n_tokens, head_dim] f32). The attention
+// kernel builds its q operand from the raw f32 q when it loads a q tile: q
+// normalised, rotated with that table, times softmax scale * log2(e), rounded to
+// f16 (each (q tile, head) is loaded by one workgroup, so q is read once, as f32,
+// and never written back). The separate-op path hands it q already normalised and
+// rotated, which it only scales. The attention block's projection GEMM writes a
+// ready f16 operand in its epilogue (k_matmul.hip) with the same arithmetic, so
+// all three give the same outputs from the same projections.
 #include <type_traits>
 
 #include "ds5_common.hpp"
@@ -83,28 +86,23 @@ __device__ __forceinline__ float serial_sum_sq(const float* sq) {
     return acc;
 }
 
-// Token t: cos/sin of its rope angles (kernels_a.zig:119-122); every kv head's
-// k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX rotation (:125-126),
-// f16 append at slot pos + t (:196-210); v rows f16. Then the q rows of every
-// head: RMSNorm, rotation, times softmax scale * log2(e), rounded to f16 into
-// q16 [n_tokens, n_q_heads, head_dim] (the attention kernel's operand). q only
-// feeds the attention products, so its sum of squares is a lane reduction.
+// Token t: cos/sin of its rope angles (kernels_a.zig:119-122), into cs[t] (cos of
+// pairs 0 .. D/2 - 1, then their sin) for the attention kernel's q rotation; every
+// kv head's k row: serial-order RMSNorm (kernels_a.zig:84-89), NeoX rotation
+// (:125-126), f16 append at slot pos + t (:196-210); v rows f16.
 template <int D>
-__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, f16* q16, RopeTable table) {
+__global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch a, RopeTable table) {
     __shared__ __attribute__((aligned(16))) float s_k[kPrepMaxRow];
     __shared__ __attribute__((aligned(16))) float s_ksq[kPrepMaxRow];  // the k squares, formed in parallel
     __shared__ float s_cos[D / 2], s_sin[D / 2];
     __shared__ float s_inv[kPrepMaxRow / 64];
     constexpr uint32_t half = D / 2;
-    constexpr uint32_t TPH = D / 16;  // q: threads per head, thread k takes dims 8k + [0, 8) and half + 8k + [0, 8)
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const uint32_t H = a.n_kv_heads, HQ = a.n_q_heads;
+    const uint32_t H = a.n_kv_heads;
     // Every load of the token is issued up front, with no wait in between (this
-    // thread's k and v quads, its first q chunk, the position and its inverse
-    // frequency; each unconditional with a clamped index, since a load under a
-    // branch makes the compiler wait at the join), so one memory round trip covers
-    // them all. (Staging k in LDS straight from its loads made every thread wait
-    // for k before issuing q and v: three round trips instead of one.)
+    // thread's k and v quads, the position and its inverse frequency; each
+    // unconditional with a clamped index, since a load under a branch makes the
+    // compiler wait at the join), so one memory round trip covers them all.
     const float pos = (float)a.positions[t];
     const float inv_freq = table.inv[min(tid, half - 1)];  // the threads < half use it
     static_assert(D / 2 <= kPrepThreads, "one rope angle per thread");
@@ -113,24 +111,17 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
     const float4* krow = (const float4*)(a.k + (uint64_t)t * H * D);
     const float4 kq0 = krow[min(tid, nk4 - 1)];
     const float4 kq1 = krow[min(tid + kPrepThreads, nk4 - 1)];
-    const float* qbase = a.q + (uint64_t)t * HQ * D;
-    float x0[8], x1[8];
-    {
-        const uint32_t e = min(tid, HQ * TPH - 1);
-        const float* row = qbase + (e / TPH) * D + 8 * (e % TPH);
-        *(float4*)&x0[0] = *(const float4*)(row);
-        *(float4*)&x0[4] = *(const float4*)(row + 4);
-        *(float4*)&x1[0] = *(const float4*)(row + half);
-        *(float4*)&x1[4] = *(const float4*)(row + half + 4);
-    }
     const float4* vrow = (const float4*)(a.v + (uint64_t)t * H * D);
     const float4 v0 = vrow[min(tid, nk4 - 1)];
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     if (tid < half) {
         const float ang = qk_rope_angle(pos, a.freq_scale, inv_freq);
-        s_cos[tid] = cosf(ang);
-        s_sin[tid] = sinf(ang);
+        const float c = cosf(ang), sn = sinf(ang);
+        s_cos[tid] = c;
+        s_sin[tid] = sn;
+        a.cs[(uint64_t)t * D + tid] = c;
+        a.cs[(uint64_t)t * D + half + tid] = sn;
     }
     if (tid < nk4) {
         ((float4*)s_k)[tid] = kq0;
@@ -149,34 +140,6 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
         const f16x4 y = {(f16)v.x, (f16)v.y, (f16)v.z, (f16)v.w};
         *(f16x4*)(a.v_cache + ((uint64_t)h * a.max_ctx + a.pos + t) * D + i) = y;
     }
-    // q rows: RMSNorm (lane-reduced sum of squares), rotation, scale, f16
-    for (uint32_t e = tid; e < HQ * TPH; e += kPrepThreads) {
-        const uint32_t hq = e / TPH, k8 = 8 * (e % TPH);
-        if (e != tid) {
-            const float* row = qbase + hq * D + k8;
-            *(float4*)&x0[0] = *(const float4*)(row);
-            *(float4*)&x0[4] = *(const float4*)(row + 4);
-            *(float4*)&x1[0] = *(const float4*)(row + half);
-            *(float4*)&x1[4] = *(const float4*)(row + half + 4);
-        }
-        float ss = qk_pairs_sumsq(x0, x1);
-#pragma unroll
-        for (uint32_t m = 1; m < TPH; m <<= 1) ss += __shfl_xor(ss, (int)m, 64);
-        const float inv = rms_inv(ss, (float)D, a.eps);
-        f16x8 y0v, y1v;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t i = k8 + j;
-            float y0, y1;
-            qk_rotate(qk_norm_mul(x0[j], inv, a.q_norm[i]), qk_norm_mul(x1[j], inv, a.q_norm[i + half]), s_cos[i],
-                      s_sin[i], y0, y1);
-            y0v[j] = qk_scaled_f16(y0, a.q_scale);
-            y1v[j] = qk_scaled_f16(y1, a.q_scale);
-        }
-        f16* dst = q16 + ((uint64_t)t * HQ + hq) * D;
-        *(f16x8*)(dst + k8) = y0v;
-        *(f16x8*)(dst + half + k8) = y1v;
-    }
     __syncthreads();
     // k rows: serial-order RMSNorm, rotation, f16 append
     for (uint32_t e = tid; e < H * half; e += kPrepThreads) {
@@ -192,17 +155,6 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
     }
 }
 
-// Separate-op path: q already normalised and rotated; q16 = f16(q * q_scale).
-__global__ __launch_bounds__(256) void q_pack_kernel(const float* q, f16* q16, uint64_t n8, float q_scale) {
-    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n8; i += (uint64_t)gridDim.x * 256) {
-        const float4 a = *(const float4*)(q + 8 * i), b = *(const float4*)(q + 8 * i + 4);
-        const f16x8 y = {qk_scaled_f16(a.x, q_scale), qk_scaled_f16(a.y, q_scale), qk_scaled_f16(a.z, q_scale),
-                         qk_scaled_f16(a.w, q_scale), qk_scaled_f16(b.x, q_scale), qk_scaled_f16(b.y, q_scale),
-                         qk_scaled_f16(b.z, q_scale), qk_scaled_f16(b.w, q_scale)};
-        *(f16x8*)(q16 + 8 * i) = y;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
@@ -215,8 +167,20 @@ constexpr int kAhead = kStages - 1;
 constexpr int kOpAhead = 3;    // LDS operand reads in flight ahead of their product
 constexpr float kRescaleLog2 = 8.0f;
 
+// Where the attention kernel's q operand comes from:
+//   kQOperand: a ready f16 operand (the attention block's projection GEMM writes it)
+//   kQRotated: f32 q that is already normalised and rotated (the separate ops):
+//              f16(q * q_scale)
+//   kQRaw:     the raw f32 projection (the fused step): RMSNorm, rotation with the
+//              pre-pass's cos/sin table, times q_scale, f16
+enum QMode : int { kQOperand = 0, kQRotated = 1, kQRaw = 2 };
+
 struct PrefillParams {
-    const f16* q16;          // [n_tokens, n_q_heads, head_dim], scaled by softmax scale * log2(e)
+    const f16* q16;          // kQOperand: [n_tokens, n_q_heads, head_dim], scaled by softmax scale * log2(e)
+    const float* q;          // kQRotated, kQRaw: [n_tokens, n_q_heads, head_dim] f32
+    const float* q_norm;     // kQRaw: [head_dim]
+    const float* cs;         // kQRaw: [n_tokens, head_dim], cos of pairs 0 .. head_dim/2 - 1, then sin
+    float eps, q_scale;      // q_scale = softmax scale * log2(e)
     const f16* k_cache;
     const f16* v_cache;
     float* out;
@@ -361,11 +325,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // current half's exponentials and the current PV products beside the next half's
 // row max (see step), so its matrix-core and VALU work overlap in one instruction
 // stream.
-template <int D>
+template <int D, int QM>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
     constexpr int KS = G::KS, DT = G::DT, RSK = G::RSK, RSV = G::RSV;
-    __shared__ __attribute__((aligned(1024))) char s_kv[kStages * G::STAGE];  // stage s: K then V
+    // stage s: K then V; then a 256-byte sink for the q prefetch's direct-to-LDS loads
+    __shared__ __attribute__((aligned(1024))) char s_kv[kStages * G::STAGE + (QM == kQOperand ? 0 : 256)];
 
     const int lane = threadIdx.x & 63;
     const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head slot (kHeads: the producer)
@@ -447,18 +412,102 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // Rows past the last token and the heads of an unfilled group read clamped, valid
     // q rows: their scores stay in their own columns of S and O and are never written.
     f16x8 qop[KS], qnext[KS];
+    auto q_row = [&](uint32_t qtile) -> uint32_t { return min(qtile * kQRows + r32, p.n_tokens - 1); };
     auto load_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
-        const uint32_t tc = min(qtile * kQRows + r32, p.n_tokens - 1);
-        const f16* qrow = p.q16 + ((uint64_t)tc * p.n_q_heads + hq) * D + 8 * h;
+        const f16* qrow = p.q16 + ((uint64_t)q_row(qtile) * p.n_q_heads + hq) * D + 8 * h;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) dst[ks] = *(const f16x8*)(qrow + 16 * ks);
     };
+    // The operand from f32 q (kQRotated, kQRaw). With kQRaw this is the arithmetic of
+    // the pre-pass and of the projection GEMM's epilogue, so all three give the same
+    // operand bit for bit: the lane's k-steps ks and ks + KS/2 hold the rope pairs
+    // (i, i + D/2) of chunk c = 2 ks + h (dims 8c + [0, 8)); its share of the sum of
+    // squares is qk_pairs_sumsq of that pair of chunks; the shares of chunks c and
+    // c ^ 1 sit in lanes l and l ^ 32 and are added first, then those of c and c ^ 2,
+    // then c and c ^ 4 -- the xor order in which the other two add them.
+    auto make_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
+        constexpr int HK = KS / 2;
+        const uint32_t tc = q_row(qtile);
+        const float* qrow = p.q + ((uint64_t)tc * p.n_q_heads + hq) * D + 8 * h;
+        float x[KS][8];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            *(float4*)&x[ks][0] = *(const float4*)(qrow + 16 * ks);
+            *(float4*)&x[ks][4] = *(const float4*)(qrow + 16 * ks + 4);
+        }
+        if constexpr (QM == kQRotated) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) dst[ks][j] = qk_scaled_f16(x[ks][j], p.q_scale);
+        } else {
+            static_assert(HK == 4 || HK == 2, "head_dim 128 or 64");
+            float l1[HK];
+#pragma unroll
+            for (int j = 0; j < HK; j++) l1[j] = swap32_op(qk_pairs_sumsq(x[j], x[j + HK]), OpAdd{});
+            float ss;
+            if constexpr (HK == 4)
+                ss = (l1[0] + l1[1]) + (l1[2] + l1[3]);
+            else
+                ss = l1[0] + l1[1];
+            const float inv = rms_inv(ss, (float)D, p.eps);
+            // Per k-step pair: the norm weights and cos/sin of its 8 rope pairs, loaded
+            // one pair ahead of their use (scheduling fences keep the loads from being
+            // hoisted all at once: with every pair's 32 values in registers the kernel
+            // would spill).
+            const float* crow = p.cs + (uint64_t)tc * D + 8 * h;
+            const float* wrow = p.q_norm + 8 * h;
+            float pc[2][4][8];  // [buffer][w0, w1, cos, sin][j]
+            auto load_pc = [&](float(&d)[4][8], int ks) {
+                const float* src[4] = {wrow + 16 * ks, wrow + D / 2 + 16 * ks, crow + 16 * ks, crow + D / 2 + 16 * ks};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    *(float4*)&d[u][0] = *(const float4*)(src[u]);
+                    *(float4*)&d[u][4] = *(const float4*)(src[u] + 4);
+                }
+            };
+            load_pc(pc[0], 0);
+#pragma unroll
+            for (int ks = 0; ks < HK; ks++) {
+                if (ks + 1 < HK) load_pc(pc[(ks + 1) & 1], ks + 1);
+                const float(&c)[4][8] = pc[ks & 1];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    float y0, y1;
+                    qk_rotate(qk_norm_mul(x[ks][j], inv, c[0][j]), qk_norm_mul(x[ks + HK][j], inv, c[1][j]), c[2][j],
+                              c[3][j], y0, y1);
+                    dst[ks][j] = qk_scaled_f16(y0, p.q_scale);
+                    dst[ks + HK][j] = qk_scaled_f16(y1, p.q_scale);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    // The light tile's f32 q rows (and with kQRaw their cos/sin rows) pulled into the
+    // L2 a few rounds before the switch builds the operand from them: dword loads of
+    // one word per 128-byte line into an LDS sink nobody reads (a direct-to-LDS load
+    // needs no register; nothing waits for these until make_q's own loads, which the
+    // compiler waits for and which were issued after them).
+    auto prefetch_q = [&](uint32_t qtile) {
+        constexpr int LPR = D * 4 / 128;  // 128-byte lines per row of one head
+        constexpr int N = kQRows * LPR / 64;
+        static_assert(kQRows * LPR % 64 == 0, "whole prefetch loads");
+        const uint32_t sink = __builtin_amdgcn_readfirstlane(lds_addr(s_kv + kStages * G::STAGE));
+#pragma unroll
+        for (int n = 0; n < N; n++) {
+            const uint32_t line = 64 * n + lane, row = min(qtile * kQRows + line / LPR, p.n_tokens - 1);
+            const uint32_t c = 128 * (line % LPR);
+            const uint64_t qa = (uint64_t)(p.q + ((uint64_t)row * p.n_q_heads + hq) * D) + c;
+            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(qa), "s"(sink) : "m0");
+            if constexpr (QM == kQRaw) {
+                const uint64_t ca = (uint64_t)(p.cs + (uint64_t)row * D) + c;
+                asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(ca), "s"(sink)
+                             : "m0");
+            }
+        }
+    };
 
-    f32x16 O[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
+    f32x16 O[DT];  // zeroed after the prologue's q operand (light_state: after the switch's)
     // The scores are kept relative to the row's reference m (the lazy running max,
     // an f16 value): every score product starts with a 16-deep product whose only
     // nonzero term is 1 x (-m) (onecol . mneg), so the products leave s - m and the
@@ -473,8 +522,6 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // step's PV products (every row of Lsum^T is the row-sum vector; element 0 is read).
     // The sum is of the same f16 weights the products take.
     f32x16 Lsum;
-#pragma unroll
-    for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
     f16x8 ones;
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = (f16)1.0f;
@@ -646,75 +693,112 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         }
     };
 
-    // ---- prologue: both q tiles' operands (the producer streams items 0 .. kAhead - 1
-    // meanwhile); the scores of item 0's first half and their row max before round 0.
-    load_q(qop, heavy);
+    // Scores of item i's first half from its stage (no shift: the caller's reference
+    // is 0), the K operands of its second half read ahead, and their row max.
+    auto first_scores = [&](f32x16& S, uint32_t i) {
+        const char* sk = s_kv + k_stage(i) + kb;
+#pragma unroll
+        for (int r = 0; r < 16; r++) S[r] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) S = mfma_32x32x16(*(const f16x8*)(sk + 32 * ks), qop[ks], S);
+#pragma unroll
+        for (int n = 0; n < AHEAD; n++) kop[n] = *(const f16x8*)(kptr(k_stage(i), 1) + 32 * n);
+        mx = half_max(S);  // (a masked half's max is taken again after its mask)
+    };
+
+    auto zero_acc = [&]() {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
+    };
+
+    // ---- prologue: the heavy tile's q operand (the producer streams items 0 .. kAhead
+    // - 1 meanwhile); the scores of item 0's first half and their row max before round 0.
     f32x16 Sa, Sb;  // scores of the current item's first and second half
-    wait_vm<0>();
-    lds_sync();
-    {
-        const char* sk = s_kv + k_stage(0) + kb;
-#pragma unroll
-        for (int r = 0; r < 16; r++) Sa[r] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) Sa = mfma_32x32x16(*(const f16x8*)(sk + 32 * ks), qop[ks], Sa);
-#pragma unroll
-        for (int n = 0; n < AHEAD; n++) kop[n] = *(const f16x8*)(kptr(k_stage(0), 1) + 32 * n);
-        mx = half_max(Sa);  // (a masked half's max is taken again after its mask)
+    if constexpr (QM == kQOperand) {
+        load_q(qop, heavy);
+        wait_vm<0>();
+    } else {
+        make_q(qop, heavy);
     }
+    lds_sync();
+    first_scores(Sa, 0);
+    zero_acc();
+
+    // The light tile's state after the heavy tile's rows are written.
+    auto light_state = [&]() {
+        t = pair * kQRows + r32;
+        keep = live && t < p.n_tokens;
+        zero_acc();
+        thr = -INFINITY;
+    };
+    // f32 q modes: the round at which the light tile's rows are prefetched (three
+    // rounds, about 7K cycles, before the switch needs them).
+    const uint32_t pf_round = H > 3 ? H - 3 : 0;
 
     // Round r (item r): step 0 (weights and PV of its first half; scores of its second
     // half), then step 1 (weights and PV of its second half; scores of item r + 1's
     // first half, from stage (r + 1) % kStages), then the round's barrier. A special
-    // round also masks the halves that cross the diagonal, loads the light tile's q
-    // operand or switches to the light tile; the others run the plain form, so the
-    // loop over a run of plain rounds has no branch but the rare rescale.
+    // round also masks the halves that cross the diagonal, loads (kQOperand) or
+    // prefetches (f32 q) the light tile's q, or switches to the light tile; the others
+    // run the plain form, so the loop over a run of plain rounds has no branch but the
+    // rare rescale. The switch round's step 1 forms item r + 1's first scores with the
+    // heavy tile's operand (nine wasted products: a step without next scores there, in
+    // a branch of its own, made the compiler spill); then the heavy tile's rows are
+    // written, the light tile's operand takes the heavy tile's registers (loaded
+    // earlier, or built from f32 q), and item r + 1's first scores are formed again as
+    // in the prologue, from reference 0 -- the same arithmetic in every q mode, so the
+    // modes give the same outputs from the same operand.
     auto round = [&](uint32_t r, auto special) {
         constexpr bool SPECIAL = decltype(special)::value;
         const uint32_t st = k_stage(r), st1 = k_stage(r + 1);
         if constexpr (SPECIAL) {
-            // The light tile's q operand loads one round in (not with the heavy tile's:
-            // at the start every workgroup loads its q at once, and that burst is time
-            // no product overlaps), or in round 0 when item 1 already starts the light
-            // tile.
-            if (has_light && r == min(1u, H - 1)) load_q(qnext, pair);
+            if constexpr (QM == kQOperand) {
+                // The light tile's q operand loads one round in (not with the heavy
+                // tile's: at the start every workgroup loads its q at once, and that
+                // burst is time no product overlaps), or in round 0 when item 1 already
+                // starts the light tile.
+                if (has_light && r == min(1u, H - 1)) load_q(qnext, pair);
+            } else {
+                if (has_light && r == pf_round) prefetch_q(pair);
+            }
             mask_if_needed(Sa, r, 0);
         }
         step(Sa, Sb, 0, st, kptr(st, 1), kptr(st1, 0), std::true_type{}, std::true_type{});
-        if constexpr (SPECIAL) {
-            if (r + 1 == H) {  // item H's scores (the next step) start the light tile
-                wait_vm<0>();
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) qop[ks] = qnext[ks];
-            }
-            mask_if_needed(Sb, r, 1);
-        }
+        if constexpr (SPECIAL) mask_if_needed(Sb, r, 1);
         step(Sb, Sa, 1, st, kptr(st1, 0), kptr(st1, 1), std::true_type{}, std::true_type{});
         if constexpr (SPECIAL) {
-            if (r + 1 == H) {  // the heavy tile is done: its rows, then the light tile's state
+            if (r + 1 == H) {  // the heavy tile is done: its rows, then the light tile's
                 write_rows();
-                t = pair * kQRows + r32;
-                keep = live && t < p.n_tokens;
+                if constexpr (QM == kQOperand) {
+                    wait_vm<0>();
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) O[dt][i] = 0.0f;
-                thr = -INFINITY;
-#pragma unroll
-                for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
+                    for (int ks = 0; ks < KS; ks++) qop[ks] = qnext[ks];
+                } else {
+                    make_q(qop, pair);
+                }
+                m_sh = 0.0f;
+                mneg[0] = (f16)0.0f;
+                first_scores(Sa, r + 1);
+                light_state();
             }
         }
         lds_sync();
     };
-    // The special rounds: the light tile's q load (round min(1, H - 1)) and switch
-    // (round H - 1), and the items whose second half crosses a q tile's first row
-    // (key tile kt of q tile qt with 64 kt + 63 > pos + 32 qt, i.e. kt >= first_masked).
+    // The special rounds: the light tile's q load or prefetch (round min(1, H - 1) or
+    // pf_round) and switch (round H - 1), and the items whose second half crosses a q
+    // tile's first row (key tile kt of q tile qt with 64 kt + 63 > pos + 32 qt, i.e.
+    // kt >= first_masked).
     auto first_masked = [&](uint32_t qtile) -> uint32_t { return (p.pos + qtile * kQRows + 1) / kKTile; };
     const uint32_t mh = min(first_masked(heavy), H), ml = H + first_masked(pair);
+    const uint32_t q_round = QM == kQOperand ? min(1u, H - 1) : pf_round;
     auto next_special = [&](uint32_t r) -> uint32_t {  // the first special round >= r
         uint32_t ns = n_items;
         if (has_light) {
-            ns = r <= min(1u, H - 1) ? min(1u, H - 1) : r <= H - 1 ? H - 1 : n_items;
+            ns = r <= q_round ? q_round : r <= H - 1 ? H - 1 : n_items;
             ns = min(ns, max(r, ml));
         }
         if (r < H && mh < H) ns = min(ns, max(r, mh));
@@ -741,29 +825,32 @@ bool prefill_prep_supported(uint32_t n_kv_heads, uint32_t head_dim) {
     return (uint64_t)n_kv_heads * head_dim <= kPrepMaxRow && (head_dim == 64 || head_dim == 128);
 }
 
-int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a, f16* q16) {
+int launch_kv_prep(ds5_hip_ctx* ctx, const KvPrepLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
     if (a.head_dim == 128)
         DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel<128>, dim3(a.n_tokens), dim3(kPrepThreads), 0,
-                         ctx->stream, a, q16, *a.table);
+                         ctx->stream, a, *a.table);
     else
         DS5_TIMED_LAUNCH(ctx, "prefill_prep_kernel", prefill_prep_kernel<64>, dim3(a.n_tokens), dim3(kPrepThreads), 0,
-                         ctx->stream, a, q16, *a.table);
+                         ctx->stream, a, *a.table);
     return ds5_after_launch(ctx, "prefill_prep_kernel");
 }
 
-int launch_q_pack(ds5_hip_ctx* ctx, const float* q, f16* q16, uint64_t n, float q_scale) {
-    if (n == 0) return DS5_OK;
-    const uint64_t n8 = n / 8;
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n8 + 255) / 256, 2048);
-    DS5_TIMED_LAUNCH(ctx, "q_pack_kernel", q_pack_kernel, dim3(blocks), dim3(256), 0, ctx->stream, q, q16, n8, q_scale);
-    return ds5_after_launch(ctx, "q_pack_kernel");
+template <int D, int QM>
+static void launch_prefill_k(ds5_hip_ctx* ctx, const PrefillParams& p) {
+    DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", (prefill_attention_kernel<D, QM>), dim3(p.n_items), dim3(kThreads),
+                     0, ctx->stream, p);
 }
 
 int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
     PrefillParams p{};
     p.q16 = a.q16;
+    p.q = a.q;
+    p.q_norm = a.q_norm;
+    p.cs = a.cs;
+    p.eps = a.eps;
+    p.q_scale = a.q_scale;
     p.k_cache = a.k_cache;
     p.v_cache = a.v_cache;
     p.out = a.out;
@@ -777,12 +864,15 @@ int launch_prefill(ds5_hip_ctx* ctx, const PrefillLaunch& a) {
     p.n_hgroups = (p.group + kHeads - 1) / kHeads;
     p.n_items = a.n_kv_heads * p.n_hgroups * p.n_pairs;
     p.items_per_xcd = p.n_items % 8 == 0 ? p.n_items / 8 : 0;
-    const dim3 grid(p.n_items);
-    if (a.head_dim == 128)
-        DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", prefill_attention_kernel<128>, grid, dim3(kThreads), 0,
-                         ctx->stream, p);
-    else
-        DS5_TIMED_LAUNCH(ctx, "prefill_attention_kernel", prefill_attention_kernel<64>, grid, dim3(kThreads), 0,
-                         ctx->stream, p);
+    const int qm = a.q16 ? kQOperand : a.cs ? kQRaw : kQRotated;
+    if (a.head_dim == 128) {
+        if (qm == kQOperand) launch_prefill_k<128, kQOperand>(ctx, p);
+        else if (qm == kQRaw) launch_prefill_k<128, kQRaw>(ctx, p);
+        else launch_prefill_k<128, kQRotated>(ctx, p);
+    } else {
+        if (qm == kQOperand) launch_prefill_k<64, kQOperand>(ctx, p);
+        else if (qm == kQRaw) launch_prefill_k<64, kQRaw>(ctx, p);
+        else launch_prefill_k<64, kQRotated>(ctx, p);
+    }
     return ds5_after_launch(ctx, "prefill_attention_kernel");
 }

@@ -15,8 +15,8 @@ Replicated:
   qw3_amd/csrc/k_matmul.hip  the direct-to-LDS loads of matmul_q8_mfma_kernel (x
                              planes, raw Q8_0 rows) and matmul_path's slack rule
   qw3_amd/csrc/k_prefill.hip TilePlan / dma_tile of prefill_attention_kernel (every
-                             direct-to-LDS load of every item) and its q-operand
-                             loads
+                             direct-to-LDS load of every item), its q-operand and f32 q
+                             loads, the cos/sin rows and the light tile's prefetch
 """
 import numpy as np
 import pytest
@@ -406,8 +406,20 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
                 break
             qt = heavy if sel == 0 else pair
             q0 = qt * P_QROWS
-            # q operand: lane (r32, h): row min(q0 + r32, T - 1), head hq, halves 8h + 16 ks .. + 8
+            # q operand (f16 operand or f32 q): lane (r32, h): row min(q0 + r32, T - 1),
+            # head hq, elements 8h + 16 ks .. + 8; f32 q with its cos/sin row (D floats
+            # of row tc) and the prefetch: line 64 n + lane of the tile, row
+            # min(q0 + line / LPR, T - 1), bytes 128 (line % LPR) of the row
             tc = np.minimum(q0 + np.arange(32), T - 1)
+            lane = np.arange(64)
+            els = (8 * (lane[:, None] // 32) + 16 * np.arange(D // 16)[None, :])[..., None] + np.arange(8)
+            assert els.min() >= 0 and els.max() < D
+            LPR = D * 4 // 128
+            lines = 64 * np.arange(P_QROWS * LPR // 64)[:, None] + lane[None, :]
+            pf_row = np.minimum(q0 + lines // LPR, T - 1)
+            pf_byte = 128 * (lines % LPR)
+            assert (pf_byte + 4).max() <= 4 * D
+            assert (tc * D + D).max() <= T * D and (pf_row * D * 4 + pf_byte + 4).max() <= T * D * 4  # cs rows
             for hg in range(n_hgroups):
                 for hw in range(P_HEADS):
                     hin = hg * P_HEADS + hw
@@ -415,6 +427,8 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
                         hqi = kvh * group + (hin if hin < group else 0)
                         off = (tc * hq + hqi) * D
                         assert off.min() >= 0 and (off + D).max() <= T * hq * D
+                        pf = (pf_row * hq + hqi) * D * 4 + pf_byte
+                        assert pf.min() >= 0 and (pf + 4).max() <= T * hq * D * 4
     for key0, end in calls:
         assert 0 < end <= max_ctx
         for plan in (pk, pv):

@@ -62,11 +62,21 @@ def test_noalloc_matches_step_two_calls(ctx, hip, first, second):
 
 
 def test_noalloc_rejects_oversize_before_device_work(ctx, hip):
-    """C2's 2048-token prefill needs 16 MiB of f16 q operand: more than the scratch holds."""
+    """A fused prefill step of 8193 tokens needs its rope table, 8193 x 128 f32 (just
+    over 4 MiB): more than the scratch holds. Nothing runs, nothing is appended."""
     s = synth.CONFIGS[2]["shape"]
-    T, cap, pos = 2048, 2048, 0
-    assert T * s.n_q_heads * s.head_dim * 2 > hip.NOALLOC_SCRATCH_BYTES
-    q, k, v, qn, kn, positions, kc, vc = _inputs(2, 0, s, cap, pos, T)
+    T = cap = 8193
+    pos = 0
+    assert T * s.head_dim * 4 > hip.NOALLOC_SCRATCH_BYTES
+    rng = np.random.default_rng(7)
+    q = np.ones((T, s.n_q_heads, s.head_dim), np.float32)
+    k = np.ones((T, s.n_kv_heads, s.head_dim), np.float32)
+    v = np.ones((T, s.n_kv_heads, s.head_dim), np.float32)
+    qn = np.ones(s.head_dim, np.float32)
+    kn = np.ones(s.head_dim, np.float32)
+    positions = np.arange(T, dtype=np.int32)
+    kc = rng.integers(0, 0x7800, (s.n_kv_heads, cap, s.head_dim), dtype=np.uint16)
+    vc = kc.copy()
     bufs = [ctx.from_numpy(np.ascontiguousarray(a)) for a in (q, k, v, qn, kn, positions, kc, vc)]
     out = ctx.createBuffer(T * s.n_q_heads * s.head_dim * 4)
     args = hip.AttentionStepArgs(*bufs, out, hip.DTYPE_F16, pos, T, s.n_q_heads, s.n_kv_heads, s.head_dim, cap,
