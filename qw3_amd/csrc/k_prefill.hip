@@ -164,7 +164,7 @@ constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA N)
 constexpr int kKTile = 64;     // keys per LDS stage
 constexpr int kStages = 4;     // K/V ring: a stage is refilled three rounds ahead of its use
 constexpr int kAhead = kStages - 1;
-constexpr int kOpAhead = 3;    // LDS operand reads in flight ahead of their product
+constexpr int kOpAhead = 4;    // LDS operand reads in flight ahead of their product
 constexpr float kRescaleLog2 = 8.0f;
 
 // Where the attention kernel's q operand comes from:
@@ -329,8 +329,7 @@ template <int D, int QM>
 __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillParams p) {
     using G = PGeo<D>;
     constexpr int KS = G::KS, DT = G::DT, RSK = G::RSK, RSV = G::RSV;
-    // stage s: K then V; then a 256-byte sink for the q prefetch's direct-to-LDS loads
-    __shared__ __attribute__((aligned(1024))) char s_kv[kStages * G::STAGE + (QM == kQOperand ? 0 : 256)];
+    __shared__ __attribute__((aligned(1024))) char s_kv[kStages * G::STAGE];  // stage s: K then V
 
     const int lane = threadIdx.x & 63;
     const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head slot (kHeads: the producer)
@@ -387,6 +386,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             } else {
                 wait_vm<0>();
             }
+            if (has_light && r + 1 == H) lds_sync();  // the switch's extra barrier
             lds_sync();
         }
         return;
@@ -404,110 +404,143 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // + 4 (i16 & 3), i.e. bytes 64 dt + 32 (g16 & 1) + 8 (i16 & 3) of the row.
     const int vb = (4 * (g16 >> 1) + (i16 >> 2)) * RSV + 32 * (g16 & 1) + 8 * (i16 & 3);
 
-    // the wavefront's q tile: lane (r32, h) holds query row t
-    uint32_t t = heavy * kQRows + r32;
-    bool keep = live && t < p.n_tokens;
-
-    // q operand of lane (r32, h): row t, dims 16 ks + 8 h + [0, 8) for every k-step.
-    // Rows past the last token and the heads of an unfilled group read clamped, valid
-    // q rows: their scores stay in their own columns of S and O and are never written.
-    f16x8 qop[KS], qnext[KS];
-    auto q_row = [&](uint32_t qtile) -> uint32_t { return min(qtile * kQRows + r32, p.n_tokens - 1); };
-    auto load_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
-        const f16* qrow = p.q16 + ((uint64_t)q_row(qtile) * p.n_q_heads + hq) * D + 8 * h;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) dst[ks] = *(const f16x8*)(qrow + 16 * ks);
+    // Staging area of this wavefront inside a K/V stage that no wavefront reads at the
+    // time (a quarter stage each): the q operand and the output rows go through it so
+    // that their global loads and stores run along rows. In the MFMA layout a lane
+    // holds one q row and the 64 lanes of an access span 32 rows, so every load or
+    // store instruction would touch 32 cache lines; along rows it touches 8.
+    constexpr int QSTR = 2 * D + 16;   // f16 q operand row stride (bank-conflict free reads)
+    constexpr int OSTR = 32 * 4 + 16;  // f32 output row stride (one 32-dim block of O)
+    static_assert(32 * QSTR <= G::STAGE / 4 && 32 * OSTR <= G::STAGE / 4 && G::STAGE % 64 == 0,
+                  "staging fits a quarter stage");
+    auto area_of = [&](uint32_t stage_off) -> char* { return s_kv + stage_off + hw * (G::STAGE / 4); };
+    // The lane index through an empty asm: address arithmetic of the prologue, the
+    // switch and the end is then computed where it is used; otherwise the compiler
+    // hoists it out of the round loop and spills it.
+    auto lane_here = [&]() -> uint32_t {
+        uint32_t l = lane;
+        asm volatile("" : "+v"(l));
+        return l;
     };
-    // The operand from f32 q (kQRotated, kQRaw). With kQRaw this is the arithmetic of
-    // the pre-pass and of the projection GEMM's epilogue, so all three give the same
-    // operand bit for bit: the lane's k-steps ks and ks + KS/2 hold the rope pairs
-    // (i, i + D/2) of chunk c = 2 ks + h (dims 8c + [0, 8)); its share of the sum of
-    // squares is qk_pairs_sumsq of that pair of chunks; the shares of chunks c and
-    // c ^ 1 sit in lanes l and l ^ 32 and are added first, then those of c and c ^ 2,
-    // then c and c ^ 4 -- the xor order in which the other two add them.
-    auto make_q = [&](f16x8(&dst)[KS], uint32_t qtile) {
-        constexpr int HK = KS / 2;
-        const uint32_t tc = q_row(qtile);
-        const float* qrow = p.q + ((uint64_t)tc * p.n_q_heads + hq) * D + 8 * h;
-        float x[KS][8];
+
+    // q operand of lane (r32, h): row q0 + r32 of the q tile, dims 16 ks + 8 h + [0, 8)
+    // for every k-step, read from the staged f16 rows. Rows are staged along rows:
+    //   kQOperand: lane (g, m) copies 8 f16 of row RPI it + g, dims 8 m + [0, 8);
+    //   f32 q:     lane (g, m) takes dims 4 m + [0, 4) and D/2 + 4 m + [0, 4) of row
+    //              RPI it + g: four rope pairs. kQRaw: RMSNorm, rotation with the
+    //              pre-pass's cos/sin, then both: times q_scale, f16.
+    // With kQRaw this is the arithmetic of the pre-pass and of the projection GEMM's
+    // epilogue, operation for operation, so all three give the same operand: the sum
+    // of squares of rope-pair chunks c = dims 8c + [0, 8) and c + D/16 runs in element
+    // order (lane 2c's four pairs, continued on lane 2c + 1), then the chunk sums are
+    // added in xor order (c ^ 1, c ^ 2, c ^ 4). Rows past the last token and the heads
+    // of an unfilled group read clamped, valid rows: their scores stay in their own
+    // columns of S and O and are never written.
+    f16x8 qop[KS];
+    auto q_build = [&](f16x8(&dst)[KS], uint32_t qtile, char* area) {
+        const uint32_t q0 = qtile * kQRows, lane = lane_here();
+        auto row_of = [&](uint32_t row) -> uint64_t {
+            return (uint64_t)min(q0 + row, p.n_tokens - 1) * p.n_q_heads + hq;
+        };
+        if constexpr (QM == kQOperand) {
+            constexpr int LPR = D / 8, RPI = 64 / LPR, NIT = kQRows / RPI;
+            const uint32_t m = lane % LPR, g = lane / LPR;
+            f16x8 v[NIT];
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            *(float4*)&x[ks][0] = *(const float4*)(qrow + 16 * ks);
-            *(float4*)&x[ks][4] = *(const float4*)(qrow + 16 * ks + 4);
-        }
-        if constexpr (QM == kQRotated) {
+            for (int it = 0; it < NIT; it++) v[it] = *(const f16x8*)(p.q16 + row_of(RPI * it + g) * D + 8 * m);
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) dst[ks][j] = qk_scaled_f16(x[ks][j], p.q_scale);
+            for (int it = 0; it < NIT; it++) *(f16x8*)(area + (RPI * it + g) * QSTR + 16 * m) = v[it];
         } else {
-            static_assert(HK == 4 || HK == 2, "head_dim 128 or 64");
-            float l1[HK];
+            constexpr int HALF = D / 2, LPR = D / 8, RPI = 64 / LPR, NIT = kQRows / RPI;
+            const uint32_t m = lane % LPR, g = lane / LPR;
+            float4 a[NIT], b[NIT], c[NIT], sn[NIT];
 #pragma unroll
-            for (int j = 0; j < HK; j++) l1[j] = swap32_op(qk_pairs_sumsq(x[j], x[j + HK]), OpAdd{});
-            float ss;
-            if constexpr (HK == 4)
-                ss = (l1[0] + l1[1]) + (l1[2] + l1[3]);
-            else
-                ss = l1[0] + l1[1];
-            const float inv = rms_inv(ss, (float)D, p.eps);
-            // Per k-step pair: the norm weights and cos/sin of its 8 rope pairs, loaded
-            // one pair ahead of their use (scheduling fences keep the loads from being
-            // hoisted all at once: with every pair's 32 values in registers the kernel
-            // would spill).
-            const float* crow = p.cs + (uint64_t)tc * D + 8 * h;
-            const float* wrow = p.q_norm + 8 * h;
-            float pc[2][4][8];  // [buffer][w0, w1, cos, sin][j]
-            auto load_pc = [&](float(&d)[4][8], int ks) {
-                const float* src[4] = {wrow + 16 * ks, wrow + D / 2 + 16 * ks, crow + 16 * ks, crow + D / 2 + 16 * ks};
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    *(float4*)&d[u][0] = *(const float4*)(src[u]);
-                    *(float4*)&d[u][4] = *(const float4*)(src[u] + 4);
-                }
-            };
-            load_pc(pc[0], 0);
-#pragma unroll
-            for (int ks = 0; ks < HK; ks++) {
-                if (ks + 1 < HK) load_pc(pc[(ks + 1) & 1], ks + 1);
-                const float(&c)[4][8] = pc[ks & 1];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    float y0, y1;
-                    qk_rotate(qk_norm_mul(x[ks][j], inv, c[0][j]), qk_norm_mul(x[ks + HK][j], inv, c[1][j]), c[2][j],
-                              c[3][j], y0, y1);
-                    dst[ks][j] = qk_scaled_f16(y0, p.q_scale);
-                    dst[ks + HK][j] = qk_scaled_f16(y1, p.q_scale);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+            for (int it = 0; it < NIT; it++) {
+                const float* qr = p.q + row_of(RPI * it + g) * D;
+                a[it] = *(const float4*)(qr + 4 * m);
+                b[it] = *(const float4*)(qr + HALF + 4 * m);
             }
-        }
-    };
-    // The light tile's f32 q rows (and with kQRaw their cos/sin rows) pulled into the
-    // L2 a few rounds before the switch builds the operand from them: dword loads of
-    // one word per 128-byte line into an LDS sink nobody reads (a direct-to-LDS load
-    // needs no register; nothing waits for these until make_q's own loads, which the
-    // compiler waits for and which were issued after them).
-    auto prefetch_q = [&](uint32_t qtile) {
-        constexpr int LPR = D * 4 / 128;  // 128-byte lines per row of one head
-        constexpr int N = kQRows * LPR / 64;
-        static_assert(kQRows * LPR % 64 == 0, "whole prefetch loads");
-        const uint32_t sink = __builtin_amdgcn_readfirstlane(lds_addr(s_kv + kStages * G::STAGE));
-#pragma unroll
-        for (int n = 0; n < N; n++) {
-            const uint32_t line = 64 * n + lane, row = min(qtile * kQRows + line / LPR, p.n_tokens - 1);
-            const uint32_t c = 128 * (line % LPR);
-            const uint64_t qa = (uint64_t)(p.q + ((uint64_t)row * p.n_q_heads + hq) * D) + c;
-            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(qa), "s"(sink) : "m0");
+            float4 w0 = {}, w1 = {};
+            float inv[NIT];
             if constexpr (QM == kQRaw) {
-                const uint64_t ca = (uint64_t)(p.cs + (uint64_t)row * D) + c;
-                asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(ca), "s"(sink)
-                             : "m0");
+#pragma unroll
+                for (int it = 0; it < NIT; it++) {
+                    const float* cr = p.cs + (uint64_t)min(q0 + RPI * it + g, p.n_tokens - 1) * D;
+                    c[it] = *(const float4*)(cr + 4 * m);
+                    sn[it] = *(const float4*)(cr + HALF + 4 * m);
+                }
+                w0 = *(const float4*)(p.q_norm + 4 * m);
+                w1 = *(const float4*)(p.q_norm + HALF + 4 * m);
+                // chunk sums: lane 2c adds its 4 pairs from 0, lane 2c + 1 continues from
+                // lane 2c's partial (DPP row_shr:1 within the 16-lane row)
+                float tot[NIT];
+#pragma unroll
+                for (int it = 0; it < NIT; it++) {
+#pragma clang fp contract(off)
+                    const float t0 = a[it].x * a[it].x + b[it].x * b[it].x;
+                    const float t1 = a[it].y * a[it].y + b[it].y * b[it].y;
+                    const float t2 = a[it].z * a[it].z + b[it].z * b[it].z;
+                    const float t3 = a[it].w * a[it].w + b[it].w * b[it].w;
+                    const float pe = ((t0 + t1) + t2) + t3;  // lane 2c: 0 + t0 = t0 exactly
+                    // DPP moves read other lanes, so every lane must run them: they are
+                    // formed unconditionally (the empty asm keeps the compiler from
+                    // moving them under a lane mask) and selected afterwards.
+                    float pm = dpp_mov<0x111>(pe);  // row_shr:1: lane m - 1's partial
+                    asm volatile("" : "+v"(pm));
+                    float v = (m & 1) ? (((pm + t0) + t1) + t2) + t3 : 0.0f;
+                    // xor 2, 4, 8 within the 16-lane row: lane m takes lane m ^ k from
+                    // row_shr:k when bit k is set, else from row_shl:k
+                    auto xor_add = [&](auto shr, auto shl, uint32_t k) {
+                        float x = dpp_mov<decltype(shr)::value>(v), y = dpp_mov<decltype(shl)::value>(v);
+                        asm volatile("" : "+v"(x), "+v"(y));
+                        v += (m & k) ? x : y;
+                    };
+                    xor_add(std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0x102>{}, 2);
+                    xor_add(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0x104>{}, 4);
+                    if constexpr (LPR == 16)
+                        xor_add(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0x108>{}, 8);
+                    tot[it] = v;  // the row's sum of squares on its odd lanes
+                }
+                // one 1/rms per row: lane l takes row l % 32, then every lane its rows'
+                const uint32_t rr = lane % kQRows, src = (rr % RPI) * LPR + 1;
+                float mine = 0.0f;
+#pragma unroll
+                for (int it = 0; it < NIT; it++) {
+                    const float tv = __shfl(tot[it], (int)src, 64);
+                    if (rr / RPI == (uint32_t)it) mine = tv;
+                }
+                const float invr = rms_inv(mine, (float)D, p.eps);
+#pragma unroll
+                for (int it = 0; it < NIT; it++) inv[it] = __shfl(invr, (int)(RPI * it + g), 64);
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const float x0[4] = {a[it].x, a[it].y, a[it].z, a[it].w}, x1[4] = {b[it].x, b[it].y, b[it].z, b[it].w};
+                f16x4 y0v, y1v;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float y0 = x0[e], y1 = x1[e];
+                    if constexpr (QM == kQRaw) {
+                        const float c_[4] = {c[it].x, c[it].y, c[it].z, c[it].w};
+                        const float s_[4] = {sn[it].x, sn[it].y, sn[it].z, sn[it].w};
+                        const float w0_[4] = {w0.x, w0.y, w0.z, w0.w}, w1_[4] = {w1.x, w1.y, w1.z, w1.w};
+                        qk_rotate(qk_norm_mul(x0[e], inv[it], w0_[e]), qk_norm_mul(x1[e], inv[it], w1_[e]), c_[e], s_[e],
+                                  y0, y1);
+                    }
+                    y0v[e] = qk_scaled_f16(y0, p.q_scale);
+                    y1v[e] = qk_scaled_f16(y1, p.q_scale);
+                }
+                char* rowp = area + (RPI * it + g) * QSTR;
+                *(f16x4*)(rowp + 8 * m) = y0v;
+                *(f16x4*)(rowp + D + 8 * m) = y1v;
             }
         }
+        // (one wavefront wrote these rows: its LDS accesses complete in order)
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) dst[ks] = *(const f16x8*)(area + r32 * QSTR + 32 * ks + 16 * h);
     };
 
-    f32x16 O[DT];  // zeroed after the prologue's q operand (light_state: after the switch's)
+    f32x16 O[DT];  // zeroed after the prologue's q operand (and after the switch's)
     // The scores are kept relative to the row's reference m (the lazy running max,
     // an f16 value): every score product starts with a 16-deep product whose only
     // nonzero term is 1 x (-m) (onecol . mneg), so the products leave s - m and the
@@ -667,20 +700,34 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         if constexpr (NEXT) mx = max_xor32(a);
     };
 
-    // The wavefront's rows of its q tile when every key of the tile went through it:
-    // O over its row sum.
-    auto write_rows = [&]() {
-        const float l = Lsum[0];
-        if (keep) {
-            const float inv_l = 1.0f / l;
-            float* out = p.out + ((uint64_t)t * p.n_q_heads + hq) * D;
+    // The wavefront's rows of q tile `qtile` when every key of the tile went through
+    // it: O over its row sum, one 32-dim block at a time through the staging area
+    // (lane (r32, h) holds dims 8 i4 + 4 h + [0, 4) of row r32 in O[dt][4 i4 ..]), then
+    // stored along rows: lane l, row 8 it + l / 8, dims 4 (l % 8) + [0, 4).
+    // Blocks staged per pass: as many as the quarter stage holds.
+    constexpr int OBLK = (G::STAGE / 4) / (32 * OSTR) < DT ? (G::STAGE / 4) / (32 * OSTR) : DT;
+    static_assert(OBLK >= 1 && DT % OBLK == 0, "whole passes");
+    auto write_rows = [&](uint32_t qtile, char* area) {
+        const float inv_l = 1.0f / Lsum[0];
+        const uint32_t q0 = qtile * kQRows, lane = lane_here();
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++)
+        for (int d0 = 0; d0 < DT; d0 += OBLK) {
+#pragma unroll
+            for (int u = 0; u < OBLK; u++)
 #pragma unroll
                 for (int i4 = 0; i4 < 4; i4++)
-                    *(float4*)(out + dt * 32 + 8 * i4 + 4 * h) =
-                        float4{O[dt][4 * i4] * inv_l, O[dt][4 * i4 + 1] * inv_l, O[dt][4 * i4 + 2] * inv_l,
-                               O[dt][4 * i4 + 3] * inv_l};
+                    *(float4*)(area + (32 * u + r32) * OSTR + 32 * i4 + 16 * h) =
+                        float4{O[d0 + u][4 * i4] * inv_l, O[d0 + u][4 * i4 + 1] * inv_l, O[d0 + u][4 * i4 + 2] * inv_l,
+                               O[d0 + u][4 * i4 + 3] * inv_l};
+#pragma unroll
+            for (int u = 0; u < OBLK; u++)
+#pragma unroll
+                for (int it = 0; it < kQRows / 8; it++) {
+                    const uint32_t row = 8 * it + lane / 8, c4 = lane % 8;
+                    const float4 v = *(const float4*)(area + (32 * u + row) * OSTR + 16 * c4);
+                    if (live && q0 + row < p.n_tokens)
+                        *(float4*)(p.out + ((uint64_t)(q0 + row) * p.n_q_heads + hq) * D + 32 * (d0 + u) + 4 * c4) = v;
+                }
         }
     };
 
@@ -715,90 +762,59 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         for (int i = 0; i < 16; i++) Lsum[i] = 0.0f;
     };
 
-    // ---- prologue: the heavy tile's q operand (the producer streams items 0 .. kAhead
-    // - 1 meanwhile); the scores of item 0's first half and their row max before round 0.
+    // ---- prologue: the heavy tile's q operand, staged in stage kAhead (the producer
+    // streams items 0 .. kAhead - 1 into the others meanwhile and fills this one only
+    // after the barrier); the scores of item 0's first half and their row max.
     f32x16 Sa, Sb;  // scores of the current item's first and second half
-    if constexpr (QM == kQOperand) {
-        load_q(qop, heavy);
-        wait_vm<0>();
-    } else {
-        make_q(qop, heavy);
-    }
+    q_build(qop, heavy, area_of(k_stage(kAhead)));
     lds_sync();
     first_scores(Sa, 0);
     zero_acc();
 
-    // The light tile's state after the heavy tile's rows are written.
-    auto light_state = [&]() {
-        t = pair * kQRows + r32;
-        keep = live && t < p.n_tokens;
-        zero_acc();
-        thr = -INFINITY;
-    };
-    // f32 q modes: the round at which the light tile's rows are prefetched (three
-    // rounds, about 7K cycles, before the switch needs them).
-    const uint32_t pf_round = H > 3 ? H - 3 : 0;
-
     // Round r (item r): step 0 (weights and PV of its first half; scores of its second
     // half), then step 1 (weights and PV of its second half; scores of item r + 1's
     // first half, from stage (r + 1) % kStages), then the round's barrier. A special
-    // round also masks the halves that cross the diagonal, loads (kQOperand) or
-    // prefetches (f32 q) the light tile's q, or switches to the light tile; the others
-    // run the plain form, so the loop over a run of plain rounds has no branch but the
-    // rare rescale. The switch round's step 1 forms item r + 1's first scores with the
-    // heavy tile's operand (nine wasted products: a step without next scores there, in
-    // a branch of its own, made the compiler spill); then the heavy tile's rows are
-    // written, the light tile's operand takes the heavy tile's registers (loaded
-    // earlier, or built from f32 q), and item r + 1's first scores are formed again as
-    // in the prologue, from reference 0 -- the same arithmetic in every q mode, so the
-    // modes give the same outputs from the same operand.
+    // round also masks the halves that cross the diagonal or switches to the light
+    // tile; the others run the plain form, so the loop over a run of plain rounds has
+    // no branch but the rare rescale.
+    // The switch (round H - 1): step 1 forms item r + 1's first scores with the heavy
+    // tile's operand (nine wasted products: a step without next scores there, in a
+    // branch of its own, made the compiler spill); a barrier (the producer takes it too)
+    // frees item r's stage, which is refilled only in round r + 1; there the heavy
+    // tile's rows are written and the light tile's operand is staged; item r + 1's
+    // first scores are formed again as in the prologue, from reference 0 -- the same
+    // arithmetic in every q mode, so the modes give the same outputs from the same
+    // operand.
     auto round = [&](uint32_t r, auto special) {
         constexpr bool SPECIAL = decltype(special)::value;
         const uint32_t st = k_stage(r), st1 = k_stage(r + 1);
-        if constexpr (SPECIAL) {
-            if constexpr (QM == kQOperand) {
-                // The light tile's q operand loads one round in (not with the heavy
-                // tile's: at the start every workgroup loads its q at once, and that
-                // burst is time no product overlaps), or in round 0 when item 1 already
-                // starts the light tile.
-                if (has_light && r == min(1u, H - 1)) load_q(qnext, pair);
-            } else {
-                if (has_light && r == pf_round) prefetch_q(pair);
-            }
-            mask_if_needed(Sa, r, 0);
-        }
+        if constexpr (SPECIAL) mask_if_needed(Sa, r, 0);
         step(Sa, Sb, 0, st, kptr(st, 1), kptr(st1, 0), std::true_type{}, std::true_type{});
         if constexpr (SPECIAL) mask_if_needed(Sb, r, 1);
         step(Sb, Sa, 1, st, kptr(st1, 0), kptr(st1, 1), std::true_type{}, std::true_type{});
         if constexpr (SPECIAL) {
             if (r + 1 == H) {  // the heavy tile is done: its rows, then the light tile's
-                write_rows();
-                if constexpr (QM == kQOperand) {
-                    wait_vm<0>();
-#pragma unroll
-                    for (int ks = 0; ks < KS; ks++) qop[ks] = qnext[ks];
-                } else {
-                    make_q(qop, pair);
-                }
+                lds_sync();
+                write_rows(heavy, area_of(st));
+                q_build(qop, pair, area_of(st));
                 m_sh = 0.0f;
                 mneg[0] = (f16)0.0f;
                 first_scores(Sa, r + 1);
-                light_state();
+                zero_acc();
+                thr = -INFINITY;
             }
         }
         lds_sync();
     };
-    // The special rounds: the light tile's q load or prefetch (round min(1, H - 1) or
-    // pf_round) and switch (round H - 1), and the items whose second half crosses a q
-    // tile's first row (key tile kt of q tile qt with 64 kt + 63 > pos + 32 qt, i.e.
-    // kt >= first_masked).
+    // The special rounds: the switch (round H - 1) and the items whose second half
+    // crosses a q tile's first row (key tile kt of q tile qt with 64 kt + 63 > pos +
+    // 32 qt, i.e. kt >= first_masked).
     auto first_masked = [&](uint32_t qtile) -> uint32_t { return (p.pos + qtile * kQRows + 1) / kKTile; };
     const uint32_t mh = min(first_masked(heavy), H), ml = H + first_masked(pair);
-    const uint32_t q_round = QM == kQOperand ? min(1u, H - 1) : pf_round;
     auto next_special = [&](uint32_t r) -> uint32_t {  // the first special round >= r
         uint32_t ns = n_items;
         if (has_light) {
-            ns = r <= q_round ? q_round : r <= H - 1 ? H - 1 : n_items;
+            ns = r <= H - 1 ? H - 1 : n_items;
             ns = min(ns, max(r, ml));
         }
         if (r < H && mh < H) ns = min(ns, max(r, mh));
@@ -809,7 +825,9 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         for (; r < stop; r++) round(r, std::false_type{});
         if (r + 1 < n_items) round(r++, std::true_type{});
     }
-    // the last item: its second half's scores, then nothing ahead
+    // the last item: its second half's scores, then nothing ahead; the rows go through
+    // the stage of item n_items - 2 (every wavefront passed the barrier after it, and
+    // nothing refills it; with one item, stage 3, never filled)
     {
         const uint32_t r = n_items - 1, st = k_stage(r);
         mask_if_needed(Sa, r, 0);
@@ -817,7 +835,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         mask_if_needed(Sb, r, 1);
         step(Sb, Sa, 1, st, nullptr, nullptr, std::false_type{}, std::false_type{});
     }
-    write_rows();
+    write_rows(has_light ? pair : heavy, area_of(k_stage(n_items + kStages - 2)));
 }
 }  // namespace
 

@@ -15,8 +15,8 @@ Replicated:
   qw3_amd/csrc/k_matmul.hip  the direct-to-LDS loads of matmul_q8_mfma_kernel (x
                              planes, raw Q8_0 rows) and matmul_path's slack rule
   qw3_amd/csrc/k_prefill.hip TilePlan / dma_tile of prefill_attention_kernel (every
-                             direct-to-LDS load of every item), its q-operand and f32 q
-                             loads, the cos/sin rows and the light tile's prefetch
+                             direct-to-LDS load of every item), its staged q-row and
+                             cos/sin-row loads and its output row stores
 """
 import numpy as np
 import pytest
@@ -406,29 +406,30 @@ def check_prefill(pos, T, hq, hkv, D, max_ctx):
                 break
             qt = heavy if sel == 0 else pair
             q0 = qt * P_QROWS
-            # q operand (f16 operand or f32 q): lane (r32, h): row min(q0 + r32, T - 1),
-            # head hq, elements 8h + 16 ks .. + 8; f32 q with its cos/sin row (D floats
-            # of row tc) and the prefetch: line 64 n + lane of the tile, row
-            # min(q0 + line / LPR, T - 1), bytes 128 (line % LPR) of the row
-            tc = np.minimum(q0 + np.arange(32), T - 1)
+            # q rows, staged along rows: kQOperand lane (g, m) reads f16 elements
+            # 8 m + [0, 8) of row min(q0 + RPI it + g, T - 1); f32 q lane (g, m) reads
+            # elements 4 m + [0, 4) and D/2 + 4 m + [0, 4) of that row, and the same of
+            # its cos/sin row (D floats per token)
             lane = np.arange(64)
-            els = (8 * (lane[:, None] // 32) + 16 * np.arange(D // 16)[None, :])[..., None] + np.arange(8)
-            assert els.min() >= 0 and els.max() < D
-            LPR = D * 4 // 128
-            lines = 64 * np.arange(P_QROWS * LPR // 64)[:, None] + lane[None, :]
-            pf_row = np.minimum(q0 + lines // LPR, T - 1)
-            pf_byte = 128 * (lines % LPR)
-            assert (pf_byte + 4).max() <= 4 * D
-            assert (tc * D + D).max() <= T * D and (pf_row * D * 4 + pf_byte + 4).max() <= T * D * 4  # cs rows
-            for hg in range(n_hgroups):
-                for hw in range(P_HEADS):
-                    hin = hg * P_HEADS + hw
-                    for kvh in range(hkv):
-                        hqi = kvh * group + (hin if hin < group else 0)
-                        off = (tc * hq + hqi) * D
-                        assert off.min() >= 0 and (off + D).max() <= T * hq * D
-                        pf = (pf_row * hq + hqi) * D * 4 + pf_byte
-                        assert pf.min() >= 0 and (pf + 4).max() <= T * hq * D * 4
+            for LPR, els in ((D // 8, 8 * (lane % (D // 8))[:, None] + np.arange(8)),
+                             (D // 8, np.concatenate([4 * (lane % (D // 8))[:, None] + np.arange(4),
+                                                      D // 2 + 4 * (lane % (D // 8))[:, None] + np.arange(4)], 1))):
+                RPI = 64 // LPR
+                rows = np.minimum(q0 + (RPI * np.arange(P_QROWS // RPI)[:, None] + lane[None, :] // LPR), T - 1)
+                assert els.min() >= 0 and els.max() < D
+                assert rows.min() >= 0 and (rows * D + D).max() <= T * D  # cos/sin rows
+                for hg in range(n_hgroups):
+                    for hw in range(P_HEADS):
+                        hin = hg * P_HEADS + hw
+                        for kvh in range(hkv):
+                            hqi = kvh * group + (hin if hin < group else 0)
+                            off = (rows * hq + hqi) * D
+                            assert off.min() >= 0 and (off + D).max() <= T * hq * D
+            # output rows: lane l stores row q0 + 8 it + l / 8 (rows past T are skipped),
+            # elements 32 dt + 4 (l % 8) + [0, 4)
+            orow = q0 + 8 * np.arange(P_QROWS // 8)[:, None] + lane[None, :] // 8
+            ocol = 32 * np.arange(D // 32)[:, None] + 4 * (lane % 8)[None, :]
+            assert (ocol + 4).max() <= D and ((orow[orow < T] + 1) * hq * D).max() <= T * hq * D
     for key0, end in calls:
         assert 0 < end <= max_ctx
         for plan in (pk, pv):
