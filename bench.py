@@ -345,6 +345,90 @@ class MoeSweep:
             self.H.moe(self.ctx, a)
 
 
+class DecodeLayerSweep:
+    """One decode token through n_layers whole layers at the Qwen3-30B-A3B shape, in the
+    engine's fused order (forward.zig:322-494; qw3_amd/engine.py fused mode): attn_norm,
+    the attention block (q/k/v projections + the fused step over an 8K f16 cache), Wo
+    and the residual, ffn_norm, the MoE block on the device, the residual. Distinct
+    weights, caches and expert banks per layer (synthetic; the banks are device copies
+    of one random template, 642 MB per layer, 30.8 GB for 48 layers), the residual
+    stream x shared and reset from x0 at the start of each sweep (an 8 KB copy)."""
+
+    def __init__(self, H, ctx, layers=48, hidden=2048, hq=32, hkv=4, d=128, ctx_len=8192, E=128, K=8, ffn=768,
+                 seed=21):
+        self.H, self.ctx, self.layers = H, ctx, layers
+        g = np.random.default_rng(seed)
+        nb = hidden // 32
+        eps, theta = 1e-6, 1e6
+
+        def q8(rows, k, scale):
+            w = g.integers(0, 256, (rows, k // 32, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([scale], np.float16).view(np.uint8)
+            return w.reshape(rows, k // 32 * 34)
+
+        def norm_w(n):
+            return ctx.from_numpy((1 + 0.02 * g.standard_normal(n)).astype(np.float32))
+
+        f4 = 4
+        mk = ctx.createBuffer
+        self.x0 = ctx.from_numpy(g.standard_normal((1, hidden)).astype(np.float32))
+        self.x, self.h, self.h2 = mk(hidden * f4), mk(hidden * f4), mk(hidden * f4)
+        q, k, v = mk(hq * d * f4), mk(hkv * d * f4), mk(hkv * d * f4)
+        attn, self.proj = mk(hq * d * f4), mk(hidden * f4)
+        pos = ctx_len - 1
+        positions = ctx.from_numpy(np.array([pos], np.int32))
+        gu_t, dn_t = ctx.from_numpy(q8(E * ffn, hidden, 0.002)), ctx.from_numpy(q8(E * hidden, ffn, 0.002))
+        gu_bytes, dn_bytes = E * ffn * nb * 34, E * hidden * (ffn // 32) * 34
+        empty = H.Buf(None, 0, 0)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        self.layer_args = []
+        cache_elems = hkv * ctx_len * d
+        for li in range(layers):
+            wq, wk, wv = (ctx.from_numpy(q8(n, hidden, 0.002)) for n in (hq * d, hkv * d, hkv * d))
+            wo = ctx.from_numpy(q8(hidden, hq * d, 0.002))
+            kc, vc = mk(2 * cache_elems), mk(2 * cache_elems)
+            ctx.fill_normal_f16(kc, cache_elems, 1000 + 2 * li)
+            ctx.fill_normal_f16(vc, cache_elems, 1001 + 2 * li)
+            gate, up, down = mk(gu_bytes), mk(gu_bytes), mk(dn_bytes)
+            ctx.copy_device(gate, gu_t, gu_bytes)
+            ctx.copy_device(up, gu_t, gu_bytes)
+            ctx.copy_device(down, dn_t, dn_bytes)
+            router = ctx.from_numpy((0.03 * g.standard_normal((E, hidden))).astype(np.float32))
+            an, fn, qn, kn = norm_w(hidden), norm_w(hidden), norm_w(d), norm_w(d)
+            step = H.AttentionStepArgs(q, k, v, qn, kn, positions, kc, vc, attn, H.DTYPE_F16, pos, 1, hq, hkv, d,
+                                       ctx_len, eps, theta, 1.0, scale)
+            self.layer_args.append((
+                H.RmsNormArgs(self.x, an, self.h, 1, hidden, eps),
+                H.AttentionBlockArgs(self.h, wq, wk, wv, H.DTYPE_Q8_0, hidden, step),
+                H.MatmulAddArgs(attn, wo, H.DTYPE_Q8_0, self.x, self.x, 1, hidden, hq * d),
+                H.RmsNormArgs(self.x, fn, self.h2, 1, hidden, eps),
+                H.MoeArgs(self.h2, router, H.DTYPE_F32, gate, up, down, H.DTYPE_Q8_0, self.proj, empty, empty, 1,
+                          hidden, ffn, E, K, 1),
+                H.AddArgs(self.x, self.proj, self.x, hidden)))
+        del gu_t, dn_t
+        self.hidden = hidden
+        self.marks = False
+
+    def layer(self, a):
+        H, ctx = self.H, self.ctx
+        H.rmsNorm(ctx, a[0])
+        H.attentionBlock(ctx, a[1])
+        H.matmulAdd(ctx, a[2])
+        H.rmsNorm(ctx, a[3])
+        ctx.zero(self.proj, self.hidden * 4)
+        H.moe(ctx, a[4])
+        H.add(ctx, a[5])
+
+    def sweep(self):
+        self.ctx.copy_device(self.x, self.x0, self.hidden * 4)
+        if self.marks:
+            self.ctx.timing_mark()
+        for a in self.layer_args:
+            self.layer(a)
+            if self.marks:
+                self.ctx.timing_mark()
+
+
 class ProjPrefill:
     """The q/k/v projections of a 2048-token prefill (forward.zig:337-339 at m = T):
     x [T, hidden] f32 . W^T for wq [n_q_heads*d, hidden], wk and wv [n_kv_heads*d,
@@ -643,11 +727,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time per cycled decode leg (C0, C1)")
     ap.add_argument("--leg-seconds", type=float, default=0.5,
                     help="minimum device time of each secondary timed leg (graph replays / eager kernel timing)")
-    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,QKVP,BLK",
+    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,LAYER,QKVP,BLK",
                     help="comma list of legs: C0-C4 (BASELINE configs; C1 is the headline), FLOOR (launch and "
                          "bare-read floors), SIX (C1 through the six separate ops), QKV / QKVP (decode / prefill "
-                         "q/k/v projections), WO (output projection + residual), MOE (decode MoE block), BLK (prefill "
-                         "attention block: projections + step, fused vs the two calls)")
+                         "q/k/v projections), WO (output projection + residual), MOE (decode MoE block), LAYER (48 whole "
+                         "decode layers in the engine's fused order), BLK (prefill attention block: projections + "
+                         "step, fused vs the two calls)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -980,6 +1065,43 @@ def main():
                   "device (ds5_hip_moe)")
         log(f"[bench] MOE {us:.3f} us/layer ({w.bytes_per_layer / (us * 1e3):.1f} GB/s); kernels "
             + ", ".join(f"{k} {v:.2f} us" for k, v in per.items()))
+        del w
+
+    if "LAYER" in only:
+        log("[bench] LAYER: one decode token through 48 whole layers, Qwen3-30B-A3B shape, fused engine order")
+        w = DecodeLayerSweep(H, ctx)
+        stepsl = max(5, args.steps // 4)
+        elapsed, _ = time_graph(ctx, w, stepsl, 2)
+        us = elapsed / (w.layers * stepsl) * 1e6
+        # per-layer device time of eager sweeps (the engine's timing marks)
+        w.marks = True
+        ctx.timing_begin()
+        for _ in range(3):
+            w.sweep()
+        ns = np.array(ctx.timing_read(), np.float64)
+        w.marks = False
+        ns = ns[[i for i in range(len(ns)) if (i + 1) % (w.layers + 1) != 0]] / 1e3  # drop the gaps between sweeps
+        names = ("rms_norm_rows_kernel", "matmul_rows_kernel", "decode_split_kernel", "decode_merge_kernel",
+                 "router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel",
+                 "add_kernel", "zero_words_kernel")
+        ks = kernel_stats(ctx, w, names, leg)
+        n_layer_runs = max(1, ks["decode_split_kernel"][1])  # one split launch per layer
+        per_layer = {k: round(ks[k][0] * ks[k][1] / n_layer_runs / 1e3, 3) for k in names if ks[k][1]}
+        parts = {"qkv_projection_decode": "us_per_layer", "wo_projection_residual_decode": "us_per_layer",
+                 "moe_block_decode": "us_per_layer"}
+        part_us = {k: extra[k][f] for k, f in parts.items() if k in extra}
+        if "C1" in configs:
+            part_us["attention_step_C1"] = configs["C1"]["gpu"]["us_per_layer"]
+        extra["decode_layer"] = dict(
+            us_per_layer=round(us, 3), layers=w.layers, steps=stepsl,
+            eager_us_per_layer=dict(mean=round(float(ns.mean()), 3), min=round(float(ns.min()), 3),
+                                    max=round(float(ns.max()), 3)),
+            separate_legs_us=part_us, separate_legs_sum_us=round(sum(part_us.values()), 3) if len(part_us) == 4 else None,
+            kernel_us_per_layer=per_layer, kernel_sum_us_per_layer=round(sum(per_layer.values()), 3),
+            shape="1 token, hidden 2048, 32q/4kv d128, 8K f16 cache, Q8_0 wq/wk/wv/wo, 128 experts top 8 ffn 768; "
+                  "attn_norm, attention block, Wo + residual, ffn_norm, MoE, residual (7 calls per layer)")
+        log(f"[bench] LAYER {us:.3f} us/layer (graph of 48 layers); eager per-layer marks mean {ns.mean():.3f} "
+            f"min {ns.min():.3f} max {ns.max():.3f} us; separate legs {part_us}; kernels per layer {per_layer}")
         del w
 
     if "QKVP" in only:

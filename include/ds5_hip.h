@@ -106,6 +106,21 @@ void* ds5_hip_stream(ds5_hip_ctx* ctx);
 int ds5_hip_set_kernel_timing(ds5_hip_ctx* ctx, int enable);
 int ds5_hip_kernel_time(ds5_hip_ctx* ctx, const char* kernel, uint64_t* launches, double* total_ns);
 
+/* Device-time marks for per-layer timing of a forward pass: the reference's
+ * beginTiming / layerNs / endTiming (src/kernels/gpu/kernels.zig:442-472),
+ * written to run metadata as gpu_ns_per_layer_boundary (src/main.zig:420-444).
+ * timing_begin forgets earlier marks; timing_mark records an event on the
+ * context stream (enqueued work before it is timed, nothing synchronises;
+ * ShapeMismatch while the stream is capturing); timing_read synchronises and
+ * writes the device nanoseconds between consecutive marks -- count = marks - 1
+ * values, at most max of them. The engine marks before its first layer and
+ * after every layer, so value i is layer i's device time (the reference's
+ * boundary batch also spans the previous layer's post-router work, because its
+ * router syncs the host mid-layer; here nothing does). */
+int ds5_hip_timing_begin(ds5_hip_ctx* ctx);
+int ds5_hip_timing_mark(ds5_hip_ctx* ctx);
+int ds5_hip_timing_read(ds5_hip_ctx* ctx, uint64_t* ns, uint32_t max, uint32_t* count);
+
 /* Stream capture into a replayable HIP graph (no reference counterpart; the
  * Metal glue batches a layer's dispatches into one command buffer,
  * kernels/gpu/kernels.zig:112-119). Ops called between capture_begin and

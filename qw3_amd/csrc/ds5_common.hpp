@@ -75,6 +75,9 @@ struct ds5_hip_ctx {
     };
     std::vector<Pending> pending;
     std::map<std::string, std::pair<double, uint64_t>> kernel_ns;  // name -> (total ns, launches)
+    // Device-time marks (ds5_hip_timing_*): events recorded on the stream, reused.
+    std::vector<hipEvent_t> marks;
+    size_t marks_used = 0;
 };
 
 // Per-kernel timing: a pooled event pair per launch, resolved at submit / query time.

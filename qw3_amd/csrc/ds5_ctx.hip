@@ -135,6 +135,7 @@ void ds5_hip_deinit(ds5_hip_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (void* p : ctx->owned) (void)hipFree(p);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->marks) (void)hipEventDestroy(e);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
     if (ctx->ev_begin) (void)hipEventDestroy(ctx->ev_begin);
     if (ctx->ev_end) (void)hipEventDestroy(ctx->ev_end);
@@ -246,6 +247,45 @@ int ds5_hip_graph_launch(ds5_hip_ctx* ctx, void* graph_exec) {
 
 void ds5_hip_graph_destroy(void* graph_exec) {
     if (graph_exec) (void)hipGraphExecDestroy((hipGraphExec_t)graph_exec);
+}
+
+int ds5_hip_timing_begin(ds5_hip_ctx* ctx) {
+    if (!ctx) return DS5_DEVICE_FAILURE;
+    ctx->marks_used = 0;
+    return DS5_OK;
+}
+
+int ds5_hip_timing_mark(ds5_hip_ctx* ctx) {
+    if (!ctx) return DS5_DEVICE_FAILURE;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    int rc = ds5_hip_status(ctx, hipStreamIsCapturing(ctx->stream, &cs), "hipStreamIsCapturing");
+    if (rc) return rc;
+    if (cs != hipStreamCaptureStatusNone) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "timing_mark: the stream is capturing");
+    if (ctx->marks_used == ctx->marks.size()) {
+        hipEvent_t e = nullptr;
+        rc = ds5_hip_status(ctx, hipEventCreate(&e), "hipEventCreate");
+        if (rc) return rc;
+        ctx->marks.push_back(e);
+    }
+    rc = ds5_hip_status(ctx, hipEventRecord(ctx->marks[ctx->marks_used], ctx->stream), "hipEventRecord");
+    if (!rc) ctx->marks_used++;
+    return rc;
+}
+
+int ds5_hip_timing_read(ds5_hip_ctx* ctx, uint64_t* ns, uint32_t max, uint32_t* count) {
+    if (!ctx || !count || (max && !ns)) return DS5_SHAPE_MISMATCH;
+    *count = 0;
+    int rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "timing sync");
+    if (rc) return rc;
+    const size_t n = ctx->marks_used > 1 ? ctx->marks_used - 1 : 0;
+    for (size_t i = 0; i < n && i < max; i++) {
+        float ms = 0.0f;
+        rc = ds5_hip_status(ctx, hipEventElapsedTime(&ms, ctx->marks[i], ctx->marks[i + 1]), "hipEventElapsedTime");
+        if (rc) return rc;
+        ns[i] = (uint64_t)((double)ms * 1.0e6);
+    }
+    *count = (uint32_t)n;
+    return DS5_OK;
 }
 
 int ds5_hip_set_kernel_timing(ds5_hip_ctx* ctx, int enable) {

@@ -25,19 +25,22 @@ constexpr int kNormTile = 4096;    // floats of a block's rows staged in LDS (ro
 
 // Rows of at most kNormTile elements: R = kNormTile / dim rows per block (at
 // most 64). The block loads its R rows (contiguous in memory) with every load
-// in flight into LDS at a row stride of dim + 1 floats; thread r then adds row
-// r's squares in element order -- the reference's serial sum, each square
-// rounded on its own -- reading one LDS word per step (the stride puts the R
-// rows' words in distinct banks); then the block writes (v * inv) * w.
+// in flight, and stages each element's square (rounded on its own, as the
+// reference's acc += v * v rounds the product) in LDS at a row stride of
+// dim + 4 floats: rows start on 16-byte boundaries, 4 banks apart. Thread r then
+// adds row r's squares in element order -- the reference's serial sum -- reading
+// four at a time with the reads running ahead of the dependent adds (one LDS word
+// per dependent step had made a 2048-wide row take ~25 us); then the block writes
+// (v * inv) * w.
 __global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float* x, const float* __restrict__ w,
                                                                      float* out, uint32_t n_rows, uint32_t dim,
                                                                      uint32_t rows_per_block, float eps) {
-    __shared__ float s_x[kNormTile + 64];
+    __shared__ __attribute__((aligned(16))) float s_sq[kNormTile + 4 * 64];
     __shared__ float s_inv[64];
     const uint32_t row0 = blockIdx.x * rows_per_block;
     const uint32_t nr = min(rows_per_block, n_rows - row0);
     const uint32_t n = nr * dim;
-    const uint32_t stride = dim + 1;
+    const uint32_t stride = dim + 4;
     const float* src = x + (uint64_t)row0 * dim;
     constexpr int kPer = kNormTile / kNormThreads;  // elements per thread
     float v[kPer];
@@ -49,16 +52,50 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float
 #pragma unroll
     for (int k = 0; k < kPer; k++) {
         const uint32_t i = threadIdx.x + k * kNormThreads;
-        if (i < n) s_x[(i / dim) * stride + i % dim] = v[k];
+        if (i < n) s_sq[(i / dim) * stride + i % dim] = v[k] * v[k];
     }
     __syncthreads();
     if (threadIdx.x < nr) {
-        const float* row = s_x + threadIdx.x * stride;
+        const float* row = s_sq + threadIdx.x * stride;
         float sumsq = 0.0f;
-        for (uint32_t j = 0; j < dim; j++) {
-            const float e = row[j];
-            sumsq += e * e;
+        // 32 squares per batch in two alternating register sets: a batch's reads are
+        // issued before the previous batch's adds (the scheduling fences keep them
+        // there), so the dependent chain never waits for LDS
+        constexpr int B = 8;  // float4 per batch
+        const uint32_t nb = dim / (4 * B), db = nb * 4 * B;
+        float4 ba[B], bb[B];
+        auto rd = [&](float4(&d)[B], uint32_t batch) {
+#pragma unroll
+            for (int b = 0; b < B; b++) d[b] = *(const float4*)(row + 4 * B * batch + 4 * b);
+        };
+        auto add = [&](const float4(&d)[B]) {
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                sumsq += d[b].x;
+                sumsq += d[b].y;
+                sumsq += d[b].z;
+                sumsq += d[b].w;
+            }
+        };
+        // pairs of batches, every read unconditional (a read under a branch makes the
+        // compiler's wait at the join count it as outstanding on both paths)
+        const uint32_t np = nb / 2;
+        if (np) rd(ba, 0);
+        for (uint32_t i = 0; i < np; i++) {
+            rd(bb, 2 * i + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            add(ba);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(ba, min(2 * i + 2, 2 * np - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add(bb);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if (nb & 1) {
+            rd(ba, nb - 1);
+            add(ba);
+        }
+        for (uint32_t j = db; j < dim; j++) sumsq += row[j];
         s_inv[threadIdx.x] = rms_inv(sumsq, (float)dim, eps);
     }
     __syncthreads();

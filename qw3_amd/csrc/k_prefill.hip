@@ -437,40 +437,57 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // of an unfilled group read clamped, valid rows: their scores stay in their own
     // columns of S and O and are never written.
     f16x8 qop[KS];
-    auto q_build = [&](f16x8(&dst)[KS], uint32_t qtile, char* area) {
+    // q_load issues every load of a q tile's rows (q, then with kQRaw the cos/sin rows
+    // and the norm weights); q_form builds the operand from them, so that the switch
+    // can issue the light tile's loads before it writes the heavy tile's rows.
+    constexpr int QLPR = D / 8, QRPI = 64 / QLPR, QNIT = kQRows / QRPI;  // lanes per row, rows per load, loads
+    struct QRows {
+        f16x8 v[QNIT];                         // kQOperand
+        float4 a[QNIT], b[QNIT], c[QNIT], sn[QNIT];  // f32 q: pairs 4 m + [0, 4) and D/2 + 4 m + [0, 4)
+        float4 w0, w1;
+    };
+    auto q_load = [&](QRows& in, uint32_t qtile) {
         const uint32_t q0 = qtile * kQRows, lane = lane_here();
+        const uint32_t m = lane % QLPR, g = lane / QLPR;
         auto row_of = [&](uint32_t row) -> uint64_t {
             return (uint64_t)min(q0 + row, p.n_tokens - 1) * p.n_q_heads + hq;
         };
         if constexpr (QM == kQOperand) {
-            constexpr int LPR = D / 8, RPI = 64 / LPR, NIT = kQRows / RPI;
-            const uint32_t m = lane % LPR, g = lane / LPR;
-            f16x8 v[NIT];
 #pragma unroll
-            for (int it = 0; it < NIT; it++) v[it] = *(const f16x8*)(p.q16 + row_of(RPI * it + g) * D + 8 * m);
-#pragma unroll
-            for (int it = 0; it < NIT; it++) *(f16x8*)(area + (RPI * it + g) * QSTR + 16 * m) = v[it];
+            for (int it = 0; it < QNIT; it++) in.v[it] = *(const f16x8*)(p.q16 + row_of(QRPI * it + g) * D + 8 * m);
         } else {
-            constexpr int HALF = D / 2, LPR = D / 8, RPI = 64 / LPR, NIT = kQRows / RPI;
-            const uint32_t m = lane % LPR, g = lane / LPR;
-            float4 a[NIT], b[NIT], c[NIT], sn[NIT];
 #pragma unroll
-            for (int it = 0; it < NIT; it++) {
-                const float* qr = p.q + row_of(RPI * it + g) * D;
-                a[it] = *(const float4*)(qr + 4 * m);
-                b[it] = *(const float4*)(qr + HALF + 4 * m);
+            for (int it = 0; it < QNIT; it++) {
+                const float* qr = p.q + row_of(QRPI * it + g) * D;
+                in.a[it] = *(const float4*)(qr + 4 * m);
+                in.b[it] = *(const float4*)(qr + D / 2 + 4 * m);
             }
-            float4 w0 = {}, w1 = {};
-            float inv[NIT];
             if constexpr (QM == kQRaw) {
 #pragma unroll
-                for (int it = 0; it < NIT; it++) {
-                    const float* cr = p.cs + (uint64_t)min(q0 + RPI * it + g, p.n_tokens - 1) * D;
-                    c[it] = *(const float4*)(cr + 4 * m);
-                    sn[it] = *(const float4*)(cr + HALF + 4 * m);
+                for (int it = 0; it < QNIT; it++) {
+                    const float* cr = p.cs + (uint64_t)min(q0 + QRPI * it + g, p.n_tokens - 1) * D;
+                    in.c[it] = *(const float4*)(cr + 4 * m);
+                    in.sn[it] = *(const float4*)(cr + D / 2 + 4 * m);
                 }
-                w0 = *(const float4*)(p.q_norm + 4 * m);
-                w1 = *(const float4*)(p.q_norm + HALF + 4 * m);
+                in.w0 = *(const float4*)(p.q_norm + 4 * m);
+                in.w1 = *(const float4*)(p.q_norm + D / 2 + 4 * m);
+            }
+        }
+    };
+    auto q_form = [&](f16x8(&dst)[KS], const QRows& in, char* area) {
+        const uint32_t lane = lane_here();
+        if constexpr (QM == kQOperand) {
+            constexpr int LPR = QLPR, RPI = QRPI, NIT = QNIT;
+            const uint32_t m = lane % LPR, g = lane / LPR;
+#pragma unroll
+            for (int it = 0; it < NIT; it++) *(f16x8*)(area + (RPI * it + g) * QSTR + 16 * m) = in.v[it];
+        } else {
+            constexpr int LPR = QLPR, RPI = QRPI, NIT = QNIT;
+            const uint32_t m = lane % LPR, g = lane / LPR;
+            const float4 *a = in.a, *b = in.b, *c = in.c, *sn = in.sn;
+            const float4 w0 = in.w0, w1 = in.w1;
+            float inv[NIT];
+            if constexpr (QM == kQRaw) {
                 // chunk sums: lane 2c adds its 4 pairs from 0, lane 2c + 1 continues from
                 // lane 2c's partial (DPP row_shr:1 within the 16-lane row)
                 float tot[NIT];
@@ -766,7 +783,11 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // streams items 0 .. kAhead - 1 into the others meanwhile and fills this one only
     // after the barrier); the scores of item 0's first half and their row max.
     f32x16 Sa, Sb;  // scores of the current item's first and second half
-    q_build(qop, heavy, area_of(k_stage(kAhead)));
+    {
+        QRows in;
+        q_load(in, heavy);
+        q_form(qop, in, area_of(k_stage(kAhead)));
+    }
     lds_sync();
     first_scores(Sa, 0);
     zero_acc();
@@ -781,7 +802,8 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // tile's operand (nine wasted products: a step without next scores there, in a
     // branch of its own, made the compiler spill); a barrier (the producer takes it too)
     // frees item r's stage, which is refilled only in round r + 1; there the heavy
-    // tile's rows are written and the light tile's operand is staged; item r + 1's
+    // tile's rows are written and the light tile's operand is staged (its loads issued
+    // before the barrier, so that their latency overlaps the row stores); item r + 1's
     // first scores are formed again as in the prologue, from reference 0 -- the same
     // arithmetic in every q mode, so the modes give the same outputs from the same
     // operand.
@@ -794,9 +816,11 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         step(Sb, Sa, 1, st, kptr(st1, 0), kptr(st1, 1), std::true_type{}, std::true_type{});
         if constexpr (SPECIAL) {
             if (r + 1 == H) {  // the heavy tile is done: its rows, then the light tile's
+                QRows in;
+                q_load(in, pair);
                 lds_sync();
                 write_rows(heavy, area_of(st));
-                q_build(qop, pair, area_of(st));
+                q_form(qop, in, area_of(st));
                 m_sh = 0.0f;
                 mneg[0] = (f16)0.0f;
                 first_scores(Sa, r + 1);

@@ -94,6 +94,36 @@ class Engine:
         self.zeros = np.zeros(max_batch * hidden, np.float32)
         self.pos = 0
         self.trace = None  # trace(layer, op, numpy array) at forward.zig's trace points
+        self.timing = False
+
+    def begin_timing(self) -> None:
+        """kernels/gpu/kernels.zig:446-449 beginTiming: forward passes from now on mark
+        the device time of every layer."""
+        self.ctx.timing_begin()
+        self.timing = True
+
+    def layer_ns(self) -> list[int]:
+        """kernels/gpu/kernels.zig:465-467 layerNs: the device ns of each layer of the
+        forward passes since begin_timing, in order (run metadata's
+        gpu_ns_per_layer_boundary, main.zig:420-444). Every layer is bracketed by marks
+        on the stream, so entry i is exactly layer i's device time; the reference's
+        boundary batch also spans the previous layer's post-router work, because its
+        router syncs mid-layer. Synchronises."""
+        ns = self.ctx.timing_read()
+        # marks: before each pass's first layer and after each layer; a pass's first
+        # interval after the previous pass's last mark spans the host gap between passes
+        n_layers = self.cfg["n_layers"]
+        per_pass = n_layers + 1
+        out = []
+        for i, v in enumerate(ns):
+            if (i + 1) % per_pass != 0:
+                out.append(v)
+        return out
+
+    def end_timing(self) -> None:
+        """kernels/gpu/kernels.zig:469-473 endTiming."""
+        self.timing = False
+        self.ctx.timing_begin()
 
     def reset(self) -> None:
         """forward.zig:288-290."""
@@ -132,6 +162,8 @@ class Engine:
         self._trace(-1, "embed", self.x, n * hidden)
         ctx.upload(self.positions, 0, np.arange(self.pos, self.pos + n, dtype=np.int32))
 
+        if self.timing:
+            ctx.timing_mark()
         for li in range(c["n_layers"]):
             attn_norm, _ = self.w.layer(li, "attn_norm.weight")
             H.rmsNorm(ctx, H.RmsNormArgs(self.x, attn_norm, self.h, n, hidden, eps))
@@ -214,6 +246,8 @@ class Engine:
                                   c["expert_ffn_dim"], c["n_experts"])
             self._trace(li, "experts", self.proj, n * hidden)
             H.add(ctx, H.AddArgs(self.x, self.proj, self.x, n * hidden))
+            if self.timing:
+                ctx.timing_mark()
             self._trace(li, "block", self.x, n * hidden)
 
         out_norm = self.w.buf["output_norm.weight"]

@@ -194,6 +194,9 @@ SIGNATURES = {
     "ds5_hip_capture_end": ([_P, C.POINTER(C.c_void_p)], C.c_int),
     "ds5_hip_graph_launch": ([_P, C.c_void_p], C.c_int),
     "ds5_hip_graph_destroy": ([C.c_void_p], None),
+    "ds5_hip_timing_begin": ([_P], C.c_int),
+    "ds5_hip_timing_mark": ([_P], C.c_int),
+    "ds5_hip_timing_read": ([_P, C.POINTER(C.c_uint64), C.c_uint32, C.POINTER(C.c_uint32)], C.c_int),
     "ds5_hip_set_kernel_timing": ([_P, C.c_int], C.c_int),
     "ds5_hip_kernel_time": ([_P, C.c_char_p, C.POINTER(C.c_uint64), C.POINTER(C.c_double)], C.c_int),
     "ds5_hip_rms_norm": ([_P, C.POINTER(RmsNormArgs)], C.c_int),
@@ -334,6 +337,21 @@ class Ctx:
             rc = LIB.ds5_hip_capture_end(self._h, C.byref(g))
         self.check(rc)
         return Graph(self, g)
+
+    def timing_begin(self) -> None:
+        """Forget earlier device-time marks (kernels/gpu/kernels.zig:446-449 beginTiming)."""
+        self.check(LIB.ds5_hip_timing_begin(self._h))
+
+    def timing_mark(self) -> None:
+        """Record a device-time mark on the stream (no synchronisation)."""
+        self.check(LIB.ds5_hip_timing_mark(self._h))
+
+    def timing_read(self, max_count: int = 4096) -> list[int]:
+        """Device ns between consecutive marks (synchronises; kernels.zig:465-467 layerNs)."""
+        buf = (C.c_uint64 * max(1, max_count))()
+        n = C.c_uint32()
+        self.check(LIB.ds5_hip_timing_read(self._h, buf, max_count, C.byref(n)))
+        return [int(buf[i]) for i in range(min(n.value, max_count))]
 
     def set_kernel_timing(self, enable: bool) -> None:
         self.check(LIB.ds5_hip_set_kernel_timing(self._h, int(enable)))

@@ -139,3 +139,96 @@ def test_engine_rejections(ctx, hip, weights):
     with pytest.raises(ValueError, match="ContextOverflow"):
         eng.forward([3])
     assert eng.pos == 2
+
+
+def test_layer_timing(ctx, hip, model, weights):
+    """Per-layer device time of forward passes (kernels/gpu/kernels.zig:442-472
+    beginTiming / layerNs, written by main.zig:420-444 as gpu_ns_per_layer_boundary):
+    a prefill and a decode step give one positive value per layer each, and they add up
+    to no more than the passes' wall time."""
+    import time
+    from qw3_amd import engine as E
+    cfg, _, prompts = model
+    eng = _engine(ctx, hip, weights, "f16", True)
+    eng.begin_timing()
+    t0 = time.perf_counter()
+    logits = eng.forward(prompts[0]["token_ids"])
+    eng.forward([E.argmax(logits[-1])])
+    wall_ns = (time.perf_counter() - t0) * 1e9
+    ns = eng.layer_ns()
+    print(f"[engine] layer ns: {ns}", flush=True)
+    assert len(ns) == 2 * cfg["n_layers"]
+    assert all(v > 0 for v in ns)
+    assert sum(ns) <= wall_ns
+    eng.end_timing()
+    eng.forward([1])
+    assert eng.layer_ns() == []
+
+
+def _q8_rows(g, rows, k, scale):
+    w = g.integers(0, 256, (rows, k // 32, 34), dtype=np.uint8)
+    w[:, :, 0:2] = np.array([scale], np.float16).view(np.uint8)
+    return w.reshape(rows, k // 32 * 34)
+
+
+def _d128_model():
+    """A two-layer synthetic model with head_dim 128 (Qwen3's) and Q8_0 weights, so a
+    prefill of 16 tokens or more takes the attention block's GEMM-epilogue path."""
+    cfg = dict(n_layers=2, hidden_dim=256, n_q_heads=4, n_kv_heads=2, head_dim=128, n_experts=4, top_k=2,
+               expert_ffn_dim=128, vocab_size=256, rms_eps=1e-6, rope_theta=1e6, norm_topk_prob=True, max_ctx=64)
+    g = np.random.default_rng(31)
+    hid, hd, ffn, E = cfg["hidden_dim"], cfg["head_dim"], cfg["expert_ffn_dim"], cfg["n_experts"]
+    w = {"token_embd.weight": _q8_rows(g, cfg["vocab_size"], hid, 0.02),
+         "output_norm.weight": (1 + 0.02 * g.standard_normal(hid)).astype(np.float32),
+         "output.weight": _q8_rows(g, cfg["vocab_size"], hid, 0.002)}
+    for li in range(cfg["n_layers"]):
+        b = f"blk.{li}."
+        w[b + "attn_norm.weight"] = (1 + 0.02 * g.standard_normal(hid)).astype(np.float32)
+        w[b + "attn_q.weight"] = _q8_rows(g, cfg["n_q_heads"] * hd, hid, 0.002)
+        w[b + "attn_k.weight"] = _q8_rows(g, cfg["n_kv_heads"] * hd, hid, 0.002)
+        w[b + "attn_v.weight"] = _q8_rows(g, cfg["n_kv_heads"] * hd, hid, 0.002)
+        w[b + "attn_q_norm.weight"] = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+        w[b + "attn_k_norm.weight"] = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+        w[b + "attn_output.weight"] = _q8_rows(g, hid, cfg["n_q_heads"] * hd, 0.002)
+        w[b + "ffn_norm.weight"] = (1 + 0.02 * g.standard_normal(hid)).astype(np.float32)
+        w[b + "ffn_gate_inp.weight"] = (0.03 * g.standard_normal((E, hid))).astype(np.float32)
+        w[b + "ffn_gate_exps.weight"] = _q8_rows(g, E * ffn, hid, 0.002)
+        w[b + "ffn_up_exps.weight"] = _q8_rows(g, E * ffn, hid, 0.002)
+        w[b + "ffn_down_exps.weight"] = _q8_rows(g, E * hid, ffn, 0.002)
+    return cfg, w
+
+
+def test_attention_block_inside_engine_d128(ctx, hip):
+    """The fused engine at head_dim 128: a 20-token prefill runs the q/k/v projections'
+    GEMM with the pre-pass in its epilogue (attentionBlock), then two decode steps at
+    pos > 0. With a trace callback the same engine runs matmulGroup then attentionStep
+    instead; the ABI says the two are equal bit for bit, so logits and every cache row
+    must be."""
+    from qw3_amd import engine as E
+    cfg, w = _d128_model()
+    wts = E.Weights(ctx, w, cfg)
+    toks = [int(t) for t in np.random.default_rng(3).integers(0, cfg["vocab_size"], 20)]
+    engines = [E.Engine(ctx, wts, max_batch=32, context_capacity=32, kv_dtype=hip.DTYPE_F16, fused=True)
+               for _ in range(2)]
+    engines[1].trace = lambda layer, op, a: None
+    outs = []
+    for i, eng in enumerate(engines):
+        ctx.set_kernel_timing(True)
+        got = [eng.forward(toks)]
+        launches = {k: ctx.kernel_time(k)[0] for k in ("matmul_q8_mfma_kernel", "prefill_prep_kernel")}
+        ctx.set_kernel_timing(False)
+        print(f"[engine] d128 engine {i}: prefill launches {launches}", flush=True)
+        if i == 0:  # the block's fused path: the GEMM epilogue, no pre-pass kernel
+            assert launches["matmul_q8_mfma_kernel"] >= cfg["n_layers"] and launches["prefill_prep_kernel"] == 0
+        else:
+            assert launches["prefill_prep_kernel"] == cfg["n_layers"]
+        for t in (5, 9):
+            got.append(eng.forward([t]))
+        caches = [ctx.to_numpy(b, np.uint16) for b in eng.k_cache + eng.v_cache]
+        outs.append((got, caches))
+    (ga, ca), (gb, cb) = outs
+    for a, b in zip(ga, gb):
+        assert np.isfinite(a).all()
+        assert np.array_equal(a, b)
+    for a, b in zip(ca, cb):
+        assert np.array_equal(a, b)
