@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "ds5_hip.h"
+#include "ds5_index.hpp"
 
 // ---------------------------------------------------------------------------
 // Vector types (clang ext_vector_type: what the MFMA builtins take)

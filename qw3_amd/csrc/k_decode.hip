@@ -44,12 +44,12 @@
 
 namespace {
 
-constexpr int kTile = 32;   // positions per wavefront tile
-constexpr int kWaves = 4;   // wavefronts per workgroup (one per SIMD)
+constexpr int kTile = ds5idx::kDecTile;    // positions per wavefront tile
+constexpr int kWaves = ds5idx::kDecWaves;  // wavefronts per workgroup (one per SIMD)
 constexpr int kThreads = kWaves * 64;
-constexpr int kHeads = 16;  // q heads per workgroup (the MFMA N dimension)
-constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (p <= 2^8 between rescales)
-constexpr uint32_t kMaxSplits = 64;   // splits per sequence at most
+constexpr int kHeads = ds5idx::kDecHeads;  // q heads per workgroup (the MFMA N dimension)
+constexpr float kRescaleLog2 = 8.0f;       // lazy-rescale threshold (p <= 2^8 between rescales)
+constexpr uint32_t kMaxSplits = ds5idx::kDecMaxSplits;  // splits per sequence at most
 constexpr uint32_t kPlanMaxSeqs = 4096;  // paged plan: lengths staged in the V staging area
 
 struct DecodeParams {
@@ -124,10 +124,8 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_byte_ptr) {
 // Page of sequence b holding position pos; out-of-range entries read page 0
 // and raise `bad` (the workgroup then poisons its output).
 __device__ __forceinline__ uint64_t page_base(const DecodeParams& p, uint32_t b, uint32_t pos, bool& bad) {
-    const int32_t pg = p.page_table[(uint64_t)b * p.max_pages + pos / p.page_size];
-    const bool ok = (uint32_t)pg < p.n_pages;
-    bad |= !ok;
-    return (uint64_t)(ok ? pg : 0) * p.page_size;
+    const int32_t pg = p.page_table[ds5idx::dec_page_index(b, p.max_pages, pos, p.page_size)];
+    return ds5idx::dec_page_first(pg, p.n_pages, p.page_size, bad);
 }
 
 // Issues the K/V loads of tile [p0, p0 + 32) of a split ending at `end`.
@@ -142,19 +140,19 @@ __device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p
     uint64_t rowA = 0, rowB = 0;  // paged: first slot of each 16-position half-tile
     if constexpr (PAGED) {
         // page_size is a multiple of 16 and p0 a multiple of 32: each half is inside one page
-        const uint32_t posB = min(p0 + 16, end - 1);
-        rowA = page_base(p, b, p0, bad) + p0 % p.page_size;
-        rowB = page_base(p, b, posB, bad) + (p0 + 16) % p.page_size;
+        // (half 1's page is the one holding min(p0 + 16, end - 1), its offset that of p0 + 16)
+        rowA = page_base(p, b, ds5idx::dec_half_pos(p0, end, 0), bad) + p0 % p.page_size;
+        rowB = page_base(p, b, ds5idx::dec_half_pos(p0, end, 1), bad) + (p0 + 16) % p.page_size;
     }
 #pragma unroll
     for (int st = 0; st < 2; st++) {
         uint64_t row;
         if constexpr (PAGED)
-            row = (st ? rowB : rowA) + c16;
+            row = ds5idx::dec_k_row_paged(rowA, rowB, st, c16);
         else
-            row = min((uint32_t)(p0 + 16 * st + c16), end - 1);
+            row = ds5idx::dec_k_row(p0, end, st, c16);
 #pragma unroll
-        for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = ld16<!PAGED>(kbase + row * D + kk * 32 + 8 * g);
+        for (int kk = 0; kk < G::KK; kk++) T.k[st][kk] = ld16<!PAGED>(kbase + row * D + ds5idx::dec_k_col(kk, g));
     }
 #pragma unroll
     for (int r = 0; r < G::VC; r++) {
@@ -162,10 +160,10 @@ __device__ __forceinline__ void issue_tile(TileRegs<D>& T, const DecodeParams& p
         const int tr = c / G::RC;  // row within the tile
         uint64_t row;
         if constexpr (PAGED)
-            row = (r < G::VC / 2 ? rowA : rowB) + (tr & 15);
+            row = ds5idx::dec_v_row_paged(rowA, rowB, r, G::VC, tr);
         else
-            row = min((uint32_t)(p0 + tr), end - 1);
-        T.v[r] = ld16<true>(vbase + row * D + (c % G::RC) * 8);
+            row = ds5idx::dec_v_row(p0, end, tr);
+        T.v[r] = ld16<true>(vbase + row * D + ds5idx::dec_v_col(c, G::RC));
     }
 }
 
@@ -372,7 +370,6 @@ struct PagedItem {
     uint32_t split, chunk;
 };
 
-__device__ __forceinline__ uint32_t plan_items(uint32_t len, uint32_t c) { return len == 0 ? 1u : (len + c - 1) / c; }
 
 // s_len: n_seqs words of LDS; s_red: kThreads / 64 + 2 words
 __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_len, uint32_t* s_red) {
@@ -381,8 +378,7 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t n = p.n_seqs;
     for (uint32_t i = tid; i < n; i += kThreads) {
-        const int32_t len = p.seq_lens[i];
-        s_len[i] = (len < 1 || (uint32_t)len > p.max_len) ? 0u : (uint32_t)len;
+        s_len[i] = ds5idx::plan_len(p.seq_lens[i], p.max_len);
     }
     __syncthreads();
     // thread t owns sequences [b0, b1)
@@ -390,7 +386,7 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     const uint32_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
     auto count = [&](uint32_t c) {
         uint32_t k = 0;
-        for (uint32_t i = b0; i < b1; i++) k += plan_items(s_len[i], c);
+        for (uint32_t i = b0; i < b1; i++) k += ds5idx::plan_items(s_len[i], c);
         return k;
     };
     auto block_sum = [&](uint32_t v) {
@@ -406,8 +402,8 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     };
     // binary search over c = cmin + kStep k: the count does not grow with c, and
     // c = max_len (rounded up) gives one item per sequence, which the cap admits
-    const uint32_t cmin = max(kStep, (p.max_len + kMaxSplits - 1) / kMaxSplits + kStep - 1) / kStep * kStep;
-    uint32_t lo = 0, hi = ((p.max_len + kStep - 1) / kStep * kStep - min(cmin, (p.max_len + kStep - 1) / kStep * kStep)) / kStep;
+    const uint32_t cmin = ds5idx::plan_cmin(p.max_len, kStep, kMaxSplits), cmax = ds5idx::plan_cmax(p.max_len, kStep);
+    uint32_t lo = 0, hi = (cmax - min(cmin, cmax)) / kStep;
     while (lo < hi) {  // uniform
         const uint32_t mid = (lo + hi) / 2;
         if (block_sum(count(cmin + kStep * mid)) <= p.plan_cap)
@@ -423,9 +419,8 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     // owner of item x.
     uint32_t mf = 0, mt = 0;
     for (uint32_t i = b0; i < b1; i++) {
-        const uint32_t L = s_len[i];
-        mf += L / chunk;
-        mt += (L == 0 || L % chunk != 0) ? 1u : 0u;
+        mf += ds5idx::plan_whole(s_len[i], chunk);
+        mt += ds5idx::plan_partial(s_len[i], chunk);
     }
     auto block_scan = [&](uint32_t v, uint32_t& total) {
         uint32_t incl = v;
@@ -453,7 +448,7 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     if (x < F && x >= ef && x < ef + mf) {  // whole chunk
         uint32_t acc = ef;
         for (uint32_t i = b0; i < b1; i++) {
-            const uint32_t k = s_len[i] / chunk;
+            const uint32_t k = ds5idx::plan_whole(s_len[i], chunk);
             if (x < acc + k) {
                 s_red[NW] = i;
                 s_red[NW + 1] = x - acc;
@@ -464,11 +459,10 @@ __device__ PagedItem paged_plan(const DecodeParams& p, uint32_t x, uint32_t* s_l
     } else if (x >= F && x - F >= et && x - F < et + mt) {  // partial last chunk
         uint32_t acc = et;
         for (uint32_t i = b0; i < b1; i++) {
-            const uint32_t L = s_len[i];
-            if (L == 0 || L % chunk != 0) {
+            if (ds5idx::plan_partial(s_len[i], chunk)) {
                 if (x - F == acc) {
                     s_red[NW] = i;
-                    s_red[NW + 1] = L / chunk;
+                    s_red[NW + 1] = ds5idx::plan_whole(s_len[i], chunk);
                     break;
                 }
                 acc++;
@@ -967,17 +961,9 @@ int launch_decode_d(ds5_hip_ctx* ctx, const DecodeLaunch& a, const DecodeParams&
 // kMaxSplits splits (bounds the partials).
 static DecodeGeometry decode_geometry_of(const ds5_hip_ctx* ctx, uint32_t n_seqs, uint32_t n_kv_heads, uint32_t n_sub,
                                          uint32_t max_len) {
-    constexpr uint32_t kStep = kWaves * kTile;
-    uint32_t chunk = ctx->decode_chunk;
-    if (chunk == 0) {
-        const uint64_t units = (uint64_t)n_seqs * n_kv_heads * n_sub;
-        const uint64_t target = 4ull * (ctx->cu_count > 0 ? ctx->cu_count : 256);
-        chunk = (uint32_t)std::min<uint64_t>((max_len * units + target - 1) / target, max_len);
-    }
-    chunk = std::max<uint32_t>((chunk + kStep - 1) / kStep * kStep, kStep);
-    chunk = std::max<uint32_t>(chunk, (max_len + kMaxSplits - 1) / kMaxSplits);
-    chunk = (chunk + kStep - 1) / kStep * kStep;
-    return DecodeGeometry{chunk, (max_len + chunk - 1) / chunk};
+    DecodeGeometry g{};
+    ds5idx::dec_geometry(ctx->cu_count, ctx->decode_chunk, n_seqs, n_kv_heads, n_sub, max_len, g.chunk, g.n_splits);
+    return g;
 }
 
 // The workspace a launch requests for n_part partial rows: O and (m, l) per row,

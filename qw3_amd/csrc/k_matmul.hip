@@ -421,9 +421,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     uint32_t xoff[NX];  // byte offset in the plane: row min(m0 + r, m - 1), chunk c, block 0
 #pragma unroll
     for (int i = 0; i < NX; i++) {
-        const uint32_t o = 1024u * (wave_u + W * i) + 16u * lane;
-        const uint32_t r = (o % (BM * 64)) / 64, c = (uint32_t)(lane & 3) ^ ((r >> 2) & 3);
-        xoff[i] = min(m0 + r, m - 1) * k * 2 + 16 * c;
+        xoff[i] = ds5idx::gemm_x_off(1024u * (wave_u + W * i) + 16u * lane, (uint32_t)lane, BM, m0, m, k);
     }
     auto issue_x = [&](uint32_t b, int stage) {
 #pragma unroll
@@ -446,12 +444,9 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     uint32_t qoff_e[NQ], qoff_o[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
-        const uint32_t d = min(64u * i + lane, (uint32_t)(kWRows * kRowDw - 1));
-        const uint32_t lr = d / kRowDw;
-        const uint32_t row = 16 * wave_u + (kThreads / 4) * (lr / 16) + lr % 16;
-        const uint32_t rb = min(n0 + row, n - 1) * (uint32_t)row_bytes;
-        qoff_e[i] = (rb & ~3u) + 4 * (d % kRowDw);
-        qoff_o[i] = ((rb + 2) & ~3u) + 4 * (d % kRowDw);
+        const uint32_t d = ds5idx::gemm_q_dword(i, (uint32_t)lane, kWRows, kRowDw);
+        const uint32_t row = ds5idx::gemm_q_row(d, wave_u, kThreads, kRowDw);
+        ds5idx::gemm_q_off(d, row, n0, n, (uint32_t)row_bytes, kRowDw, qoff_e[i], qoff_o[i]);
     }
     const uint32_t q_lds = smem_lds + 3 * kXStage + wave_u * kQWave;
     auto issue_q = [&](uint32_t b, int stage) {

@@ -158,10 +158,10 @@ __global__ __launch_bounds__(kPrepThreads) void prefill_prep_kernel(KvPrepLaunch
 // ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
-constexpr int kHeads = 4;      // q heads per workgroup, one compute wavefront each
+constexpr int kHeads = ds5idx::kPfHeads;  // q heads per workgroup, one compute wavefront each
 constexpr int kThreads = (kHeads + 1) * 64;  // + the producer wavefront
-constexpr int kQRows = 32;     // q rows per wavefront tile (MFMA N)
-constexpr int kKTile = 64;     // keys per LDS stage
+constexpr int kQRows = ds5idx::kPfQRows;  // q rows per wavefront tile (MFMA N)
+constexpr int kKTile = ds5idx::kPfKTile;  // keys per LDS stage
 constexpr int kStages = 4;     // K/V ring: a stage is refilled three rounds ahead of its use
 constexpr int kAhead = kStages - 1;
 constexpr int kOpAhead = 4;    // LDS operand reads in flight ahead of their product
@@ -199,8 +199,8 @@ struct PGeo {
     // is 1 (mod 16) chunks; the V transpose read puts 4 consecutive rows x 4
     // adjacent chunks in a cycle, so the V stride is 4 (mod 16) chunks. Every
     // read address is then a per-lane base plus an immediate.
-    static constexpr int RSK = RB + 16;
-    static constexpr int RSV = RB + 64;
+    static constexpr int RSK = ds5idx::pf_rsk(D);
+    static constexpr int RSV = ds5idx::pf_rsv(D);
     static constexpr int KSTAGE = kKTile * RSK;    // bytes of K per stage
     static constexpr int VSTAGE = kKTile * RSV;    // bytes of V per stage
     static constexpr int STAGE = KSTAGE + VSTAGE;
@@ -260,11 +260,7 @@ struct TilePlan {
     uint32_t off[NB];
     __device__ __forceinline__ explicit TilePlan(int lane) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const int pos = 1024 * b + 16 * lane;
-            const int r = pos / RS, c = (pos % RS) / 16;
-            off[b] = (uint32_t)(r * 2 * D + (c < D / 8 ? 16 * c : 0));
-        }
+        for (int b = 0; b < NB; b++) off[b] = ds5idx::pf_tile_off(b, lane, D, RS);
     }
 };
 
@@ -297,11 +293,10 @@ __device__ __forceinline__ void dma_tile(uint32_t stage_lds, const f16* base, ui
                          : "m0");
         }
     } else {
-        const uint32_t last_row = kv_end - key0 - 1;  // rows of this tile below kv_end, minus one
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const uint32_t lds = __builtin_amdgcn_readfirstlane(stage_lds + 1024 * b);
-            const uint32_t off = min(tp.off[b] / (2 * D), last_row) * (2 * D) + tp.off[b] % (2 * D);
+            const uint32_t off = ds5idx::pf_clamped_off(tp.off[b], key0, kv_end, D);
             asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(tile), "s"(lds)
                          : "m0");
         }
@@ -450,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
         const uint32_t q0 = qtile * kQRows, lane = lane_here();
         const uint32_t m = lane % QLPR, g = lane / QLPR;
         auto row_of = [&](uint32_t row) -> uint64_t {
-            return (uint64_t)min(q0 + row, p.n_tokens - 1) * p.n_q_heads + hq;
+            return (uint64_t)ds5idx::pf_q_token(q0, row, p.n_tokens) * p.n_q_heads + hq;
         };
         if constexpr (QM == kQOperand) {
 #pragma unroll
@@ -465,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             if constexpr (QM == kQRaw) {
 #pragma unroll
                 for (int it = 0; it < QNIT; it++) {
-                    const float* cr = p.cs + (uint64_t)min(q0 + QRPI * it + g, p.n_tokens - 1) * D;
+                    const float* cr = p.cs + (uint64_t)ds5idx::pf_q_token(q0, QRPI * it + g, p.n_tokens) * D;
                     in.c[it] = *(const float4*)(cr + 4 * m);
                     in.sn[it] = *(const float4*)(cr + D / 2 + 4 * m);
                 }
