@@ -424,6 +424,30 @@ def test_paged_decode_large_batch_unplanned(ctx, hip, oracle):
     _paged_case(ctx, hip, oracle, 4100, 1, 40, seed=9, check_seqs=[0, 1, 777, 2048, 4095, 4096, 4099])
 
 
+def test_paged_decode_large_batch_unplanned_splits(hip, oracle):
+    """The unplanned grid with several splits: 4100 sequences of 1..300 positions with
+    the split size fixed at 128 (DS5_HIP_DECODE_CHUNK, read when a context starts), so
+    sequences of at most 128 positions have one split whose workgroup writes the output
+    itself, and longer ones two or three splits that the merge combines, in the same
+    launch. A sample of both kinds against the oracle."""
+    import os
+    os.environ["DS5_HIP_DECODE_CHUNK"] = "128"
+    try:
+        c = hip.Ctx.init(0)
+    finally:
+        del os.environ["DS5_HIP_DECODE_CHUNK"]
+    try:
+        lay = synth.paged_layout(4100, 1, 300, 16, seed=21)
+        lens = lay.seq_lens
+        short = [int(b) for b in np.nonzero(lens <= 128)[0][:4]]
+        long_ = [int(b) for b in np.nonzero(lens > 256)[0][:4]] + [int(b) for b in np.nonzero((lens > 128) & (lens <= 256))[0][:2]]
+        assert len(short) == 4 and len(long_) == 6
+        print(f"[paged] unplanned splits: short {short}, long {long_}", flush=True)
+        _paged_case(c, hip, oracle, 4100, 1, 300, seed=21, check_seqs=short + long_ + [4099])
+    finally:
+        c.deinit()
+
+
 def test_paged_decode_invalid_entries(ctx, hip, oracle):
     """Device-side entries the host cannot check: a page id outside the pool and
     sequence lengths outside [1, max_seq_len] are never dereferenced; those
