@@ -164,7 +164,7 @@ constexpr int kQRows = ds5idx::kPfQRows;  // q rows per wavefront tile (MFMA N)
 constexpr int kKTile = ds5idx::kPfKTile;  // keys per LDS stage
 constexpr int kStages = 4;     // K/V ring: a stage is refilled three rounds ahead of its use
 constexpr int kAhead = kStages - 1;
-constexpr int kOpAhead = 4;    // LDS operand reads in flight ahead of their product
+constexpr int kOpAhead = 5;    // LDS operand reads in flight ahead of their product
 constexpr float kRescaleLog2 = 8.0f;
 
 // Where the attention kernel's q operand comes from:
