@@ -934,14 +934,23 @@ def main():
             el, _ = time_graph(ctx, fw, max(5, args.steps), 2)
             fl[mode] = round(el / (fw.layers * max(5, args.steps)) * 1e6, 3)
             del fw
+        for mode in ("read", "both"):  # C3's K+V per layer: 2 x 4 kv heads x 32768 x 128 f16 = 64 MiB
+            fw = FloorSweep(H, ctx, layers=47, nbytes=64 << 20, mode=mode)
+            el, _ = time_graph(ctx, fw, max(5, args.steps // 4), 2)
+            fl[mode + "64"] = round(el / (fw.layers * max(5, args.steps // 4)) * 1e6, 3)
+            del fw
         extra["floors"] = dict(
             empty_launch_us=fl["empty"], read_16MiB_us=fl["read"], read_plus_empty_us=fl["both"],
             read_16MiB_gbs=round((16 << 20) / (fl["read"] * 1e3), 1),
+            read_64MiB_us=fl["read64"], read_64MiB_plus_empty_us=fl["both64"],
+            read_64MiB_gbs=round((64 << 20) / (fl["read64"] * 1e3), 1),
             note="per layer in a 48-layer graph: one dependent launch of an empty kernel; one launch reading a "
                  "distinct 16 MiB buffer once (C1's K+V per layer) with the decode's 16-byte non-temporal loads; "
-                 "both (the split + merge launch count)")
+                 "both (the split + merge launch count); the same for 64 MiB (C3's K+V per layer) in a 47-layer "
+                 "graph")
         log(f"[bench] floors: empty launch {fl['empty']:.3f} us, 16 MiB read {fl['read']:.3f} us, "
-            f"read + empty {fl['both']:.3f} us per layer")
+            f"read + empty {fl['both']:.3f} us per layer; 64 MiB read {fl['read64']:.3f} us, read + empty "
+            f"{fl['both64']:.3f} us per layer")
 
     if 0 in W and "C0" in only:
         w = W[0]

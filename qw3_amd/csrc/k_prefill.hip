@@ -40,10 +40,11 @@
 // kernel builds its q operand from the raw f32 q when it loads a q tile: q
 // normalised, rotated with that table, times softmax scale * log2(e), rounded to
 // f16 (each (q tile, head) is loaded by one workgroup, so q is read once, as f32,
-// and never written back). The separate-op path hands it q already normalised and
-// rotated, which it only scales. The attention block's projection GEMM writes a
-// ready f16 operand in its epilogue (k_matmul.hip) with the same arithmetic, so
-// all three give the same outputs from the same projections.
+// and never written back). The attention block's projection GEMM writes a ready
+// f16 operand in its epilogue (k_matmul.hip) with the same arithmetic, so the
+// fused step and the attention block give the same outputs from the same
+// projections. The separate-op path hands the kernel q already normalised (by
+// the serial-order rmsNorm) and rotated, which it only scales.
 #include <type_traits>
 
 #include "ds5_common.hpp"
