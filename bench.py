@@ -1094,8 +1094,8 @@ def main():
         ns = np.array(ctx.timing_read(), np.float64)
         w.marks = False
         ns = ns[[i for i in range(len(ns)) if (i + 1) % (w.layers + 1) != 0]] / 1e3  # drop the gaps between sweeps
-        names = ("rms_norm_rows_kernel", "matmul_rows_kernel", "decode_split_kernel", "decode_merge_kernel",
-                 "router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel",
+        names = ("rms_norm_tree_kernel", "rms_norm_rows_kernel", "matmul_rows_kernel", "decode_split_kernel",
+                 "decode_merge_kernel", "router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel",
                  "add_kernel", "zero_words_kernel")
         ks = kernel_stats(ctx, w, names, leg)
         n_layer_runs = max(1, ks["decode_split_kernel"][1])  # one split launch per layer

@@ -139,7 +139,10 @@ void ds5_hip_graph_destroy(void* graph_exec);
 
 /* contracts.zig:218-225 RmsNormArgs. y = x * (1/sqrt(mean(x^2) + eps)) * w
  * rowwise; `out` may alias `x`. Replaces kernels_a.zig:68-91 rmsNorm and the
- * Metal rmsnorm_f32 dispatch (kernels/gpu/kernels.zig:146-157). */
+ * Metal rmsnorm_f32 dispatch (kernels/gpu/kernels.zig:146-157). Rows of up to
+ * 256 elements sum their squares in the CPU path's serial order; longer rows in
+ * the Metal kernel's order (kernels/shaders/kernels_a.metal:127-165: 256
+ * strided fma partials, then a halving tree). */
 typedef struct ds5_rms_norm_args {
     ds5_buf x;      /* f32 [n_rows, dim] */
     ds5_buf weight; /* f32 [dim] */

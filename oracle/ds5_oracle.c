@@ -358,6 +358,42 @@ int ds5o_rms_norm(const ds5o_rms_norm_args* a) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* rmsNorm, the reference GPU kernel's order -- kernels_a.metal:127-165       */
+/* (rmsnorm_f32, RMSNORM_TG = 256 threads per row): thread t accumulates      */
+/* s = fma(x[i], x[i], s) over i = t, t + 256, ...; partial[t] += partial[t + */
+/* stride] for stride = 128 .. 1; inv = 1 / sqrt(partial[0] / dim + eps);    */
+/* out[i] = x[i] * inv * w[i]. The same preconditions as ds5o_rms_norm.       */
+/* ------------------------------------------------------------------------ */
+
+int ds5o_rms_norm_tree(const ds5o_rms_norm_args* a) {
+    enum { TG = 256 };
+    const uint64_t n_rows = a->n_rows, dim = a->dim;
+    if (dim == 0) return DS5O_SHAPE_MISMATCH;
+    if (a->x.len < n_rows * dim * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->out.len < n_rows * dim * 4) return DS5O_SHAPE_MISMATCH;
+    if (a->weight.len < dim * 4) return DS5O_SHAPE_MISMATCH;
+
+    const float* x = (const float*)view(a->x);
+    const float* w = (const float*)view(a->weight);
+    float* out = (float*)view(a->out);
+    float partial[TG];
+    for (uint64_t r = 0; r < n_rows; r++) {
+        const float* xr = x + r * dim;
+        float* orow = out + r * dim;
+        for (uint64_t t = 0; t < TG; t++) {
+            float s = 0.0f;
+            for (uint64_t i = t; i < dim; i += TG) s = fmaf(xr[i], xr[i], s);
+            partial[t] = s;
+        }
+        for (uint64_t stride = TG / 2; stride > 0; stride >>= 1)
+            for (uint64_t t = 0; t < stride; t++) partial[t] += partial[t + stride];
+        const float inv = 1.0f / sqrtf(partial[0] / (float)dim + a->eps);
+        for (uint64_t i = 0; i < dim; i++) orow[i] = xr[i] * inv * w[i];
+    }
+    return DS5O_OK;
+}
+
+/* ------------------------------------------------------------------------ */
 /* rope -- kernels_a.zig:97-130 (NeoX pairing i <-> i + head_dim/2)          */
 /* ------------------------------------------------------------------------ */
 

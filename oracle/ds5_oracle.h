@@ -10,6 +10,9 @@
  * -ffp-contract=off, so a*b+c is never fused, like Zig's strict float mode):
  *
  *   ds5o_rms_norm       src/kernels/cpu/kernels_a.zig:68-91
+ *   ds5o_rms_norm_tree  src/kernels/shaders/kernels_a.metal:127-165 (the
+ *                       reference GPU kernel's reduction order, 256 fma
+ *                       partials and a halving tree)
  *   ds5o_rope           src/kernels/cpu/kernels_a.zig:97-130
  *   ds5o_kv_append      src/kernels/cpu/kernels_a.zig:169-217
  *   ds5o_gqa_attention  src/kernels/cpu/kernels_b.zig:29-133
@@ -126,6 +129,7 @@ typedef struct ds5o_expert_mlp_args { /* contracts.zig:319-331 ExpertMlpArgs */
 } ds5o_expert_mlp_args;
 int ds5o_expert_mlp_swiglu(const ds5o_expert_mlp_args* a);
 int ds5o_rms_norm(const ds5o_rms_norm_args* a);
+int ds5o_rms_norm_tree(const ds5o_rms_norm_args* a);
 int ds5o_rope(const ds5o_rope_args* a);
 int ds5o_kv_append(const ds5o_kv_append_args* a);
 int ds5o_gqa_attention(const ds5o_attn_args* a);

@@ -114,7 +114,8 @@ def lib() -> C.CDLL:
             spec.loader.exec_module(mod)
             mod.build()
         L = C.CDLL(LIB_PATH)
-        for name, argt in (("ds5o_rms_norm", RmsNormArgs), ("ds5o_rope", RopeArgs),
+        for name, argt in (("ds5o_rms_norm", RmsNormArgs), ("ds5o_rms_norm_tree", RmsNormArgs),
+                           ("ds5o_rope", RopeArgs),
                            ("ds5o_kv_append", KvAppendArgs), ("ds5o_gqa_attention", AttnArgs),
                            ("ds5o_attention_step", StepArgs), ("ds5o_matmul", MatmulArgs),
                            ("ds5o_add", AddArgs), ("ds5o_router_topk", RouterArgs),
@@ -245,6 +246,24 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float, n_rows: int | None = None
     out = np.empty_like(x) if out is None else out
     _check(lib().ds5o_rms_norm(RmsNormArgs(buf(x), buf(w), buf(out), n_rows, dim, eps)))
     return out
+
+
+def rms_norm_tree(x: np.ndarray, w: np.ndarray, eps: float, n_rows: int | None = None,
+                  dim: int | None = None, out: np.ndarray | None = None) -> np.ndarray:
+    """rmsNorm in the reference GPU kernel's reduction order (kernels_a.metal:127-165)."""
+    dim = w.size if dim is None else dim
+    n_rows = x.size // dim if n_rows is None else n_rows
+    out = np.empty_like(x) if out is None else out
+    _check(lib().ds5o_rms_norm_tree(RmsNormArgs(buf(x), buf(w), buf(out), n_rows, dim, eps)))
+    return out
+
+
+def rms_norm_device_order(x: np.ndarray, w: np.ndarray, eps: float, n_rows: int | None = None,
+                          dim: int | None = None) -> np.ndarray:
+    """The order ds5_hip_rms_norm uses: serial for rows of up to 256 elements, the
+    GPU kernel's tree for longer rows."""
+    dim = w.size if dim is None else dim
+    return (rms_norm if dim <= 256 else rms_norm_tree)(x, w, eps, n_rows, dim)
 
 
 def rope(x: np.ndarray, positions: np.ndarray, theta: float, freq_scale: float = 1.0,

@@ -3,7 +3,7 @@
 // Each entry point checks the reference's preconditions, in the reference's
 // order, before anything is enqueued (the GPU kernels have no error channel,
 // as PORTING-kernels-a.md / -b.md require of the Metal glue), then dispatches:
-//   rmsNorm       kernels_a.zig:68-91   -> rms_norm_kernel
+//   rmsNorm       kernels_a.zig:68-91   -> rms_norm_rows_kernel (rows <= 256), rms_norm_tree_kernel
 //   rope          kernels_a.zig:97-130  -> rope_kernel
 //   kvAppend      kernels_a.zig:169-217 -> kv_append_kernel
 //   gqaAttention  kernels_b.zig:29-133  -> decode_split_kernel (+ merge),

@@ -1,10 +1,13 @@
 // k_norm_rope.hip -- rmsNorm, rope and kvAppend on gfx950 (the separate ops).
 //
-// Arithmetic follows the reference CPU path operation for operation so that
-// results are bit-exact where the operations are IEEE-exact:
-//   rmsNorm  kernels_a.zig:84-89: sumsq is a serial f32 sum in element order,
-//            inv = 1/sqrt(sumsq/dim + eps) (correctly rounded div and sqrt),
-//            o = (v*inv)*w -- one thread owns a row for the sum.
+// Arithmetic follows the reference operation for operation so that results are
+// bit-exact where the operations are IEEE-exact:
+//   rmsNorm  kernels_a.zig:84-89 for rows of up to 256 elements: sumsq is a
+//            serial f32 sum in element order, inv = 1/sqrt(sumsq/dim + eps)
+//            (correctly rounded div and sqrt), o = (v*inv)*w -- one thread owns
+//            a row for the sum. Longer rows: the reference GPU kernel's order
+//            (kernels_a.metal:127-165), 256 strided fma partials and a halving
+//            tree, then the same inv and o.
 //   rope     kernels_a.zig:117-126: angle = (pos*freq_scale)*inv_freq[i] with
 //            the host-built inv_freq table (std.math.pow(f32) evaluation);
 //            x0' = x0*c - x1*s, x1' = x0*s + x1*c, never fused into fma.
@@ -18,13 +21,15 @@
 
 namespace {
 
-constexpr int kRowsPerBlock = 64;  // large-dim kernel: one wavefront, one row per lane
-constexpr int kColTile = 64;
 constexpr int kNormThreads = 256;
-constexpr int kNormTile = 4096;    // floats of a block's rows staged in LDS (rows of up to 4096 elements)
+constexpr int kNormTile = 4096;  // floats of a block's rows staged in LDS
+// Rows of at most kSerialMaxDim elements (the per-head q/k norms) take the
+// reference CPU path's serial sum; longer rows (the hidden-state norms) the
+// reference GPU kernel's reduction order (rms_norm_tree_kernel).
+constexpr uint32_t kSerialMaxDim = 256;
 
-// Rows of at most kNormTile elements: R = kNormTile / dim rows per block (at
-// most 64). The block loads its R rows (contiguous in memory) with every load
+// Rows of at most kSerialMaxDim elements: R = min(64, kNormTile / dim) rows per
+// block. The block loads its R rows (contiguous in memory) with every load
 // in flight, and stages each element's square (rounded on its own, as the
 // reference's acc += v * v rounds the product) in LDS at a row stride of
 // dim + 4 floats: rows start on 16-byte boundaries, 4 banks apart. Thread r then
@@ -111,51 +116,52 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float
     }
 }
 
-// Rows longer than kNormTile: one row per lane, the row's columns staged in
-// tiles transposed through LDS so global reads stay coalesced.
-__device__ void rows_sumsq(const float* __restrict__ x, uint32_t row0, uint32_t n_rows, uint32_t dim,
-                           float (*tile)[kColTile + 1], float* sumsq_out) {
-    const int lane = threadIdx.x;
-    float sumsq = 0.0f;
-    for (uint32_t c0 = 0; c0 < dim; c0 += kColTile) {
-        const uint32_t ncol = min((uint32_t)kColTile, dim - c0);
-        for (int r = 0; r < kRowsPerBlock; r++) {
-            const uint32_t row = row0 + r;
-            float v = 0.0f;
-            if (row < n_rows && (uint32_t)lane < ncol) v = x[(uint64_t)row * dim + c0 + lane];
-            tile[r][lane] = v;
+// Rows of more than kSerialMaxDim elements: the reduction order of the reference's
+// GPU kernel (kernels_a.metal:127-165), whose serial CPU sum is latency-bound on a
+// long row (a 2048-wide row took ~12.6 us as a chain of dependent adds). One
+// workgroup of 256 threads per row: thread t accumulates the squares of elements
+// t, t + 256, t + 512, ... with fused multiply-adds, then the 256 partials add in
+// a halving tree, partial[t] += partial[t + s] for s = 128, 64, ..., 1 (the two
+// strides that cross wavefronts through LDS, the rest by lane shifts within
+// wavefront 0); inv = 1/sqrt(sum/dim + eps) correctly rounded, o = (v*inv)*w.
+// A thread loads its elements eight at a time, every load of a batch in flight;
+// the batch's last loads may fall past the row and are clamped and zeroed, and
+// fma(0, 0, s) = s for the non-negative s. out may alias x: a thread writes only
+// the elements it read.
+constexpr int kTreeThreads = 256;
+__global__ __launch_bounds__(kTreeThreads) void rms_norm_tree_kernel(const float* x, const float* __restrict__ w,
+                                                                     float* out, uint32_t dim, float eps) {
+    __shared__ float s_part[kTreeThreads];
+    __shared__ float s_inv;
+    constexpr int B = 8;
+    const uint32_t t = threadIdx.x;
+    const float* xr = x + (uint64_t)blockIdx.x * dim;
+    float s = 0.0f;
+    for (uint32_t i0 = t; i0 < dim; i0 += B * kTreeThreads) {
+        float v[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const uint32_t i = i0 + j * kTreeThreads;
+            v[j] = xr[i < dim ? i : dim - 1];
+            v[j] = i < dim ? v[j] : 0.0f;
         }
-        __syncthreads();
-        for (uint32_t j = 0; j < ncol; j++) {
-            const float v = tile[lane][j];
-            sumsq += v * v;
-        }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < B; j++) s = __builtin_fmaf(v[j], v[j], s);
     }
-    *sumsq_out = sumsq;
-}
-
-__global__ __launch_bounds__(kRowsPerBlock) void rms_norm_kernel(const float* x, const float* __restrict__ w,
-                                                                 float* out, uint32_t n_rows, uint32_t dim,
-                                                                 float eps) {
-    __shared__ float tile[kRowsPerBlock][kColTile + 1];
-    __shared__ float s_inv[kRowsPerBlock];
-    const uint32_t row0 = blockIdx.x * kRowsPerBlock;
-    const int lane = threadIdx.x;
-    float sumsq;
-    rows_sumsq(x, row0, n_rows, dim, tile, &sumsq);
-    s_inv[lane] = rms_inv(sumsq, (float)dim, eps);
+    s_part[t] = s;
     __syncthreads();
-    // out may alias x: every element is read before the same thread writes it.
-    for (int r = 0; r < kRowsPerBlock; r++) {
-        const uint32_t row = row0 + r;
-        if (row >= n_rows) break;
-        const float inv = s_inv[r];
-        for (uint32_t c = lane; c < dim; c += kRowsPerBlock) {
-            const uint64_t idx = (uint64_t)row * dim + c;
-            out[idx] = x[idx] * inv * w[c];
-        }
+    if (t < 128) s_part[t] = s + s_part[t + 128];
+    __syncthreads();
+    if (t < 64) {
+        float v = s_part[t] + s_part[t + 64];
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) v += __shfl_down(v, k, 64);
+        if (t == 0) s_inv = rms_inv(v, (float)dim, eps);
     }
+    __syncthreads();
+    const float inv = s_inv;
+    float* orow = out + (uint64_t)blockIdx.x * dim;
+    for (uint32_t i = t; i < dim; i += kTreeThreads) orow[i] = xr[i] * inv * w[i];
 }
 
 // One block per token group: the token's cos/sin (one per pair index, shared by
@@ -232,17 +238,16 @@ inline uint32_t grid_for(uint64_t total, uint32_t block) {
 
 int launch_rms_norm(ds5_hip_ctx* ctx, const RmsNormLaunch& a) {
     if (a.n_rows == 0) return DS5_OK;
-    if (a.dim <= kNormTile) {
+    if (a.dim <= kSerialMaxDim) {
         const uint32_t rpb = std::min<uint32_t>(64, kNormTile / a.dim);
         const uint32_t blocks = (a.n_rows + rpb - 1) / rpb;
         DS5_TIMED_LAUNCH(ctx, "rms_norm_rows_kernel", rms_norm_rows_kernel, dim3(blocks), dim3(kNormThreads), 0,
                          ctx->stream, a.x, a.w, a.out, a.n_rows, a.dim, rpb, a.eps);
         return ds5_after_launch(ctx, "rms_norm_rows_kernel");
     }
-    const uint32_t blocks = (a.n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    DS5_TIMED_LAUNCH(ctx, "rms_norm_kernel", rms_norm_kernel, dim3(blocks), dim3(kRowsPerBlock), 0, ctx->stream, a.x, a.w, a.out,
-                       a.n_rows, a.dim, a.eps);
-    return ds5_after_launch(ctx, "rms_norm_kernel");
+    DS5_TIMED_LAUNCH(ctx, "rms_norm_tree_kernel", rms_norm_tree_kernel, dim3(a.n_rows), dim3(kTreeThreads), 0,
+                     ctx->stream, a.x, a.w, a.out, a.dim, a.eps);
+    return ds5_after_launch(ctx, "rms_norm_tree_kernel");
 }
 
 int launch_rope(ds5_hip_ctx* ctx, const RopeLaunch& a) {

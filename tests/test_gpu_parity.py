@@ -74,6 +74,41 @@ def test_rmsnorm_random_rows_bit_exact(ctx, hip, oracle, dim, scale):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("dim", [257, 300, 512, 1000, 2048, 4096, 5000, 8192])
+def test_rmsnorm_long_rows_tree_order(ctx, hip, oracle, dim):
+    """Rows of more than 256 elements take the reference GPU kernel's reduction order
+    (kernels_a.metal:127-165): bit-identical to the oracle's restatement of it, and within
+    the fixtures' atol 1e-5 / rtol 1e-4 of the serial CPU order (the reference's own note
+    on that kernel). 1, 3 and 67 rows, magnitudes over 8 decades, in place and not."""
+    g = np.random.default_rng(dim)
+    w = (1.0 + 0.02 * g.standard_normal(dim)).astype(np.float32)
+    wb = dev(ctx, w)
+    for n in (1, 3, 67):
+        x = (g.standard_normal((n, dim)) * np.exp(g.uniform(-9, 9, (n, 1)))).astype(np.float32)
+        xb, out = dev(ctx, x), ctx.createBuffer(x.nbytes)
+        hip.rmsNorm(ctx, hip.RmsNormArgs(xb, wb, out, n, dim, 1e-6))
+        got = ctx.to_numpy(out, np.float32, x.shape)
+        want = oracle.rms_norm_tree(x, w, 1e-6, n, dim)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (dim, n)
+        assert oracle.compare(oracle.rms_norm(x, w, 1e-6, n, dim), got, 1e-5, 1e-4).passed, (dim, n)
+        hip.rmsNorm(ctx, hip.RmsNormArgs(xb, wb, xb, n, dim, 1e-6))  # out aliases x
+        assert np.array_equal(host(ctx, xb, x).view(np.uint32), want.view(np.uint32)), (dim, n)
+
+
+def test_rmsnorm_tree_order_special_row(ctx, hip, oracle):
+    """The row whose f32 sum separates the orders (4096 at element 0, ones at elements 1
+    and 3: 2^24 + 2 in the kernel's order, 2^24 serially) gives the oracle's tree result."""
+    dim = 512
+    x = np.zeros((1, dim), np.float32)
+    x[0, 0], x[0, 1], x[0, 3] = 4096.0, 1.0, 1.0
+    w = np.linspace(0.5, 1.5, dim).astype(np.float32)
+    xb = dev(ctx, x)
+    hip.rmsNorm(ctx, hip.RmsNormArgs(xb, dev(ctx, w), xb, 1, dim, 1e-6))
+    got = host(ctx, xb, x)
+    assert np.array_equal(got, oracle.rms_norm_tree(x, w, 1e-6))
+    assert not np.array_equal(got, oracle.rms_norm(x, w, 1e-6))
+
+
 @pytest.mark.parametrize("i", range(3))
 def test_rope_fixtures(ctx, hip, oracle, i):
     c = _cases(oracle, "rope")[i]

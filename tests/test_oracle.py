@@ -301,6 +301,90 @@ def test_rmsnorm_matches_float64(oracle):
     np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-6)
 
 
+# rmsNorm in the reference GPU kernel's order (kernels_a.metal:127-165), the order
+# ds5_hip_rms_norm uses for rows of more than 256 elements.
+
+def _norm_from_sum(x, w, s, eps):
+    """(x * inv) * w with inv = 1 / sqrt(s / dim + eps), each step rounded to f32 (numpy's
+    float32 operations round correctly)."""
+    dim = np.float32(x.size)
+    inv = np.float32(1.0) / np.sqrt(np.float32(s) / dim + np.float32(eps))
+    return (x * inv) * w
+
+
+def test_rmsnorm_tree_reduction_order(oracle):
+    """Rows whose f32 sum depends on the order: 4096^2 = 2^24 absorbs a lone 1 (a tie,
+    rounded to even) but not a 2. With ones at elements 1 and 3, the kernel's order (thread
+    t takes elements t, t + 256, ...; partials halve as p[t] += p[t + s], s = 128 .. 1)
+    adds p[3] into p[1] before p[1] meets p[0]: the sum is 2^24 + 2. The serial order, an
+    adjacent-pair tree and contiguous per-thread chunks each meet the ones one at a time
+    and leave 2^24."""
+    dim, eps = 512, 1e-6
+    x = np.zeros(dim, np.float32)
+    x[0], x[1], x[3] = 4096.0, 1.0, 1.0
+    w = np.linspace(0.5, 1.5, dim).astype(np.float32)
+    got = oracle.rms_norm_tree(x.copy(), w, eps)
+    assert np.array_equal(got, _norm_from_sum(x, w, 2.0 ** 24 + 2, eps))
+    serial = oracle.rms_norm(x.copy(), w, eps)
+    assert np.array_equal(serial, _norm_from_sum(x, w, 2.0 ** 24, eps))
+    assert not np.array_equal(got, serial)
+
+
+def test_rmsnorm_tree_accumulates_with_fma(oracle):
+    """A thread's second element is added with one rounding (s = fma(b, b, a^2)): for
+    rows holding only x[0] = 1 and x[256] = b, the sum is f32(1 + b^2) computed exactly
+    (b^2 has 48 bits, exact in float64), which differs from f32(f32(b^2) + 1) for these b."""
+    dim, eps = 300, 1e-6
+    w = np.ones(dim, np.float32)
+    n = 0
+    for b in np.float32(1.0) + np.arange(1, 4000, dtype=np.float32) * np.float32(2.0 ** -23):
+        fused = np.float32(1.0 + float(b) * float(b))
+        unfused = np.float32(np.float32(b * b) + np.float32(1.0))
+        if fused == unfused:
+            continue
+        x = np.zeros(dim, np.float32)
+        x[0], x[256] = 1.0, b
+        got = oracle.rms_norm_tree(x.copy(), w, eps)
+        assert np.array_equal(got, _norm_from_sum(x, w, fused, eps)), b
+        n += 1
+        if n == 8:
+            break
+    assert n == 8
+
+
+def test_rmsnorm_tree_exact_sums_equal_serial(oracle):
+    """Small-integer rows: every partial sum is an exact integer, so any order gives the
+    same sum; the tree must then equal the serial form bit for bit (no element dropped or
+    counted twice at dims that are not multiples of 256)."""
+    g = np.random.default_rng(17)
+    for dim in (257, 300, 511, 1000, 4097):
+        x = g.integers(-3, 4, (3, dim)).astype(np.float32)
+        w = (1 + 0.02 * g.standard_normal(dim)).astype(np.float32)
+        assert np.array_equal(oracle.rms_norm_tree(x, w, 1e-6), oracle.rms_norm(x, w, 1e-6)), dim
+
+
+def test_rmsnorm_tree_matches_float64(oracle):
+    g = np.random.default_rng(5)
+    for dim in (300, 2048, 4096, 5000):
+        x = (g.standard_normal((5, dim)) * 3).astype(np.float32)
+        w = (1 + 0.02 * g.standard_normal(dim)).astype(np.float32)
+        got = oracle.rms_norm_tree(x, w, 1e-6)
+        xd = x.astype(np.float64)
+        want = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-6) * w
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("i", range(6))
+def test_rmsnorm_tree_within_fixture_tolerance(oracle, i):
+    """The reference's note on its GPU kernel (kernels_a.metal:14-16): the tree order stays
+    inside the fixtures' atol 1e-5 / rtol 1e-4."""
+    c = _cases(oracle, "rmsnorm")[i]
+    p, tol = c["params"], c["tolerance"]
+    x, w, want = (oracle.load_ds5t(f"{FIXTURES}/{c['tensors'][n]}").data for n in ("input", "weight", "output"))
+    got = oracle.rms_norm_tree(x.copy(), w, p["eps"], p["n_rows"], p["dim"])
+    assert oracle.compare(want, got, tol["atol"], tol["rtol"]).passed
+
+
 def test_rope_is_a_rotation(oracle):
     # Norm of every (i, i+d/2) pair is preserved; composing rotations adds angles.
     g = np.random.default_rng(4)
