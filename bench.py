@@ -1095,8 +1095,8 @@ def main():
         w.marks = False
         ns = ns[[i for i in range(len(ns)) if (i + 1) % (w.layers + 1) != 0]] / 1e3  # drop the gaps between sweeps
         names = ("rms_norm_tree_kernel", "rms_norm_rows_kernel", "matmul_rows_kernel", "decode_split_kernel",
-                 "decode_merge_kernel", "router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel", "moe_down_combine_kernel",
-                 "add_kernel", "zero_words_kernel")
+                 "decode_merge_kernel", "router_logits_kernel", "router_select_kernel", "moe_gate_up_kernel",
+                 "moe_down_combine_kernel", "add_kernel", "zero_words_kernel")
         ks = kernel_stats(ctx, w, names, leg)
         n_layer_runs = max(1, ks["decode_split_kernel"][1])  # one split launch per layer
         per_layer = {k: round(ks[k][0] * ks[k][1] / n_layer_runs / 1e3, 3) for k in names if ks[k][1]}
