@@ -318,7 +318,11 @@ int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* args)
  * into out. Equal to ds5_hip_router_topk then ds5_hip_expert_mlp_swiglu on
  * those pairs. Checked as the two calls are (router first); ids / weights,
  * when given (len >= 2 * and 4 * n_tokens * top_k), receive the router's
- * outputs on the device. */
+ * outputs on the device. residual, when given (len >= 4 * n_tokens * dim):
+ * out = residual + the experts' sum, the sum started from zero -- the
+ * engine's zeroed accumulator, the experts into it and add(x, proj -> x) of
+ * forward.zig:445-468, bit for bit, without the accumulator, its clear and the
+ * add launch; out may be residual. */
 typedef struct ds5_moe_args {
     ds5_buf x;                 /* f32 [n_tokens, dim] */
     ds5_buf router_w;          /* router_dtype: n_experts rows of dim */
@@ -336,6 +340,7 @@ typedef struct ds5_moe_args {
     uint32_t n_experts;
     uint32_t top_k;
     uint32_t norm_topk_prob;
+    ds5_buf residual;          /* optional f32 [n_tokens, dim] */
 } ds5_moe_args;
 int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* args);
 

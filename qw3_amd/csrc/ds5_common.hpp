@@ -200,6 +200,7 @@ struct ExpertLaunch {
     const uint32_t* offsets;
     uint32_t top_k;
     float* out;
+    const float* res;  // set: out = res + the experts' sum from zero; null: the sum accumulates into out
     float* h;
     float* y;
     uint32_t n_tokens, n_pairs, dim, ffn;

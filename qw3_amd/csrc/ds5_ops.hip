@@ -407,6 +407,8 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
         return rc;
     if ((a->ids.len && !covers(a->ids, TK * 2)) || (a->weights.len && !covers(a->weights, TK * 4)))
         return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: ids / weights outputs too small");
+    if (a->residual.len && !covers(a->residual, (uint64_t)a->n_tokens * a->dim * 4))
+        return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: residual too small");
     if (a->n_tokens == 0) return DS5_OK;
     if (TK > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: too many pairs");
     if (int rc = set_device(ctx)) return rc;
@@ -421,6 +423,7 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     ExpertLaunch l = expert_launch(a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)TK,
                                    a->dim, a->ffn_dim, a->n_experts, s);
     l.top_k = a->top_k;  // token t's pairs are t * top_k .. (t + 1) * top_k - 1
+    l.res = a->residual.len ? (const float*)ds5_ptr(a->residual) : nullptr;  // every token has top_k >= 1 pairs
     return launch_experts(ctx, l);
 }
 

@@ -491,21 +491,26 @@ constexpr uint32_t kDownRows = 8;
 template <bool Q8>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
     const float* __restrict__ h, const uint8_t* __restrict__ down, const ds5_pair* __restrict__ pairs,
-    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offsets, uint32_t top_k, float* __restrict__ out,
-    uint32_t dim, uint32_t ffn, uint64_t row_f, uint64_t stride) {
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offsets, uint32_t top_k, float* out,
+    const float* res, uint32_t dim, uint32_t ffn, uint64_t row_f, uint64_t stride) {
 #pragma clang fp contract(off)
     // the arguments in one scalar round trip (before the first early exit)
-    asm volatile("" ::"s"(h), "s"(down), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(dim),
-                 "s"(ffn), "s"(row_f), "s"(stride));
+    asm volatile("" ::"s"(h), "s"(down), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(res),
+                 "s"(dim), "s"(ffn), "s"(row_f), "s"(stride));
     __shared__ float ys[kMoeWaves][kDownRows], wts[kMoeWaves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t groups = dim / kDownRows;
     const uint32_t t = blockIdx.x / groups, i0 = (blockIdx.x % groups) * kDownRows;
     const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
-    if (q0 == q1) return;  // no pairs: out stays as it is (workgroup-uniform)
+    const uint64_t o = (uint64_t)t * dim + i0 + threadIdx.x;
+    if (q0 == q1) {  // no pairs (workgroup-uniform): out stays as it is, or residual + 0
+        if (res && threadIdx.x < kDownRows) out[o] = res[o] + 0.0f;
+        return;
+    }
     const uint32_t nb = ffn / 32;
+    // the sum starts from out, or from zero when the residual is added at the end
     float acc = 0.0f;
-    if (threadIdx.x < kDownRows) acc = out[(uint64_t)t * dim + i0 + threadIdx.x];
+    if (!res && threadIdx.x < kDownRows) acc = out[o];
     for (uint32_t qb = q0; qb < q1; qb += kMoeWaves) {
         const uint32_t q = qb + wv;
         if (q < q1) {  // wave-uniform
@@ -568,29 +573,32 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
         }
         __syncthreads();
     }
-    if (threadIdx.x < kDownRows) out[(uint64_t)t * dim + i0 + threadIdx.x] = acc;
+    if (threadIdx.x < kDownRows) out[o] = res ? res[o] + acc : acc;
 }
 
 // out[t][i] += w_p * y[p][i] over token t's pairs in list order: pair q of the
-// token is order[offsets[t] + q] (or t * top_k + q when offsets is null).
+// token is order[offsets[t] + q] (or t * top_k + q when offsets is null). With
+// res: out = res + that sum started from zero.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y,
                                                           const ds5_pair* __restrict__ pairs,
                                                           const uint32_t* __restrict__ order,
                                                           const uint32_t* __restrict__ offsets, uint32_t top_k,
-                                                          float* __restrict__ out, uint32_t n_tokens, uint32_t dim) {
+                                                          float* out, const float* res, uint32_t n_tokens,
+                                                          uint32_t dim) {
 #pragma clang fp contract(off)
     // the arguments in one scalar round trip (before the first early exit)
-    asm volatile("" ::"s"(y), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(n_tokens), "s"(dim));
+    asm volatile("" ::"s"(y), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(res), "s"(n_tokens),
+                 "s"(dim));
     const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (id >= (uint64_t)n_tokens * dim) return;
     const uint32_t t = (uint32_t)(id / dim), i = (uint32_t)(id % dim);
     const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
-    float acc = out[id];
+    float acc = res ? 0.0f : out[id];
     for (uint32_t q = q0; q < q1; q++) {
         const uint32_t p = order ? order[q] : q;
         acc += pairs[p].weight * y[(uint64_t)p * dim + i];
     }
-    out[id] = acc;
+    out[id] = res ? res[id] + acc : acc;
 }
 
 // Serial fallback for banks the GEMV kernels cannot read (a Q8_0 view that is
@@ -717,8 +725,8 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
             }
             if (int rc = ds5_after_launch(ctx, "moe_down_kernel")) return rc;
             DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)),
-                             dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.n_tokens,
-                             a.dim);
+                             dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res,
+                             a.n_tokens, a.dim);
             return ds5_after_launch(ctx, "moe_combine_kernel");
         }
         const dim3 g3((unsigned)(outs / kDownRows));  // dim % 32 == 0 on this path
@@ -727,15 +735,15 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
             DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<true>, g3, blk, 0, ctx->stream,
-                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.dim, a.ffn, a.row_f,
-                             a.stride_d);
+                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.dim, a.ffn,
+                             a.row_f, a.stride_d);
         } else {
             DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<false>, g1, blk, xs_bytes, ctx->stream, a.x, a.gate,
                              a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);
             if (int rc = ds5_after_launch(ctx, "moe_gate_up_kernel")) return rc;
             DS5_TIMED_LAUNCH(ctx, "moe_down_combine_kernel", moe_down_combine_kernel<false>, g3, blk, 0, ctx->stream,
-                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.dim, a.ffn, a.row_f,
-                             a.stride_d);
+                             a.h, a.down, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.dim, a.ffn,
+                             a.row_f, a.stride_d);
         }
         return ds5_after_launch(ctx, "moe_down_combine_kernel");
     } else {
@@ -750,6 +758,6 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     }
     const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
     DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
-                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.n_tokens, a.dim);
+                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.n_tokens, a.dim);
     return ds5_after_launch(ctx, "moe_combine_kernel");
 }

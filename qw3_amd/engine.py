@@ -19,7 +19,10 @@ Two modes:
   are never written in f32; with a trace callback set, the same work as its two
   calls, `matmulGroup` then `attentionStep`, which the block equals bit for bit, so
   the projection trace points exist), Wo and its residual as one `matmulAdd`, and
-  the MoE block as one `moe` (router and experts with the pairs kept on the device).
+  the MoE block and its residual as one `moe` (router and experts with the pairs kept
+  on the device, x + the experts' sum written in the combine; with a trace callback
+  set, `moe` into the zeroed accumulator then `add`, which it equals bit for bit, so
+  the experts trace point exists).
 Both produce the residual stream of forward.zig within the reference's layer
 tolerance; the per-op calls of the fused mode are bit-identical to the separate ones
 where the ABI says so (matmulGroup, matmulAdd, moe).
@@ -224,6 +227,16 @@ class Engine:
             gate, dg = self.w.layer(li, "ffn_gate_exps.weight")
             up, _ = self.w.layer(li, "ffn_up_exps.weight")
             down, _ = self.w.layer(li, "ffn_down_exps.weight")
+            if self.fused and self.trace is None:
+                # x = x + the experts' sum in one call: the sum starts from zero and the
+                # residual is added once, as the zeroed accumulator and the add give it
+                H.moe(ctx, H.MoeArgs(self.h2, router, dr, gate, up, down, dg, self.x, H.Buf(), H.Buf(), n,
+                                     hidden, c["expert_ffn_dim"], c["n_experts"], c["top_k"],
+                                     int(c["norm_topk_prob"]), self.x))
+                if self.timing:
+                    ctx.timing_mark()
+                self._trace(li, "block", self.x, n * hidden)
+                continue
             # proj doubles as the MoE accumulator and must start at zero (forward.zig:452-454):
             # the eight-op mode uploads zeros as the reference does; the fused mode clears it
             # on the device (no host copy or synchronisation inside the layer)

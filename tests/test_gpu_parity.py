@@ -1044,6 +1044,52 @@ def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T, E):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [1, 5, 300])
+def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
+    """ds5_hip_moe with a residual (out = residual + the experts' sum from zero) equals the
+    engine's three calls -- zero the accumulator, ds5_hip_moe into it, ds5_hip_add(x, acc ->
+    x) -- bit for bit, in place (out = residual) and into another buffer; residual values
+    include -0.0 (-0 + 0 = +0 through the add) and large magnitudes. T = 300: the serial
+    banks (a view that is not 4-byte aligned), whose experts run as separate kernels."""
+    g = np.random.default_rng(100 + T)
+    dim, ffn, E, K = (2048, 768, 64, 8) if T < 300 else (256, 64, 8, 2)
+    rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    res = (g.standard_normal((T, dim)) * np.exp(g.uniform(-6, 6, (T, 1)))).astype(np.float32)
+    res[:, :7] = -0.0
+    xb, rwb = ctx.from_numpy(x), ctx.from_numpy(rw)
+    if T < 300:
+        banks = [ctx.from_numpy(v) for v in (G, U, D)]
+    else:  # views one byte into their allocations: the serial kernels
+        banks = []
+        for v in (G, U, D):
+            raw = np.zeros(v.size + 1, np.uint8)
+            raw[1:] = v.reshape(-1)
+            b = ctx.from_numpy(raw)
+            banks.append(hip.Buf(b.handle, b.offset + 1, v.size))
+    empty = hip.Buf()
+    acc, xr = ctx.createBuffer(T * dim * 4), ctx.from_numpy(res)
+    ctx.zero(acc, T * dim * 4)
+    hip.moe(ctx, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, acc, empty, empty, T, dim, ffn, E, K, 1))
+    hip.add(ctx, hip.AddArgs(xr, acc, xr, T * dim))
+    want = ctx.to_numpy(xr, np.float32, (T, dim))
+    inplace = ctx.from_numpy(res)
+    hip.moe(ctx, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, inplace, empty, empty, T, dim, ffn, E,
+                             K, 1, inplace))
+    other, rb = ctx.createBuffer(T * dim * 4), ctx.from_numpy(res)
+    hip.moe(ctx, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, other, empty, empty, T, dim, ffn, E, K,
+                             1, rb))
+    for b in (inplace, other):
+        got = ctx.to_numpy(b, np.float32, (T, dim))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(ctx.to_numpy(rb, np.float32, (T, dim)).view(np.uint32), res.view(np.uint32))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.moe(ctx, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, other, empty, empty, T, dim, ffn, E,
+                                 K, 1, hip.Buf(rb.handle, rb.offset, T * dim * 4 - 4)))
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):
