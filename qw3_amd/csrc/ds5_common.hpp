@@ -440,15 +440,24 @@ DS5_DEVICE_INLINE float rms_inv(float sumsq, float dim, float eps) {
 }
 
 // The q/k arithmetic of a prefill step, shared by every kernel that produces the
-// cache rows and the attention q operand (the pre-pass and the projection GEMM's
-// epilogue), each operation rounded on its own so they agree bit for bit:
+// cache rows and the attention q operand (the pre-pass, the attention kernel and
+// the projection GEMM's epilogue), each operation rounded on its own so they
+// agree bit for bit:
+//   k rows, the reference's operations (the cache is compared row for row):
 //   qk_serial_sumsq: sum of squares in element order (kernels_a.zig:85-86)
 //   qk_norm_mul:     (v * inv) * w                  (kernels_a.zig:89)
 //   qk_rope_angle:   (pos * freq_scale) * inv_freq   (kernels_a.zig:120)
 //   qk_rotate:       x0 c - x1 s, x0 s + x1 c        (kernels_a.zig:125-126)
-//   qk_pairs_sumsq:  one lane's share of a q head's sum of squares, 8 rope
-//                    pairs (i, i + D/2); q only feeds attention, so the head's
-//                    lanes then add their shares in a fixed xor order
+//   the q operand, which only feeds attention as an f16 value (its f32 rounding
+//   steps are far below the final f16 rounding), in fewer operations:
+//   qk_quarter_sumsq: the squares of 4 rope pairs (i, i + D/2), accumulated
+//                    x0[0]^2, x1[0]^2, x0[1]^2, ... with fma; a head's D/8
+//                    quarters (pairs 4j .. 4j + 3) then add in a balanced tree
+//                    in index order ((p0 + p1) + (p2 + p3)) + ...
+//   qk_q_pair:       u0 = x0 w0, u1 = x1 w1 (the norm weights), y0 = u0 c - u1 s,
+//                    y1 = u1 c + u0 s (each one fma over a rounded product),
+//                    then f16 of y r, r = inv * q_scale: the norm, the rotation
+//                    and the softmax scale * log2(e) in 8 operations per pair
 //   qk_scaled_f16:   f16 of the f32 product y * s, rounded twice (to f32, then
 //                    to f16). The backend turns a product that is converted
 //                    to f16 into one mixed-precision fma (v_fma_mixlo_f16, a
@@ -491,10 +500,25 @@ DS5_DEVICE_INLINE _Float16 qk_scaled_f16(float y, float s) {
     return (_Float16)p;
 }
 
-DS5_DEVICE_INLINE float qk_pairs_sumsq(const float (&x0)[8], const float (&x1)[8]) {
+DS5_DEVICE_INLINE float qk_quarter_sumsq(float a0, float b0, float a1, float b1, float a2, float b2, float a3,
+                                         float b3) {
 #pragma clang fp contract(off)
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) ss += x0[j] * x0[j] + x1[j] * x1[j];
-    return ss;
+    float p = a0 * a0;
+    p = __builtin_fmaf(b0, b0, p);
+    p = __builtin_fmaf(a1, a1, p);
+    p = __builtin_fmaf(b1, b1, p);
+    p = __builtin_fmaf(a2, a2, p);
+    p = __builtin_fmaf(b2, b2, p);
+    p = __builtin_fmaf(a3, a3, p);
+    return __builtin_fmaf(b3, b3, p);
+}
+
+DS5_DEVICE_INLINE void qk_q_pair(float x0, float x1, float w0, float w1, float c, float s, float r, _Float16& o0,
+                                 _Float16& o1) {
+#pragma clang fp contract(off)
+    const float u0 = x0 * w0, u1 = x1 * w1;
+    const float y0 = __builtin_fmaf(u0, c, -(u1 * s));
+    const float y1 = __builtin_fmaf(u1, c, u0 * s);
+    o0 = qk_scaled_f16(y0, r);
+    o1 = qk_scaled_f16(y1, r);
 }

@@ -333,8 +333,9 @@ __device__ __forceinline__ void lds_dma(uint32_t off, uint64_t base, uint32_t ld
 // the epilogue turns it into what the prefill attention reads -- k: RMSNorm
 // (serial sum) and rotation, f16 into the cache row pos + t of its kv head; v:
 // f16 into the cache; q: RMSNorm, rotation, times q_scale, f16 into the q
-// operand [t, n_q_heads, 128] -- with the pre-pass's arithmetic (the qk_*
-// helpers), so the results equal the separate projection and step.
+// operand [t, n_q_heads, 128] -- with the arithmetic of the pre-pass (k) and of
+// the attention kernel's own q operand (q) (the qk_* helpers), so the results
+// equal the separate projection and step.
 struct AttnPrepEpi {
     const float* q_norm;
     const float* k_norm;
@@ -611,24 +612,28 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                 }
                 dst = ep.v_cache + ((uint64_t)head * ep.max_ctx + ep.pos + tok) * D;
             } else {
-                float inv;
-                if (entry == 0) {  // q: the head's lanes add their shares in xor order
-                    float ss = qk_pairs_sumsq(x0, x1);
+                if (entry == 0) {
+                    // q: the thread's two quarters (pairs k8 .. k8 + 3 and k8 + 4 .. k8 + 7),
+                    // then the head's 8 threads in the balanced tree's order (xor 1, 2, 4)
+                    float ss = qk_quarter_sumsq(x0[0], x1[0], x0[1], x1[1], x0[2], x1[2], x0[3], x1[3]) +
+                               qk_quarter_sumsq(x0[4], x1[4], x0[5], x1[5], x0[6], x1[6], x0[7], x1[7]);
 #pragma unroll
                     for (int mm = 1; mm < 8; mm <<= 1) ss += __shfl_xor(ss, mm, 64);
-                    inv = rms_inv(ss, (float)D, ep.eps);
-                } else {  // k: the reference's serial sum of the row
-                    inv = rms_inv(qk_serial_sumsq(trow, D), (float)D, ep.eps);
-                }
+                    const float r = rms_inv(ss, (float)D, ep.eps) * ep.q_scale;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    float y0, y1;
-                    qk_rotate(qk_norm_mul(x0[j], inv, w0[j]), qk_norm_mul(x1[j], inv, w1[j]), c[rr][j], sn[rr][j],
-                              y0, y1);
-                    if (entry == 0) {
-                        y0v[j] = qk_scaled_f16(y0, ep.q_scale);
-                        y1v[j] = qk_scaled_f16(y1, ep.q_scale);
-                    } else {
+                    for (int j = 0; j < 8; j++) {
+                        _Float16 o0, o1;
+                        qk_q_pair(x0[j], x1[j], w0[j], w1[j], c[rr][j], sn[rr][j], r, o0, o1);
+                        y0v[j] = o0;
+                        y1v[j] = o1;
+                    }
+                } else {  // k: the reference's serial sum of the row
+                    const float inv = rms_inv(qk_serial_sumsq(trow, D), (float)D, ep.eps);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        float y0, y1;
+                        qk_rotate(qk_norm_mul(x0[j], inv, w0[j]), qk_norm_mul(x1[j], inv, w1[j]), c[rr][j], sn[rr][j],
+                                  y0, y1);
                         y0v[j] = (f16)y0;
                         y1v[j] = (f16)y1;
                     }

@@ -423,15 +423,13 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
     // for every k-step, read from the staged f16 rows. Rows are staged along rows:
     //   kQOperand: lane (g, m) copies 8 f16 of row RPI it + g, dims 8 m + [0, 8);
     //   f32 q:     lane (g, m) takes dims 4 m + [0, 4) and D/2 + 4 m + [0, 4) of row
-    //              RPI it + g: four rope pairs. kQRaw: RMSNorm, rotation with the
-    //              pre-pass's cos/sin, then both: times q_scale, f16.
-    // With kQRaw this is the arithmetic of the pre-pass and of the projection GEMM's
-    // epilogue, operation for operation, so all three give the same operand: the sum
-    // of squares of rope-pair chunks c = dims 8c + [0, 8) and c + D/16 runs in element
-    // order (lane 2c's four pairs, continued on lane 2c + 1), then the chunk sums are
-    // added in xor order (c ^ 1, c ^ 2, c ^ 4). Rows past the last token and the heads
-    // of an unfilled group read clamped, valid rows: their scores stay in their own
-    // columns of S and O and are never written.
+    //              RPI it + g: four rope pairs (quarter m of the row). kQRotated:
+    //              times q_scale, f16. kQRaw: RMSNorm, rotation with the pre-pass's
+    //              cos/sin and the scale (qk_quarter_sumsq, the quarters' balanced
+    //              tree, qk_q_pair), operation for operation the arithmetic of the
+    //              projection GEMM's q epilogue, so both give the same operand.
+    // Rows past the last token and the heads of an unfilled group read clamped, valid
+    // rows: their scores stay in their own columns of S and O and are never written.
     f16x8 qop[KS];
     // q_load issues every load of a q tile's rows (q, then with kQRaw the cos/sin rows
     // and the norm weights); q_form builds the operand from them, so that the switch
@@ -482,49 +480,39 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
             const uint32_t m = lane % LPR, g = lane / LPR;
             const float4 *a = in.a, *b = in.b, *c = in.c, *sn = in.sn;
             const float4 w0 = in.w0, w1 = in.w1;
-            float inv[NIT];
+            float r[NIT];  // kQRaw: the row's 1/rms times q_scale
             if constexpr (QM == kQRaw) {
-                // chunk sums: lane 2c adds its 4 pairs from 0, lane 2c + 1 continues from
-                // lane 2c's partial (DPP row_shr:1 within the 16-lane row)
+                // lane m of a row holds quarter m (pairs 4m .. 4m + 3); the quarters add
+                // in a balanced tree in index order: xor 1 and xor 2 (quad_perm), the
+                // quads of 8 lanes (row_half_mirror), the halves of 16 (row_mirror). DPP
+                // moves read other lanes, so every lane runs them (the empty asm keeps the
+                // compiler from moving them under a lane mask).
                 float tot[NIT];
 #pragma unroll
                 for (int it = 0; it < NIT; it++) {
-#pragma clang fp contract(off)
-                    const float t0 = a[it].x * a[it].x + b[it].x * b[it].x;
-                    const float t1 = a[it].y * a[it].y + b[it].y * b[it].y;
-                    const float t2 = a[it].z * a[it].z + b[it].z * b[it].z;
-                    const float t3 = a[it].w * a[it].w + b[it].w * b[it].w;
-                    const float pe = ((t0 + t1) + t2) + t3;  // lane 2c: 0 + t0 = t0 exactly
-                    // DPP moves read other lanes, so every lane must run them: they are
-                    // formed unconditionally (the empty asm keeps the compiler from
-                    // moving them under a lane mask) and selected afterwards.
-                    float pm = dpp_mov<0x111>(pe);  // row_shr:1: lane m - 1's partial
-                    asm volatile("" : "+v"(pm));
-                    float v = (m & 1) ? (((pm + t0) + t1) + t2) + t3 : 0.0f;
-                    // xor 2, 4, 8 within the 16-lane row: lane m takes lane m ^ k from
-                    // row_shr:k when bit k is set, else from row_shl:k
-                    auto xor_add = [&](auto shr, auto shl, uint32_t k) {
-                        float x = dpp_mov<decltype(shr)::value>(v), y = dpp_mov<decltype(shl)::value>(v);
-                        asm volatile("" : "+v"(x), "+v"(y));
-                        v += (m & k) ? x : y;
+                    float v = qk_quarter_sumsq(a[it].x, b[it].x, a[it].y, b[it].y, a[it].z, b[it].z, a[it].w, b[it].w);
+                    auto tree_add = [&](auto ctrl) {
+                        float o = dpp_mov<decltype(ctrl)::value>(v);
+                        asm volatile("" : "+v"(o));
+                        v += o;
                     };
-                    xor_add(std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0x102>{}, 2);
-                    xor_add(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0x104>{}, 4);
-                    if constexpr (LPR == 16)
-                        xor_add(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0x108>{}, 8);
-                    tot[it] = v;  // the row's sum of squares on its odd lanes
+                    tree_add(std::integral_constant<int, 0xB1>{});
+                    tree_add(std::integral_constant<int, 0x4E>{});
+                    tree_add(std::integral_constant<int, 0x141>{});
+                    if constexpr (LPR == 16) tree_add(std::integral_constant<int, 0x140>{});
+                    tot[it] = v;  // the row's sum of squares on each of its lanes
                 }
                 // one 1/rms per row: lane l takes row l % 32, then every lane its rows'
-                const uint32_t rr = lane % kQRows, src = (rr % RPI) * LPR + 1;
+                const uint32_t rr = lane % kQRows, src = (rr % RPI) * LPR;
                 float mine = 0.0f;
 #pragma unroll
                 for (int it = 0; it < NIT; it++) {
                     const float tv = __shfl(tot[it], (int)src, 64);
                     if (rr / RPI == (uint32_t)it) mine = tv;
                 }
-                const float invr = rms_inv(mine, (float)D, p.eps);
+                const float rs = rms_inv(mine, (float)D, p.eps) * p.q_scale;
 #pragma unroll
-                for (int it = 0; it < NIT; it++) inv[it] = __shfl(invr, (int)(RPI * it + g), 64);
+                for (int it = 0; it < NIT; it++) r[it] = __shfl(rs, (int)(RPI * it + g), 64);
             }
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
@@ -532,16 +520,18 @@ __global__ __launch_bounds__(kThreads) void prefill_attention_kernel(PrefillPara
                 f16x4 y0v, y1v;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    float y0 = x0[e], y1 = x1[e];
                     if constexpr (QM == kQRaw) {
                         const float c_[4] = {c[it].x, c[it].y, c[it].z, c[it].w};
                         const float s_[4] = {sn[it].x, sn[it].y, sn[it].z, sn[it].w};
                         const float w0_[4] = {w0.x, w0.y, w0.z, w0.w}, w1_[4] = {w1.x, w1.y, w1.z, w1.w};
-                        qk_rotate(qk_norm_mul(x0[e], inv[it], w0_[e]), qk_norm_mul(x1[e], inv[it], w1_[e]), c_[e], s_[e],
-                                  y0, y1);
+                        _Float16 o0, o1;
+                        qk_q_pair(x0[e], x1[e], w0_[e], w1_[e], c_[e], s_[e], r[it], o0, o1);
+                        y0v[e] = o0;
+                        y1v[e] = o1;
+                    } else {
+                        y0v[e] = qk_scaled_f16(x0[e], p.q_scale);
+                        y1v[e] = qk_scaled_f16(x1[e], p.q_scale);
                     }
-                    y0v[e] = qk_scaled_f16(y0, p.q_scale);
-                    y1v[e] = qk_scaled_f16(y1, p.q_scale);
                 }
                 char* rowp = area + (RPI * it + g) * QSTR;
                 *(f16x4*)(rowp + 8 * m) = y0v;
