@@ -347,8 +347,8 @@ class MoeSweep:
 
 class DecodeLayerSweep:
     """One decode token through n_layers whole layers at the Qwen3-30B-A3B shape, in the
-    engine's fused order (forward.zig:322-494; qw3_amd/engine.py fused mode): attn_norm,
-    the attention block (q/k/v projections + the fused step over an 8K f16 cache), Wo
+    engine's fused order (forward.zig:322-494; qw3_amd/engine.py fused mode): the
+    attention block (attn_norm, q/k/v projections + the fused step over an 8K f16 cache), Wo
     and the residual, ffn_norm, the MoE block on the device with the residual. Distinct
     weights, caches and expert banks per layer (synthetic; the banks are device copies
     of one random template, 642 MB per layer, 30.8 GB for 48 layers), the residual
@@ -372,7 +372,7 @@ class DecodeLayerSweep:
         f4 = 4
         mk = ctx.createBuffer
         self.x0 = ctx.from_numpy(g.standard_normal((1, hidden)).astype(np.float32))
-        self.x, self.h, self.h2 = mk(hidden * f4), mk(hidden * f4), mk(hidden * f4)
+        self.x, self.h2 = mk(hidden * f4), mk(hidden * f4)
         q, k, v = mk(hq * d * f4), mk(hkv * d * f4), mk(hkv * d * f4)
         attn = mk(hq * d * f4)
         pos = ctx_len - 1
@@ -398,8 +398,8 @@ class DecodeLayerSweep:
             step = H.AttentionStepArgs(q, k, v, qn, kn, positions, kc, vc, attn, H.DTYPE_F16, pos, 1, hq, hkv, d,
                                        ctx_len, eps, theta, 1.0, scale)
             self.layer_args.append((
-                H.RmsNormArgs(self.x, an, self.h, 1, hidden, eps),
-                H.AttentionBlockArgs(self.h, wq, wk, wv, H.DTYPE_Q8_0, hidden, step),
+                None,
+                H.AttentionBlockArgs(self.x, wq, wk, wv, H.DTYPE_Q8_0, hidden, step, an, eps),
                 H.MatmulAddArgs(attn, wo, H.DTYPE_Q8_0, self.x, self.x, 1, hidden, hq * d),
                 H.RmsNormArgs(self.x, fn, self.h2, 1, hidden, eps),
                 H.MoeArgs(self.h2, router, H.DTYPE_F32, gate, up, down, H.DTYPE_Q8_0, self.x, empty, empty, 1,
@@ -410,8 +410,7 @@ class DecodeLayerSweep:
 
     def layer(self, a):
         H, ctx = self.H, self.ctx
-        H.rmsNorm(ctx, a[0])
-        H.attentionBlock(ctx, a[1])
+        H.attentionBlock(ctx, a[1])  # attn_norm inside
         H.matmulAdd(ctx, a[2])
         H.rmsNorm(ctx, a[3])
         H.moe(ctx, a[4])  # x + the experts' sum (the engine's fused order)
@@ -1109,7 +1108,7 @@ def main():
             separate_legs_us=part_us, separate_legs_sum_us=round(sum(part_us.values()), 3) if len(part_us) == 4 else None,
             kernel_us_per_layer=per_layer, kernel_sum_us_per_layer=round(sum(per_layer.values()), 3),
             shape="1 token, hidden 2048, 32q/4kv d128, 8K f16 cache, Q8_0 wq/wk/wv/wo, 128 experts top 8 ffn 768; "
-                  "attn_norm, attention block, Wo + residual, ffn_norm, MoE + residual (5 calls per layer)")
+                  "attention block with attn_norm, Wo + residual, ffn_norm, MoE + residual (4 calls per layer)")
         log(f"[bench] LAYER {us:.3f} us/layer (graph of 48 layers); eager per-layer marks mean {ns.mean():.3f} "
             f"min {ns.min():.3f} max {ns.max():.3f} us; separate legs {part_us}; kernels per layer {per_layer}")
         del w

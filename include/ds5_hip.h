@@ -432,13 +432,19 @@ int ds5_hip_attention_step(ds5_hip_ctx* ctx, const ds5_attention_step_args* args
  * pre-pass launches; every other case runs the two calls. step.q / step.k /
  * step.v are scratch. */
 typedef struct ds5_attention_block_args {
-    ds5_buf x;         /* f32 [n_tokens, hidden]: the attn_norm output */
+    ds5_buf x;         /* f32 [n_tokens, hidden]: the attn_norm output (or its input, with x_norm) */
     ds5_buf wq;        /* [n_q_heads * head_dim rows of hidden] in w_dtype */
     ds5_buf wk;        /* [n_kv_heads * head_dim rows of hidden] */
     ds5_buf wv;        /* [n_kv_heads * head_dim rows of hidden] */
     uint32_t w_dtype;  /* DS5_DTYPE_F32 or DS5_DTYPE_Q8_0 */
     uint32_t hidden;
     ds5_attention_step_args step; /* q/k/v scratch, norms, positions, caches, out, shapes */
+    ds5_buf x_norm;    /* optional f32 [hidden]: the block first applies
+                        * ds5_hip_rms_norm(x, x_norm, x_norm_eps) (forward.zig:325-334's
+                        * attn_norm), bit for bit, inside the projection kernels where
+                        * they read x (rows of more than 256 elements), else into a
+                        * context buffer; its checks come first */
+    float x_norm_eps;
 } ds5_attention_block_args;
 int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* args);
 

@@ -54,6 +54,10 @@ struct ds5_hip_ctx {
     // Split-K partial results: grown on demand, owned by the context.
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    // A second growable buffer for a row-normalised x that must live beside the
+    // workspace (the fused calls' rmsNorm when it cannot run inside the kernels).
+    void* aux = nullptr;
+    size_t aux_bytes = 0;
     // The library's static device scratch array on this context's device (its
     // address from hipGetSymbolAddress, taken once per device at init). While
     // use_scratch is set -- the allocation-free entry point -- the workspace
@@ -90,6 +94,7 @@ int ds5_fail(ds5_hip_ctx* ctx, int code, const char* fmt, ...) __attribute__((fo
 int ds5_hip_status(ds5_hip_ctx* ctx, hipError_t err, const char* what);
 int ds5_after_launch(ds5_hip_ctx* ctx, const char* what);
 int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out);
+int ds5_aux_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out);
 // Looks up (once per device) the address of the static scratch array on the
 // context's device, which must be current, and records it in the context.
 int ds5_scratch_init(ds5_hip_ctx* ctx);
@@ -144,6 +149,11 @@ struct MatmulGroupLaunch {
     float* out[kMatmulGroupMax];
     const float* res[kMatmulGroupMax];  // per entry, as MatmulLaunch::res
     uint32_t n[kMatmulGroupMax];
+    // x normalised first (k > 256: the reference GPU kernel's tree order) by the row
+    // kernel or the GEMM's x split as they read it; null: x as it is. Only the Rows
+    // and Gemm paths take it.
+    const float* norm_w;
+    float norm_eps;
 };
 int launch_matmul_group(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, const MatmulPath* paths);
 // The attention block's q/k/v projections with the prefill pre-pass in the GEMM's
@@ -165,6 +175,8 @@ struct QkvPrepLaunch {
     uint32_t pos, max_ctx;
     float eps, q_scale;
     void* ws;
+    const float* norm_w;  // x normalised first, as MatmulGroupLaunch::norm_w (null: none)
+    float norm_eps;
 };
 size_t qkv_prep_workspace_bytes(uint32_t m, uint32_t k, uint32_t head_dim);
 int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a);
@@ -437,6 +449,34 @@ DS5_DEVICE_INLINE float sqrt_rn(float x) { return (float)__builtin_sqrt((double)
 // RMSNorm scale of kernels_a.zig:87.
 DS5_DEVICE_INLINE float rms_inv(float sumsq, float dim, float eps) {
     return __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(sumsq, dim) + eps));
+}
+
+// rmsNorm of rows longer than 256 elements takes the reduction order of the
+// reference's GPU kernel (kernels_a.metal:127-165): thread t < 256 of a block
+// accumulates s = fma(v, v, s) over the row's elements t, t + 256, t + 512, ...
+// in that order (kTreeParts partials), then the partials add in a halving tree,
+// p[t] += p[t + s] for s = 128, 64, ..., 1. tree_rms_inv takes each thread's
+// partial (threads >= 256 pass anything) and returns the row's rms_inv to every
+// thread; part: kTreeParts floats of LDS, inv: one float of LDS; every thread of
+// the block (at least 256) calls it, as it holds barriers.
+constexpr uint32_t kTreeParts = 256;
+// ds5_hip_rms_norm: rows of up to this many elements take the reference CPU
+// path's serial sum, longer rows the tree order above.
+constexpr uint32_t kRmsSerialMaxDim = 256;
+DS5_DEVICE_INLINE float tree_rms_inv(float s, uint32_t dim, float eps, float* part, float* inv) {
+    const uint32_t t = threadIdx.x;
+    if (t < kTreeParts) part[t] = s;
+    __syncthreads();
+    if (t < kTreeParts / 2) part[t] = s + part[t + kTreeParts / 2];
+    __syncthreads();
+    if (t < 64) {
+        float v = part[t] + part[t + 64];
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) v += __shfl_down(v, k, 64);
+        if (t == 0) *inv = rms_inv(v, (float)dim, eps);
+    }
+    __syncthreads();
+    return *inv;
 }
 
 // The q/k arithmetic of a prefill step, shared by every kernel that produces the

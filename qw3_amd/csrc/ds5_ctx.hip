@@ -36,6 +36,32 @@ int ds5_after_launch(ds5_hip_ctx* ctx, const char* what) {
     return ds5_hip_status(ctx, hipGetLastError(), what);
 }
 
+// Grows a context-owned buffer to at least `bytes`. A larger buffer is a new
+// allocation; the old one stays owned by the context until deinit, because
+// enqueued kernels and captured graphs may still reference it. Growing needs a
+// synchronise and an allocation, neither of which a stream capture allows.
+static int grow_buffer(ds5_hip_ctx* ctx, size_t bytes, void*& buf, size_t& have, const char* what) {
+    if (bytes > have) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        int rc = ds5_hip_status(ctx, hipStreamIsCapturing(ctx->stream, &cap), "workspace capture query");
+        if (rc) return rc;
+        if (cap != hipStreamCaptureStatusNone)
+            return ds5_fail(ctx, DS5_DEVICE_FAILURE,
+                            "%s must grow to %zu bytes during a stream capture: run the same call once "
+                            "before capturing it", what, bytes);
+        rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "workspace sync");
+        if (rc) return rc;
+        const size_t want = std::max<size_t>(bytes, 4u << 20);
+        void* p = nullptr;
+        rc = ds5_hip_status(ctx, hipMalloc(&p, want), "workspace alloc");
+        if (rc) return rc;
+        if (buf) ctx->owned.push_back(buf);
+        buf = p;
+        have = want;
+    }
+    return DS5_OK;
+}
+
 int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
     if (ctx->use_scratch) {
         // allocation-free call: the static scratch array, never an allocation
@@ -45,29 +71,14 @@ int ds5_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
         *out = ctx->scratch;
         return DS5_OK;
     }
-    if (bytes > ctx->workspace_bytes) {
-        // A larger workspace is a new allocation; the old one stays owned by the
-        // context until deinit, because enqueued kernels and captured graphs may
-        // still reference it. Growing it needs a synchronise and an allocation,
-        // neither of which a stream capture allows.
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        int rc = ds5_hip_status(ctx, hipStreamIsCapturing(ctx->stream, &cap), "workspace capture query");
-        if (rc) return rc;
-        if (cap != hipStreamCaptureStatusNone)
-            return ds5_fail(ctx, DS5_DEVICE_FAILURE,
-                            "workspace must grow to %zu bytes during a stream capture: run the same call once "
-                            "before capturing it", bytes);
-        rc = ds5_hip_status(ctx, hipStreamSynchronize(ctx->stream), "workspace sync");
-        if (rc) return rc;
-        const size_t want = std::max<size_t>(bytes, 4u << 20);
-        void* p = nullptr;
-        rc = ds5_hip_status(ctx, hipMalloc(&p, want), "workspace alloc");
-        if (rc) return rc;
-        if (ctx->workspace) ctx->owned.push_back(ctx->workspace);
-        ctx->workspace = p;
-        ctx->workspace_bytes = want;
-    }
+    if (int rc = grow_buffer(ctx, bytes, ctx->workspace, ctx->workspace_bytes, "workspace")) return rc;
     *out = ctx->workspace;
+    return DS5_OK;
+}
+
+int ds5_aux_workspace(ds5_hip_ctx* ctx, size_t bytes, void** out) {
+    if (int rc = grow_buffer(ctx, bytes, ctx->aux, ctx->aux_bytes, "workspace")) return rc;
+    *out = ctx->aux;
     return DS5_OK;
 }
 
@@ -137,6 +148,7 @@ void ds5_hip_deinit(ds5_hip_ctx* ctx) {
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->marks) (void)hipEventDestroy(e);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->aux) (void)hipFree(ctx->aux);
     if (ctx->ev_begin) (void)hipEventDestroy(ctx->ev_begin);
     if (ctx->ev_end) (void)hipEventDestroy(ctx->ev_end);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -427,6 +427,21 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     return launch_experts(ctx, l);
 }
 
+// The group's launch and each entry's kernel path (the checks done).
+static void group_launch_of(const ds5_matmul_group_args* a, MatmulGroupLaunch& g, MatmulPath* paths) {
+    g.x = (const float*)ds5_ptr(a->x);
+    g.q8 = a->w_dtype == DS5_DTYPE_Q8_0;
+    g.m = a->m;
+    g.k = a->k;
+    g.count = a->count;
+    for (uint32_t e = 0; e < a->count; e++) {
+        g.w[e] = (const uint8_t*)ds5_ptr(a->w[e]);
+        g.out[e] = (float*)ds5_ptr(a->out[e]);
+        g.n[e] = a->n[e];
+        paths[e] = matmul_path(MatmulLaunch{g.x, g.w[e], g.q8, g.out[e], g.m, g.n[e], g.k}, a->w[e].len);
+    }
+}
+
 int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
     if (a->count == 0 || a->count > DS5_MATMUL_GROUP_MAX)
@@ -437,18 +452,8 @@ int ds5_hip_matmul_group(ds5_hip_ctx* ctx, const ds5_matmul_group_args* a) {
     if (a->m == 0) return DS5_OK;
     if (int rc = set_device(ctx)) return rc;
     MatmulGroupLaunch g{};
-    g.x = (const float*)ds5_ptr(a->x);
-    g.q8 = a->w_dtype == DS5_DTYPE_Q8_0;
-    g.m = a->m;
-    g.k = a->k;
-    g.count = a->count;
     MatmulPath paths[kMatmulGroupMax];
-    for (uint32_t e = 0; e < a->count; e++) {
-        g.w[e] = (const uint8_t*)ds5_ptr(a->w[e]);
-        g.out[e] = (float*)ds5_ptr(a->out[e]);
-        g.n[e] = a->n[e];
-        paths[e] = matmul_path(MatmulLaunch{g.x, g.w[e], g.q8, g.out[e], g.m, g.n[e], g.k}, a->w[e].len);
-    }
+    group_launch_of(a, g, paths);
     return launch_matmul_group(ctx, g, paths);
 }
 
@@ -681,6 +686,14 @@ int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* a)
     if (!a) return DS5_SHAPE_MISMATCH;
     const ds5_attention_step_args& s = a->step;
     const uint32_t hd = s.head_dim;
+    // x_norm: rmsNorm(x -> h) first (its checks first), then the block on h
+    const bool norm = a->x_norm.len != 0;
+    if (norm) {
+        const uint64_t T = s.n_tokens, H = a->hidden;
+        if (H == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention_block: hidden == 0");
+        if (!covers(a->x, T * H * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention_block: x too small");
+        if (!covers(a->x_norm, H * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "attention_block: x_norm too small");
+    }
     ds5_matmul_group_args g{};
     g.x = a->x;
     g.w_dtype = a->w_dtype;
@@ -701,19 +714,40 @@ int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* a)
     if (int rc = check_step(ctx, &s)) return rc;
     if (s.n_tokens == 0) return DS5_OK;
     if (int rc = set_device(ctx)) return rc;
+    MatmulGroupLaunch gl{};
+    MatmulPath paths[kMatmulGroupMax];
+    group_launch_of(&g, gl, paths);
+    // The norm runs inside the projection's kernels (the row kernel or the GEMM's x
+    // split, as they read x) for rows of more than 256 elements (the tree order) when
+    // every projection takes one of them; otherwise rmsNorm writes h to the context's
+    // second buffer first and the block runs on h.
+    const bool all_rows = paths[0] == MatmulPath::Rows && paths[1] == MatmulPath::Rows && paths[2] == MatmulPath::Rows;
+    const bool all_gemm = paths[0] == MatmulPath::Gemm && paths[1] == MatmulPath::Gemm && paths[2] == MatmulPath::Gemm;
+    const bool norm_inside = norm && a->hidden > kRmsSerialMaxDim && aligned16(a->x_norm) && (all_rows || all_gemm);
+    if (norm && !norm_inside) {
+        void* h = nullptr;
+        const uint64_t bytes = (uint64_t)s.n_tokens * a->hidden * 4;
+        if (int rc = ds5_aux_workspace(ctx, bytes, &h)) return rc;
+        if (int rc = launch_rms_norm(ctx, RmsNormLaunch{(const float*)ds5_ptr(a->x), (const float*)ds5_ptr(a->x_norm),
+                                                        (float*)h, s.n_tokens, a->hidden, a->x_norm_eps}))
+            return rc;
+        ds5_attention_block_args b = *a;
+        b.x = ds5_buf{h, 0, bytes};
+        b.x_norm = ds5_buf{};
+        return ds5_hip_attention_block(ctx, &b);
+    }
+    if (norm_inside) {
+        gl.norm_w = (const float*)ds5_ptr(a->x_norm);
+        gl.norm_eps = a->x_norm_eps;
+    }
     // Fused: the prefill pre-pass in the projection GEMM's epilogue (the paths the two
     // calls would take: the GEMM for every weight, the fused MFMA prefill step).
-    bool fused = a->w_dtype == DS5_DTYPE_Q8_0 && hd == 128 && s.n_tokens >= 2 &&
-                 mfma_shape(s.kv_dtype, hd, {s.q, s.k, s.v, s.k_cache, s.v_cache, s.out}) &&
-                 prefill_prep_supported(s.n_kv_heads, hd) && aligned16(a->x) && aligned16(s.q_norm) &&
-                 aligned16(s.k_norm);
-    for (uint32_t e = 0; fused && e < 3; e++) {
-        const MatmulLaunch l{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(g.w[e]), true,
-                             (float*)ds5_ptr(g.out[e]), g.m, g.n[e], g.k};
-        fused = matmul_path(l, g.w[e].len) == MatmulPath::Gemm;
-    }
+    const bool fused = a->w_dtype == DS5_DTYPE_Q8_0 && hd == 128 && s.n_tokens >= 2 &&
+                       mfma_shape(s.kv_dtype, hd, {s.q, s.k, s.v, s.k_cache, s.v_cache, s.out}) &&
+                       prefill_prep_supported(s.n_kv_heads, hd) && aligned16(a->x) && aligned16(s.q_norm) &&
+                       aligned16(s.k_norm) && all_gemm;
     if (!fused) {
-        if (int rc = ds5_hip_matmul_group(ctx, &g)) return rc;
+        if (int rc = launch_matmul_group(ctx, gl, paths)) return rc;
         return ds5_hip_attention_step(ctx, &s);
     }
     const uint64_t T = s.n_tokens;
@@ -744,6 +778,8 @@ int ds5_hip_attention_block(ds5_hip_ctx* ctx, const ds5_attention_block_args* a)
     qp.eps = s.eps;
     qp.q_scale = s.scale * kLog2e;
     qp.ws = (char*)ws + q16_bytes;
+    qp.norm_w = gl.norm_w;
+    qp.norm_eps = gl.norm_eps;
     if (int rc = launch_qkv_prep(ctx, qp)) return rc;
     PrefillLaunch l{};
     l.q16 = (const f16*)ws;

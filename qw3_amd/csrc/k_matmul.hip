@@ -48,9 +48,14 @@ static_assert(kMatmulGroupMax == 4, "DS5_GROUP_ARGS lists four entries");
 // Launch: grid.x = sum of ceil(n[e] / 8), one pass of tokens m0..m0+MT-1. Rows
 // past n (an entry's last workgroup) load row n - 1 and store nothing: every
 // wavefront reaches the barrier.
-template <int MT, int JB, bool Q8>
+// NORM: x is first normalised, x' = (x * inv) * nw with inv of the reference GPU
+// kernel's tree order (tree_rms_inv; rows of more than 256 elements), as the
+// workgroup stages it: ds5_hip_rms_norm then the product, bit for bit, with the
+// norm worked out while the weights are in flight.
+template <int MT, int JB, bool Q8, bool NORM>
 __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __restrict__ x, const WeightGroup g,
-                                                                 uint32_t m, uint32_t k, uint32_t m0) {
+                                                                 uint32_t m, uint32_t k, uint32_t m0,
+                                                                 const float* __restrict__ nw, float eps) {
     // this workgroup's entry (uniform; selected without indexing the argument arrays,
     // with selects rather than branches so that every field loads in one round trip)
     // (out may be the residual itself: each output is read, then written, by one lane)
@@ -89,6 +94,11 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
             const uint32_t e = min(threadIdx.x + (uint32_t)kMmThreads * u, kc - 1);
             xv[t][u] = ((const float4*)x)[(uint64_t)(m0 + min((uint32_t)t, mt - 1)) * kc + e];
         }
+    float4 wn[NORM ? kXPer : 1];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int u = 0; u < kXPer; u++) wn[u] = ((const float4*)nw)[min(threadIdx.x + (uint32_t)kMmThreads * u, kc - 1)];
+    }
 
     // 2. the row's weights, all in flight before x is needed (loads complete in
     //    issue order, so staging x waits for x alone)
@@ -120,14 +130,40 @@ __global__ __launch_bounds__(kMmThreads) void matmul_rows_kernel(const float* __
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. stage x, then each lane takes the x of its blocks
+    auto slot = [&](int t, uint32_t e) { return t * kXChunks + (e & ~7u) + ((e & 7u) ^ ((e >> 3) & 7u)); };
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int u = 0; u < kXPer; u++) {
             const uint32_t e = threadIdx.x + (uint32_t)kMmThreads * u;
-            if (e < kc) xs[t * kXChunks + (e & ~7u) + ((e & 7u) ^ ((e >> 3) & 7u))] = xv[t][u];
+            if (e < kc) xs[slot(t, e)] = xv[t][u];
         }
     __syncthreads();
+    if constexpr (NORM) {
+        // each token's partials from the staged row (element i: chunk i / 4, lane i % 4),
+        // the tree, then the staged row rewritten as (x * inv) * nw
+        __shared__ float s_part[kTreeParts];
+        __shared__ float s_inv;
+        const float* xf = (const float*)xs;
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            float sq = 0.0f;
+            if (threadIdx.x < kTreeParts)
+                for (uint32_t i = threadIdx.x; i < k; i += kTreeParts) {
+                    const float v = xf[4 * slot(t, i >> 2) + (i & 3)];
+                    sq = __builtin_fmaf(v, v, sq);
+                }
+            const float inv = tree_rms_inv(sq, k, eps, s_part, &s_inv);
+#pragma unroll
+            for (int u = 0; u < kXPer; u++) {
+                const uint32_t e = threadIdx.x + (uint32_t)kMmThreads * u;
+                const float4 v = xv[t][u], ww = wn[u];
+                if (e < kc)
+                    xs[slot(t, e)] = float4{v.x * inv * ww.x, v.y * inv * ww.y, v.z * inv * ww.z, v.w * inv * ww.w};
+            }
+        }
+        __syncthreads();
+    }
 
     // 4. per-block partial sums (x of the lane's block read from LDS just before
     //    use), then the wavefront's fixed-order reduction
@@ -229,14 +265,21 @@ struct XSplitRope {
 
 // One workgroup per x row: max |x|, its exponent E, then hi / lo of x * 2^(14 - E).
 // A row of zeros (or with a non-finite maximum) keeps E = 0. ROPE: also the
-// row's token's rope cos / sin.
+// row's token's rope cos / sin. nw (if not null): the row is first normalised,
+// x' = (x * inv) * nw with inv in the reference GPU kernel's tree order
+// (tree_rms_inv), exactly as ds5_hip_rms_norm writes rows of more than 256
+// elements.
 template <bool ROPE>
 __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const float* __restrict__ x,
                                                                        uint16_t* __restrict__ hi,
                                                                        uint16_t* __restrict__ lo,
                                                                        int* __restrict__ row_exp, uint32_t k,
-                                                                       XSplitRope rope, RopeTable table) {
+                                                                       XSplitRope rope, RopeTable table,
+                                                                       const float* __restrict__ nw, float eps) {
+    static_assert(kSplitThreads >= kTreeParts, "one tree partial per thread");
     __shared__ float red[kSplitThreads / 64];
+    __shared__ float s_part[kTreeParts];
+    __shared__ float s_inv;
     const uint64_t row = blockIdx.x;
     if constexpr (ROPE) {
         const float pos = (float)rope.positions[row];
@@ -248,9 +291,24 @@ __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const flo
     }
     const float4* xr = (const float4*)(x + row * k);
     const uint32_t kc = k / 4;
+    float inv = 1.0f;
+    if (nw) {  // uniform
+        float sq = 0.0f;
+        for (uint32_t i = threadIdx.x; i < k; i += kTreeParts) {
+            const float v = x[row * k + i];
+            sq = __builtin_fmaf(v, v, sq);
+        }
+        inv = tree_rms_inv(sq, k, eps, s_part, &s_inv);
+    }
+    auto load = [&](uint32_t c) {
+        const float4 v = xr[c];
+        if (!nw) return v;
+        const float4 w = ((const float4*)nw)[c];
+        return float4{v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w};
+    };
     float mx = 0.0f;
     for (uint32_t c = threadIdx.x; c < kc; c += kSplitThreads) {
-        const float4 v = xr[c];
+        const float4 v = load(c);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     mx = wave_allreduce(mx, OpMax{});
@@ -264,7 +322,7 @@ __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const flo
     uint2* h2 = (uint2*)(hi + row * k);
     uint2* l2 = (uint2*)(lo + row * k);
     for (uint32_t c = threadIdx.x; c < kc; c += kSplitThreads) {
-        const float4 v = xr[c];
+        const float4 v = load(c);
         const float f[4] = {v.x, v.y, v.z, v.w};
         uint32_t hb[4], lb[4];
 #pragma unroll
@@ -709,7 +767,7 @@ __global__ __launch_bounds__(kMmThreads) void add_kernel(const uint8_t* x, const
     }
 }
 
-template <int MT, int JB, bool Q8>
+template <int MT, int JB, bool Q8, bool NORM>
 int launch_rows(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, uint32_t m0) {
     constexpr uint32_t kRowsPerBlock = kMmThreads / 64;
     WeightGroup g{};
@@ -724,37 +782,42 @@ int launch_rows(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, uint32_t m0) {
         g.count += a.n[e] ? 1 : 0;  // entries without rows are dropped
     }
     if (wgs == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "matmul_rows_kernel", (matmul_rows_kernel<MT, JB, Q8>), dim3(wgs), dim3(kMmThreads), 0,
-                     ctx->stream, a.x, g, a.m, a.k, m0);
+    DS5_TIMED_LAUNCH(ctx, "matmul_rows_kernel", (matmul_rows_kernel<MT, JB, Q8, NORM>), dim3(wgs), dim3(kMmThreads), 0,
+                     ctx->stream, a.x, g, a.m, a.k, m0, a.norm_w, a.norm_eps);
     return ds5_after_launch(ctx, "matmul_rows_kernel");
 }
 
 
 // Tokens per pass: up to 4 / JB (the x registers hold MT * JB * 32 floats per lane),
 // and no more than the tokens there are (a 1-token decode runs MT = 1).
-template <int JB, bool Q8>
+template <int JB, bool Q8, bool NORM>
 int launch_passes(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     constexpr uint32_t kMaxMt = 4 / JB;
     const uint32_t mt = a.m >= kMaxMt ? kMaxMt : (a.m >= 2 ? 2 : 1);
     for (uint32_t m0 = 0; m0 < a.m; m0 += mt) {
         int rc;
         if (mt == 4)
-            rc = launch_rows<(kMaxMt >= 4 ? 4 : 1), JB, Q8>(ctx, a, m0);
+            rc = launch_rows<(kMaxMt >= 4 ? 4 : 1), JB, Q8, NORM>(ctx, a, m0);
         else if (mt == 2)
-            rc = launch_rows<(kMaxMt >= 2 ? 2 : 1), JB, Q8>(ctx, a, m0);
+            rc = launch_rows<(kMaxMt >= 2 ? 2 : 1), JB, Q8, NORM>(ctx, a, m0);
         else
-            rc = launch_rows<1, JB, Q8>(ctx, a, m0);
+            rc = launch_rows<1, JB, Q8, NORM>(ctx, a, m0);
         if (rc) return rc;
     }
     return DS5_OK;
 }
 
+template <bool Q8, bool NORM>
+int launch_rows_n(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
+    const uint32_t nb = a.k / 32;
+    if (nb <= 64) return launch_passes<1, Q8, NORM>(ctx, a);
+    if (nb <= 128) return launch_passes<2, Q8, NORM>(ctx, a);
+    return launch_passes<4, Q8, NORM>(ctx, a);
+}
+
 template <bool Q8>
 int launch_rows_q(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
-    const uint32_t nb = a.k / 32;
-    if (nb <= 64) return launch_passes<1, Q8>(ctx, a);
-    if (nb <= 128) return launch_passes<2, Q8>(ctx, a);
-    return launch_passes<4, Q8>(ctx, a);
+    return a.norm_w ? launch_rows_n<Q8, true>(ctx, a) : launch_rows_n<Q8, false>(ctx, a);
 }
 
 // The split x is made once and shared by the group's products.
@@ -766,7 +829,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     uint16_t* lo = hi + (size_t)a.m * a.k;
     int* row_exp = (int*)(lo + (size_t)a.m * a.k);
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{});
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{}, a.norm_w, a.norm_eps);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     uint32_t tiles = 0;
@@ -804,7 +867,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     float* cs = (float*)((char*)a.ws + qkv_prep_cs_offset(a.m, a.k));
     XSplitRope rope{a.positions, cs, a.head_dim / 2, a.freq_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<true>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table);
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table, a.norm_w, a.norm_eps);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     const uint32_t ns[3] = {a.n_q_heads * a.head_dim, a.n_kv_heads * a.head_dim, a.n_kv_heads * a.head_dim};
@@ -865,6 +928,9 @@ static int launch_generic(ds5_hip_ctx* ctx, const float* x, const uint8_t* w, bo
 }
 
 static int launch_same_path(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a, MatmulPath path) {
+    if (a.norm_w && (path == MatmulPath::Generic || a.k <= kRmsSerialMaxDim))
+        return ds5_fail(ctx, DS5_DEVICE_FAILURE, "matmul: an in-kernel norm needs the row or GEMM path and k > %u",
+                        kRmsSerialMaxDim);
     if (path == MatmulPath::Rows) return a.q8 ? launch_rows_q<true>(ctx, a) : launch_rows_q<false>(ctx, a);
     if (path == MatmulPath::Gemm)
         return a.m >= 128 ? launch_gemm<128, 128, 4, 2>(ctx, a) : launch_gemm<32, 64, 2, 2>(ctx, a);

@@ -26,7 +26,7 @@ constexpr int kNormTile = 4096;  // floats of a block's rows staged in LDS
 // Rows of at most kSerialMaxDim elements (the per-head q/k norms) take the
 // reference CPU path's serial sum; longer rows (the hidden-state norms) the
 // reference GPU kernel's reduction order (rms_norm_tree_kernel).
-constexpr uint32_t kSerialMaxDim = 256;
+constexpr uint32_t kSerialMaxDim = kRmsSerialMaxDim;
 
 // Rows of at most kSerialMaxDim elements: R = min(64, kNormTile / dim) rows per
 // block. The block loads its R rows (contiguous in memory) with every load
@@ -123,7 +123,8 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float
 // t, t + 256, t + 512, ... with fused multiply-adds, then the 256 partials add in
 // a halving tree, partial[t] += partial[t + s] for s = 128, 64, ..., 1 (the two
 // strides that cross wavefronts through LDS, the rest by lane shifts within
-// wavefront 0); inv = 1/sqrt(sum/dim + eps) correctly rounded, o = (v*inv)*w.
+// wavefront 0; tree_rms_inv, shared with the kernels that normalise a row as they
+// stage it); inv = 1/sqrt(sum/dim + eps) correctly rounded, o = (v*inv)*w.
 // A thread loads its elements eight at a time, every load of a batch in flight;
 // the batch's last loads may fall past the row and are clamped and zeroed, and
 // fma(0, 0, s) = s for the non-negative s. out may alias x: a thread writes only
@@ -131,8 +132,9 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_rows_kernel(const float
 constexpr int kTreeThreads = 256;
 __global__ __launch_bounds__(kTreeThreads) void rms_norm_tree_kernel(const float* x, const float* __restrict__ w,
                                                                      float* out, uint32_t dim, float eps) {
-    __shared__ float s_part[kTreeThreads];
+    __shared__ float s_part[kTreeParts];
     __shared__ float s_inv;
+    static_assert(kTreeThreads == kTreeParts, "one partial per thread");
     constexpr int B = 8;
     const uint32_t t = threadIdx.x;
     const float* xr = x + (uint64_t)blockIdx.x * dim;
@@ -148,18 +150,7 @@ __global__ __launch_bounds__(kTreeThreads) void rms_norm_tree_kernel(const float
 #pragma unroll
         for (int j = 0; j < B; j++) s = __builtin_fmaf(v[j], v[j], s);
     }
-    s_part[t] = s;
-    __syncthreads();
-    if (t < 128) s_part[t] = s + s_part[t + 128];
-    __syncthreads();
-    if (t < 64) {
-        float v = s_part[t] + s_part[t + 64];
-#pragma unroll
-        for (int k = 32; k > 0; k >>= 1) v += __shfl_down(v, k, 64);
-        if (t == 0) s_inv = rms_inv(v, (float)dim, eps);
-    }
-    __syncthreads();
-    const float inv = s_inv;
+    const float inv = tree_rms_inv(s, dim, eps, s_part, &s_inv);
     float* orow = out + (uint64_t)blockIdx.x * dim;
     for (uint32_t i = t; i < dim; i += kTreeThreads) orow[i] = xr[i] * inv * w[i];
 }

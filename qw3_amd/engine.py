@@ -13,12 +13,13 @@ router's ids and weights come back to build the expert pairs (forward.zig:432-46
 Two modes:
 - `fused=False`: exactly the eight provider ops of `assertKernelApi`
   (src/shared/contracts.zig:356-367), one call per reference call;
-- `fused=True`: the optional decls the engine takes via `@hasDecl`: the q/k/v
-  projections and the q/k norm + rope + append + attention as one `attentionBlock`
-  (at a prefill the pre-pass runs in the projection GEMM's epilogue, so q, k and v
-  are never written in f32; with a trace callback set, the same work as its two
-  calls, `matmulGroup` then `attentionStep`, which the block equals bit for bit, so
-  the projection trace points exist), Wo and its residual as one `matmulAdd`, and
+- `fused=True`: the optional decls the engine takes via `@hasDecl`: attn_norm, the
+  q/k/v projections and the q/k norm + rope + append + attention as one
+  `attentionBlock` (attn_norm inside the projection kernels as they read x; at a
+  prefill the pre-pass runs in the projection GEMM's epilogue, so q, k and v are
+  never written in f32; with a trace callback set, the same work as its calls,
+  `rmsNorm`, `matmulGroup` then `attentionStep`, which the block equals bit for bit,
+  so those trace points exist), Wo and its residual as one `matmulAdd`, and
   the MoE block and its residual as one `moe` (router and experts with the pairs kept
   on the device, x + the experts' sum written in the combine; with a trace callback
   set, `moe` into the zeroed accumulator then `add`, which it equals bit for bit, so
@@ -169,10 +170,13 @@ class Engine:
             ctx.timing_mark()
         for li in range(c["n_layers"]):
             attn_norm, _ = self.w.layer(li, "attn_norm.weight")
-            H.rmsNorm(ctx, H.RmsNormArgs(self.x, attn_norm, self.h, n, hidden, eps))
-            self._trace(li, "attn_norm", self.h, n * hidden)
             (wq, dq), (wk, dk), (wv, dv) = (self.w.layer(li, s) for s in
                                             ("attn_q.weight", "attn_k.weight", "attn_v.weight"))
+            # the attention block takes attn_norm itself (h never written) when nothing traces h
+            block = self.fused and dq == dk == dv and self.trace is None
+            if not block:
+                H.rmsNorm(ctx, H.RmsNormArgs(self.x, attn_norm, self.h, n, hidden, eps))
+                self._trace(li, "attn_norm", self.h, n * hidden)
             q_norm, _ = self.w.layer(li, "attn_q_norm.weight")
             k_norm, _ = self.w.layer(li, "attn_k_norm.weight")
             step = None
@@ -181,8 +185,8 @@ class Engine:
                     self.q, self.k, self.v, q_norm, k_norm, self.positions, self.k_cache[li], self.v_cache[li],
                     self.attn, self.kv_dtype, self.pos, n, hq, hkv, hd, self.capacity, eps, c["rope_theta"], 1.0,
                     scale)
-            if self.fused and dq == dk == dv and self.trace is None:
-                H.attentionBlock(ctx, H.AttentionBlockArgs(self.h, wq, wk, wv, dq, hidden, step))
+            if block:
+                H.attentionBlock(ctx, H.AttentionBlockArgs(self.x, wq, wk, wv, dq, hidden, step, attn_norm, eps))
             elif self.fused and dq == dk == dv:
                 H.matmulGroup(ctx, H.MatmulGroupArgs.of(self.h, dq, n, hidden, [
                     (wq, self.q, q_dim), (wk, self.k, kv_dim), (wv, self.v, kv_dim)]))
@@ -195,7 +199,7 @@ class Engine:
             self._trace(li, "v_proj", self.v, n * kv_dim)
             # fused: q_norm, k_norm, rope_q and rope_k happen inside the step (no trace points)
             if self.fused:
-                if not (dq == dk == dv and self.trace is None):
+                if not block:
                     H.attentionStep(ctx, step)
             else:
                 H.rmsNorm(ctx, H.RmsNormArgs(self.q, q_norm, self.q, n * hq, hd, eps))

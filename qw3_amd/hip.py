@@ -165,7 +165,7 @@ class AttentionStepArgs(C.Structure):
 class AttentionBlockArgs(C.Structure):
     """ds5_attention_block_args: the q/k/v projections of x then the attention step."""
     _fields_ = [("x", Buf), ("wq", Buf), ("wk", Buf), ("wv", Buf), ("w_dtype", C.c_uint32), ("hidden", C.c_uint32),
-                ("step", AttentionStepArgs)]
+                ("step", AttentionStepArgs), ("x_norm", Buf), ("x_norm_eps", C.c_float)]
 
 
 class PagedDecodeArgs(C.Structure):

@@ -31,6 +31,7 @@ CASES = {
     "c2_hidden2048": (2048, 0, 32, 4, 128, 2048, "q8", True, False),  # the C2 prefill with its projections
     "t8_rows": (8, 0, 32, 4, 128, 512, "q8", False, True),         # row kernel: the two calls
     "t1_decode": (1, 20, 32, 4, 128, 512, "q8", False, True),      # decode: the two calls
+    "t1_hidden2048": (1, 40, 32, 4, 128, 2048, "q8", False, True),  # decode at the Qwen3-30B-A3B width
     "f32_weights": (40, 0, 32, 4, 128, 256, "f32", False, True),
     "d64": (64, 0, 32, 4, 64, 256, "q8", False, True),             # head_dim 64: the two calls
 }
@@ -150,6 +151,38 @@ def test_attention_block_errors(ctx, hip, oracle):
     ctx.submit()
     assert np.array_equal(ctx.to_numpy(a.k_cache, np.uint16, inp.kc.shape), inp.kc)
     assert np.array_equal(ctx.to_numpy(a.v_cache, np.uint16, inp.vc.shape), inp.vc)
+
+
+@pytest.mark.parametrize("case", ["t16", "t300_64q", "c2_hidden2048", "t8_rows", "t1_decode", "f32_weights",
+                                  "t130_2group", "d64", "t1_hidden2048"])
+def test_attention_block_with_norm(ctx, hip, oracle, case):
+    """The block with x_norm (attn_norm applied first) equals ds5_hip_rms_norm(x -> h) then
+    the block on h, bit for bit (output and every cache row): the norm inside the row
+    kernel (decode), inside the GEMM's x split (prefill), or written to the context's
+    second buffer (hidden <= 256: the serial order; the other paths). The raw x has rows
+    of widely varying magnitude, so the norm is not the identity."""
+    inp = _Inputs(ctx, hip, oracle, case)
+    T, hidden = inp.T, inp.hidden
+    g = np.random.default_rng(7 + T)
+    x = (inp.x * np.exp(g.uniform(-3, 3, (T, 1)))).astype(np.float32)
+    nw = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
+    xb, nwb = ctx.from_numpy(x), ctx.from_numpy(nw)
+    eps = 1e-6
+    print(f"  case {case}: T={T} hidden={hidden}", flush=True)
+    a = inp.step_args(ctx, hip)
+    hip.attentionBlock(ctx, hip.AttentionBlockArgs(xb, *inp.wb, inp.dtype, hidden, a, nwb, eps))
+    h = ctx.createBuffer(T * hidden * 4)
+    hip.rmsNorm(ctx, hip.RmsNormArgs(xb, nwb, h, T, hidden, eps))
+    b = inp.step_args(ctx, hip)
+    hip.attentionBlock(ctx, hip.AttentionBlockArgs(h, *inp.wb, inp.dtype, hidden, b))
+    for name, p, q in zip(("out", "k_cache", "v_cache"), inp.results(ctx, a), inp.results(ctx, b)):
+        same = p.view(np.uint8) == q.view(np.uint8)
+        print(f"  {name}: {int((~same).sum())} bytes differ", flush=True)
+        assert same.all()
+    assert np.array_equal(ctx.to_numpy(xb, np.float32, x.shape), x)  # x itself is left as it was
+    with pytest.raises(hip.ShapeMismatch):
+        hip.attentionBlock(ctx, hip.AttentionBlockArgs(xb, *inp.wb, inp.dtype, hidden, inp.step_args(ctx, hip),
+                                                       hip.Buf(nwb.handle, nwb.offset, hidden * 4 - 4), eps))
 
 
 @pytest.mark.parametrize("case", ["t300_64q", "t8_rows"])
