@@ -349,7 +349,7 @@ class DecodeLayerSweep:
     """One decode token through n_layers whole layers at the Qwen3-30B-A3B shape, in the
     engine's fused order (forward.zig:322-494; qw3_amd/engine.py fused mode): the
     attention block (attn_norm, q/k/v projections + the fused step over an 8K f16 cache), Wo
-    and the residual, ffn_norm, the MoE block on the device with the residual. Distinct
+    and the residual, the MoE block on the device with ffn_norm and the residual. Distinct
     weights, caches and expert banks per layer (synthetic; the banks are device copies
     of one random template, 642 MB per layer, 30.8 GB for 48 layers), the residual
     stream x shared and reset from x0 at the start of each sweep (an 8 KB copy)."""
@@ -372,7 +372,7 @@ class DecodeLayerSweep:
         f4 = 4
         mk = ctx.createBuffer
         self.x0 = ctx.from_numpy(g.standard_normal((1, hidden)).astype(np.float32))
-        self.x, self.h2 = mk(hidden * f4), mk(hidden * f4)
+        self.x = mk(hidden * f4)
         q, k, v = mk(hq * d * f4), mk(hkv * d * f4), mk(hkv * d * f4)
         attn = mk(hq * d * f4)
         pos = ctx_len - 1
@@ -401,9 +401,9 @@ class DecodeLayerSweep:
                 None,
                 H.AttentionBlockArgs(self.x, wq, wk, wv, H.DTYPE_Q8_0, hidden, step, an, eps),
                 H.MatmulAddArgs(attn, wo, H.DTYPE_Q8_0, self.x, self.x, 1, hidden, hq * d),
-                H.RmsNormArgs(self.x, fn, self.h2, 1, hidden, eps),
-                H.MoeArgs(self.h2, router, H.DTYPE_F32, gate, up, down, H.DTYPE_Q8_0, self.x, empty, empty, 1,
-                          hidden, ffn, E, K, 1, self.x)))
+                None,
+                H.MoeArgs(self.x, router, H.DTYPE_F32, gate, up, down, H.DTYPE_Q8_0, self.x, empty, empty, 1,
+                          hidden, ffn, E, K, 1, self.x, fn, eps)))
         del gu_t, dn_t
         self.hidden = hidden
         self.marks = False
@@ -412,8 +412,7 @@ class DecodeLayerSweep:
         H, ctx = self.H, self.ctx
         H.attentionBlock(ctx, a[1])  # attn_norm inside
         H.matmulAdd(ctx, a[2])
-        H.rmsNorm(ctx, a[3])
-        H.moe(ctx, a[4])  # x + the experts' sum (the engine's fused order)
+        H.moe(ctx, a[4])  # ffn_norm inside, x + the experts' sum (the engine's fused order)
 
     def sweep(self):
         self.ctx.copy_device(self.x, self.x0, self.hidden * 4)
@@ -1108,7 +1107,7 @@ def main():
             separate_legs_us=part_us, separate_legs_sum_us=round(sum(part_us.values()), 3) if len(part_us) == 4 else None,
             kernel_us_per_layer=per_layer, kernel_sum_us_per_layer=round(sum(per_layer.values()), 3),
             shape="1 token, hidden 2048, 32q/4kv d128, 8K f16 cache, Q8_0 wq/wk/wv/wo, 128 experts top 8 ffn 768; "
-                  "attention block with attn_norm, Wo + residual, ffn_norm, MoE + residual (4 calls per layer)")
+                  "attention block with attn_norm, Wo + residual, MoE with ffn_norm and residual (3 calls per layer)")
         log(f"[bench] LAYER {us:.3f} us/layer (graph of 48 layers); eager per-layer marks mean {ns.mean():.3f} "
             f"min {ns.min():.3f} max {ns.max():.3f} us; separate legs {part_us}; kernels per layer {per_layer}")
         del w

@@ -341,6 +341,12 @@ typedef struct ds5_moe_args {
     uint32_t top_k;
     uint32_t norm_topk_prob;
     ds5_buf residual;          /* optional f32 [n_tokens, dim] */
+    ds5_buf x_norm;            /* optional f32 [dim]: ds5_hip_rms_norm(x, x_norm, x_norm_eps)
+                                * first (forward.zig:420-428's ffn_norm), bit for bit, inside
+                                * the router's logits kernel (f32 router, rows of more than
+                                * 256 elements) or else into a context buffer; its checks
+                                * come first; x itself is left as it is (it may be residual) */
+    float x_norm_eps;
 } ds5_moe_args;
 int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* args);
 

@@ -196,6 +196,12 @@ struct RouterLaunch {
     float* weights;
     ds5_pair* pairs;  // may be null
     float* logits;    // scratch [n_tokens, n_experts]
+    // x normalised first (f32 rows of dim % 4 == 0 and dim > 256, x and w 16-byte
+    // aligned: the logits kernel's fast path; the tree order), the normalised rows
+    // written to h_out for the experts; null: x as it is
+    const float* x_norm_w;
+    float x_norm_eps;
+    float* h_out;
 };
 int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a);
 

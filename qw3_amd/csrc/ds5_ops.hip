@@ -286,22 +286,23 @@ struct MoeScratch {
     float* y;
     uint16_t* ids;
     float* weights;
+    float* h2;  // the normalised x, when the router applies the norm
 };
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static int moe_scratch(ds5_hip_ctx* ctx, uint64_t T, uint64_t E, uint64_t P, uint64_t dim, uint64_t ffn,
                        MoeScratch* s) {
-    const size_t sz[8] = {up256(T * E * 4), up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4),
-                          up256(P * ffn * 4), up256(P * dim * 4), up256(P * 2), up256(P * 4)};
+    const size_t sz[9] = {up256(T * E * 4), up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4),
+                          up256(P * ffn * 4), up256(P * dim * 4), up256(P * 2), up256(P * 4), up256(T * dim * 4)};
     size_t total = 0;
     for (size_t v : sz) total += v;
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, total, &ws)) return rc;
     char* p = (char*)ws;
-    void** dst[8] = {(void**)&s->logits, (void**)&s->pairs, (void**)&s->order, (void**)&s->offsets,
-                     (void**)&s->h, (void**)&s->y, (void**)&s->ids, (void**)&s->weights};
-    for (int i = 0; i < 8; i++) {
+    void** dst[9] = {(void**)&s->logits, (void**)&s->pairs, (void**)&s->order, (void**)&s->offsets,
+                     (void**)&s->h, (void**)&s->y, (void**)&s->ids, (void**)&s->weights, (void**)&s->h2};
+    for (int i = 0; i < 9; i++) {
         *dst[i] = p;
         p += sz[i];
     }
@@ -399,6 +400,14 @@ int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* a) {
 int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     if (!a) return DS5_SHAPE_MISMATCH;
     const uint64_t TK = (uint64_t)a->n_tokens * a->top_k;
+    // x_norm: rmsNorm(x -> h) first (its checks first), then the block on h
+    const bool norm = a->x_norm.len != 0;
+    if (norm) {
+        const uint64_t T = a->n_tokens, D = a->dim;
+        if (D == 0) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: dim == 0");
+        if (!covers(a->x, T * D * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: x too small");
+        if (!covers(a->x_norm, D * 4)) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: x_norm too small");
+    }
     if (int rc = check_router(ctx, "moe", a->x, a->router_w, a->router_dtype, a->n_tokens, a->dim, a->n_experts,
                               a->top_k, true))
         return rc;
@@ -412,6 +421,24 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     if (a->n_tokens == 0) return DS5_OK;
     if (TK > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: too many pairs");
     if (int rc = set_device(ctx)) return rc;
+    // The norm runs inside the router's logits kernel (its f32 fast path, rows of more
+    // than 256 elements: the tree order), which also writes h for the experts; otherwise
+    // rmsNorm writes h to the context's second buffer first and the block runs on h.
+    const bool norm_inside = norm && a->dim > kRmsSerialMaxDim && a->dim % 4 == 0 &&
+                             a->router_dtype == DS5_DTYPE_F32 && aligned16(a->x) && aligned16(a->router_w) &&
+                             aligned16(a->x_norm);
+    if (norm && !norm_inside) {
+        void* h = nullptr;
+        const uint64_t bytes = (uint64_t)a->n_tokens * a->dim * 4;
+        if (int rc = ds5_aux_workspace(ctx, bytes, &h)) return rc;
+        if (int rc = launch_rms_norm(ctx, RmsNormLaunch{(const float*)ds5_ptr(a->x), (const float*)ds5_ptr(a->x_norm),
+                                                        (float*)h, a->n_tokens, a->dim, a->x_norm_eps}))
+            return rc;
+        ds5_moe_args b = *a;
+        b.x = ds5_buf{h, 0, bytes};
+        b.x_norm = ds5_buf{};
+        return ds5_hip_moe(ctx, &b);
+    }
     MoeScratch s{};
     if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, a->dim, a->ffn_dim, &s)) return rc;
     RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->router_w), a->router_dtype,
@@ -419,8 +446,14 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
                    a->norm_topk_prob != 0,
                    a->ids.len ? (uint16_t*)ds5_ptr(a->ids) : s.ids,
                    a->weights.len ? (float*)ds5_ptr(a->weights) : s.weights, s.pairs, s.logits};
+    if (norm_inside) {
+        r.x_norm_w = (const float*)ds5_ptr(a->x_norm);
+        r.x_norm_eps = a->x_norm_eps;
+        r.h_out = s.h2;
+    }
     if (int rc = launch_router(ctx, r)) return rc;
-    ExpertLaunch l = expert_launch(a->x, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)TK,
+    const ds5_buf ex = norm_inside ? ds5_buf{s.h2, 0, (uint64_t)a->n_tokens * a->dim * 4} : a->x;
+    ExpertLaunch l = expert_launch(ex, a->gate, a->up, a->down, a->w_dtype, a->out, a->n_tokens, (uint32_t)TK,
                                    a->dim, a->ffn_dim, a->n_experts, s);
     l.top_k = a->top_k;  // token t's pairs are t * top_k .. (t + 1) * top_k - 1
     l.res = a->residual.len ? (const float*)ds5_ptr(a->residual) : nullptr;  // every token has top_k >= 1 pairs

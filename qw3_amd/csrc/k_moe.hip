@@ -154,7 +154,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const flo
                                                                        const uint8_t* __restrict__ w,
                                                                        uint64_t row_bytes, uint32_t dim,
                                                                        uint32_t n_experts, uint32_t rows,
-                                                                       float* __restrict__ logits) {
+                                                                       float* __restrict__ logits,
+                                                                       const float* __restrict__ nw, float eps,
+                                                                       float* __restrict__ h_out) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float router_smem[];
     float* xs = router_smem;
@@ -172,12 +174,42 @@ __global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const flo
             f32x4* p4s = (f32x4*)ws;
             constexpr int kN = kRouterRowBytes / 16 / kRouterThreads;
             f32x4 wv[kN], xv[kN];
+            if (nw) {  // uniform: ffn_norm first, h = (x * inv) * nw, inv in the tree order
+                // the rows first, so their latency covers the norm
 #pragma unroll
-            for (int k = 0; k < kN; k++) {
-                const uint32_t u = threadIdx.x + kRouterThreads * k;
-                if (u < total) {
-                    wv[k] = g4[u];
-                    xv[k] = xg4[u % n4];
+                for (int k = 0; k < kN; k++) {
+                    const uint32_t u = threadIdx.x + kRouterThreads * k;
+                    if (u < total) wv[k] = g4[u];
+                }
+                f32x4* xs4 = (f32x4*)xs;
+                for (uint32_t c = threadIdx.x; c < n4; c += kRouterThreads) xs4[c] = xg4[c];
+                __syncthreads();
+                __shared__ float s_part[kTreeParts];
+                __shared__ float s_inv;
+                float sq = 0.0f;
+                for (uint32_t i = threadIdx.x; i < dim; i += kTreeParts) sq = __builtin_fmaf(xs[i], xs[i], sq);
+                const float inv = tree_rms_inv(sq, dim, eps, s_part, &s_inv);
+                for (uint32_t c = threadIdx.x; c < n4; c += kRouterThreads) {
+                    const f32x4 v = xs4[c], ww = ((const f32x4*)nw)[c];
+                    const f32x4 hv = f32x4{v[0] * inv * ww[0], v[1] * inv * ww[1], v[2] * inv * ww[2],
+                                           v[3] * inv * ww[3]};
+                    xs4[c] = hv;
+                    if (blockIdx.y == 0) ((f32x4*)(h_out + (uint64_t)t * dim))[c] = hv;  // for the experts
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < kN; k++) {
+                    const uint32_t u = threadIdx.x + kRouterThreads * k;
+                    if (u < total) xv[k] = xs4[u % n4];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < kN; k++) {
+                    const uint32_t u = threadIdx.x + kRouterThreads * k;
+                    if (u < total) {
+                        wv[k] = g4[u];
+                        xv[k] = xg4[u % n4];
+                    }
                 }
             }
 #pragma unroll
@@ -668,7 +700,8 @@ static int launch_router_t(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     }
     const dim3 grid(a.n_tokens, (a.n_experts + rows - 1) / rows);
     DS5_TIMED_LAUNCH(ctx, "router_logits_kernel", (router_logits_kernel<DT, CP>), grid, dim3(kRouterThreads), smem,
-                     ctx->stream, a.x, a.w, a.row_bytes, a.dim, a.n_experts, rows, a.logits);
+                     ctx->stream, a.x, a.w, a.row_bytes, a.dim, a.n_experts, rows, a.logits, a.x_norm_w,
+                     a.x_norm_eps, a.h_out);
     return ds5_after_launch(ctx, "router_logits_kernel");
 }
 

@@ -20,10 +20,11 @@ Two modes:
   never written in f32; with a trace callback set, the same work as its calls,
   `rmsNorm`, `matmulGroup` then `attentionStep`, which the block equals bit for bit,
   so those trace points exist), Wo and its residual as one `matmulAdd`, and
-  the MoE block and its residual as one `moe` (router and experts with the pairs kept
-  on the device, x + the experts' sum written in the combine; with a trace callback
-  set, `moe` into the zeroed accumulator then `add`, which it equals bit for bit, so
-  the experts trace point exists).
+  ffn_norm, the MoE block and its residual as one `moe` (ffn_norm inside the router's
+  logits kernel, router and experts with the pairs kept on the device, x + the
+  experts' sum written in the combine; with a trace callback set, `rmsNorm`, `moe`
+  into the zeroed accumulator then `add`, which it equals bit for bit, so those trace
+  points exist).
 Both produce the residual stream of forward.zig within the reference's layer
 tolerance; the per-op calls of the fused mode are bit-identical to the separate ones
 where the ABI says so (matmulGroup, matmulAdd, moe).
@@ -225,22 +226,23 @@ class Engine:
             self._trace(li, "attn_resid", self.x, n * hidden)
 
             ffn_norm, _ = self.w.layer(li, "ffn_norm.weight")
-            H.rmsNorm(ctx, H.RmsNormArgs(self.x, ffn_norm, self.h2, n, hidden, eps))
-            self._trace(li, "ffn_norm", self.h2, n * hidden)
             router, dr = self.w.layer(li, "ffn_gate_inp.weight")
             gate, dg = self.w.layer(li, "ffn_gate_exps.weight")
             up, _ = self.w.layer(li, "ffn_up_exps.weight")
             down, _ = self.w.layer(li, "ffn_down_exps.weight")
             if self.fused and self.trace is None:
-                # x = x + the experts' sum in one call: the sum starts from zero and the
-                # residual is added once, as the zeroed accumulator and the add give it
-                H.moe(ctx, H.MoeArgs(self.h2, router, dr, gate, up, down, dg, self.x, H.Buf(), H.Buf(), n,
+                # x = x + the experts' sum of ffn_norm(x) in one call: the norm inside it,
+                # the sum started from zero and the residual added once, as rmsNorm, the
+                # zeroed accumulator and the add give them
+                H.moe(ctx, H.MoeArgs(self.x, router, dr, gate, up, down, dg, self.x, H.Buf(), H.Buf(), n,
                                      hidden, c["expert_ffn_dim"], c["n_experts"], c["top_k"],
-                                     int(c["norm_topk_prob"]), self.x))
+                                     int(c["norm_topk_prob"]), self.x, ffn_norm, eps))
                 if self.timing:
                     ctx.timing_mark()
                 self._trace(li, "block", self.x, n * hidden)
                 continue
+            H.rmsNorm(ctx, H.RmsNormArgs(self.x, ffn_norm, self.h2, n, hidden, eps))
+            self._trace(li, "ffn_norm", self.h2, n * hidden)
             # proj doubles as the MoE accumulator and must start at zero (forward.zig:452-454):
             # the eight-op mode uploads zeros as the reference does; the fused mode clears it
             # on the device (no host copy or synchronisation inside the layer)

@@ -129,7 +129,8 @@ class MoeArgs(C.Structure):
     _fields_ = [("x", Buf), ("router_w", Buf), ("router_dtype", C.c_uint32), ("gate", Buf), ("up", Buf),
                 ("down", Buf), ("w_dtype", C.c_uint32), ("out", Buf), ("ids", Buf), ("weights", Buf),
                 ("n_tokens", C.c_uint32), ("dim", C.c_uint32), ("ffn_dim", C.c_uint32), ("n_experts", C.c_uint32),
-                ("top_k", C.c_uint32), ("norm_topk_prob", C.c_uint32), ("residual", Buf)]
+                ("top_k", C.c_uint32), ("norm_topk_prob", C.c_uint32), ("residual", Buf), ("x_norm", Buf),
+                ("x_norm_eps", C.c_float)]
 
 
 MATMUL_GROUP_MAX = 4

@@ -1090,6 +1090,47 @@ def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
                                  K, 1, hip.Buf(rb.handle, rb.offset, T * dim * 4 - 4)))
 
 
+@pytest.mark.parametrize("T,dim,rdt", [(1, 2048, "f32"), (5, 2048, "f32"), (3, 2048, "f16"), (2, 256, "f32")])
+def test_moe_norm_equals_rmsnorm_then_moe(ctx, hip, oracle, T, dim, rdt):
+    """ds5_hip_moe with x_norm (ffn_norm applied first) and the residual equals
+    ds5_hip_rms_norm(x -> h2) then ds5_hip_moe(h2) with the residual, bit for bit, and
+    leaves x as it was when out is another buffer: the norm inside the router's f32 logits
+    kernel (rows above 256 elements), or written to the context's second buffer first (an
+    f16 router; dim 256: the serial order). The router ids and weights agree too."""
+    g = np.random.default_rng(300 + T + dim)
+    ffn, E, K = (768, 64, 8) if dim == 2048 else (64, 8, 2)
+    rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
+    rwv = rw if rdt == "f32" else rw.astype(np.float16)
+    rdtype = hip.DTYPE_F32 if rdt == "f32" else hip.DTYPE_F16
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    banks = [ctx.from_numpy(v) for v in (mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn))]
+    x = (g.standard_normal((T, dim)) * np.exp(g.uniform(-3, 3, (T, 1)))).astype(np.float32)
+    nw = (1.0 + 0.05 * g.standard_normal(dim)).astype(np.float32)
+    xb, rwb, nwb = ctx.from_numpy(x), ctx.from_numpy(rwv), ctx.from_numpy(nw)
+    empty = hip.Buf()
+    ids1, w1 = ctx.createBuffer(T * K * 2), ctx.createBuffer(T * K * 4)
+    out1 = ctx.createBuffer(T * dim * 4)
+    hip.moe(ctx, hip.MoeArgs(xb, rwb, rdtype, *banks, hip.DTYPE_Q8_0, out1, ids1, w1, T, dim, ffn, E, K, 1, xb, nwb,
+                             1e-6))
+    h2 = ctx.createBuffer(T * dim * 4)
+    hip.rmsNorm(ctx, hip.RmsNormArgs(xb, nwb, h2, T, dim, 1e-6))
+    ids2, w2 = ctx.createBuffer(T * K * 2), ctx.createBuffer(T * K * 4)
+    out2 = ctx.createBuffer(T * dim * 4)
+    hip.moe(ctx, hip.MoeArgs(h2, rwb, rdtype, *banks, hip.DTYPE_Q8_0, out2, ids2, w2, T, dim, ffn, E, K, 1, xb))
+    a, b = ctx.to_numpy(out1, np.float32, (T, dim)), ctx.to_numpy(out2, np.float32, (T, dim))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(ctx.to_numpy(ids1, np.uint16, (T, K)), ctx.to_numpy(ids2, np.uint16, (T, K)))
+    assert np.array_equal(ctx.to_numpy(w1, np.uint32, (T, K)), ctx.to_numpy(w2, np.uint32, (T, K)))
+    assert np.array_equal(ctx.to_numpy(xb, np.float32, (T, dim)).view(np.uint32), x.view(np.uint32))
+    inplace = ctx.from_numpy(x)  # out = residual = x: the engine's form
+    hip.moe(ctx, hip.MoeArgs(inplace, rwb, rdtype, *banks, hip.DTYPE_Q8_0, inplace, empty, empty, T, dim, ffn, E, K, 1,
+                             inplace, nwb, 1e-6))
+    assert np.array_equal(ctx.to_numpy(inplace, np.float32, (T, dim)).view(np.uint32), b.view(np.uint32))
+    with pytest.raises(hip.ShapeMismatch):
+        hip.moe(ctx, hip.MoeArgs(xb, rwb, rdtype, *banks, hip.DTYPE_Q8_0, out1, empty, empty, T, dim, ffn, E, K, 1,
+                                 xb, hip.Buf(nwb.handle, nwb.offset, dim * 4 - 4), 1e-6))
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):
