@@ -69,6 +69,9 @@ struct ds5_hip_ctx {
     // plan: workgroups per launch the plan aims at (0 = two per CU).
     uint32_t decode_chunk = 0;
     uint32_t plan_items = 0;
+    // DS5_HIP_MOE_TWO_LAUNCH: the experts' down GEMV and the combine as the two
+    // launches that serve outputs beyond one grid, at any size (tests of that path)
+    bool moe_two_launch = false;
     // Optional per-kernel timing: events recorded around every launch on the
     // context stream, resolved at submit / query time.
     bool kernel_timing = false;

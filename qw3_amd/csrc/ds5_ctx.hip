@@ -136,6 +136,7 @@ int ds5_hip_init(int device_index, ds5_hip_ctx** out) {
     }
     if (const char* s = getenv("DS5_HIP_DECODE_CHUNK")) ctx->decode_chunk = (uint32_t)strtoul(s, nullptr, 10);
     if (const char* s = getenv("DS5_HIP_PLAN_ITEMS")) ctx->plan_items = (uint32_t)strtoul(s, nullptr, 10);
+    if (const char* s = getenv("DS5_HIP_MOE_TWO_LAUNCH")) ctx->moe_two_launch = strtoul(s, nullptr, 10) != 0;
     *out = ctx;
     return DS5_OK;
 }

@@ -494,7 +494,64 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(const float
     if (lane == 0) h[r] = g / (1.0f + expf(-g)) * u;  // silu(g) * u, kernels_c.zig:70-72
 }
 
+// Q8_0 down rows, 8 per wavefront: lane (r, s) = (lane / 8, lane % 8) takes row r of
+// `rows` (row_f bytes apart) and the blocks s, s + 8, s + 16, ... of the pair's h
+// (hp), adding scale * (q . h) per block in that order with every load of a batch of
+// kPer blocks in flight; then the row's 8 slots add in a fixed tree (xor 1, xor 2,
+// the two quads): every lane of row r returns the row's dot product. All 64 lanes
+// run the DPP moves (the loop ends uniformly after the batches).
+constexpr uint32_t kDownRows = 8;
+__device__ __forceinline__ float down_rows8_q8(const float* __restrict__ hp, const uint8_t* rows,
+                                               const uint8_t* __restrict__ down, uint64_t row_f, uint32_t nb,
+                                               int lane) {
+#pragma clang fp contract(off)
+    const int r = lane >> 3, s = lane & 7;
+    float a = 0.0f;
+    constexpr int kPer = 3;
+    for (uint32_t b0 = s; b0 < nb; b0 += 8 * kPer) {
+        uint32_t d[kPer][9], sh[kPer];
+        float4 xv[kPer][8];
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const uint32_t bb = min(b0 + 8 * j, nb - 1);  // past the row: a valid block, not added
+            const uint64_t off = (uint64_t)(rows - down) + (uint64_t)r * row_f + (uint64_t)bb * kQ8Bytes;
+            sh[j] = (uint32_t)off & 3u;
+            const uint32_t* pw = (const uint32_t*)(down + (off - sh[j]));
+#pragma unroll
+            for (int k = 0; k < 9; k++) d[j][k] = pw[k];
+            const float4* xs = (const float4*)(hp + 32 * bb);
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[j][k] = xs[k];
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            if (b0 + 8 * j < nb) {
+                float xr[32];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    xr[4 * k] = xv[j][k].x;
+                    xr[4 * k + 1] = xv[j][k].y;
+                    xr[4 * k + 2] = xv[j][k].z;
+                    xr[4 * k + 3] = xv[j][k].w;
+                }
+                const Q8Block blk = q8_unpack(d[j], sh[j]);
+                a = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), a);
+            }
+        }
+    }
+    float o = dpp_mov<0xB1>(a);  // quad_perm [1, 0, 3, 2]
+    asm volatile("" : "+v"(o));
+    a += o;
+    o = dpp_mov<0x4E>(a);  // quad_perm [2, 3, 0, 1]
+    asm volatile("" : "+v"(o));
+    a += o;
+    o = dpp_mov<0x141>(a);  // row_half_mirror: the other quad of the 8 lanes
+    asm volatile("" : "+v"(o));
+    return a + o;
+}
+
 // One wavefront per (pair, output row i); h rows 16-byte aligned (ffn % 32 == 0).
+// Q8_0: one wavefront per (pair, 8 output rows), down_rows8_q8's lanes and order.
 template <bool Q8>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* __restrict__ h,
                                                                   const uint8_t* __restrict__ down,
@@ -506,20 +563,30 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(const float* _
                  "s"(stride));
     const int lane = threadIdx.x & 63;
     const uint64_t r = (uint64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
-    if (r >= (uint64_t)n_pairs * dim) return;  // wave-uniform
-    const uint32_t p = (uint32_t)(r / dim), i = (uint32_t)(r % dim);
-    const uint64_t row = (uint64_t)pairs[p].expert * stride + (uint64_t)i * row_f;
-    const float v = wave_allreduce(lane_dot<Q8>(h + (uint64_t)p * ffn, down + row, down, ffn, lane), OpAdd{});
-    if (lane == 0) y[r] = v;
+    if constexpr (Q8) {  // wavefront r: rows 8 (r % (dim / 8)) .. + 7 of pair r / (dim / 8)
+        const uint32_t groups = dim / kDownRows;
+        if (r >= (uint64_t)n_pairs * groups) return;  // wave-uniform
+        const uint32_t p = (uint32_t)(r / groups), i0 = (uint32_t)(r % groups) * kDownRows;
+        const uint8_t* rows = down + (uint64_t)pairs[p].expert * stride + (uint64_t)i0 * row_f;
+        const float v = down_rows8_q8(h + (uint64_t)p * ffn, rows, down, row_f, ffn / 32, lane);
+        if ((lane & 7) == 0) y[(uint64_t)p * dim + i0 + (lane >> 3)] = v;
+    } else {
+        if (r >= (uint64_t)n_pairs * dim) return;  // wave-uniform
+        const uint32_t p = (uint32_t)(r / dim), i = (uint32_t)(r % dim);
+        const uint64_t row = (uint64_t)pairs[p].expert * stride + (uint64_t)i * row_f;
+        const float v = wave_allreduce(lane_dot<Q8>(h + (uint64_t)p * ffn, down + row, down, ffn, lane), OpAdd{});
+        if (lane == 0) y[r] = v;
+    }
 }
 
 // The down GEMV and the combine in one launch: workgroup (token t, output rows
 // i0 .. i0 + 7), wavefront w computing y[p][i] of those 8 rows for the token's
-// pair q0 + w (+ 8, ...) with moe_down_kernel's lane layout and order (its h
-// block read once for the 8 rows), then thread r adding w_p * y[p][i0 + r] into
-// out[t][i0 + r] in list order, as moe_combine_kernel does: bit-identical to the
-// two launches, without the y round trip through memory. dim % 8 == 0.
-constexpr uint32_t kDownRows = 8;
+// pair q0 + w (+ 8, ...) with moe_down_kernel's lane layout and order (Q8_0:
+// down_rows8_q8, all 64 lanes busy even when a row has fewer than 64 blocks; f32:
+// one block per lane and step, the h block read once for the 8 rows), then thread
+// r adding w_p * y[p][i0 + r] into out[t][i0 + r] in list order, as
+// moe_combine_kernel does: bit-identical to the two launches, without the y round
+// trip through memory. dim % 8 == 0.
 template <bool Q8>
 __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
     const float* __restrict__ h, const uint8_t* __restrict__ down, const ds5_pair* __restrict__ pairs,
@@ -550,37 +617,24 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
             const ds5_pair pr = pairs[p];
             const uint8_t* rows = down + (uint64_t)pr.expert * stride + (uint64_t)i0 * row_f;
             const float* hp = h + (uint64_t)p * ffn;
-            float a[kDownRows];
+            if constexpr (Q8) {
+                const float v = down_rows8_q8(hp, rows, down, row_f, nb, lane);
+                if ((lane & 7) == 0) ys[wv][lane >> 3] = v;
+            } else {
+                float a[kDownRows];
 #pragma unroll
-            for (uint32_t r = 0; r < kDownRows; r++) a[r] = 0.0f;
-            for (uint32_t b = lane; b < nb; b += 64) {
-                float xr[32];
-                const float4* xs = (const float4*)(hp + 32 * b);
+                for (uint32_t r = 0; r < kDownRows; r++) a[r] = 0.0f;
+                for (uint32_t b = lane; b < nb; b += 64) {
+                    float xr[32];
+                    const float4* xs = (const float4*)(hp + 32 * b);
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 v = xs[k];
-                    xr[4 * k] = v.x;
-                    xr[4 * k + 1] = v.y;
-                    xr[4 * k + 2] = v.z;
-                    xr[4 * k + 3] = v.w;
-                }
-                if constexpr (Q8) {
-                    uint32_t d[kDownRows][9];
-                    uint32_t sh[kDownRows];
-#pragma unroll
-                    for (uint32_t r = 0; r < kDownRows; r++) {
-                        const uint64_t off = (uint64_t)(rows - down) + r * row_f + (uint64_t)b * kQ8Bytes;
-                        sh[r] = (uint32_t)off & 3u;
-                        const uint32_t* pw = (const uint32_t*)(down + (off - sh[r]));
-#pragma unroll
-                        for (int k = 0; k < 9; k++) d[r][k] = pw[k];
+                    for (int k = 0; k < 8; k++) {
+                        const float4 v = xs[k];
+                        xr[4 * k] = v.x;
+                        xr[4 * k + 1] = v.y;
+                        xr[4 * k + 2] = v.z;
+                        xr[4 * k + 3] = v.w;
                     }
-#pragma unroll
-                    for (uint32_t r = 0; r < kDownRows; r++) {
-                        const Q8Block blk = q8_unpack(d[r], sh[r]);
-                        a[r] = __builtin_fmaf(blk.scale, q8_dot(blk.q, xr), a[r]);
-                    }
-                } else {
 #pragma unroll
                     for (uint32_t r = 0; r < kDownRows; r++) {
                         const float* wr = (const float*)(rows + r * row_f) + 32 * b;
@@ -590,11 +644,11 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_combine_kernel(
                         a[r] = a[r] + ((s4[0] + s4[1]) + (s4[2] + s4[3]));
                     }
                 }
-            }
 #pragma unroll
-            for (uint32_t r = 0; r < kDownRows; r++) {
-                const float v = wave_allreduce(a[r], OpAdd{});
-                if (lane == 0) ys[wv][r] = v;
+                for (uint32_t r = 0; r < kDownRows; r++) {
+                    const float v = wave_allreduce(a[r], OpAdd{});
+                    if (lane == 0) ys[wv][r] = v;
+                }
             }
             if (lane == 0) wts[wv] = pr.weight;
         }
@@ -740,9 +794,10 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     if (a.fast) {
         const dim3 blk(kMoeWaves * 64);
         const size_t xs_bytes = (size_t)a.dim * sizeof(float);  // the token's x, staged per gate/up workgroup
-        const dim3 g1((unsigned)((gu_rows + kMoeWaves - 1) / kMoeWaves)), g2((unsigned)((dn_rows + kMoeWaves - 1) / kMoeWaves));
+        const uint64_t dn_waves = a.q8 ? dn_rows / kDownRows : dn_rows;  // Q8_0: 8 rows per wavefront (dim % 32 == 0)
+        const dim3 g1((unsigned)((gu_rows + kMoeWaves - 1) / kMoeWaves)), g2((unsigned)((dn_waves + kMoeWaves - 1) / kMoeWaves));
         const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
-        if (outs > 0x7fffffffu) {  // more outputs than one grid holds workgroups: down, then the combine
+        if (outs > 0x7fffffffu || ctx->moe_two_launch) {  // more outputs than one grid holds workgroups: down, then the combine
             if (a.q8) {
                 DS5_TIMED_LAUNCH(ctx, "moe_gate_up_kernel", moe_gate_up_kernel<true>, g1, blk, xs_bytes, ctx->stream, a.x,
                                  a.gate, a.up, a.pairs, a.h, a.n_pairs, a.dim, a.ffn, a.row_h, a.stride_gu);

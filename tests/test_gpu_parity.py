@@ -1131,6 +1131,57 @@ def test_moe_norm_equals_rmsnorm_then_moe(ctx, hip, oracle, T, dim, rdt):
                                  xb, hip.Buf(nwb.handle, nwb.offset, dim * 4 - 4), 1e-6))
 
 
+@pytest.mark.parametrize("T,ffn", [(1, 768), (5, 768), (3, 2048), (2, 96)])
+def test_moe_two_launch_down_equals_fused_down(hip, oracle, T, ffn):
+    """The experts' down GEMV and combine as two launches (moe_down_kernel, then
+    moe_combine_kernel: the path for outputs beyond one grid, forced here with
+    DS5_HIP_MOE_TWO_LAUNCH, read when a context starts) equal the one-launch
+    moe_down_combine_kernel bit for bit, with and without the residual; ffn 96 and 768
+    leave lanes of the 8-slot layout without blocks, ffn 2048 gives each slot 8."""
+    import os
+    os.environ["DS5_HIP_MOE_TWO_LAUNCH"] = "1"
+    try:
+        c2 = hip.Ctx.init(0)
+    finally:
+        del os.environ["DS5_HIP_MOE_TWO_LAUNCH"]
+    c1 = hip.Ctx.init(0)
+    try:
+        g = np.random.default_rng(400 + T + ffn)
+        dim, E, K = 256, 16, 4
+        rw = (g.standard_normal((E, dim)) * 0.1).astype(np.float32)
+        mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+        G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+        x = g.standard_normal((T, dim)).astype(np.float32)
+        r = g.standard_normal((T, dim)).astype(np.float32)
+        outs = []
+        for c in (c1, c2):
+            xb, rwb, rb = c.from_numpy(x), c.from_numpy(rw), c.from_numpy(r)
+            banks = [c.from_numpy(v) for v in (G, U, D)]
+            acc, res_out = c.from_numpy(r), c.createBuffer(T * dim * 4)
+            hip.moe(c, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, acc, hip.Buf(), hip.Buf(), T, dim,
+                                   ffn, E, K, 1))
+            hip.moe(c, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, res_out, hip.Buf(), hip.Buf(), T,
+                                   dim, ffn, E, K, 1, rb))
+            c.set_kernel_timing(True)
+            try:
+                hip.moe(c, hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, c.createBuffer(T * dim * 4),
+                                       hip.Buf(), hip.Buf(), T, dim, ffn, E, K, 1))
+                c.submit()
+                launches = {kn: c.kernel_time(kn)[0] for kn in ("moe_down_combine_kernel", "moe_down_kernel",
+                                                                 "moe_combine_kernel")}
+            finally:
+                c.set_kernel_timing(False)
+            outs.append((c.to_numpy(acc, np.float32, (T, dim)), c.to_numpy(res_out, np.float32, (T, dim)), launches))
+        (a1, b1, l1), (a2, b2, l2) = outs
+        assert l1 == {"moe_down_combine_kernel": 1, "moe_down_kernel": 0, "moe_combine_kernel": 0}, l1
+        assert l2 == {"moe_down_combine_kernel": 0, "moe_down_kernel": 1, "moe_combine_kernel": 1}, l2
+        assert np.array_equal(a1.view(np.uint32), a2.view(np.uint32))
+        assert np.array_equal(b1.view(np.uint32), b2.view(np.uint32))
+    finally:
+        c1.deinit()
+        c2.deinit()
+
+
 def test_matmul_device_errors(ctx, hip):
     x, w, out = ctx.createBuffer(4 * 64), ctx.createBuffer(2 * 68), ctx.createBuffer(8)
     with pytest.raises(hip.UnsupportedDtype):
