@@ -207,6 +207,11 @@ struct RouterLaunch {
     float* h_out;
 };
 int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a);
+// The router's logits run in token x expert tiles (router_logits_tile_kernel) from
+// this many tokens, for f32 or f16 rows (dim % 4 == 0, x 16-byte and the rows 16- or
+// 8-byte aligned) without an in-kernel norm.
+constexpr uint32_t kRouterTileMinTokens = 32;
+bool router_tiled(uint32_t w_dtype, uint32_t n_tokens, uint32_t dim, const void* x, const void* w);
 
 // SwiGLU experts over device dispatch pairs; out accumulates. Token t's pairs
 // are order[offsets[t] .. offsets[t + 1]) in list order, or t*top_k .. when
@@ -226,8 +231,33 @@ struct ExpertLaunch {
     float* y;
     uint32_t n_tokens, n_pairs, dim, ffn;
     uint64_t row_h, row_f, stride_gu, stride_d;
+    // grouped: the products on the matrix cores over the pairs sorted by expert
+    // (Q8_0 banks, many pairs per expert); the scratch below, h holding the gate
+    // products and u the up products, y the down products in pair order
+    bool grouped;
+    uint32_t n_experts, max_tiles;
+    uint16_t *xhi, *xlo, *hhi, *hlo;
+    int *xexp, *hexp;
+    float* u;
+    uint32_t *perm, *xrow, *n_tiles;
+    uint4* tiles;
 };
+// The grouped path's row tiles: at most P / 128 + E of 128 rows (each expert's last
+// one partial).
+inline uint32_t moe_max_tiles(uint32_t n_pairs, uint32_t n_experts) { return n_pairs / 128 + n_experts + 1; }
+constexpr uint32_t kMoeGroupedMaxExperts = 2048;
 int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a);
+// The experts over rows sorted by expert on the matrix cores (k_matmul.hip): x rows
+// gathered by row_map and split into f16 planes; grouped Q8_0 products whose row
+// tiles come from a device table (first row, end row, expert); h = silu(g) * u split.
+int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, const uint32_t* row_map, uint32_t rows, uint32_t k,
+                        uint16_t* hi, uint16_t* lo, int* row_exp);
+int launch_moe_h_split(ds5_hip_ctx* ctx, const float* g, const float* u, uint32_t rows, uint32_t k, uint16_t* hi,
+                       uint16_t* lo, int* row_exp);
+int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp, uint32_t k,
+                           const uint8_t* const* w, float* const* out, const uint32_t* n, uint32_t count,
+                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint64_t w_stride,
+                           const uint32_t* out_rows);
 
 struct RmsNormLaunch {
     const float* x;

@@ -277,6 +277,15 @@ static bool experts_fast(ds5_buf x, ds5_buf gate, ds5_buf up, ds5_buf down, uint
     return true;
 }
 
+// The experts run grouped (sorted by expert, on the matrix cores) when their Q8_0
+// banks take the wavefront kernels and the pairs share experts: from two pairs per
+// expert on average, each expert's weights are read once instead of once per pair.
+static bool experts_grouped(bool fast, uint32_t dt, uint64_t P, uint64_t E, uint64_t dim, uint64_t ffn) {
+    return fast && dt == DS5_DTYPE_Q8_0 && E > 0 && E <= kMoeGroupedMaxExperts && P >= 2 * E &&
+           P * std::max(dim, ffn) * 2 < (1ull << 32) && row_bytes_of(dt, std::max(dim, ffn)) * std::max(dim, ffn) <
+                                                                (1ull << 31);
+}
+
 struct MoeScratch {
     float* logits;
     ds5_pair* pairs;
@@ -287,25 +296,42 @@ struct MoeScratch {
     uint16_t* ids;
     float* weights;
     float* h2;  // the normalised x, when the router applies the norm
+    // grouped experts
+    uint16_t *xhi, *xlo, *hhi, *hlo;
+    int *xexp, *hexp;
+    float* u;
+    uint32_t *perm, *xrow, *n_tiles;
+    uint4* tiles;
 };
 
 static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Scratch for the router (E experts' logits; 0: none) and the experts; nE: the
+// bank's expert count when the experts run grouped (0: not grouped).
 static int moe_scratch(ds5_hip_ctx* ctx, uint64_t T, uint64_t E, uint64_t P, uint64_t dim, uint64_t ffn,
-                       MoeScratch* s) {
-    const size_t sz[9] = {up256(T * E * 4), up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4),
-                          up256(P * ffn * 4), up256(P * dim * 4), up256(P * 2), up256(P * 4), up256(T * dim * 4)};
-    size_t total = 0;
+                       MoeScratch* s, uint64_t nE = 0) {
+    const uint64_t G = nE ? P : 0;  // rows of the grouped planes
+    const size_t sz[19] = {up256(T * E * 4), up256(P * sizeof(ds5_pair)), up256(P * 4), up256((T + 1) * 4),
+                           up256(P * ffn * 4), up256(P * dim * 4), up256(P * 2), up256(P * 4), up256(T * dim * 4),
+                           up256(G * dim * 2), up256(G * dim * 2), up256(G * ffn * 2), up256(G * ffn * 2),
+                           up256(G * 4), up256(G * 4), up256(G * ffn * 4), up256(G * 4), up256(G * 4),
+                           up256(nE ? 16 : 0)};
+    const size_t tiles_sz = nE ? up256((size_t)moe_max_tiles((uint32_t)P, (uint32_t)nE) * 16) : 0;
+    size_t total = tiles_sz;
     for (size_t v : sz) total += v;
     void* ws = nullptr;
     if (int rc = ds5_workspace(ctx, total, &ws)) return rc;
     char* p = (char*)ws;
-    void** dst[9] = {(void**)&s->logits, (void**)&s->pairs, (void**)&s->order, (void**)&s->offsets,
-                     (void**)&s->h, (void**)&s->y, (void**)&s->ids, (void**)&s->weights, (void**)&s->h2};
-    for (int i = 0; i < 9; i++) {
+    void** dst[19] = {(void**)&s->logits, (void**)&s->pairs, (void**)&s->order, (void**)&s->offsets,
+                      (void**)&s->h, (void**)&s->y, (void**)&s->ids, (void**)&s->weights, (void**)&s->h2,
+                      (void**)&s->xhi, (void**)&s->xlo, (void**)&s->hhi, (void**)&s->hlo, (void**)&s->xexp,
+                      (void**)&s->hexp, (void**)&s->u, (void**)&s->perm, (void**)&s->xrow, (void**)&s->n_tiles};
+    for (int i = 0; i < 19; i++) {
         *dst[i] = p;
         p += sz[i];
     }
+    s->tiles = nE ? (uint4*)p : nullptr;
+    if (!nE) s->n_tiles = nullptr;
     return DS5_OK;
 }
 
@@ -331,6 +357,22 @@ static ExpertLaunch expert_launch(const ds5_buf& x, const ds5_buf& gate, const d
     l.row_f = row_bytes_of(dt, ffn);
     l.stride_gu = l.row_h * ffn;
     l.stride_d = l.row_f * dim;
+    l.grouped = s.tiles != nullptr && s.n_tiles != nullptr && experts_grouped(l.fast, dt, P, E, dim, ffn);
+    if (l.grouped) {
+        l.n_experts = E;
+        l.max_tiles = moe_max_tiles(P, E);
+        l.xhi = s.xhi;
+        l.xlo = s.xlo;
+        l.hhi = s.hhi;
+        l.hlo = s.hlo;
+        l.xexp = s.xexp;
+        l.hexp = s.hexp;
+        l.u = s.u;
+        l.perm = s.perm;
+        l.xrow = s.xrow;
+        l.n_tiles = s.n_tiles;
+        l.tiles = s.tiles;
+    }
     return l;
 }
 
@@ -380,7 +422,10 @@ int ds5_hip_expert_mlp_swiglu(ds5_hip_ctx* ctx, const ds5_expert_mlp_args* a) {
         for (uint64_t p = 0; p < P; p++) order[fill[a->pairs[p].token]++] = (uint32_t)p;
     }
     MoeScratch s{};
-    if (int rc = moe_scratch(ctx, a->n_tokens, 0, P, a->dim, a->ffn_dim, &s)) return rc;
+    const bool grouped = experts_grouped(experts_fast(a->x, a->gate, a->up, a->down, a->w_dtype, a->dim, a->ffn_dim,
+                                                      a->n_experts),
+                                         a->w_dtype, P, a->n_experts, a->dim, a->ffn_dim);
+    if (int rc = moe_scratch(ctx, a->n_tokens, 0, P, a->dim, a->ffn_dim, &s, grouped ? a->n_experts : 0)) return rc;
     int rc = ds5_hip_status(ctx, hipMemcpyAsync(s.pairs, a->pairs, P * sizeof(ds5_pair), hipMemcpyHostToDevice,
                                                 ctx->stream), "pairs");
     if (!rc) rc = ds5_hip_status(ctx, hipMemcpyAsync(s.order, order.data(), P * 4, hipMemcpyHostToDevice, ctx->stream),
@@ -421,12 +466,14 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
     if (a->n_tokens == 0) return DS5_OK;
     if (TK > 0xffffffffull) return ds5_fail(ctx, DS5_SHAPE_MISMATCH, "moe: too many pairs");
     if (int rc = set_device(ctx)) return rc;
-    // The norm runs inside the router's logits kernel (its f32 fast path, rows of more
-    // than 256 elements: the tree order), which also writes h for the experts; otherwise
-    // rmsNorm writes h to the context's second buffer first and the block runs on h.
+    // The norm runs inside the router's per-token logits kernel (its f32 fast path, rows
+    // of more than 256 elements: the tree order), which also writes h for the experts;
+    // otherwise (also where the logits run in tiles) rmsNorm writes h to the context's
+    // second buffer first and the block runs on h.
     const bool norm_inside = norm && a->dim > kRmsSerialMaxDim && a->dim % 4 == 0 &&
                              a->router_dtype == DS5_DTYPE_F32 && aligned16(a->x) && aligned16(a->router_w) &&
-                             aligned16(a->x_norm);
+                             aligned16(a->x_norm) &&
+                             !router_tiled(a->router_dtype, a->n_tokens, a->dim, ds5_ptr(a->x), ds5_ptr(a->router_w));
     if (norm && !norm_inside) {
         void* h = nullptr;
         const uint64_t bytes = (uint64_t)a->n_tokens * a->dim * 4;
@@ -440,7 +487,15 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
         return ds5_hip_moe(ctx, &b);
     }
     MoeScratch s{};
-    if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, a->dim, a->ffn_dim, &s)) return rc;
+    const ds5_buf ex_in = norm_inside ? ds5_buf{} : a->x;  // the experts' x view (h2 when the router normalises)
+    const bool grouped = experts_grouped(
+        norm_inside ? (a->dim % 32 == 0 && a->ffn_dim % 32 == 0 &&
+                       experts_fast(ds5_buf{nullptr, 0, 0}, a->gate, a->up, a->down, a->w_dtype, a->dim, a->ffn_dim,
+                                    a->n_experts))
+                    : experts_fast(ex_in, a->gate, a->up, a->down, a->w_dtype, a->dim, a->ffn_dim, a->n_experts),
+        a->w_dtype, TK, a->n_experts, a->dim, a->ffn_dim);
+    if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, a->dim, a->ffn_dim, &s, grouped ? a->n_experts : 0))
+        return rc;
     RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->router_w), a->router_dtype,
                    row_bytes_of(a->router_dtype, a->dim), a->n_tokens, a->dim, a->n_experts, a->top_k,
                    a->norm_topk_prob != 0,

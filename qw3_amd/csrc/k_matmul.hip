@@ -263,49 +263,13 @@ struct XSplitRope {
     float freq_scale;
 };
 
-// One workgroup per x row: max |x|, its exponent E, then hi / lo of x * 2^(14 - E).
-// A row of zeros (or with a non-finite maximum) keeps E = 0. ROPE: also the
-// row's token's rope cos / sin. nw (if not null): the row is first normalised,
-// x' = (x * inv) * nw with inv in the reference GPU kernel's tree order
-// (tree_rms_inv), exactly as ds5_hip_rms_norm writes rows of more than 256
-// elements.
-template <bool ROPE>
-__global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const float* __restrict__ x,
-                                                                       uint16_t* __restrict__ hi,
-                                                                       uint16_t* __restrict__ lo,
-                                                                       int* __restrict__ row_exp, uint32_t k,
-                                                                       XSplitRope rope, RopeTable table,
-                                                                       const float* __restrict__ nw, float eps) {
-    static_assert(kSplitThreads >= kTreeParts, "one tree partial per thread");
-    __shared__ float red[kSplitThreads / 64];
-    __shared__ float s_part[kTreeParts];
-    __shared__ float s_inv;
-    const uint64_t row = blockIdx.x;
-    if constexpr (ROPE) {
-        const float pos = (float)rope.positions[row];
-        for (uint32_t i = threadIdx.x; i < rope.half; i += kSplitThreads) {
-            const float ang = qk_rope_angle(pos, rope.freq_scale, table.inv[i]);
-            rope.cs[row * 2 * rope.half + i] = cosf(ang);
-            rope.cs[row * 2 * rope.half + rope.half + i] = sinf(ang);
-        }
-    }
-    const float4* xr = (const float4*)(x + row * k);
+// Row `row` of the split planes from load(c) (float4 chunk c of the row's k values):
+// max |v|, its exponent E, then hi / lo of v * 2^(14 - E). A row of zeros (or with a
+// non-finite maximum) keeps E = 0. red: kSplitThreads / 64 floats of LDS.
+template <class F>
+__device__ __forceinline__ void split_row(F load, uint64_t row, uint32_t k, uint16_t* __restrict__ hi,
+                                          uint16_t* __restrict__ lo, int* __restrict__ row_exp, float* red) {
     const uint32_t kc = k / 4;
-    float inv = 1.0f;
-    if (nw) {  // uniform
-        float sq = 0.0f;
-        for (uint32_t i = threadIdx.x; i < k; i += kTreeParts) {
-            const float v = x[row * k + i];
-            sq = __builtin_fmaf(v, v, sq);
-        }
-        inv = tree_rms_inv(sq, k, eps, s_part, &s_inv);
-    }
-    auto load = [&](uint32_t c) {
-        const float4 v = xr[c];
-        if (!nw) return v;
-        const float4 w = ((const float4*)nw)[c];
-        return float4{v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w};
-    };
     float mx = 0.0f;
     for (uint32_t c = threadIdx.x; c < kc; c += kSplitThreads) {
         const float4 v = load(c);
@@ -335,6 +299,73 @@ __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const flo
         h2[c] = uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
         l2[c] = uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
     }
+}
+
+// One workgroup per x row: split_row of x. ROPE: also the
+// row's token's rope cos / sin. nw (if not null): the row is first normalised,
+// x' = (x * inv) * nw with inv in the reference GPU kernel's tree order
+// (tree_rms_inv), exactly as ds5_hip_rms_norm writes rows of more than 256
+// elements.
+template <bool ROPE>
+__global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const float* __restrict__ x,
+                                                                       uint16_t* __restrict__ hi,
+                                                                       uint16_t* __restrict__ lo,
+                                                                       int* __restrict__ row_exp, uint32_t k,
+                                                                       XSplitRope rope, RopeTable table,
+                                                                       const float* __restrict__ nw, float eps,
+                                                                       const uint32_t* __restrict__ row_map) {
+    static_assert(kSplitThreads >= kTreeParts, "one tree partial per thread");
+    __shared__ float red[kSplitThreads / 64];
+    __shared__ float s_part[kTreeParts];
+    __shared__ float s_inv;
+    const uint64_t row = blockIdx.x;
+    if constexpr (ROPE) {
+        const float pos = (float)rope.positions[row];
+        for (uint32_t i = threadIdx.x; i < rope.half; i += kSplitThreads) {
+            const float ang = qk_rope_angle(pos, rope.freq_scale, table.inv[i]);
+            rope.cs[row * 2 * rope.half + i] = cosf(ang);
+            rope.cs[row * 2 * rope.half + rope.half + i] = sinf(ang);
+        }
+    }
+    const uint64_t xrow = row_map ? row_map[row] : row;  // row_map: the planes' rows gather x rows
+    const float4* xr = (const float4*)(x + xrow * k);
+    float inv = 1.0f;
+    if (nw) {  // uniform
+        float sq = 0.0f;
+        for (uint32_t i = threadIdx.x; i < k; i += kTreeParts) {
+            const float v = x[xrow * k + i];
+            sq = __builtin_fmaf(v, v, sq);
+        }
+        inv = tree_rms_inv(sq, k, eps, s_part, &s_inv);
+    }
+    auto load = [&](uint32_t c) {
+        const float4 v = xr[c];
+        if (!nw) return v;
+        const float4 w = ((const float4*)nw)[c];
+        return float4{v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w};
+    };
+    split_row(load, row, k, hi, lo, row_exp, red);
+}
+
+// The planes of a MoE layer's expert products, for rows sorted by expert: row r of
+// h = silu(g) * u (kernels_c.zig:70-72, silu(v) = v / (1 + exp(-v))) from the gate
+// and up products g, u [rows, k] f32, split as matmul_x_split_kernel splits x.
+__global__ __launch_bounds__(kSplitThreads) void moe_h_split_kernel(const float* __restrict__ g,
+                                                                   const float* __restrict__ u,
+                                                                   uint16_t* __restrict__ hi,
+                                                                   uint16_t* __restrict__ lo,
+                                                                   int* __restrict__ row_exp, uint32_t k) {
+#pragma clang fp contract(off)
+    __shared__ float red[kSplitThreads / 64];
+    const uint64_t row = blockIdx.x;
+    const float4* gr = (const float4*)(g + row * k);
+    const float4* ur = (const float4*)(u + row * k);
+    auto load = [&](uint32_t c) {
+        const float4 a = gr[c], b = ur[c];
+        return float4{a.x / (1.0f + expf(-a.x)) * b.x, a.y / (1.0f + expf(-a.y)) * b.y,
+                      a.z / (1.0f + expf(-a.z)) * b.z, a.w / (1.0f + expf(-a.w)) * b.w};
+    };
+    split_row(load, row, k, hi, lo, row_exp, red);
 }
 
 // Four int8 (one dword) as four f16: bytes biased to q + 128, placed under the
@@ -405,12 +436,26 @@ struct AttnPrepEpi {
     float eps, q_scale;
 };
 
-template <int BM, int BN, int WM, int WN, int EPI>
+// GRP: the experts' products of a MoE layer over rows sorted by expert.
+// Workgroup row tile y is tiles[y] = (first row, end row, expert): its x rows are
+// those of the sorted planes in [first, end) (rows past the end read end - 1, a
+// row of the same expert, and store nothing), its weights the expert's matrix,
+// w + expert * w_stride; tiles past *count stop at once. Output row r goes to
+// row out_rows[r] (null: r).
+struct MoeGemmTiles {
+    const uint4* tiles;
+    const uint32_t* count;
+    uint64_t w_stride;
+    const uint32_t* out_rows;
+};
+
+template <int BM, int BN, int WM, int WN, int EPI, bool GRP = false>
 __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint16_t* __restrict__ xhi,
                                                                       const uint16_t* __restrict__ xlo,
                                                                       const int* __restrict__ row_exp,
                                                                       const WeightGroup g, uint32_t m, uint32_t k,
-                                                                      const AttnPrepEpi ep) {
+                                                                      const AttnPrepEpi ep,
+                                                                      const MoeGemmTiles mt) {
     asm volatile("" ::DS5_GROUP_ARGS(g), "s"(xhi), "s"(xlo), "s"(row_exp), "s"(m), "s"(k));
     // this workgroup's entry and column tile (uniform); out may be the residual itself
     const uint8_t* __restrict__ w = g.w[0];
@@ -428,6 +473,14 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
             tile = blockIdx.x - g.wg0[e];
             entry = e;
         }
+    uint32_t m0 = blockIdx.y * BM;
+    if constexpr (GRP) {
+        if (blockIdx.y >= *mt.count) return;  // workgroup-uniform, before any barrier
+        const uint4 te = mt.tiles[blockIdx.y];
+        m0 = te.x;
+        m = te.y;
+        w += (uint64_t)te.z * mt.w_stride;
+    }
     constexpr int kThreads = WM * WN * 64;
     constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
     static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN, "tile split");
@@ -449,7 +502,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t m0 = blockIdx.y * BM, n0 = tile * BN;
+    const uint32_t n0 = tile * BN;
     const uint32_t nb = k / 32;
     const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
 
@@ -713,11 +766,12 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
             const uint32_t row = m0 + wm0 + 16 * i + 4 * grp + e;
             if (row >= m) continue;
             const int sh = row_exp[row] - kXExpBias;
+            const uint32_t orow = GRP && mt.out_rows ? mt.out_rows[row] : row;
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint32_t col = n0 + wn0 + 16 * j + r16;
                 if (col < n) {
-                    const uint64_t o = (uint64_t)row * n + col;
+                    const uint64_t o = (uint64_t)orow * n + col;
                     const float v = __builtin_ldexpf(acc[i][j][e], sh);
                     out[o] = res ? res[o] + v : v;
                 }
@@ -829,7 +883,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     uint16_t* lo = hi + (size_t)a.m * a.k;
     int* row_exp = (int*)(lo + (size_t)a.m * a.k);
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{}, a.norm_w, a.norm_eps);
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{}, a.norm_w, a.norm_eps, nullptr);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     uint32_t tiles = 0;
@@ -845,11 +899,52 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     if (tiles == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
-                     AttnPrepEpi{});
+                     AttnPrepEpi{}, MoeGemmTiles{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
 
 }  // namespace
+
+// The MoE experts' matrix-core path (rows sorted by expert): the x rows gathered and
+// split, the grouped products, h = silu(g) * u split.
+int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, const uint32_t* row_map, uint32_t rows, uint32_t k,
+                        uint16_t* hi, uint16_t* lo, int* row_exp) {
+    if (rows == 0) return DS5_OK;
+    DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(rows), dim3(kSplitThreads), 0,
+                     ctx->stream, x, hi, lo, row_exp, k, XSplitRope{}, RopeTable{}, nullptr, 0.0f, row_map);
+    return ds5_after_launch(ctx, "matmul_x_split_kernel");
+}
+
+int launch_moe_h_split(ds5_hip_ctx* ctx, const float* g, const float* u, uint32_t rows, uint32_t k, uint16_t* hi,
+                       uint16_t* lo, int* row_exp) {
+    if (rows == 0) return DS5_OK;
+    DS5_TIMED_LAUNCH(ctx, "moe_h_split_kernel", moe_h_split_kernel, dim3(rows), dim3(kSplitThreads), 0, ctx->stream,
+                     g, u, hi, lo, row_exp, k);
+    return ds5_after_launch(ctx, "moe_h_split_kernel");
+}
+
+int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp, uint32_t k,
+                           const uint8_t* const* w, float* const* out, const uint32_t* n, uint32_t count,
+                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint64_t w_stride,
+                           const uint32_t* out_rows) {
+    constexpr int BM = 128, BN = 128, WM = 4, WN = 2;
+    WeightGroup g{};
+    uint32_t nt = 0;
+    for (uint32_t e = 0; e < count; e++) {
+        g.w[e] = w[e];
+        g.out[e] = out[e];
+        g.n[e] = n[e];
+        g.wg0[e] = nt;
+        nt += (n[e] + BN - 1) / BN;
+    }
+    g.count = count;
+    if (nt == 0 || max_tiles == 0) return DS5_OK;
+    const MoeGemmTiles mt{tiles, n_tiles, w_stride, out_rows};
+    DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, true>),
+                     dim3(nt, max_tiles), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k, AttnPrepEpi{},
+                     mt);
+    return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
+}
 
 // The rope table follows the x split at the next 16-byte boundary (the epilogue
 // reads it in float4s).
@@ -867,7 +962,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     float* cs = (float*)((char*)a.ws + qkv_prep_cs_offset(a.m, a.k));
     XSplitRope rope{a.positions, cs, a.head_dim / 2, a.freq_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<true>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table, a.norm_w, a.norm_eps);
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table, a.norm_w, a.norm_eps, nullptr);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     const uint32_t ns[3] = {a.n_q_heads * a.head_dim, a.n_kv_heads * a.head_dim, a.n_kv_heads * a.head_dim};
@@ -883,7 +978,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     AttnPrepEpi ep{a.q_norm, a.k_norm, cs, a.q16, a.k_cache, a.v_cache, a.pos, a.n_q_heads, a.max_ctx, a.eps, a.q_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1>),
                      dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
-                     ep);
+                     ep, MoeGemmTiles{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
 

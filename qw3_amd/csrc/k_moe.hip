@@ -251,6 +251,112 @@ __global__ __launch_bounds__(kRouterThreads) void router_logits_kernel(const flo
     }
 }
 
+// Logits for many tokens (router_logits_tile_kernel): workgroup (16 RT tokens, 16 RT
+// experts) stages chunks of kRtK elements of x and of the expert rows (f16 widened
+// to f32 exactly) in LDS, transposed, two chunks in turn; thread (tx, ty) keeps the
+// RT x RT logits of tokens RT ty + a and experts RT tx + b, each dotRow's serial sum
+// (kernels_c.zig:40-68): the product rounded, then added, in element order. The
+// chains of the thread's logits interleave, so the adds' latency is covered; RT 2
+// shares each LDS read among more products, RT 1 gives four times the workgroups.
+constexpr uint32_t kRtK = 64;
+
+template <uint32_t DT>
+__device__ __forceinline__ f32x4 router_tile_w4(const uint8_t* row, uint32_t i) {
+    if constexpr (DT == DS5_DTYPE_F32) {
+        return *(const f32x4*)(row + 4 * (uint64_t)i);
+    } else {
+        const uint2 v = *(const uint2*)(row + 2 * (uint64_t)i);
+        return f32x4{f16_bits_to_f32(v.x & 0xffffu), f16_bits_to_f32(v.x >> 16), f16_bits_to_f32(v.y & 0xffffu),
+                     f16_bits_to_f32(v.y >> 16)};
+    }
+}
+
+template <uint32_t DT, int RT>
+__global__ __launch_bounds__(256) void router_logits_tile_kernel(const float* __restrict__ x,
+                                                                 const uint8_t* __restrict__ w, uint64_t row_bytes,
+                                                                 uint32_t dim, uint32_t n_tokens, uint32_t n_experts,
+                                                                 float* __restrict__ logits) {
+#pragma clang fp contract(off)
+    constexpr uint32_t TR = 16 * RT, S = TR + 1;  // tile rows; LDS row stride (conflict-free transposed stores)
+    __shared__ float xs[2][kRtK * S], ws[2][kRtK * S];
+    const uint32_t t0 = blockIdx.x * TR, e0 = blockIdx.y * TR;
+    const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    // staging unit s: tile row tid / 16 + 16 s, elements 4 (tid % 16) .. + 3 of the chunk
+    const uint32_t c4 = tid % 16;
+    const float* xr[RT];
+    const uint8_t* wr[RT];
+    f32x4 xv[RT], wv[RT];
+#pragma unroll
+    for (int s = 0; s < RT; s++) {
+        const uint32_t r = tid / 16 + 16 * s;
+        xr[s] = x + (uint64_t)min(t0 + r, n_tokens - 1) * dim;
+        wr[s] = w + (uint64_t)min(e0 + r, n_experts - 1) * row_bytes;
+        xv[s] = wv[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    auto load = [&](uint32_t k0) {
+        const uint32_t i = k0 + 4 * c4;
+        if (i < dim) {  // dim % 4 == 0: the four elements are all inside
+#pragma unroll
+            for (int s = 0; s < RT; s++) {
+                xv[s] = *(const f32x4*)(xr[s] + i);
+                wv[s] = router_tile_w4<DT>(wr[s], i);
+            }
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int s = 0; s < RT; s++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                xs[b][(4 * c4 + j) * S + tid / 16 + 16 * s] = xv[s][j];
+                ws[b][(4 * c4 + j) * S + tid / 16 + 16 * s] = wv[s][j];
+            }
+    };
+    float acc[RT][RT];
+#pragma unroll
+    for (int a = 0; a < RT; a++)
+#pragma unroll
+        for (int b = 0; b < RT; b++) acc[a][b] = 0.0f;
+    auto step = [&](const float* xb, const float* wb) {
+        float xa[RT], wb_[RT];
+#pragma unroll
+        for (int a = 0; a < RT; a++) {
+            xa[a] = xb[a];
+            wb_[a] = wb[a];
+        }
+#pragma unroll
+        for (int a = 0; a < RT; a++)
+#pragma unroll
+            for (int b = 0; b < RT; b++) acc[a][b] += xa[a] * wb_[b];
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    const uint32_t nch = (dim + kRtK - 1) / kRtK;
+    for (uint32_t c = 0; c < nch; c++) {
+        const int b = c & 1;
+        if (c + 1 < nch) load((c + 1) * kRtK);
+        const float* xb = xs[b] + RT * ty;
+        const float* wb = ws[b] + RT * tx;
+        const uint32_t kc = min(kRtK, dim - c * kRtK);  // uniform
+        if (kc == kRtK) {
+#pragma unroll 16
+            for (uint32_t i = 0; i < kRtK; i++) step(xb + i * S, wb + i * S);
+        } else {
+            for (uint32_t i = 0; i < kc; i++) step(xb + i * S, wb + i * S);
+        }
+        if (c + 1 < nch) store(b ^ 1);  // the buffer read in chunk c - 1, before the last barrier
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < RT; a++)
+#pragma unroll
+        for (int b = 0; b < RT; b++) {
+            const uint32_t t = t0 + RT * ty + a, e = e0 + RT * tx + b;
+            if (t < n_tokens && e < n_experts) logits[(uint64_t)t * n_experts + e] = acc[a][b];
+        }
+}
+
 // Softmax and top-k of one token's logits (router_select_kernel, one wavefront).
 __global__ __launch_bounds__(64) void router_select_kernel(const float* __restrict__ logits, uint32_t n_experts,
                                                            uint32_t top_k, uint32_t norm, uint16_t* __restrict__ out_ids,
@@ -767,9 +873,36 @@ static int launch_router_dt(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     return launch_router_t<DT, 1>(ctx, a);
 }
 
+bool router_tiled(uint32_t w_dtype, uint32_t n_tokens, uint32_t dim, const void* x, const void* w) {
+    const uintptr_t wa = (uintptr_t)w;
+    return n_tokens >= kRouterTileMinTokens && dim % 4 == 0 && ((uintptr_t)x & 15u) == 0 &&
+           ((w_dtype == DS5_DTYPE_F32 && (wa & 15u) == 0) || (w_dtype == DS5_DTYPE_F16 && (wa & 7u) == 0));
+}
+
+template <uint32_t DT>
+static int launch_router_tile(ds5_hip_ctx* ctx, const RouterLaunch& a) {
+    // RT 2 (32 x 32 tiles) once those fill the chip; else RT 1 (16 x 16), four times the workgroups
+    const uint64_t wg2 = (uint64_t)((a.n_tokens + 31) / 32) * ((a.n_experts + 31) / 32);
+    if (wg2 >= 256) {
+        DS5_TIMED_LAUNCH(ctx, "router_logits_tile_kernel", (router_logits_tile_kernel<DT, 2>),
+                         dim3((a.n_tokens + 31) / 32, (a.n_experts + 31) / 32), dim3(256), 0, ctx->stream, a.x, a.w,
+                         a.row_bytes, a.dim, a.n_tokens, a.n_experts, a.logits);
+    } else {
+        DS5_TIMED_LAUNCH(ctx, "router_logits_tile_kernel", (router_logits_tile_kernel<DT, 1>),
+                         dim3((a.n_tokens + 15) / 16, (a.n_experts + 15) / 16), dim3(256), 0, ctx->stream, a.x, a.w,
+                         a.row_bytes, a.dim, a.n_tokens, a.n_experts, a.logits);
+    }
+    return ds5_after_launch(ctx, "router_logits_tile_kernel");
+}
+
 int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     if (a.n_tokens == 0) return DS5_OK;
-    int rc = a.w_dtype == DS5_DTYPE_F32   ? launch_router_dt<DS5_DTYPE_F32>(ctx, a)
+    int rc;
+    if (!a.x_norm_w && router_tiled(a.w_dtype, a.n_tokens, a.dim, a.x, a.w))
+        rc = a.w_dtype == DS5_DTYPE_F32 ? launch_router_tile<DS5_DTYPE_F32>(ctx, a)
+                                        : launch_router_tile<DS5_DTYPE_F16>(ctx, a);
+    else
+        rc = a.w_dtype == DS5_DTYPE_F32   ? launch_router_dt<DS5_DTYPE_F32>(ctx, a)
              : a.w_dtype == DS5_DTYPE_F16 ? launch_router_dt<DS5_DTYPE_F16>(ctx, a)
                                           : launch_router_dt<DS5_DTYPE_Q8_0>(ctx, a);
     if (rc) return rc;
@@ -788,8 +921,101 @@ int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
     return ds5_after_launch(ctx, "router_select_kernel");
 }
 
+// Pairs sorted by expert, for the grouped products (one workgroup): each expert's
+// pair count (LDS atomics), the exclusive scans of the counts and of their 128-row
+// tiles, the tile table (first row, end row, expert), then every pair scattered to
+// its expert's rows: perm[row] = pair, xrow[row] = its token. Rows of one expert
+// land in any order (the atomics), which no result depends on: each product row
+// is computed from its own x row and its expert's weights alone.
+constexpr int kSortThreads = 1024;
+__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* __restrict__ pairs, uint32_t n_pairs,
+                                                                uint32_t n_experts, uint32_t* __restrict__ perm,
+                                                                uint32_t* __restrict__ xrow, uint4* __restrict__ tiles,
+                                                                uint32_t* __restrict__ n_tiles) {
+    extern __shared__ uint32_t sort_smem[];
+    const uint32_t E = n_experts, tid = threadIdx.x;
+    uint32_t* cnt = sort_smem;           // [E]
+    uint32_t* fill = cnt + E;            // [E]
+    uint32_t* off = fill + E;            // [E + 1] first row of each expert
+    uint32_t* toff = off + E + 1;        // [E + 1] first tile of each expert
+    uint32_t* scan = toff + E + 1;       // [2 * kSortThreads]
+    for (uint32_t e = tid; e < E; e += kSortThreads) cnt[e] = fill[e] = 0;
+    __syncthreads();
+    for (uint32_t p = tid; p < n_pairs; p += kSortThreads) atomicAdd(&cnt[pairs[p].expert], 1u);
+    __syncthreads();
+    // thread tid owns experts [c0, c1): its totals, a block scan of them, then its offsets
+    const uint32_t per = (E + kSortThreads - 1) / kSortThreads, c0 = min(tid * per, E), c1 = min(c0 + per, E);
+    uint32_t rows = 0, tl = 0;
+    for (uint32_t e = c0; e < c1; e++) {
+        rows += cnt[e];
+        tl += (cnt[e] + 127) / 128;
+    }
+    scan[tid] = rows;
+    scan[kSortThreads + tid] = tl;
+    __syncthreads();
+    for (uint32_t d = 1; d < kSortThreads; d <<= 1) {  // inclusive Hillis-Steele scan of both
+        const uint32_t a = tid >= d ? scan[tid - d] : 0u, b = tid >= d ? scan[kSortThreads + tid - d] : 0u;
+        __syncthreads();
+        scan[tid] += a;
+        scan[kSortThreads + tid] += b;
+        __syncthreads();
+    }
+    uint32_t r0 = scan[tid] - rows, t0 = scan[kSortThreads + tid] - tl;
+    for (uint32_t e = c0; e < c1; e++) {
+        off[e] = r0;
+        toff[e] = t0;
+        const uint32_t nt = (cnt[e] + 127) / 128;
+        for (uint32_t t = 0; t < nt; t++) tiles[t0 + t] = uint4{r0 + 128 * t, r0 + cnt[e], e, 0u};
+        r0 += cnt[e];
+        t0 += nt;
+    }
+    if (tid == kSortThreads - 1) {
+        off[E] = scan[tid];
+        n_tiles[0] = scan[kSortThreads + tid];
+    }
+    __syncthreads();
+    for (uint32_t p = tid; p < n_pairs; p += kSortThreads) {
+        const ds5_pair pr = pairs[p];
+        const uint32_t row = off[pr.expert] + atomicAdd(&fill[pr.expert], 1u);
+        perm[row] = p;
+        xrow[row] = pr.token;
+    }
+}
+
+// The grouped experts: sort, x rows gathered and split, gate and up products,
+// h = silu(g) * u split, down products into pair order, the combine.
+static int launch_experts_grouped(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
+    const size_t smem = ((size_t)4 * a.n_experts + 2 + 2 * kSortThreads) * sizeof(uint32_t);
+    DS5_TIMED_LAUNCH(ctx, "moe_sort_kernel", moe_sort_kernel, dim3(1), dim3(kSortThreads), smem, ctx->stream,
+                     a.pairs, a.n_pairs, a.n_experts, a.perm, a.xrow, a.tiles, a.n_tiles);
+    if (int rc = ds5_after_launch(ctx, "moe_sort_kernel")) return rc;
+    if (int rc = launch_x_split_rows(ctx, a.x, a.xrow, a.n_pairs, a.dim, a.xhi, a.xlo, a.xexp)) return rc;
+    {
+        const uint8_t* w[2] = {a.gate, a.up};
+        float* out[2] = {a.h, a.u};
+        const uint32_t n[2] = {a.ffn, a.ffn};
+        if (int rc = launch_q8_gemm_grouped(ctx, a.xhi, a.xlo, a.xexp, a.dim, w, out, n, 2, a.tiles, a.n_tiles,
+                                            a.max_tiles, a.stride_gu, nullptr))
+            return rc;
+    }
+    if (int rc = launch_moe_h_split(ctx, a.h, a.u, a.n_pairs, a.ffn, a.hhi, a.hlo, a.hexp)) return rc;
+    {
+        const uint8_t* w[1] = {a.down};
+        float* out[1] = {a.y};
+        const uint32_t n[1] = {a.dim};
+        if (int rc = launch_q8_gemm_grouped(ctx, a.hhi, a.hlo, a.hexp, a.ffn, w, out, n, 1, a.tiles, a.n_tiles,
+                                            a.max_tiles, a.stride_d, a.perm))
+            return rc;
+    }
+    const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
+    DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
+                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.n_tokens, a.dim);
+    return ds5_after_launch(ctx, "moe_combine_kernel");
+}
+
 int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     if (a.n_pairs == 0 || a.n_tokens == 0) return DS5_OK;
+    if (a.grouped) return launch_experts_grouped(ctx, a);
     const uint64_t gu_rows = (uint64_t)a.n_pairs * a.ffn, dn_rows = (uint64_t)a.n_pairs * a.dim;
     if (a.fast) {
         const dim3 blk(kMoeWaves * 64);

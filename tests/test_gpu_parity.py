@@ -857,6 +857,37 @@ def test_router_fixtures(ctx, hip, oracle, i):
     assert np.array_equal(ids, oi) and np.all(rel <= 1e-6)
 
 
+@pytest.mark.parametrize("T,dim,E,dt", [(40, 2048, 128, "f32"), (2048, 2048, 128, "f32"), (70, 100, 200, "f16"),
+                                         (1000, 196, 300, "f32")])
+def test_router_tiles_equal_per_token(ctx, hip, oracle, T, dim, E, dt):
+    """From 32 tokens the logits run in token x expert tiles (router_logits_tile_kernel:
+    16 x 16, or 32 x 32 once those fill the chip); every logit is still dotRow's serial
+    sum, so ids and weights equal, bit for bit, those of the per-token kernel (one call
+    per token); for f32 rows the ids equal the oracle's. Ragged cases: tokens and experts
+    not multiples of the tile, dim not a multiple of the 64-element chunk, f16 rows."""
+    g = np.random.default_rng(T + dim)
+    x = (g.standard_normal((T, dim)) * np.exp(g.uniform(-2, 2, (T, 1)))).astype(np.float32)
+    w = (g.standard_normal((E, dim)) * 0.05).astype(np.float32)
+    wv, wdt = (w, hip.DTYPE_F32) if dt == "f32" else (w.astype(np.float16), hip.DTYPE_F16)
+    xb, wb = ctx.from_numpy(x), ctx.from_numpy(wv)
+    K = 8
+    ctx.set_kernel_timing(True)
+    try:
+        ids, wts = hip.routerTopK(ctx, xb, wb, wdt, T, dim, E, K, True)
+        assert ctx.kernel_time("router_logits_tile_kernel")[0] == 1
+    finally:
+        ctx.set_kernel_timing(False)
+    ids1, wts1 = np.zeros_like(ids), np.zeros_like(wts)
+    for t in range(T):
+        i1, w1 = hip.routerTopK(ctx, hip.Buf(xb.handle, xb.offset + t * dim * 4, dim * 4), wb, wdt, 1, dim, E, K, True)
+        ids1[t], wts1[t] = i1[0], w1[0]
+    assert np.array_equal(ids, ids1)
+    assert np.array_equal(wts.view(np.uint32), wts1.view(np.uint32))
+    if dt == "f32":
+        oi, ow = oracle.router_topk(x, w, oracle.F32, T, dim, E, K, True)
+        assert np.array_equal(ids, oi) and np.all(np.abs(wts - ow) <= 1e-6 * np.abs(ow))
+
+
 def test_router_hand_cases(ctx, hip):
     """kernels_c.zig:403-477: raw probabilities without renormalisation; exact ties go to
     the lower id."""
@@ -1007,6 +1038,90 @@ def test_expert_mlp_vs_oracle(ctx, hip, oracle, case):
     assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
 
 
+@pytest.mark.parametrize("case", ["qwen_shape", "skewed", "narrow"])
+def test_expert_mlp_grouped_vs_oracle(ctx, hip, oracle, case):
+    """Pair lists with at least two pairs per expert run grouped by expert on the matrix
+    cores (moe_sort_kernel, the split x / h planes, one Q8_0 product per expert row tile),
+    against the oracle within the reordering bound of the wavefront kernels' test, twice
+    (the rows of one expert land in any order: the results must not depend on it).
+    qwen_shape: dim 2048, ffn 768, 64 tokens x 8 pairs over 16 experts; skewed: most pairs
+    on one expert (three row tiles, one of them partial), four experts without pairs;
+    narrow: dim 256, ffn 96 (a partial column tile), pairs interleaved across tokens."""
+    g = np.random.default_rng(500 + len(case))
+    T, dim, ffn, E, K = {"qwen_shape": (64, 2048, 768, 16, 8), "skewed": (40, 512, 256, 12, 8),
+                         "narrow": (24, 256, 96, 8, 3)}[case]
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    Gf, Uf, Df = (oracle.q8_0_dequantize(v, k).astype(np.float64) for v, k in ((G, dim), (U, dim), (D, ffn)))
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    x[3] *= 1e-3  # rows of other magnitudes (their own plane exponents)
+    x[5] = 0.0
+    pairs = np.zeros(T * K, hip.PAIR_DTYPE)
+    pairs["token"] = np.tile(np.arange(T), K) if case == "narrow" else np.repeat(np.arange(T), K)
+    if case == "skewed":
+        ex = g.integers(0, E - 4, T * K)
+        ex[g.random(T * K) < 0.85] = 2  # ~272 of 320 pairs: tiles of 128, 128 and ~16 rows
+        pairs["expert"] = ex
+    else:
+        pairs["expert"] = g.integers(0, E, T * K)
+    pairs["weight"] = g.random(T * K).astype(np.float32)
+    assert T * K >= 2 * E
+    bufs = [ctx.from_numpy(v) for v in (G, U, D)]
+    xb = ctx.from_numpy(x)
+    r = g.standard_normal((T, dim)).astype(np.float32)
+    want = oracle.expert_mlp_swiglu(x, G, U, D, oracle.Q8_0, pairs.astype(oracle.PAIR_DTYPE), T, dim, ffn, E, out=r)
+    bound = _expert_bound(x, Gf, Uf, Df, pairs, T, dim, ffn)
+    runs = []
+    for _ in range(2):
+        out = ctx.from_numpy(r)
+        ctx.set_kernel_timing(True)
+        try:
+            hip.expertMlpSwiglu(ctx, xb, *bufs, hip.DTYPE_Q8_0, pairs, out, T, dim, ffn, E)
+            ctx.submit()
+            launches = {kn: ctx.kernel_time(kn)[0] for kn in ("moe_sort_kernel", "moe_gate_up_kernel",
+                                                               "moe_h_split_kernel", "moe_combine_kernel")}
+        finally:
+            ctx.set_kernel_timing(False)
+        assert launches == {"moe_sort_kernel": 1, "moe_gate_up_kernel": 0, "moe_h_split_kernel": 1,
+                            "moe_combine_kernel": 1}, launches
+        runs.append(ctx.to_numpy(out, np.float32, (T, dim)))
+    got = runs[0]
+    assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+
+
+def test_expert_mlp_grouped_threshold(ctx, hip, oracle):
+    """Below two pairs per expert on average the wavefront kernels run (no sort), from it
+    the grouped path; both agree with the oracle within the reordering bound."""
+    g = np.random.default_rng(7)
+    dim, ffn, E = 256, 64, 8
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    Gf, Uf, Df = (oracle.q8_0_dequantize(v, k).astype(np.float64) for v, k in ((G, dim), (U, dim), (D, ffn)))
+    bufs = [ctx.from_numpy(v) for v in (G, U, D)]
+    for P, sorts in ((2 * E - 1, 0), (2 * E, 1)):
+        T = P
+        x = g.standard_normal((T, dim)).astype(np.float32)
+        pairs = np.zeros(P, hip.PAIR_DTYPE)
+        pairs["token"] = np.arange(P)
+        pairs["expert"] = np.arange(P) % E
+        pairs["weight"] = 1.0
+        out = ctx.createBuffer(T * dim * 4)
+        ctx.zero(out, T * dim * 4)
+        ctx.set_kernel_timing(True)
+        try:
+            hip.expertMlpSwiglu(ctx, ctx.from_numpy(x), *bufs, hip.DTYPE_Q8_0, pairs, out, T, dim, ffn, E)
+            ctx.submit()
+            n_sort = ctx.kernel_time("moe_sort_kernel")[0]
+        finally:
+            ctx.set_kernel_timing(False)
+        assert n_sort == sorts
+        want = oracle.expert_mlp_swiglu(x, G, U, D, oracle.Q8_0, pairs.astype(oracle.PAIR_DTYPE), T, dim, ffn, E)
+        bound = _expert_bound(x, Gf, Uf, Df, pairs, T, dim, ffn)
+        got = ctx.to_numpy(out, np.float32, (T, dim))
+        assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
+
+
 def test_expert_mlp_bad_pair_leaves_out(ctx, hip):
     """A pair out of range is ShapeMismatch before anything runs (out unchanged)."""
     bank = ctx.from_numpy(np.zeros((2 * 32, 34), np.uint8))
@@ -1017,12 +1132,13 @@ def test_expert_mlp_bad_pair_leaves_out(ctx, hip):
     assert np.all(ctx.to_numpy(out, np.float32, (1, 32)) == 3.0)
 
 
-@pytest.mark.parametrize("T,E", [(1, 32), (5, 32), (1, 128), (3, 200)])
+@pytest.mark.parametrize("T,E", [(1, 32), (5, 32), (1, 128), (3, 200), (64, 32)])
 def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T, E):
     """ds5_hip_moe (router and experts on the device, pairs never leave it) equals
     ds5_hip_router_topk then ds5_hip_expert_mlp_swiglu on the router's pairs, bit for bit;
     the device ids / weights equal the host ones. 128 and 200 experts: two and four
-    register slots per lane in the selection, the last one partly filled at 200."""
+    register slots per lane in the selection, the last one partly filled at 200. 64 tokens
+    over 32 experts: the experts run grouped by expert."""
     g = np.random.default_rng(T)
     dim, ffn, K = 2048, 768, 8
     rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
@@ -1044,12 +1160,13 @@ def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T, E):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [1, 5, 300])
+@pytest.mark.parametrize("T", [1, 5, 64, 300])
 def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
     """ds5_hip_moe with a residual (out = residual + the experts' sum from zero) equals the
     engine's three calls -- zero the accumulator, ds5_hip_moe into it, ds5_hip_add(x, acc ->
     x) -- bit for bit, in place (out = residual) and into another buffer; residual values
-    include -0.0 (-0 + 0 = +0 through the add) and large magnitudes. T = 300: the serial
+    include -0.0 (-0 + 0 = +0 through the add) and large magnitudes. T = 64: 512 pairs over
+    64 experts, grouped by expert on the matrix cores. T = 300: the serial
     banks (a view that is not 4-byte aligned), whose experts run as separate kernels."""
     g = np.random.default_rng(100 + T)
     dim, ffn, E, K = (2048, 768, 64, 8) if T < 300 else (256, 64, 8, 2)
@@ -1090,13 +1207,15 @@ def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
                                  K, 1, hip.Buf(rb.handle, rb.offset, T * dim * 4 - 4)))
 
 
-@pytest.mark.parametrize("T,dim,rdt", [(1, 2048, "f32"), (5, 2048, "f32"), (3, 2048, "f16"), (2, 256, "f32")])
+@pytest.mark.parametrize("T,dim,rdt", [(1, 2048, "f32"), (5, 2048, "f32"), (3, 2048, "f16"), (2, 256, "f32"),
+                                        (40, 2048, "f32")])
 def test_moe_norm_equals_rmsnorm_then_moe(ctx, hip, oracle, T, dim, rdt):
     """ds5_hip_moe with x_norm (ffn_norm applied first) and the residual equals
     ds5_hip_rms_norm(x -> h2) then ds5_hip_moe(h2) with the residual, bit for bit, and
     leaves x as it was when out is another buffer: the norm inside the router's f32 logits
     kernel (rows above 256 elements), or written to the context's second buffer first (an
-    f16 router; dim 256: the serial order). The router ids and weights agree too."""
+    f16 router; dim 256: the serial order; 40 tokens: the logits in tiles, the experts
+    grouped). The router ids and weights agree too."""
     g = np.random.default_rng(300 + T + dim)
     ffn, E, K = (768, 64, 8) if dim == 2048 else (64, 8, 2)
     rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
