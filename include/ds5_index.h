@@ -43,6 +43,9 @@ uint32_t ds5_index_plan_partial(uint32_t len, uint32_t chunk);
  * index, tile row and even/odd-block offsets [nq][64]. */
 void ds5_index_gemm_x(uint32_t wave, uint32_t W, uint32_t nx, uint32_t BM, uint32_t m0, uint32_t m, uint32_t k,
                       uint32_t* x_off);
+/* The grouped MoE form: tile row r reads plane row x_rows[min(m0 + r, m - 1)]. */
+void ds5_index_gemm_x_rows(uint32_t wave, uint32_t W, uint32_t nx, uint32_t BM, uint32_t m0, uint32_t m, uint32_t k,
+                           const uint32_t* x_rows, uint32_t* x_off);
 void ds5_index_gemm_q(uint32_t wave, uint32_t threads, uint32_t nq, uint32_t w_rows, uint32_t row_dw, uint32_t n0,
                       uint32_t n, uint32_t row_bytes, uint32_t* q_dw, uint32_t* q_row, uint32_t* q_even,
                       uint32_t* q_odd);

@@ -235,29 +235,33 @@ struct ExpertLaunch {
     // (Q8_0 banks, many pairs per expert); the scratch below, h holding the gate
     // products and u the up products, y the down products in pair order
     bool grouped;
-    uint32_t n_experts, max_tiles;
+    uint32_t n_experts, max_tiles, tile_rows;
     uint16_t *xhi, *xlo, *hhi, *hlo;
     int *xexp, *hexp;
     float* u;
     uint32_t *perm, *xrow, *n_tiles;
     uint4* tiles;
 };
-// The grouped path's row tiles: at most P / 128 + E of 128 rows (each expert's last
-// one partial).
-inline uint32_t moe_max_tiles(uint32_t n_pairs, uint32_t n_experts) { return n_pairs / 128 + n_experts + 1; }
+// The grouped path's row tiles: at most P / rows + E of 64 or 128 rows (each expert's
+// last one partial).
+constexpr uint32_t kMoeMinTileRows = 64;
+inline uint32_t moe_max_tiles(uint32_t n_pairs, uint32_t n_experts, uint32_t tile_rows = kMoeMinTileRows) {
+    return n_pairs / tile_rows + n_experts + 1;
+}
 constexpr uint32_t kMoeGroupedMaxExperts = 2048;
 int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a);
-// The experts over rows sorted by expert on the matrix cores (k_matmul.hip): x rows
-// gathered by row_map and split into f16 planes; grouped Q8_0 products whose row
-// tiles come from a device table (first row, end row, expert); h = silu(g) * u split.
-int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, const uint32_t* row_map, uint32_t rows, uint32_t k,
-                        uint16_t* hi, uint16_t* lo, int* row_exp);
+// The experts over rows sorted by expert on the matrix cores (k_matmul.hip): the
+// tokens' x rows split into f16 planes; grouped Q8_0 products whose row tiles (of
+// tile_rows rows) come from a device table (first row, end row, expert), x_rows (if
+// not null) mapping each sorted row to its plane row; h = silu(g) * u split.
+int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, uint32_t rows, uint32_t k, uint16_t* hi, uint16_t* lo,
+                        int* row_exp);
 int launch_moe_h_split(ds5_hip_ctx* ctx, const float* g, const float* u, uint32_t rows, uint32_t k, uint16_t* hi,
                        uint16_t* lo, int* row_exp);
 int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp, uint32_t k,
                            const uint8_t* const* w, float* const* out, const uint32_t* n, uint32_t count,
-                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint64_t w_stride,
-                           const uint32_t* out_rows);
+                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint32_t tile_rows,
+                           uint64_t w_stride, const uint32_t* x_rows, const uint32_t* out_rows);
 
 struct RmsNormLaunch {
     const float* x;

@@ -84,6 +84,15 @@ void ds5_index_gemm_x(uint32_t wave, uint32_t W, uint32_t nx, uint32_t BM, uint3
         for (uint32_t lane = 0; lane < 64; lane++)
             x_off[i * 64 + lane] = ds5idx::gemm_x_off(1024u * (wave + W * i) + 16u * lane, lane, BM, m0, m, k);
 }
+// The grouped MoE form: tile row r reads plane row x_rows[min(m0 + r, m - 1)].
+void ds5_index_gemm_x_rows(uint32_t wave, uint32_t W, uint32_t nx, uint32_t BM, uint32_t m0, uint32_t m, uint32_t k,
+                           const uint32_t* x_rows, uint32_t* x_off) {
+    for (uint32_t i = 0; i < nx; i++)
+        for (uint32_t lane = 0; lane < 64; lane++) {
+            const uint32_t r = ds5idx::gemm_x_tile_row(1024u * (wave + W * i) + 16u * lane, BM);
+            x_off[i * 64 + lane] = ds5idx::gemm_x_off_row(r, lane, x_rows[ds5idx::umin(m0 + r, m - 1)], k);
+        }
+}
 void ds5_index_gemm_q(uint32_t wave, uint32_t threads, uint32_t nq, uint32_t w_rows, uint32_t row_dw, uint32_t n0,
                       uint32_t n, uint32_t row_bytes, uint32_t* q_dw, uint32_t* q_row, uint32_t* q_even,
                       uint32_t* q_odd) {

@@ -116,9 +116,14 @@ DS5_HD uint32_t plan_partial(uint32_t len, uint32_t chunk) { return (len == 0 ||
 //    d % 9 of local row d / 9 = tile row 16 wave + (threads / 4) (lr / 16) + lr % 16;
 //    the offsets from the block's scalar base (w + 34 b, or w + 34 b - 2 for odd b).
 // ---------------------------------------------------------------------------
+DS5_HD uint32_t gemm_x_tile_row(uint32_t o, uint32_t BM) { return (o % (BM * 64)) / 64; }
+// the offset of tile row r's swizzled chunk in plane row `row`
+DS5_HD uint32_t gemm_x_off_row(uint32_t r, uint32_t lane, uint32_t row, uint32_t k) {
+    return row * k * 2 + 16 * ((lane & 3) ^ ((r >> 2) & 3));
+}
 DS5_HD uint32_t gemm_x_off(uint32_t o, uint32_t lane, uint32_t BM, uint32_t m0, uint32_t m, uint32_t k) {
-    const uint32_t r = (o % (BM * 64)) / 64, c = (lane & 3) ^ ((r >> 2) & 3);
-    return umin(m0 + r, m - 1) * k * 2 + 16 * c;
+    const uint32_t r = gemm_x_tile_row(o, BM);
+    return gemm_x_off_row(r, lane, umin(m0 + r, m - 1), k);
 }
 DS5_HD uint32_t gemm_q_row(uint32_t d, uint32_t wave, uint32_t threads, uint32_t row_dw) {
     const uint32_t lr = d / row_dw;

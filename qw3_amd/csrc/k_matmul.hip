@@ -312,8 +312,7 @@ __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const flo
                                                                        uint16_t* __restrict__ lo,
                                                                        int* __restrict__ row_exp, uint32_t k,
                                                                        XSplitRope rope, RopeTable table,
-                                                                       const float* __restrict__ nw, float eps,
-                                                                       const uint32_t* __restrict__ row_map) {
+                                                                       const float* __restrict__ nw, float eps) {
     static_assert(kSplitThreads >= kTreeParts, "one tree partial per thread");
     __shared__ float red[kSplitThreads / 64];
     __shared__ float s_part[kTreeParts];
@@ -327,13 +326,12 @@ __global__ __launch_bounds__(kSplitThreads) void matmul_x_split_kernel(const flo
             rope.cs[row * 2 * rope.half + rope.half + i] = sinf(ang);
         }
     }
-    const uint64_t xrow = row_map ? row_map[row] : row;  // row_map: the planes' rows gather x rows
-    const float4* xr = (const float4*)(x + xrow * k);
+    const float4* xr = (const float4*)(x + row * k);
     float inv = 1.0f;
     if (nw) {  // uniform
         float sq = 0.0f;
         for (uint32_t i = threadIdx.x; i < k; i += kTreeParts) {
-            const float v = x[xrow * k + i];
+            const float v = x[row * k + i];
             sq = __builtin_fmaf(v, v, sq);
         }
         inv = tree_rms_inv(sq, k, eps, s_part, &s_inv);
@@ -437,15 +435,16 @@ struct AttnPrepEpi {
 };
 
 // GRP: the experts' products of a MoE layer over rows sorted by expert.
-// Workgroup row tile y is tiles[y] = (first row, end row, expert): its x rows are
-// those of the sorted planes in [first, end) (rows past the end read end - 1, a
-// row of the same expert, and store nothing), its weights the expert's matrix,
-// w + expert * w_stride; tiles past *count stop at once. Output row r goes to
-// row out_rows[r] (null: r).
+// Workgroup row tile y is tiles[y] = (first row, end row, expert): its rows are the
+// sorted rows [first, end) (rows past the end read end - 1, a row of the same
+// expert, and store nothing), its weights the expert's matrix, w + expert *
+// w_stride; tiles past *count stop at once. Sorted row r reads plane row x_rows[r]
+// (null: r) and its output goes to row out_rows[r] (null: r).
 struct MoeGemmTiles {
     const uint4* tiles;
     const uint32_t* count;
     uint64_t w_stride;
+    const uint32_t* x_rows;
     const uint32_t* out_rows;
 };
 
@@ -533,7 +532,13 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
     uint32_t xoff[NX];  // byte offset in the plane: row min(m0 + r, m - 1), chunk c, block 0
 #pragma unroll
     for (int i = 0; i < NX; i++) {
-        xoff[i] = ds5idx::gemm_x_off(1024u * (wave_u + W * i) + 16u * lane, (uint32_t)lane, BM, m0, m, k);
+        const uint32_t o = 1024u * (wave_u + W * i) + 16u * lane;
+        if (GRP && mt.x_rows) {  // uniform
+            const uint32_t r = ds5idx::gemm_x_tile_row(o, BM);
+            xoff[i] = ds5idx::gemm_x_off_row(r, (uint32_t)lane, mt.x_rows[min(m0 + r, m - 1)], k);
+        } else {
+            xoff[i] = ds5idx::gemm_x_off(o, (uint32_t)lane, BM, m0, m, k);
+        }
     }
     auto issue_x = [&](uint32_t b, int stage) {
 #pragma unroll
@@ -608,6 +613,13 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // GRP: the wavefront's 16-row tiles holding rows of the tile (uniform); the rest
+    // (an expert's last, partial tile) skip their products
+    int live = TM;
+    if constexpr (GRP) {
+        const int left = (int)m - (int)(m0 + wm0);
+        live = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : min(TM, (left + 15) / 16));
+    }
     auto multiply = [&](int stage, int buf) {
         f16x8_t bv[TN];
         float sv[TN];
@@ -619,6 +631,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
         }
 #pragma unroll
         for (int i = 0; i < TM; i++) {
+            if (GRP && i >= live) break;
             const int row = wm0 + 16 * i + r16;
             const int slot = row * 4 + (grp ^ ((row >> 2) & 3));
             const f16x8_t ah = __builtin_bit_cast(f16x8_t, As[stage][0][slot]);
@@ -765,7 +778,7 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
         for (int e = 0; e < 4; e++) {
             const uint32_t row = m0 + wm0 + 16 * i + 4 * grp + e;
             if (row >= m) continue;
-            const int sh = row_exp[row] - kXExpBias;
+            const int sh = row_exp[GRP && mt.x_rows ? mt.x_rows[row] : row] - kXExpBias;
             const uint32_t orow = GRP && mt.out_rows ? mt.out_rows[row] : row;
 #pragma unroll
             for (int j = 0; j < TN; j++) {
@@ -883,7 +896,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     uint16_t* lo = hi + (size_t)a.m * a.k;
     int* row_exp = (int*)(lo + (size_t)a.m * a.k);
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{}, a.norm_w, a.norm_eps, nullptr);
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, XSplitRope{}, RopeTable{}, a.norm_w, a.norm_eps);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     uint32_t tiles = 0;
@@ -907,11 +920,11 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
 
 // The MoE experts' matrix-core path (rows sorted by expert): the x rows gathered and
 // split, the grouped products, h = silu(g) * u split.
-int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, const uint32_t* row_map, uint32_t rows, uint32_t k,
-                        uint16_t* hi, uint16_t* lo, int* row_exp) {
+int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, uint32_t rows, uint32_t k, uint16_t* hi, uint16_t* lo,
+                        int* row_exp) {
     if (rows == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<false>, dim3(rows), dim3(kSplitThreads), 0,
-                     ctx->stream, x, hi, lo, row_exp, k, XSplitRope{}, RopeTable{}, nullptr, 0.0f, row_map);
+                     ctx->stream, x, hi, lo, row_exp, k, XSplitRope{}, RopeTable{}, nullptr, 0.0f);
     return ds5_after_launch(ctx, "matmul_x_split_kernel");
 }
 
@@ -923,11 +936,10 @@ int launch_moe_h_split(ds5_hip_ctx* ctx, const float* g, const float* u, uint32_
     return ds5_after_launch(ctx, "moe_h_split_kernel");
 }
 
-int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp, uint32_t k,
-                           const uint8_t* const* w, float* const* out, const uint32_t* n, uint32_t count,
-                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint64_t w_stride,
-                           const uint32_t* out_rows) {
-    constexpr int BM = 128, BN = 128, WM = 4, WN = 2;
+template <int BM, int BN, int WM, int WN>
+static int launch_q8_gemm_grouped_t(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp,
+                                    uint32_t k, const uint8_t* const* w, float* const* out, const uint32_t* n,
+                                    uint32_t count, uint32_t max_tiles, const MoeGemmTiles& mt) {
     WeightGroup g{};
     uint32_t nt = 0;
     for (uint32_t e = 0; e < count; e++) {
@@ -939,11 +951,22 @@ int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t*
     }
     g.count = count;
     if (nt == 0 || max_tiles == 0) return DS5_OK;
-    const MoeGemmTiles mt{tiles, n_tiles, w_stride, out_rows};
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, true>),
                      dim3(nt, max_tiles), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k, AttnPrepEpi{},
                      mt);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
+}
+
+int launch_q8_gemm_grouped(ds5_hip_ctx* ctx, const uint16_t* hi, const uint16_t* lo, const int* row_exp, uint32_t k,
+                           const uint8_t* const* w, float* const* out, const uint32_t* n, uint32_t count,
+                           const uint4* tiles, const uint32_t* n_tiles, uint32_t max_tiles, uint32_t tile_rows,
+                           uint64_t w_stride, const uint32_t* x_rows, const uint32_t* out_rows) {
+    const MoeGemmTiles mt{tiles, n_tiles, w_stride, x_rows, out_rows};
+    if (tile_rows == 64)
+        return launch_q8_gemm_grouped_t<64, 128, 2, 2>(ctx, hi, lo, row_exp, k, w, out, n, count, max_tiles, mt);
+    if (tile_rows == 128)
+        return launch_q8_gemm_grouped_t<128, 128, 4, 2>(ctx, hi, lo, row_exp, k, w, out, n, count, max_tiles, mt);
+    return ds5_fail(ctx, DS5_DEVICE_FAILURE, "moe: row tiles of %u rows", tile_rows);
 }
 
 // The rope table follows the x split at the next 16-byte boundary (the epilogue
@@ -962,7 +985,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     float* cs = (float*)((char*)a.ws + qkv_prep_cs_offset(a.m, a.k));
     XSplitRope rope{a.positions, cs, a.head_dim / 2, a.freq_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_x_split_kernel", matmul_x_split_kernel<true>, dim3(a.m), dim3(kSplitThreads), 0,
-                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table, a.norm_w, a.norm_eps, nullptr);
+                     ctx->stream, a.x, hi, lo, row_exp, a.k, rope, *a.table, a.norm_w, a.norm_eps);
     if (int rc = ds5_after_launch(ctx, "matmul_x_split_kernel")) return rc;
     WeightGroup g{};
     const uint32_t ns[3] = {a.n_q_heads * a.head_dim, a.n_kv_heads * a.head_dim, a.n_kv_heads * a.head_dim};

@@ -922,8 +922,8 @@ int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
 }
 
 // Pairs sorted by expert, for the grouped products (one workgroup): each expert's
-// pair count (LDS atomics), the exclusive scans of the counts and of their 128-row
-// tiles, the tile table (first row, end row, expert), then every pair scattered to
+// pair count (LDS atomics), the exclusive scans of the counts and of their row
+// tiles (tile_rows rows each), the tile table (first row, end row, expert), then every pair scattered to
 // its expert's rows: perm[row] = pair, xrow[row] = its token. Rows of one expert
 // land in any order (the atomics), which no result depends on: each product row
 // is computed from its own x row and its expert's weights alone.
@@ -931,7 +931,7 @@ constexpr int kSortThreads = 1024;
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* __restrict__ pairs, uint32_t n_pairs,
                                                                 uint32_t n_experts, uint32_t* __restrict__ perm,
                                                                 uint32_t* __restrict__ xrow, uint4* __restrict__ tiles,
-                                                                uint32_t* __restrict__ n_tiles) {
+                                                                uint32_t* __restrict__ n_tiles, uint32_t tile_rows) {
     extern __shared__ uint32_t sort_smem[];
     const uint32_t E = n_experts, tid = threadIdx.x;
     uint32_t* cnt = sort_smem;           // [E]
@@ -948,7 +948,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* 
     uint32_t rows = 0, tl = 0;
     for (uint32_t e = c0; e < c1; e++) {
         rows += cnt[e];
-        tl += (cnt[e] + 127) / 128;
+        tl += (cnt[e] + tile_rows - 1) / tile_rows;
     }
     scan[tid] = rows;
     scan[kSortThreads + tid] = tl;
@@ -964,8 +964,8 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* 
     for (uint32_t e = c0; e < c1; e++) {
         off[e] = r0;
         toff[e] = t0;
-        const uint32_t nt = (cnt[e] + 127) / 128;
-        for (uint32_t t = 0; t < nt; t++) tiles[t0 + t] = uint4{r0 + 128 * t, r0 + cnt[e], e, 0u};
+        const uint32_t nt = (cnt[e] + tile_rows - 1) / tile_rows;
+        for (uint32_t t = 0; t < nt; t++) tiles[t0 + t] = uint4{r0 + tile_rows * t, r0 + cnt[e], e, 0u};
         r0 += cnt[e];
         t0 += nt;
     }
@@ -982,20 +982,21 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* 
     }
 }
 
-// The grouped experts: sort, x rows gathered and split, gate and up products,
-// h = silu(g) * u split, down products into pair order, the combine.
+// The grouped experts: sort, the tokens' x rows split, gate and up products (each
+// sorted row reading its token's plane row), h = silu(g) * u split, down products
+// into pair order, the combine.
 static int launch_experts_grouped(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
     const size_t smem = ((size_t)4 * a.n_experts + 2 + 2 * kSortThreads) * sizeof(uint32_t);
     DS5_TIMED_LAUNCH(ctx, "moe_sort_kernel", moe_sort_kernel, dim3(1), dim3(kSortThreads), smem, ctx->stream,
-                     a.pairs, a.n_pairs, a.n_experts, a.perm, a.xrow, a.tiles, a.n_tiles);
+                     a.pairs, a.n_pairs, a.n_experts, a.perm, a.xrow, a.tiles, a.n_tiles, a.tile_rows);
     if (int rc = ds5_after_launch(ctx, "moe_sort_kernel")) return rc;
-    if (int rc = launch_x_split_rows(ctx, a.x, a.xrow, a.n_pairs, a.dim, a.xhi, a.xlo, a.xexp)) return rc;
+    if (int rc = launch_x_split_rows(ctx, a.x, a.n_tokens, a.dim, a.xhi, a.xlo, a.xexp)) return rc;
     {
         const uint8_t* w[2] = {a.gate, a.up};
         float* out[2] = {a.h, a.u};
         const uint32_t n[2] = {a.ffn, a.ffn};
         if (int rc = launch_q8_gemm_grouped(ctx, a.xhi, a.xlo, a.xexp, a.dim, w, out, n, 2, a.tiles, a.n_tiles,
-                                            a.max_tiles, a.stride_gu, nullptr))
+                                            a.max_tiles, a.tile_rows, a.stride_gu, a.xrow, nullptr))
             return rc;
     }
     if (int rc = launch_moe_h_split(ctx, a.h, a.u, a.n_pairs, a.ffn, a.hhi, a.hlo, a.hexp)) return rc;
@@ -1004,7 +1005,7 @@ static int launch_experts_grouped(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
         float* out[1] = {a.y};
         const uint32_t n[1] = {a.dim};
         if (int rc = launch_q8_gemm_grouped(ctx, a.hhi, a.hlo, a.hexp, a.ffn, w, out, n, 1, a.tiles, a.n_tiles,
-                                            a.max_tiles, a.stride_d, a.perm))
+                                            a.max_tiles, a.tile_rows, a.stride_d, nullptr, a.perm))
             return rc;
     }
     const uint64_t outs = (uint64_t)a.n_tokens * a.dim;

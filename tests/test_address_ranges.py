@@ -41,6 +41,7 @@ def ix(hip):
         "ds5_index_plan_len": ([i32, u32], u32), "ds5_index_plan_items": ([u32, u32], u32),
         "ds5_index_plan_whole": ([u32, u32], u32), "ds5_index_plan_partial": ([u32, u32], u32),
         "ds5_index_gemm_x": ([u32] * 7 + [P], None), "ds5_index_gemm_q": ([u32] * 8 + [P] * 4, None),
+        "ds5_index_gemm_x_rows": ([u32] * 7 + [P, P], None),
         "ds5_index_prefill_tile": ([u32, C.c_int, u32, u32, P], u32), "ds5_index_pf_q_token": ([u32] * 3, u32),
     }
     for name, (a, r) in sig.items():
@@ -61,7 +62,7 @@ def test_index_header_symbols_exported(hip):
     """Every function include/ds5_index.h declares is exported by the library."""
     text = open(os.path.join(ROOT, "include", "ds5_index.h")).read()
     names = set(re.findall(r"^\s*(?:void|uint32_t|uint64_t)\s+(ds5_index_\w+)\(", text, re.M))
-    assert len(names) == 16
+    assert len(names) == 17
     for n in names:
         assert getattr(hip.LIB, n) is not None
 
@@ -349,6 +350,55 @@ def test_gemm_load_block_addresses(ix, m, n, k, tile):
             continue  # matmul_path sends this view to the serial kernel
         hi = check_gemm(ix, m, n, k, 0, w_len, *tile)
         assert hi <= w_len, (hi, w_len)
+
+
+def _moe_tiles(pairs_expert, E, rows):
+    """The grouped MoE's sorted rows and row tiles as moe_sort_kernel builds them: each
+    expert's rows consecutive in expert order, tiles of `rows` rows (first, end, expert)."""
+    cnt = np.bincount(pairs_expert, minlength=E)
+    off = np.concatenate([[0], np.cumsum(cnt)])
+    tiles = [(off[e] + rows * t, off[e] + cnt[e], e) for e in range(E) for t in range(-(-cnt[e] // rows))]
+    return np.argsort(pairs_expert, kind="stable"), tiles
+
+
+@pytest.mark.parametrize("T,K,E,dim,ffn", [(64, 8, 16, 2048, 768), (40, 8, 12, 512, 256), (24, 3, 8, 256, 96),
+                                           (2048, 8, 128, 2048, 768)])
+@pytest.mark.parametrize("tile", [(64, 128, 2, 2), (128, 128, 4, 2)])
+def test_grouped_moe_gemm_x_rows(ix, hip, T, K, E, dim, ffn, tile):
+    """The grouped MoE products' x loads: gate / up read sorted row r's token's row of the
+    T-row x planes (x_rows = the pairs' tokens in sorted order), down the P-row h planes
+    (no map); every load stays inside its planes, reads a row of the tile's own expert,
+    and the tile count stays within moe_max_tiles (P / rows + E + 1)."""
+    BM, BN, WM, WN = tile
+    W = WM * WN
+    g = np.random.default_rng(T + E)
+    P = T * K
+    tokens = np.repeat(np.arange(T), K)
+    expert = g.integers(0, E, P)
+    expert[g.random(P) < 0.3] = 1  # one heavy expert: several tiles
+    perm, tiles = _moe_tiles(expert, E, BM)
+    assert len(tiles) <= P // BM + E + 1
+    x_rows = tokens[perm].astype(np.uint32)
+    nx = 2 * BM * 64 // 1024 // W
+    lane = np.arange(64)
+    for m0, m, e in tiles:
+        for w in range(W):
+            o = 1024 * (w + W * np.arange(nx)[:, None]) + 16 * lane[None, :]
+            r = (o % (BM * 64)) // 64
+            srow = np.minimum(m0 + r, m - 1)
+            assert (expert[perm[srow]] == e).all()  # the tile's own expert, rows past the end included
+            for k, rows_map, plane_rows in ((dim, x_rows, T), (ffn, None, P)):
+                off = _u32s(nx * 64)
+                if rows_map is None:
+                    ix.ds5_index_gemm_x(w, W, nx, BM, int(m0), int(m), k, _ptr(off))
+                    want_row = srow
+                else:
+                    ix.ds5_index_gemm_x_rows(w, W, nx, BM, int(m0), int(m), k, _ptr(rows_map), _ptr(off))
+                    want_row = tokens[perm[srow]]
+                off = off.astype(np.int64).reshape(nx, 64)
+                assert (off // (2 * k) == want_row).all()
+                last = off + 64 * (k // 32 - 1) + 16  # the last block's 16 bytes
+                assert off.min() >= 0 and last.max() <= plane_rows * k * 2
 
 
 def test_gemm_slack_rule_is_needed(ix):
