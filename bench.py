@@ -345,6 +345,34 @@ class MoeSweep:
             self.H.moe(self.ctx, a)
 
 
+class MoePrefill:
+    """The MoE block over T prompt tokens (Qwen3-30B-A3B shape: dim 2048, 128 experts top 8,
+    ffn 768, Q8_0 banks, f32 router): ds5_hip_moe with the logits in tiles and the
+    experts grouped by expert on the matrix cores. Synthetic x, router and banks (one
+    random template per shape, small scales)."""
+
+    def __init__(self, H, ctx, T=2048, dim=2048, ffn=768, E=128, K=8, seed=17):
+        self.H, self.ctx, self.T = H, ctx, T
+        g = np.random.default_rng(seed)
+
+        def template(rows, k):
+            w = g.integers(0, 256, (rows, k // 32, 34), dtype=np.uint8)
+            w[:, :, 0:2] = np.array([0.002], np.float16).view(np.uint8)
+            return w.reshape(rows, k // 32 * 34)
+        gu, dn = template(E * ffn, dim), template(E * dim, ffn)
+        x = ctx.from_numpy(g.standard_normal((T, dim)).astype(np.float32))
+        rw = ctx.from_numpy((g.standard_normal((E, dim)) * 0.03).astype(np.float32))
+        empty = H.Buf(None, 0, 0)
+        self.args = H.MoeArgs(x, rw, H.DTYPE_F32, ctx.from_numpy(gu), ctx.from_numpy(gu), ctx.from_numpy(dn),
+                              H.DTYPE_Q8_0, ctx.createBuffer(T * dim * 4), empty, empty, T, dim, ffn, E, K, 1)
+        # the experts' useful products: gate and up (2 x ffn x dim) and down (dim x ffn) per pair
+        self.expert_flops = 2 * T * K * 3 * dim * ffn
+        self.router_flops = 2 * T * E * dim
+
+    def sweep(self):
+        self.H.moe(self.ctx, self.args)
+
+
 class DecodeLayerSweep:
     """One decode token through n_layers whole layers at the Qwen3-30B-A3B shape, in the
     engine's fused order (forward.zig:322-494; qw3_amd/engine.py fused mode): the
@@ -722,12 +750,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time per cycled decode leg (C0, C1)")
     ap.add_argument("--leg-seconds", type=float, default=0.5,
                     help="minimum device time of each secondary timed leg (graph replays / eager kernel timing)")
-    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,LAYER,QKVP,BLK",
+    ap.add_argument("--only", default="C0,C1,C2,C3,C4,FLOOR,SIX,QKV,WO,MOE,LAYER,QKVP,BLK,MOEP",
                     help="comma list of legs: C0-C4 (BASELINE configs; C1 is the headline), FLOOR (launch and "
                          "bare-read floors), SIX (C1 through the six separate ops), QKV / QKVP (decode / prefill "
                          "q/k/v projections), WO (output projection + residual), MOE (decode MoE block), LAYER (48 whole "
                          "decode layers in the engine's fused order), BLK (prefill attention block: projections + "
-                         "step, fused vs the two calls)")
+                         "step, fused vs the two calls), MOEP (MoE block over 2048 prompt tokens)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (the known-size reference dispatch for "
                          "the FETCH_SIZE / WRITE_SIZE traffic counters)")
@@ -1110,6 +1138,32 @@ def main():
                   "attention block with attn_norm, Wo + residual, MoE with ffn_norm and residual (3 calls per layer)")
         log(f"[bench] LAYER {us:.3f} us/layer (graph of 48 layers); eager per-layer marks mean {ns.mean():.3f} "
             f"min {ns.min():.3f} max {ns.max():.3f} us; separate legs {part_us}; kernels per layer {per_layer}")
+        del w
+
+    if "MOEP" in only:
+        log("[bench] MOEP: MoE block over 2048 prompt tokens (router top-8 of 128, experts 2048 x 768 Q8_0 grouped "
+            "by expert)")
+        w = MoePrefill(H, ctx)
+        n_rep, per_graph = max(10, args.steps // 5), 4
+        elapsed, _ = time_graph(ctx, Repeat(w, per_graph), n_rep, 2)
+        us = elapsed / (n_rep * per_graph) * 1e6
+        names = ("router_logits_tile_kernel", "router_select_kernel", "moe_sort_kernel", "matmul_x_split_kernel",
+                 "matmul_q8_mfma_kernel", "moe_h_split_kernel", "moe_combine_kernel")
+        ks = kernel_stats(ctx, w, names, leg)
+        calls = max(1, ks["moe_sort_kernel"][1])
+        per = {k: round(ks[k][0] * ks[k][1] / calls / 1e3, 3) for k in names if ks[k][1]}
+        mfma_us = per.get("matmul_q8_mfma_kernel", 0.0)
+        tf = w.expert_flops / (mfma_us * 1e6) if mfma_us else None
+        extra["moe_block_prefill"] = dict(
+            us=round(us, 3), us_per_token=round(us / w.T, 4), calls_per_graph=per_graph, kernel_us_per_call=per,
+            expert_products_tflops=round(tf, 2) if tf else None,
+            expert_products_frac=round(tf / BF16_MFMA_PEAK_TFLOPS, 4) if tf else None,
+            expert_flops=w.expert_flops,
+            shape="2048 tokens, dim 2048, 128 experts top 8 (16,384 pairs), ffn 768, Q8_0 banks, f32 router; logits "
+                  "in tiles, experts grouped by expert (x / h split into f16 hi and lo: 2 matrix-core products per "
+                  "useful one)")
+        log(f"[bench] MOEP {us:.1f} us per call ({us / w.T:.3f} us/token); kernels per call {per}; expert products "
+            f"{tf:.1f} TFLOP/s (useful)" if tf else f"[bench] MOEP {us:.1f} us per call; kernels {per}")
         del w
 
     if "QKVP" in only:

@@ -793,6 +793,49 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     out[id] = res ? res[id] + acc : acc;
 }
 
+// moe_combine_kernel over four consecutive outputs per thread (dim % 4 == 0, y, out and
+// res 16-byte aligned): the same products and adds per output, in the same order; the
+// token's pair weights and product rows loaded eight pairs at a time.
+__global__ __launch_bounds__(256) void moe_combine4_kernel(const float* __restrict__ y,
+                                                           const ds5_pair* __restrict__ pairs,
+                                                           const uint32_t* __restrict__ order,
+                                                           const uint32_t* __restrict__ offsets, uint32_t top_k,
+                                                           float* out, const float* res, uint32_t n_tokens,
+                                                           uint32_t dim) {
+#pragma clang fp contract(off)
+    asm volatile("" ::"s"(y), "s"(pairs), "s"(order), "s"(offsets), "s"(top_k), "s"(out), "s"(res), "s"(n_tokens),
+                 "s"(dim));
+    constexpr uint32_t B = 8;
+    const uint64_t id = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
+    const uint32_t d4 = dim / 4;
+    if (id >= (uint64_t)n_tokens * d4) return;
+    const uint32_t t = (uint32_t)(id / d4), i = (uint32_t)(id % d4) * 4;
+    const uint32_t q0 = offsets ? offsets[t] : t * top_k, q1 = offsets ? offsets[t + 1] : (t + 1) * top_k;
+    f32x4 acc = res ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : *(const f32x4*)(out + 4 * id);
+    for (uint32_t qb = q0; qb < q1; qb += B) {
+        float wv[B];
+        f32x4 yv[B];
+#pragma unroll
+        for (uint32_t u = 0; u < B; u++) {
+            const uint32_t q = min(qb + u, q1 - 1);
+            const uint32_t p = order ? order[q] : q;
+            wv[u] = pairs[p].weight;
+            yv[u] = *(const f32x4*)(y + (uint64_t)p * dim + i);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < B; u++)
+            if (qb + u < q1)
+#pragma unroll
+                for (int c = 0; c < 4; c++) acc[c] += wv[u] * yv[u][c];
+    }
+    if (res) {
+        const f32x4 r = *(const f32x4*)(res + 4 * id);
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] = r[c] + acc[c];
+    }
+    *(f32x4*)(out + 4 * id) = acc;
+}
+
 // Serial fallback for banks the GEMV kernels cannot read (a Q8_0 view that is
 // not 4-byte aligned, or that ends 2 bytes short of the dword past its last
 // block): one thread per (pair, row), dotRow's order.
@@ -928,6 +971,7 @@ int launch_router(ds5_hip_ctx* ctx, const RouterLaunch& a) {
 // land in any order (the atomics), which no result depends on: each product row
 // is computed from its own x row and its expert's weights alone.
 constexpr int kSortThreads = 1024;
+constexpr int kSortBatch = 8;  // pairs per thread whose loads are in flight together
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* __restrict__ pairs, uint32_t n_pairs,
                                                                 uint32_t n_experts, uint32_t* __restrict__ perm,
                                                                 uint32_t* __restrict__ xrow, uint4* __restrict__ tiles,
@@ -941,7 +985,17 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* 
     uint32_t* scan = toff + E + 1;       // [2 * kSortThreads]
     for (uint32_t e = tid; e < E; e += kSortThreads) cnt[e] = fill[e] = 0;
     __syncthreads();
-    for (uint32_t p = tid; p < n_pairs; p += kSortThreads) atomicAdd(&cnt[pairs[p].expert], 1u);
+    for (uint32_t p0 = 0; p0 < n_pairs; p0 += kSortThreads * kSortBatch) {
+        uint32_t ex[kSortBatch];
+#pragma unroll
+        for (int u = 0; u < kSortBatch; u++) {
+            const uint32_t p = p0 + tid + kSortThreads * u;
+            ex[u] = p < n_pairs ? pairs[p].expert : E;
+        }
+#pragma unroll
+        for (int u = 0; u < kSortBatch; u++)
+            if (ex[u] < E) atomicAdd(&cnt[ex[u]], 1u);
+    }
     __syncthreads();
     // thread tid owns experts [c0, c1): its totals, a block scan of them, then its offsets
     const uint32_t per = (E + kSortThreads - 1) / kSortThreads, c0 = min(tid * per, E), c1 = min(c0 + per, E);
@@ -974,12 +1028,39 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const ds5_pair* 
         n_tiles[0] = scan[kSortThreads + tid];
     }
     __syncthreads();
-    for (uint32_t p = tid; p < n_pairs; p += kSortThreads) {
-        const ds5_pair pr = pairs[p];
-        const uint32_t row = off[pr.expert] + atomicAdd(&fill[pr.expert], 1u);
-        perm[row] = p;
-        xrow[row] = pr.token;
+    for (uint32_t p0 = 0; p0 < n_pairs; p0 += kSortThreads * kSortBatch) {
+        uint32_t ex[kSortBatch], tok[kSortBatch];
+#pragma unroll
+        for (int u = 0; u < kSortBatch; u++) {
+            const uint32_t p = p0 + tid + kSortThreads * u;
+            ex[u] = p < n_pairs ? pairs[p].expert : E;
+            tok[u] = p < n_pairs ? pairs[p].token : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kSortBatch; u++)
+            if (ex[u] < E) {
+                const uint32_t row = off[ex[u]] + atomicAdd(&fill[ex[u]], 1u);
+                perm[row] = p0 + tid + kSortThreads * u;
+                xrow[row] = tok[u];
+            }
     }
+}
+
+// The combine (timed as moe_combine_kernel in either form): four outputs per thread
+// where dim and the views allow it.
+static int launch_combine(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
+    const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
+    const bool v4 = a.dim % 4 == 0 && (((uintptr_t)a.y | (uintptr_t)a.out | (uintptr_t)a.res) & 15u) == 0;
+    if (v4) {
+        DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine4_kernel, dim3((unsigned)((outs / 4 + 255) / 256)),
+                         dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res,
+                         a.n_tokens, a.dim);
+    } else {
+        DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)),
+                         dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res,
+                         a.n_tokens, a.dim);
+    }
+    return ds5_after_launch(ctx, "moe_combine_kernel");
 }
 
 // The grouped experts: sort, the tokens' x rows split, gate and up products (each
@@ -1008,10 +1089,7 @@ static int launch_experts_grouped(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
                                             a.max_tiles, a.tile_rows, a.stride_d, nullptr, a.perm))
             return rc;
     }
-    const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
-    DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
-                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.n_tokens, a.dim);
-    return ds5_after_launch(ctx, "moe_combine_kernel");
+    return launch_combine(ctx, a);
 }
 
 int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
@@ -1039,10 +1117,7 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
                                  a.pairs, a.y, a.n_pairs, a.dim, a.ffn, a.row_f, a.stride_d);
             }
             if (int rc = ds5_after_launch(ctx, "moe_down_kernel")) return rc;
-            DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)),
-                             dim3(256), 0, ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res,
-                             a.n_tokens, a.dim);
-            return ds5_after_launch(ctx, "moe_combine_kernel");
+            return launch_combine(ctx, a);
         }
         const dim3 g3((unsigned)(outs / kDownRows));  // dim % 32 == 0 on this path
         if (a.q8) {
@@ -1071,8 +1146,5 @@ int launch_experts(ds5_hip_ctx* ctx, const ExpertLaunch& a) {
                          a.row_f, a.stride_d);
         if (int rc = ds5_after_launch(ctx, "moe_down_serial_kernel")) return rc;
     }
-    const uint64_t outs = (uint64_t)a.n_tokens * a.dim;
-    DS5_TIMED_LAUNCH(ctx, "moe_combine_kernel", moe_combine_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
-                     ctx->stream, a.y, a.pairs, a.order, a.offsets, a.top_k, a.out, a.res, a.n_tokens, a.dim);
-    return ds5_after_launch(ctx, "moe_combine_kernel");
+    return launch_combine(ctx, a);
 }
