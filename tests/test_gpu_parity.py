@@ -1038,7 +1038,7 @@ def test_expert_mlp_vs_oracle(ctx, hip, oracle, case):
     assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
 
 
-@pytest.mark.parametrize("case", ["qwen_shape", "skewed", "narrow", "rows128"])
+@pytest.mark.parametrize("case", ["qwen_shape", "skewed", "narrow", "rows128", "many_experts"])
 def test_expert_mlp_grouped_vs_oracle(ctx, hip, oracle, case):
     """Pair lists with at least two pairs per expert run grouped by expert on the matrix
     cores (moe_sort_kernel, the split x / h planes, one Q8_0 product per expert row tile),
@@ -1047,10 +1047,12 @@ def test_expert_mlp_grouped_vs_oracle(ctx, hip, oracle, case):
     qwen_shape: dim 2048, ffn 768, 64 tokens x 8 pairs over 16 experts; skewed: most pairs
     on one expert (five 64-row tiles, the last partial), four experts without pairs;
     narrow: dim 256, ffn 96 (a partial column tile), pairs interleaved across tokens;
-    rows128: 128 pairs per expert, the 128-row tiles."""
+    rows128: 128 pairs per expert, the 128-row tiles; many_experts: 1100 experts (some of the
+    sort's threads own two experts each in its scans)."""
     g = np.random.default_rng(500 + len(case))
     T, dim, ffn, E, K = {"qwen_shape": (64, 2048, 768, 16, 8), "skewed": (40, 512, 256, 12, 8),
-                         "narrow": (24, 256, 96, 8, 3), "rows128": (256, 256, 96, 16, 8)}[case]
+                         "narrow": (24, 256, 96, 8, 3), "rows128": (256, 256, 96, 16, 8),
+                         "many_experts": (300, 256, 64, 1100, 8)}[case]
     mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
     G, U, D = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
     Gf, Uf, Df = (oracle.q8_0_dequantize(v, k).astype(np.float64) for v, k in ((G, dim), (U, dim), (D, ffn)))
