@@ -491,13 +491,10 @@ int ds5_hip_moe(ds5_hip_ctx* ctx, const ds5_moe_args* a) {
         return ds5_hip_moe(ctx, &b);
     }
     MoeScratch s{};
-    const ds5_buf ex_in = norm_inside ? ds5_buf{} : a->x;  // the experts' x view (h2 when the router normalises)
-    const bool grouped = experts_grouped(
-        norm_inside ? (a->dim % 32 == 0 && a->ffn_dim % 32 == 0 &&
-                       experts_fast(ds5_buf{nullptr, 0, 0}, a->gate, a->up, a->down, a->w_dtype, a->dim, a->ffn_dim,
-                                    a->n_experts))
-                    : experts_fast(ex_in, a->gate, a->up, a->down, a->w_dtype, a->dim, a->ffn_dim, a->n_experts),
-        a->w_dtype, TK, a->n_experts, a->dim, a->ffn_dim);
+    // the experts read x, or h2 (aligned scratch) when the router normalises
+    const bool fast = experts_fast(norm_inside ? ds5_buf{} : a->x, a->gate, a->up, a->down, a->w_dtype, a->dim,
+                                   a->ffn_dim, a->n_experts);
+    const bool grouped = experts_grouped(fast, a->w_dtype, TK, a->n_experts, a->dim, a->ffn_dim);
     if (int rc = moe_scratch(ctx, a->n_tokens, a->n_experts, TK, a->dim, a->ffn_dim, &s, grouped ? a->n_experts : 0))
         return rc;
     RouterLaunch r{(const float*)ds5_ptr(a->x), (const uint8_t*)ds5_ptr(a->router_w), a->router_dtype,

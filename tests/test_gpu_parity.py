@@ -1211,13 +1211,14 @@ def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
 
 
 @pytest.mark.parametrize("T,dim,rdt", [(1, 2048, "f32"), (5, 2048, "f32"), (3, 2048, "f16"), (2, 256, "f32"),
-                                        (40, 2048, "f32")])
+                                        (20, 2048, "f32"), (40, 2048, "f32")])
 def test_moe_norm_equals_rmsnorm_then_moe(ctx, hip, oracle, T, dim, rdt):
     """ds5_hip_moe with x_norm (ffn_norm applied first) and the residual equals
     ds5_hip_rms_norm(x -> h2) then ds5_hip_moe(h2) with the residual, bit for bit, and
     leaves x as it was when out is another buffer: the norm inside the router's f32 logits
     kernel (rows above 256 elements), or written to the context's second buffer first (an
-    f16 router; dim 256: the serial order; 40 tokens: the logits in tiles, the experts
+    f16 router; dim 256: the serial order; 20 tokens: the norm in the per-token logits
+    kernel, the experts grouped on its h; 40 tokens: the logits in tiles, the experts
     grouped). The router ids and weights agree too."""
     g = np.random.default_rng(300 + T + dim)
     ffn, E, K = (768, 64, 8) if dim == 2048 else (64, 8, 2)
