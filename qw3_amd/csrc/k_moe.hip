@@ -278,6 +278,7 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(const float* __
                                                                  float* __restrict__ logits) {
 #pragma clang fp contract(off)
     constexpr uint32_t TR = 16 * RT, S = TR + 1;  // tile rows; LDS row stride (conflict-free transposed stores)
+    static_assert(kRtK == 64, "staging: 16 threads of float4s per row and chunk");
     __shared__ float xs[2][kRtK * S], ws[2][kRtK * S];
     const uint32_t t0 = blockIdx.x * TR, e0 = blockIdx.y * TR;
     const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
