@@ -1125,6 +1125,46 @@ def test_expert_mlp_grouped_threshold(ctx, hip, oracle):
         assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
 
 
+@pytest.mark.parametrize("case", ["f32_banks", "experts_2049"])
+def test_expert_mlp_many_pairs_not_grouped(ctx, hip, oracle, case):
+    """Many pairs per expert but banks the grouped path does not take: f32 banks (the
+    matrix-core products read Q8_0 only), or more experts than the sort's LDS holds
+    (2049): the wavefront kernels run (no sort), against the oracle within the
+    reordering bound."""
+    g = np.random.default_rng(11 + len(case))
+    T, dim, ffn, E, K = {"f32_banks": (64, 256, 64, 8, 4), "experts_2049": (1025, 32, 32, 2049, 4)}[case]
+    q8 = case != "f32_banks"
+    mk = lambda rows, k: (g.standard_normal((rows, k)) * 0.05).astype(np.float32)
+    Gf, Uf, Df = mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn)
+    if q8:
+        G, U, D = (oracle.q8_0_quantize(v) for v in (Gf, Uf, Df))
+        Gf, Uf, Df = oracle.q8_0_dequantize(G, dim), oracle.q8_0_dequantize(U, dim), oracle.q8_0_dequantize(D, ffn)
+    else:
+        G, U, D = Gf, Uf, Df
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    pairs = np.zeros(T * K, hip.PAIR_DTYPE)
+    pairs["token"] = np.repeat(np.arange(T), K)
+    pairs["expert"] = g.integers(0, E, T * K)
+    pairs["weight"] = g.random(T * K).astype(np.float32)
+    assert T * K >= 2 * E
+    out = ctx.createBuffer(T * dim * 4)
+    ctx.zero(out, T * dim * 4)
+    ctx.set_kernel_timing(True)
+    try:
+        hip.expertMlpSwiglu(ctx, ctx.from_numpy(x), *(ctx.from_numpy(v) for v in (G, U, D)),
+                            hip.DTYPE_Q8_0 if q8 else hip.DTYPE_F32, pairs, out, T, dim, ffn, E)
+        ctx.submit()
+        launches = {kn: ctx.kernel_time(kn)[0] for kn in ("moe_sort_kernel", "moe_gate_up_kernel")}
+    finally:
+        ctx.set_kernel_timing(False)
+    assert launches == {"moe_sort_kernel": 0, "moe_gate_up_kernel": 1}, launches
+    want = oracle.expert_mlp_swiglu(x, G, U, D, oracle.Q8_0 if q8 else oracle.F32, pairs.astype(oracle.PAIR_DTYPE), T,
+                                    dim, ffn, E)
+    bound = _expert_bound(x, Gf.astype(np.float64), Uf.astype(np.float64), Df.astype(np.float64), pairs, T, dim, ffn)
+    got = ctx.to_numpy(out, np.float32, (T, dim))
+    assert np.all(np.abs(got - want) <= bound + 2 * np.spacing(np.abs(want)))
+
+
 def test_expert_mlp_bad_pair_leaves_out(ctx, hip):
     """A pair out of range is ShapeMismatch before anything runs (out unchanged)."""
     bank = ctx.from_numpy(np.zeros((2 * 32, 34), np.uint8))
