@@ -457,25 +457,34 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                                                                       const MoeGemmTiles mt) {
     asm volatile("" ::DS5_GROUP_ARGS(g), "s"(xhi), "s"(xlo), "s"(row_exp), "s"(m), "s"(k));
     // this workgroup's entry and column tile (uniform); out may be the residual itself
+    // GRP: workgroup L = y * gridDim.x + x runs on XCD L % 8; XCD q takes the row tiles
+    // q, q + 8, ... with all their column tiles in a row, so a row tile's gathered x rows
+    // come into one L2 (gridDim.y a multiple of 8: every (column, row tile) once)
+    uint32_t bx = blockIdx.x, by = blockIdx.y;
+    if constexpr (GRP) {
+        const uint32_t L = blockIdx.y * gridDim.x + blockIdx.x, i = L / 8;
+        bx = i % gridDim.x;
+        by = L % 8 + 8 * (i / gridDim.x);
+    }
     const uint8_t* __restrict__ w = g.w[0];
     float* out = g.out[0];
     const float* res = g.res[0];
-    uint32_t n = g.n[0], tile = blockIdx.x;
+    uint32_t n = g.n[0], tile = bx;
     int entry = 0;
 #pragma unroll
     for (int e = 1; e < kMatmulGroupMax; e++)
-        if ((uint32_t)e < g.count && blockIdx.x >= g.wg0[e]) {
+        if ((uint32_t)e < g.count && bx >= g.wg0[e]) {
             w = g.w[e];
             out = g.out[e];
             res = g.res[e];
             n = g.n[e];
-            tile = blockIdx.x - g.wg0[e];
+            tile = bx - g.wg0[e];
             entry = e;
         }
-    uint32_t m0 = blockIdx.y * BM;
+    uint32_t m0 = by * BM;
     if constexpr (GRP) {
-        if (blockIdx.y >= *mt.count) return;  // workgroup-uniform, before any barrier
-        const uint4 te = mt.tiles[blockIdx.y];
+        if (by >= *mt.count) return;  // workgroup-uniform, before any barrier
+        const uint4 te = mt.tiles[by];
         m0 = te.x;
         m = te.y;
         w += (uint64_t)te.z * mt.w_stride;
@@ -952,8 +961,8 @@ static int launch_q8_gemm_grouped_t(ds5_hip_ctx* ctx, const uint16_t* hi, const 
     g.count = count;
     if (nt == 0 || max_tiles == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, true>),
-                     dim3(nt, max_tiles), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k, AttnPrepEpi{},
-                     mt);
+                     dim3(nt, (max_tiles + 7) / 8 * 8), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k,
+                     AttnPrepEpi{}, mt);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
 
