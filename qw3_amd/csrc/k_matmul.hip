@@ -457,15 +457,17 @@ __global__ __launch_bounds__(WM * WN * 64) void matmul_q8_mfma_kernel(const uint
                                                                       const MoeGemmTiles mt) {
     asm volatile("" ::DS5_GROUP_ARGS(g), "s"(xhi), "s"(xlo), "s"(row_exp), "s"(m), "s"(k));
     // this workgroup's entry and column tile (uniform); out may be the residual itself
-    // GRP: workgroup L = y * gridDim.x + x runs on XCD L % 8; XCD q takes the row tiles
-    // q, q + 8, ... with all their column tiles in a row, so a row tile's gathered x rows
-    // come into one L2 (gridDim.y a multiple of 8: every (column, row tile) once)
+    // Workgroup L = y * gridDim.x + x runs on XCD L % 8. With gridDim.y a multiple of 8
+    // (the launchers pad 8 or more row tiles to one), XCD q takes the row tiles q, q + 8,
+    // ... with all their column tiles in a row, so a row tile's x rows come into one L2
+    // (every (column, row tile) once; padding row tiles return at once).
     uint32_t bx = blockIdx.x, by = blockIdx.y;
-    if constexpr (GRP) {
-        const uint32_t L = blockIdx.y * gridDim.x + blockIdx.x, i = L / 8;
-        bx = i % gridDim.x;
-        by = L % 8 + 8 * (i / gridDim.x);
+    if (gridDim.y % 8 == 0) {
+        const uint32_t L = blockIdx.y * gridDim.x + blockIdx.x, li = L / 8;
+        bx = li % gridDim.x;
+        by = L % 8 + 8 * (li / gridDim.x);
     }
+    if (!GRP && by * BM >= m) return;  // workgroup-uniform, before any barrier
     const uint8_t* __restrict__ w = g.w[0];
     float* out = g.out[0];
     const float* res = g.res[0];
@@ -896,6 +898,12 @@ int launch_rows_q(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     return a.norm_w ? launch_rows_n<Q8, true>(ctx, a) : launch_rows_n<Q8, false>(ctx, a);
 }
 
+// Row tiles of a launch: 8 or more are padded to a multiple of 8 (the kernel's XCD order).
+static uint32_t gemm_row_tiles(uint32_t m, uint32_t bm) {
+    const uint32_t t = (m + bm - 1) / bm;
+    return t >= 8 ? (t + 7) / 8 * 8 : t;
+}
+
 // The split x is made once and shared by the group's products.
 template <int BM, int BN, int WM, int WN>
 int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
@@ -920,7 +928,7 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
     }
     if (tiles == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0>),
-                     dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
+                     dim3(tiles, gemm_row_tiles(a.m, BM)), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      AttnPrepEpi{}, MoeGemmTiles{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
@@ -961,7 +969,7 @@ static int launch_q8_gemm_grouped_t(ds5_hip_ctx* ctx, const uint16_t* hi, const 
     g.count = count;
     if (nt == 0 || max_tiles == 0) return DS5_OK;
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 0, true>),
-                     dim3(nt, (max_tiles + 7) / 8 * 8), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k,
+                     dim3(nt, gemm_row_tiles(max_tiles, 1)), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, 0u, k,
                      AttnPrepEpi{}, mt);
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
@@ -1009,7 +1017,7 @@ int launch_qkv_prep(ds5_hip_ctx* ctx, const QkvPrepLaunch& a) {
     g.count = 3;
     AttnPrepEpi ep{a.q_norm, a.k_norm, cs, a.q16, a.k_cache, a.v_cache, a.pos, a.n_q_heads, a.max_ctx, a.eps, a.q_scale};
     DS5_TIMED_LAUNCH(ctx, "matmul_q8_mfma_kernel", (matmul_q8_mfma_kernel<BM, BN, WM, WN, 1>),
-                     dim3(tiles, (a.m + BM - 1) / BM), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
+                     dim3(tiles, gemm_row_tiles(a.m, BM)), dim3(WM * WN * 64), 0, ctx->stream, hi, lo, row_exp, g, a.m, a.k,
                      ep, MoeGemmTiles{});
     return ds5_after_launch(ctx, "matmul_q8_mfma_kernel");
 }
