@@ -366,6 +366,59 @@ __global__ __launch_bounds__(kSplitThreads) void moe_h_split_kernel(const float*
     split_row(load, row, k, hi, lo, row_exp, red);
 }
 
+// The same planes, one wavefront per row (rows of k <= 256 R elements): the row's h stays
+// in registers between its maximum and its split, no barrier; the arithmetic of
+// split_row operation for operation.
+template <int R>
+__global__ __launch_bounds__(256) void moe_h_split_rows_kernel(const float* __restrict__ g,
+                                                               const float* __restrict__ u,
+                                                               uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                               int* __restrict__ row_exp, uint32_t k, uint32_t rows) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wavefront-uniform; the kernel has no barrier
+    const uint32_t kc = k / 4;
+    const float4* gr = (const float4*)(g + row * k);
+    const float4* ur = (const float4*)(u + row * k);
+    float4 h[R];
+    float mx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t c = lane + 64 * r;
+        h[r] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (c < kc) {
+            const float4 a = gr[c], b = ur[c];
+            h[r] = float4{a.x / (1.0f + expf(-a.x)) * b.x, a.y / (1.0f + expf(-a.y)) * b.y,
+                          a.z / (1.0f + expf(-a.z)) * b.z, a.w / (1.0f + expf(-a.w)) * b.w};
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(h[r].x), fabsf(h[r].y)), fmaxf(fabsf(h[r].z), fabsf(h[r].w))));
+        }
+    }
+    mx = wave_allreduce(mx, OpMax{});
+    const int e = (mx > 0.0f && mx <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(mx) - 1 : 0;
+    const int sh = kXExpBias - e;
+    if (lane == 0) row_exp[row] = e;
+    uint2* h2 = (uint2*)(hi + row * k);
+    uint2* l2 = (uint2*)(lo + row * k);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t c = lane + 64 * r;
+        if (c < kc) {
+            const float f[4] = {h[r].x, h[r].y, h[r].z, h[r].w};
+            uint32_t hb[4], lb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float s = __builtin_ldexpf(f[i], sh);
+                const _Float16 hv = (_Float16)s;
+                hb[i] = __builtin_bit_cast(uint16_t, hv);
+                lb[i] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hv));
+            }
+            h2[c] = uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+            l2[c] = uint2{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
+        }
+    }
+}
+
 // Four int8 (one dword) as four f16: bytes biased to q + 128, placed under the
 // f16 pattern 0x64 (1024 + q + 128, exact), then 1152 subtracted in f16.
 __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t u) {
@@ -948,8 +1001,16 @@ int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, uint32_t rows, uint32_
 int launch_moe_h_split(ds5_hip_ctx* ctx, const float* g, const float* u, uint32_t rows, uint32_t k, uint16_t* hi,
                        uint16_t* lo, int* row_exp) {
     if (rows == 0) return DS5_OK;
-    DS5_TIMED_LAUNCH(ctx, "moe_h_split_kernel", moe_h_split_kernel, dim3(rows), dim3(kSplitThreads), 0, ctx->stream,
-                     g, u, hi, lo, row_exp, k);
+    const dim3 g4((rows + 3) / 4);
+    if (k <= 1024)
+        DS5_TIMED_LAUNCH(ctx, "moe_h_split_kernel", moe_h_split_rows_kernel<4>, g4, dim3(256), 0, ctx->stream, g, u, hi,
+                         lo, row_exp, k, rows);
+    else if (k <= 2048)
+        DS5_TIMED_LAUNCH(ctx, "moe_h_split_kernel", moe_h_split_rows_kernel<8>, g4, dim3(256), 0, ctx->stream, g, u, hi,
+                         lo, row_exp, k, rows);
+    else
+        DS5_TIMED_LAUNCH(ctx, "moe_h_split_kernel", moe_h_split_kernel, dim3(rows), dim3(kSplitThreads), 0, ctx->stream,
+                         g, u, hi, lo, row_exp, k);
     return ds5_after_launch(ctx, "moe_h_split_kernel");
 }
 
