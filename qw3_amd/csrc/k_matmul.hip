@@ -988,8 +988,9 @@ int launch_gemm(ds5_hip_ctx* ctx, const MatmulGroupLaunch& a) {
 
 }  // namespace
 
-// The MoE experts' matrix-core path (rows sorted by expert): the x rows gathered and
-// split, the grouped products, h = silu(g) * u split.
+// The MoE experts' matrix-core path (rows sorted by expert): the tokens' x rows split,
+// the grouped products (sorted rows gather their token's plane row), h = silu(g) * u
+// split.
 int launch_x_split_rows(ds5_hip_ctx* ctx, const float* x, uint32_t rows, uint32_t k, uint16_t* hi, uint16_t* lo,
                         int* row_exp) {
     if (rows == 0) return DS5_OK;
