@@ -22,6 +22,10 @@
 // owning the 32-element blocks L + 64 j, a fixed-order wavefront reduction (so
 // they agree with the reference's serial dots to rounding). The combine adds
 // each product in the reference's order, rounding as it does.
+// Many tokens: the logits in token x expert tiles (router_logits_tile_kernel, the
+// same serial sums); from two pairs per expert the experts grouped by expert
+// (moe_sort_kernel, then Q8_0 matrix-core products per expert row tile,
+// launch_experts_grouped), each expert's weights read once per tile.
 #include <type_traits>
 
 #include "ds5_common.hpp"
