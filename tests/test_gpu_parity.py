@@ -1203,6 +1203,44 @@ def test_moe_device_equals_router_then_experts(ctx, hip, oracle, T, E):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [1, 64])
+def test_moe_graph_replays_match_eager(ctx, hip, oracle, T):
+    """ds5_hip_moe with ffn_norm and a residual captured into a HIP graph, replayed three
+    times with eager work and synchronisations between the replays: each replay's output is
+    bit-identical to the eager call's. T = 1: the norm in the logits kernel, the wavefront
+    experts; T = 64: the norm as its own launch, the logits in tiles, the experts grouped
+    (sort, split planes, grouped products, combine)."""
+    g = np.random.default_rng(900 + T)
+    dim, ffn, E, K = 2048, 768, 64, 8
+    rw = (g.standard_normal((E, dim)) * 0.03).astype(np.float32)
+    mk = lambda rows, k: oracle.q8_0_quantize((g.standard_normal((rows, k)) * 0.05).astype(np.float32))
+    banks = [ctx.from_numpy(v) for v in (mk(E * ffn, dim), mk(E * ffn, dim), mk(E * dim, ffn))]
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    nw = (1.0 + 0.05 * g.standard_normal(dim)).astype(np.float32)
+    res = g.standard_normal((T, dim)).astype(np.float32)
+    xb, rwb, nwb, rb = ctx.from_numpy(x), ctx.from_numpy(rw), ctx.from_numpy(nw), ctx.from_numpy(res)
+    out, other = ctx.createBuffer(T * dim * 4), ctx.createBuffer(T * dim * 4)
+    args = lambda o: hip.MoeArgs(xb, rwb, hip.DTYPE_F32, *banks, hip.DTYPE_Q8_0, o, hip.Buf(), hip.Buf(), T, dim, ffn,
+                                 E, K, 1, rb, nwb, 1e-6)
+    hip.moe(ctx, args(out))  # eager; also sizes the workspaces before the capture
+    want = ctx.to_numpy(out, np.float32)
+    gr = ctx.capture(lambda: hip.moe(ctx, args(out)))
+    try:
+        zeros = np.zeros(T * dim, np.float32)
+        for r in range(3):
+            ctx.upload(out, 0, zeros)
+            hip.moe(ctx, args(other))  # eager work between replays
+            ctx.submit()
+            gr.launch()
+            ctx.submit()
+            got = ctx.to_numpy(out, np.float32)
+            print(f"  replay {r}: bit-identical={np.array_equal(got, want)}", flush=True)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.array_equal(ctx.to_numpy(other, np.float32).view(np.uint32), want.view(np.uint32))
+    finally:
+        gr.destroy()
+
+
 @pytest.mark.parametrize("T", [1, 5, 64, 300])
 def test_moe_residual_equals_zero_moe_add(ctx, hip, oracle, T):
     """ds5_hip_moe with a residual (out = residual + the experts' sum from zero) equals the
