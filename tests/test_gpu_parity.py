@@ -888,6 +888,28 @@ def test_router_tiles_equal_per_token(ctx, hip, oracle, T, dim, E, dt):
         assert np.array_equal(ids, oi) and np.all(np.abs(wts - ow) <= 1e-6 * np.abs(ow))
 
 
+@pytest.mark.parametrize("case", ["q8_rows", "dim_102"])
+def test_router_many_tokens_untiled(ctx, hip, oracle, case):
+    """Many tokens whose rows the tiles do not take -- Q8_0 router rows, or a dim that is not
+    a multiple of 4 -- run the per-token kernel (no tile launch); ids equal the oracle's and
+    weights are within 1e-6 of them."""
+    g = np.random.default_rng(31 + len(case))
+    T, dim, E, K = (40, 256, 64, 8) if case == "q8_rows" else (40, 102, 48, 4)
+    x = g.standard_normal((T, dim)).astype(np.float32)
+    wf = (g.standard_normal((E, dim)) * 0.05).astype(np.float32)
+    w, wdt, odt = (oracle.q8_0_quantize(wf), hip.DTYPE_Q8_0, oracle.Q8_0) if case == "q8_rows" else \
+        (wf, hip.DTYPE_F32, oracle.F32)
+    ctx.set_kernel_timing(True)
+    try:
+        ids, wts = hip.routerTopK(ctx, ctx.from_numpy(x), ctx.from_numpy(w), wdt, T, dim, E, K, True)
+        assert ctx.kernel_time("router_logits_tile_kernel")[0] == 0
+        assert ctx.kernel_time("router_logits_kernel")[0] == 1
+    finally:
+        ctx.set_kernel_timing(False)
+    oi, ow = oracle.router_topk(x, w, odt, T, dim, E, K, True)
+    assert np.array_equal(ids, oi) and np.all(np.abs(wts - ow) <= 1e-6 * np.abs(ow))
+
+
 def test_router_hand_cases(ctx, hip):
     """kernels_c.zig:403-477: raw probabilities without renormalisation; exact ties go to
     the lower id."""
